@@ -1,0 +1,239 @@
+#!/usr/bin/env python3
+"""Benchmark: exact int64 GEMM effective TOPS at 4096^3, prefix 9, on one MI355X.
+
+Workload: RNS8_BOUNDED_I64, M = N = K = 4096, A and
+B int64 uniform in [-2^25, 2^25) from SplitMix64 streams, declared bound 2^62
+with FORCE_FIXED_PREFIX and max_prefix 9 (moduli 256 ... 227). One step =
+pack A + pack B (device int64 -> residue planes) + 9-plane int8 MFMA GEMM +
+Garner reconstruct to device int64, all through the rns8 C ABI device-resident
+entry points on one HIP stream. Inputs are resident in HBM before timing.
+
+Printed JSON: value = 2*M*N*K / (ms_per_step) in TOPS (effective exact-integer
+ops); roofline = the plane-GEMM kernel against the dense int8 MFMA peak
+(2*M*N*K*P int8 ops per launch / average launch time, HIP events on the
+launch stream); cpu_baseline = the CPU oracle (own restatement of the
+reference CPU_REFERENCE path) on a bounded row sample of the same GEMM, whose
+rows are also compared bit-exactly against the GPU output.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POPS
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    # name: (semantics, m, n, k, input bits, bound, prefix budget, forced)
+    "c3": ("i64", 4096, 4096, 4096, 25, 1 << 62, 9, True),
+    "c1": ("i64", 256, 256, 256, 20, 256 << 40, 0, False),
+    "c5": ("u64", 128, 128, 65536, 23, 1 << 62, 0, False),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
+              "(the path shards by output row blocks; see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import rns8_amd as r
+    from rns8_amd import hip, inputs
+
+    sem, M, N, K, bits, bound, budget, forced = CONFIGS[args.config]
+    signed = sem == "i64"
+    dt = np.int64 if signed else np.uint64
+    log(f"[bench] config {args.config}: {sem} {M}x{N}x{K} bits={bits}")
+    if signed:
+        A = inputs.int_range(inputs.operand_seed(args.seed, "A"), (M, K), bits)
+        B = inputs.int_range(inputs.operand_seed(args.seed, "B"), (K, N), bits)
+    else:
+        A = inputs.uint_range(inputs.operand_seed(args.seed, "A"), (M, K), bits)
+        B = inputs.uint_range(inputs.operand_seed(args.seed, "B"), (K, N), bits)
+
+    ctx = r.Context()
+    semantics = r.BOUNDED_I64 if signed else r.BOUNDED_U64
+    bk = r.BOUND_GLOBAL_MAX_ABS if signed else r.BOUND_GLOBAL_MAX_UNSIGNED
+    desc = r.gemm_desc(semantics, bk, M, N, K, bound=bound, max_prefix=budget,
+                       flags=r.PLAN_FORCE_FIXED_PREFIX if forced else 0)
+    plan = r.Plan(ctx, desc)
+    P = plan.prefix
+    Am = r.Matrix(ctx, r.matrix_desc(M, K, semantics, bk, P))
+    Bm = r.Matrix(ctx, r.matrix_desc(K, N, semantics, bk, P))
+    Cm = r.Matrix(ctx, r.matrix_desc(M, N, semantics, bk, P))
+    ws = r.Workspace(ctx, plan)
+    log(f"[bench] prefix {P}")
+
+    dA = hip.malloc(A.nbytes)
+    dB = hip.malloc(B.nbytes)
+    dC = hip.malloc(M * N * 8)
+    dS = hip.malloc(64)
+    hip.to_device(dA, A)
+    hip.to_device(dB, B)
+    hip.memset(dS, 0, 64)
+    stream = hip.stream_create()
+    L = r.lib()
+    pack = L.rns8_mi355x_pack_i64_device if signed else L.rns8_mi355x_pack_u64_device
+    export = L.rns8_mi355x_export_i64_device if signed else L.rns8_mi355x_export_u64_device
+
+    ev = [hip.event_create() for _ in range(5)]
+
+    def step(version: int, timed: bool):
+        if timed:
+            hip.event_record(ev[0], stream)
+        r.check(pack(ctx.ptr, Am.ptr, dA, K, 0, stream), "pack A")
+        if timed:
+            hip.event_record(ev[1], stream)
+        r.check(pack(ctx.ptr, Bm.ptr, dB, N, 0, stream), "pack B")
+        if timed:
+            hip.event_record(ev[2], stream)
+        r.check(L.rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, stream), "gemm")
+        if timed:
+            hip.event_record(ev[3], stream)
+        r.check(export(ctx.ptr, plan.ptr, Cm.ptr, dC, N, dS, stream), "export")
+        if timed:
+            hip.event_record(ev[4], stream)
+
+    for w in range(args.warmup):
+        step(w, False)
+    hip.stream_synchronize(stream)
+    log("[bench] warmup done")
+
+    # stage timing pass (events between stages)
+    stage = np.zeros(4)
+    for s in range(args.steps):
+        step(s, True)
+        t = [hip.event_elapsed_ms(ev[i], ev[i + 1]) for i in range(4)]
+        stage += np.array(t)
+    stage /= args.steps
+    log(f"[bench] stage ms: packA {stage[0]:.4f} packB {stage[1]:.4f} gemm {stage[2]:.4f} export {stage[3]:.4f}")
+
+    # end-to-end pass: K steps back to back, bracketed by synchronization
+    hip.synchronize()
+    start, stop = hip.event_create(), hip.event_create()
+    t0 = time.perf_counter()
+    hip.event_record(start, stream)
+    for s in range(args.steps):
+        step(s, False)
+    hip.event_record(stop, stream)
+    hip.stream_synchronize(stream)
+    t1 = time.perf_counter()
+    hip.synchronize()
+    ms_total = hip.event_elapsed_ms(start, stop)
+    ms_per_step = ms_total / args.steps
+    log(f"[bench] {args.steps} steps: {ms_total:.3f} ms (host clock {1e3 * (t1 - t0):.3f} ms)")
+
+    status = np.zeros(16, dtype=np.uint32)
+    hip.from_device(status, dS)
+    Cout = np.empty((M, N), dtype=dt)
+    hip.from_device(Cout, dC)
+    ops = 2.0 * M * N * K
+    value = ops / (ms_per_step * 1e-3) / 1e12
+    gemm_ops = ops * P
+    achieved = gemm_ops / (stage[2] * 1e-3) / 1e12
+
+    result = {
+        "metric": "exact int64 GEMM effective TOPS (2MNK/s) at 4096^3 prefix 9; % int8 MFMA peak",
+        "value": round(value, 3),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int64 (int8 residue MFMA)",
+        "data": "synthetic: SplitMix64 uniform [-2^25, 2^25) int64 operands, resident in HBM",
+        "config": {
+            "workload": f"RNS8_BOUNDED_I64 {M}x{N}x{K} prefix {P} (FORCE_FIXED_PREFIX), pack+GEMM+Garner device-resident"
+            if args.config == "c3" else f"{args.config} {sem} {M}x{N}x{K} prefix {P}",
+            "m": M, "n": N, "k": K, "prefix": P, "bound": str(bound),
+            "stage_ms": {"pack_a": round(stage[0], 4), "pack_b": round(stage[1], 4), "gemm": round(stage[2], 4),
+                         "export": round(stage[3], 4)},
+            "range_status": int(status[0]),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "plane_gemm_kernel<64>",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TOPS (int8)",
+            "frac": round(achieved / PEAK_INT8_TOPS, 4),
+            "traffic": None,
+            "per_launch_ops": gemm_ops,
+        },
+        "cpu_baseline": None,
+    }
+
+    if not args.no_cpu:
+        import oracle
+
+        threads = min(16, os.cpu_count() or 1)
+        oracle.set_threads(threads)
+        rows = 8
+        t0 = time.perf_counter()
+        st, ref = (oracle.gemm_i64 if signed else oracle.gemm_u64)(A, B, P, bound, row0=0, rows=rows)
+        t_small = time.perf_counter() - t0
+        # scale the sample to about --cpu-seconds (pack of B is a fixed cost)
+        rows2 = int(min(M, max(rows, rows * args.cpu_seconds / max(t_small, 1e-3))))
+        rows2 = max(8, (rows2 // 8) * 8)
+        t0 = time.perf_counter()
+        st, ref = (oracle.gemm_i64 if signed else oracle.gemm_u64)(A, B, P, bound, row0=0, rows=rows2)
+        t_cpu = time.perf_counter() - t0
+        match = bool(st == 0 and np.array_equal(ref, Cout[:rows2]))
+        cpu_tops = 2.0 * rows2 * N * K / t_cpu / 1e12
+        result["cpu_baseline"] = {
+            "value": round(cpu_tops, 6),
+            "unit": "TOPS",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"rows 0..{rows2 - 1} of C ({rows2}x{N}x{K}, pack of full B included), {t_cpu:.2f} s",
+            "rows_bit_exact_vs_gpu": match,
+            "cpu_model": _cpu_model(),
+        }
+        log(f"[bench] cpu baseline {cpu_tops:.5f} TOPS on {rows2} rows, match={match}")
+
+    print(json.dumps(result))
+    for e in ev + [start, stop]:
+        hip.event_destroy(e)
+    hip.stream_destroy(stream)
+    for p in (dA, dB, dC, dS):
+        hip.free(p)
+    return 0
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,145 @@
+/* MI355X extensions to the rns8 C ABI: the device-resident hot path.
+ *
+ * The reference ABI (rns8/rns8.h) takes and returns host memory and ends
+ * every call with a device synchronization, so each GEMM pays PCIe transfers.
+ * These entry points run the same pack -> plane GEMM -> Garner stages on
+ * operands that already live in HBM, enqueue their kernels on a caller
+ * stream and return without synchronizing. They have no counterpart in the
+ * reference; they are what a caller that chains GEMMs on the GPU (or a
+ * benchmark measuring the kernels rather than PCIe) binds. They reuse the
+ * same handles, validation and kernels as the host entry points.
+ *
+ * Conventions
+ *   - `stream` is a hipStream_t passed as void*; NULL selects the context's
+ *     own stream. Work is ordered on that stream only.
+ *   - Device pointers must be accessible from the context's device.
+ *   - Range violations are reported through `d_status`: a device uint32_t
+ *     that the caller zeroes before the call; the export kernel sets it
+ *     nonzero if any cell violates the contract. The output contents of such
+ *     a call are unspecified (the host exports keep `dst` untouched instead).
+ *   - Validation failures return before anything is enqueued.
+ */
+#ifndef RNS8_MI355X_H
+#define RNS8_MI355X_H
+
+#include <stdint.h>
+
+#include "rns8/rns8.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Prefix a plan created from `desc` would select (validation and prefix
+ * selection of rns8_create_plan, reference api_plan_public_api.inc:3-73 and
+ * api_plan_schedule.inc:263-278), without a context or device. Finite
+ * semantics report 0. */
+RNS8_API rns8_status rns8_mi355x_select_prefix(const rns8_gemm_desc* desc, uint32_t* out_prefix);
+
+/* Device-source variants of rns8_pack_i64 / rns8_pack_u64 / rns8_pack_finite_u8
+ * (reference rns8.h:848-911): `d_src` is device memory, row stride `ld`
+ * elements. For exact-wide matrices the magnitude proof is the global
+ * maximum |x| computed on the GPU (no per-row/column refinement). */
+RNS8_API rns8_status rns8_mi355x_pack_i64_device(
+    rns8_context* ctx,
+    rns8_matrix* matrix,
+    const int64_t* d_src,
+    int64_t ld,
+    uint64_t source_version,
+    void* stream);
+RNS8_API rns8_status rns8_mi355x_pack_u64_device(
+    rns8_context* ctx,
+    rns8_matrix* matrix,
+    const uint64_t* d_src,
+    int64_t ld,
+    uint64_t source_version,
+    void* stream);
+RNS8_API rns8_status rns8_mi355x_pack_finite_u8_device(
+    rns8_context* ctx,
+    rns8_matrix* matrix,
+    uint16_t modulus,
+    const uint8_t* d_src,
+    int64_t ld,
+    uint64_t source_version,
+    void* stream);
+
+/* Asynchronous rns8_gemm_rns / rns8_gemm_finite_u8 (reference rns8.h:988,
+ * 1098): same validation and admission, kernels enqueued on `stream`. */
+RNS8_API rns8_status rns8_mi355x_gemm_rns_async(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    const rns8_matrix* A,
+    const rns8_matrix* B,
+    rns8_matrix* C,
+    rns8_workspace* workspace,
+    void* stream);
+RNS8_API rns8_status rns8_mi355x_gemm_finite_u8_async(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    uint16_t modulus,
+    const rns8_matrix* A,
+    const rns8_matrix* B,
+    rns8_matrix* C,
+    rns8_workspace* workspace,
+    void* stream);
+
+/* Device-destination variants of the exports (reference rns8.h:1146-1242). */
+RNS8_API rns8_status rns8_mi355x_export_i64_device(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    const rns8_matrix* C,
+    int64_t* d_dst,
+    int64_t ld,
+    uint32_t* d_status,
+    void* stream);
+RNS8_API rns8_status rns8_mi355x_export_u64_device(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    const rns8_matrix* C,
+    uint64_t* d_dst,
+    int64_t ld,
+    uint32_t* d_status,
+    void* stream);
+RNS8_API rns8_status rns8_mi355x_export_exact_wide_signed_limbs_device(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    const rns8_matrix* C,
+    uint64_t* d_dst,
+    int64_t ld,
+    uint32_t limb_count,
+    uint32_t* d_status,
+    void* stream);
+RNS8_API rns8_status rns8_mi355x_export_exact_wide_unsigned_limbs_device(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    const rns8_matrix* C,
+    uint64_t* d_dst,
+    int64_t ld,
+    uint32_t limb_count,
+    uint32_t* d_status,
+    void* stream);
+RNS8_API rns8_status rns8_mi355x_export_finite_u8_device(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    uint16_t modulus,
+    const rns8_matrix* C,
+    uint8_t* d_dst,
+    int64_t ld,
+    void* stream);
+
+/* Layout of a resident matrix's planes in HBM ("rns8_mi355x_planes_v1"):
+ * plane p, row r, column c lives at d_planes + p*plane_pitch + r*row_pitch + c
+ * as a centered int8 residue; padding bytes are zero. Lets device code read
+ * or produce residue planes directly. */
+RNS8_API rns8_status rns8_mi355x_get_matrix_planes(
+    const rns8_matrix* matrix,
+    void** d_planes,
+    int64_t* row_pitch,
+    int64_t* plane_pitch,
+    uint32_t* plane_count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RNS8_MI355X_H */

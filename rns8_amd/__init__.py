@@ -1,0 +1,270 @@
+"""rns8 for MI355X: Python host mirror of the rns8 C ABI.
+
+The product is the shared library rns8_amd/librns8.so (C ABI in include/,
+gfx950 kernels in rns8_amd/csrc/). This module binds it through ctypes with
+the same entry-point names, argument meaning and status codes, so tests and
+the benchmark drive exactly what a C caller would. There is no fallback: if
+the library is missing, `lib()` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import abi
+from .abi import (  # noqa: F401  (re-exported constants)
+    BACKEND_AUTO,
+    BACKEND_CPU_REFERENCE,
+    BACKEND_HIP_DIRECT,
+    BOUND_GLOBAL_MAX_ABS,
+    BOUND_GLOBAL_MAX_UNSIGNED,
+    BOUND_INPUT_RANGE_AND_K,
+    BOUND_NONE,
+    BOUNDED_I64,
+    BOUNDED_U64,
+    EXACT_WIDE_SIGNED,
+    EXACT_WIDE_UNSIGNED,
+    FINITE_FIELD_U8,
+    FINITE_RING_U8,
+    INVALID_ARGUMENT,
+    PLAN_FORCE_FIXED_PREFIX,
+    RANGE_ERROR,
+    SUCCESS,
+    UNSUPPORTED_BACKEND,
+)
+
+_LIB = None
+
+
+def lib() -> C.CDLL:
+    global _LIB
+    if _LIB is None:
+        _LIB = abi.load_library()
+    return _LIB
+
+
+class Rns8Error(RuntimeError):
+    def __init__(self, what: str, status: int):
+        super().__init__(f"{what}: {status_string(status)} ({status})")
+        self.status = status
+
+
+def status_string(status: int) -> str:
+    return lib().rns8_status_string(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != abi.SUCCESS:
+        raise Rns8Error(what, status)
+
+
+def gemm_desc(semantics, bound_kind, m, n, k, bound=0, max_prefix=0, flags=0, finite_modulus=0, lhs_bound=0,
+              rhs_bound=0, requested_backend=BACKEND_AUTO, tile_m=0, tile_n=0) -> abi.GemmDesc:
+    d = abi.new_struct(abi.GemmDesc)
+    d.semantics = semantics
+    d.bound_kind = bound_kind
+    d.requested_backend = requested_backend
+    d.m, d.n, d.k = m, n, k
+    d.bound = bound
+    d.max_prefix = max_prefix
+    d.tile_m, d.tile_n = tile_m, tile_n
+    d.finite_modulus = finite_modulus
+    d.flags = flags
+    d.lhs_bound, d.rhs_bound = lhs_bound, rhs_bound
+    return d
+
+
+def matrix_desc(rows, cols, semantics, bound_kind, max_prefix=0, logical_ld=0) -> abi.MatrixDesc:
+    d = abi.new_struct(abi.MatrixDesc)
+    d.rows, d.cols = rows, cols
+    d.logical_ld = logical_ld
+    d.semantics = semantics
+    d.logical_layout = abi.LAYOUT_ROW_MAJOR
+    d.bound_kind = bound_kind
+    d.max_prefix = max_prefix
+    return d
+
+
+def select_prefix(desc: abi.GemmDesc) -> tuple[int, int]:
+    """(status, prefix) for the plan `desc` would create (no device needed)."""
+    out = C.c_uint32(0)
+    st = lib().rns8_mi355x_select_prefix(C.byref(desc), C.byref(out))
+    return st, out.value
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class _Handle:
+    _destroy = ""
+
+    def __init__(self):
+        self.ptr = C.c_void_p()
+
+    def close(self):
+        if self.ptr:
+            getattr(lib(), self._destroy)(self.ptr)
+            self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class Context(_Handle):
+    _destroy = "rns8_destroy_context"
+
+    def __init__(self, device_id: int = -1, backend: int | None = None):
+        super().__init__()
+        opts = None
+        if backend is not None:
+            opts = abi.new_struct(abi.ContextOptions)
+            opts.requested_backend = backend
+        st = lib().rns8_create_context(device_id, C.byref(opts) if opts is not None else None, C.byref(self.ptr))
+        check(st, "rns8_create_context")
+
+
+class Plan(_Handle):
+    _destroy = "rns8_destroy_plan"
+
+    def __init__(self, ctx: Context, desc: abi.GemmDesc):
+        super().__init__()
+        self.desc = desc
+        check(lib().rns8_create_plan(ctx.ptr, C.byref(desc), C.byref(self.ptr)), "rns8_create_plan")
+
+    def schedule_info(self) -> abi.PlanScheduleInfo:
+        info = abi.new_struct(abi.PlanScheduleInfo)
+        check(lib().rns8_get_plan_schedule_info(self.ptr, C.byref(info)), "rns8_get_plan_schedule_info")
+        return info
+
+    @property
+    def prefix(self) -> int:
+        return self.schedule_info().max_selected_prefix
+
+
+class Workspace(_Handle):
+    _destroy = "rns8_destroy_workspace"
+
+    def __init__(self, ctx: Context, plan: Plan):
+        super().__init__()
+        check(lib().rns8_create_workspace(ctx.ptr, plan.ptr, C.byref(self.ptr)), "rns8_create_workspace")
+
+
+class Matrix(_Handle):
+    _destroy = "rns8_destroy_matrix"
+
+    def __init__(self, ctx: Context, desc: abi.MatrixDesc):
+        super().__init__()
+        self.rows, self.cols = desc.rows, desc.cols
+        check(lib().rns8_create_matrix(ctx.ptr, C.byref(desc), C.byref(self.ptr)), "rns8_create_matrix")
+
+    def storage_info(self) -> abi.MatrixStorageInfo:
+        info = abi.new_struct(abi.MatrixStorageInfo)
+        check(lib().rns8_get_matrix_storage_info(self.ptr, C.byref(info)), "rns8_get_matrix_storage_info")
+        return info
+
+    def planes(self):
+        p, rp, pp, n = C.c_void_p(), C.c_int64(), C.c_int64(), C.c_uint32()
+        check(lib().rns8_mi355x_get_matrix_planes(self.ptr, C.byref(p), C.byref(rp), C.byref(pp), C.byref(n)),
+              "rns8_mi355x_get_matrix_planes")
+        return p.value, rp.value, pp.value, n.value
+
+    def read_residues(self, nplanes: int | None = None) -> np.ndarray:
+        """Copy the resident planes to host as int8 [planes][rows][cols]."""
+        from . import hip
+
+        ptr, row_pitch, plane_pitch, count = self.planes()
+        count = count if nplanes is None else nplanes
+        raw = np.empty(plane_pitch * count, dtype=np.int8)
+        hip.from_device(raw, ptr)
+        out = np.empty((count, self.rows, self.cols), dtype=np.int8)
+        for p in range(count):
+            plane = raw[p * plane_pitch:p * plane_pitch + self.rows * row_pitch].reshape(self.rows, row_pitch)
+            out[p] = plane[:, :self.cols]
+        return out
+
+
+# ---- host entry points (status-returning, like the C ABI) -------------------
+
+
+def pack_i64(ctx, matrix, src: np.ndarray, source_version=0, ld=None) -> int:
+    src = np.ascontiguousarray(src, dtype=np.int64) if ld is None else src
+    return lib().rns8_pack_i64(ctx.ptr, matrix.ptr, _ptr(src), ld or src.shape[1], source_version)
+
+
+def pack_u64(ctx, matrix, src: np.ndarray, source_version=0, ld=None) -> int:
+    src = np.ascontiguousarray(src, dtype=np.uint64) if ld is None else src
+    return lib().rns8_pack_u64(ctx.ptr, matrix.ptr, _ptr(src), ld or src.shape[1], source_version)
+
+
+def pack_finite_u8(ctx, matrix, modulus, src: np.ndarray, source_version=0, ld=None) -> int:
+    src = np.ascontiguousarray(src, dtype=np.uint8) if ld is None else src
+    return lib().rns8_pack_finite_u8(ctx.ptr, matrix.ptr, modulus, _ptr(src), ld or src.shape[1], source_version)
+
+
+def gemm_rns(ctx, plan, A, B, Cm, ws) -> int:
+    return lib().rns8_gemm_rns(ctx.ptr, plan.ptr, A.ptr, B.ptr, Cm.ptr, ws.ptr)
+
+
+def gemm_finite_u8(ctx, plan, modulus, A, B, Cm, ws) -> int:
+    return lib().rns8_gemm_finite_u8(ctx.ptr, plan.ptr, modulus, A.ptr, B.ptr, Cm.ptr, ws.ptr)
+
+
+def export_i64(ctx, plan, Cm, dst: np.ndarray) -> int:
+    return lib().rns8_export_i64(ctx.ptr, plan.ptr, Cm.ptr, _ptr(dst), dst.shape[1])
+
+
+def export_u64(ctx, plan, Cm, dst: np.ndarray) -> int:
+    return lib().rns8_export_u64(ctx.ptr, plan.ptr, Cm.ptr, _ptr(dst), dst.shape[1])
+
+
+def export_finite_u8(ctx, plan, modulus, Cm, dst: np.ndarray) -> int:
+    return lib().rns8_export_finite_u8(ctx.ptr, plan.ptr, modulus, Cm.ptr, _ptr(dst), dst.shape[1])
+
+
+def export_exact_wide_signed_limbs(ctx, plan, Cm, dst: np.ndarray, limbs: int) -> int:
+    """dst: uint64 [rows][ld*limbs] (element (r, c) at dst[r, c*limbs:(c+1)*limbs])."""
+    return lib().rns8_export_exact_wide_signed_limbs(ctx.ptr, plan.ptr, Cm.ptr, _ptr(dst), dst.shape[1] // limbs, limbs)
+
+
+def export_exact_wide_unsigned_limbs(ctx, plan, Cm, dst: np.ndarray, limbs: int) -> int:
+    return lib().rns8_export_exact_wide_unsigned_limbs(ctx.ptr, plan.ptr, Cm.ptr, _ptr(dst), dst.shape[1] // limbs,
+                                                       limbs)
+
+
+def gemm_i64_oneshot(ctx, desc, A: np.ndarray, B: np.ndarray, C_out: np.ndarray | None = None):
+    A = np.ascontiguousarray(A, dtype=np.int64)
+    B = np.ascontiguousarray(B, dtype=np.int64)
+    out = C_out if C_out is not None else np.zeros((A.shape[0], B.shape[1]), dtype=np.int64)
+    st = lib().rns8_gemm_i64_oneshot(ctx.ptr, C.byref(desc), _ptr(A), A.shape[1], _ptr(B), B.shape[1], _ptr(out),
+                                     out.shape[1])
+    return st, out
+
+
+def gemm_u64_oneshot(ctx, desc, A: np.ndarray, B: np.ndarray, C_out: np.ndarray | None = None):
+    A = np.ascontiguousarray(A, dtype=np.uint64)
+    B = np.ascontiguousarray(B, dtype=np.uint64)
+    out = C_out if C_out is not None else np.zeros((A.shape[0], B.shape[1]), dtype=np.uint64)
+    st = lib().rns8_gemm_u64_oneshot(ctx.ptr, C.byref(desc), _ptr(A), A.shape[1], _ptr(B), B.shape[1], _ptr(out),
+                                     out.shape[1])
+    return st, out
+
+
+def gemm_finite_u8_oneshot(ctx, desc, modulus, A: np.ndarray, B: np.ndarray, field: bool,
+                           C_out: np.ndarray | None = None):
+    A = np.ascontiguousarray(A, dtype=np.uint8)
+    B = np.ascontiguousarray(B, dtype=np.uint8)
+    out = C_out if C_out is not None else np.zeros((A.shape[0], B.shape[1]), dtype=np.uint8)
+    fn = lib().rns8_gemm_finite_field_u8_oneshot if field else lib().rns8_gemm_finite_ring_u8_oneshot
+    st = fn(ctx.ptr, C.byref(desc), modulus, _ptr(A), A.shape[1], _ptr(B), B.shape[1], _ptr(out), out.shape[1])
+    return st, out

@@ -1,0 +1,827 @@
+// rns8 ABI execution: pack, plane GEMM, export and one-shot entry points,
+// plus the device-resident MI355X extensions (rns8_mi355x.h).
+//
+// Order of checks and statuses follows the reference:
+//   rns8_pack_*            src/core/api_pack.cpp:31-305
+//   rns8_gemm_rns          src/core/api_gemm.cpp:50-111, 838-983
+//   rns8_gemm_finite_u8    src/core/api_gemm.cpp:113-160, 1281-1330
+//   rns8_export_*          src/core/api_export.cpp:5-53, 307-803
+//   one-shot               src/core/api_oneshot.cpp:78-133, 440-677
+//   exact-wide proofs      src/core/exact_range.hpp:16-171
+// Kernels run on the context's stream (or the caller's, for the extensions);
+// host entry points synchronize before returning, like the reference.
+#include <algorithm>
+#include <cstring>
+#include <limits>
+#include <thread>
+#include <vector>
+
+#include "handles.hpp"
+#include "kernels.hpp"
+
+namespace rns8x {
+namespace {
+
+bool valid_access(int64_t rows, int64_t cols, int64_t ld) {
+  if (rows <= 0 || cols <= 0 || ld < cols) return false;
+  return rows <= std::numeric_limits<int64_t>::max() / ld;
+}
+
+bool valid_limb_access(int64_t rows, int64_t cols, int64_t ld, uint32_t limbs) {
+  if (!valid_access(rows, cols, ld) || limbs == 0 || limbs > 32) return false;
+  const int64_t max = std::numeric_limits<int64_t>::max();
+  if (ld > max / static_cast<int64_t>(limbs)) return false;
+  return rows <= max / (ld * static_cast<int64_t>(limbs));
+}
+
+uint64_t output_source_version(uint64_t a, uint64_t b) {
+  // reference api_plan_workspace_fingerprint.inc:18-23
+  uint64_t h = 1469598103934665603ull;
+  h ^= a;
+  h *= 1099511628211ull;
+  h ^= b;
+  h *= 1099511628211ull;
+  return h == 0 ? 1 : h;
+}
+
+// ---- exact-wide magnitude proofs (reference exact_range.hpp) ----------------
+
+bool exact_range_fits(rns8_semantics s, const I256& bound, const I256& product) {
+  if (bound.negative()) return false;
+  return s == RNS8_EXACT_WIDE_SIGNED ? (bound + bound) < product : bound < product;
+}
+
+void add_exact_value(ExactAxis& a, const I256& v, bool first) {
+  const I256 mag = v.abs();
+  a.max_magnitude = imax(a.max_magnitude, mag);
+  a.absolute_sum = a.absolute_sum + mag;
+  a.sum = a.sum + v;
+  if (first) {
+    a.minimum = v;
+    a.maximum = v;
+  } else {
+    a.minimum = imin(a.minimum, v);
+    a.maximum = imax(a.maximum, v);
+  }
+  a.sum_known = true;
+}
+
+I256 axis_center(const ExactAxis& a) { return (a.minimum + a.maximum).half_trunc(); }
+
+I256 axis_deviation_max(const ExactAxis& a, const I256& c) { return imax((a.minimum - c).abs(), (a.maximum - c).abs()); }
+
+// exact_range.hpp:52-78 (two linear scans of the host input)
+template <typename T>
+void native_exact_ranges(const T* src, int64_t rows, int64_t cols, int64_t ld, I256& maximum,
+                         std::vector<ExactAxis>& row_axes, std::vector<ExactAxis>& col_axes) {
+  row_axes.assign(static_cast<std::size_t>(rows), ExactAxis{});
+  col_axes.assign(static_cast<std::size_t>(cols), ExactAxis{});
+  auto value = [](T x) { return std::is_signed<T>::value ? I256::from_i64(static_cast<int64_t>(x))
+                                                         : I256::from_u64(static_cast<uint64_t>(x)); };
+  maximum = I256();
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t c = 0; c < cols; ++c) {
+      const I256 v = value(src[r * ld + c]);
+      add_exact_value(row_axes[r], v, c == 0);
+      add_exact_value(col_axes[c], v, r == 0);
+    }
+    maximum = imax(maximum, row_axes[r].max_magnitude);
+  }
+  std::vector<I256> col_center(static_cast<std::size_t>(cols));
+  for (int64_t c = 0; c < cols; ++c) col_center[c] = axis_center(col_axes[c]);
+  for (int64_t r = 0; r < rows; ++r) {
+    const I256 rc = axis_center(row_axes[r]);
+    for (int64_t c = 0; c < cols; ++c) {
+      const I256 v = value(src[r * ld + c]);
+      row_axes[r].deviation_sum = row_axes[r].deviation_sum + (v - rc).abs();
+      col_axes[c].deviation_sum = col_axes[c].deviation_sum + (v - col_center[c]).abs();
+    }
+  }
+}
+
+// exact_range.hpp:80-99
+I256 axis_product_bound(const ExactAxis& a, const ExactAxis& b, int64_t k) {
+  const I256 kk = I256::from_u64(static_cast<uint64_t>(k));
+  I256 bound = kk * a.max_magnitude * b.max_magnitude;
+  bound = imin(bound, a.absolute_sum * b.max_magnitude);
+  bound = imin(bound, a.max_magnitude * b.absolute_sum);
+  if (a.sum_known && b.sum_known) {
+    const I256 ca = axis_center(a), cb = axis_center(b);
+    const I256 da = axis_deviation_max(a, ca), db = axis_deviation_max(b, cb);
+    I256 rem = kk * da * db;
+    rem = imin(rem, a.deviation_sum * db);
+    rem = imin(rem, da * b.deviation_sum);
+    const I256 center_term = ca * b.sum + cb * a.sum - kk * ca * cb;
+    bound = imin(bound, center_term.abs() + rem);
+  }
+  return bound;
+}
+
+ExactAxis uniform_axis(const I256& maximum, int64_t length) {
+  ExactAxis a;
+  a.max_magnitude = maximum;
+  a.absolute_sum = I256::from_u64(static_cast<uint64_t>(length)) * maximum;
+  return a;
+}
+
+// exact_range.hpp:104-141 + 143-157: output bound of C = A x B and the
+// per-row / per-column summaries C carries into a later GEMM.
+rns8_status exact_gemm_range(const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B, I256& bound,
+                             std::vector<ExactAxis>* out_rows, std::vector<ExactAxis>* out_cols) {
+  if (!exact_wide(plan.desc.semantics)) return RNS8_SUCCESS;
+  if (A.exact_prefix < plan.prefix || B.exact_prefix < plan.prefix) return RNS8_RANGE_ERROR;
+  const int64_t m = plan.desc.m, n = plan.desc.n, k = plan.desc.k;
+  const bool a_rows = A.exact_rows.size() == static_cast<std::size_t>(m);
+  const bool b_cols = B.exact_cols.size() == static_cast<std::size_t>(n);
+  bound = I256::from_u64(static_cast<uint64_t>(k)) * A.exact_max * B.exact_max;
+  if (out_rows) out_rows->clear();
+  if (out_cols) out_cols->clear();
+  if (a_rows || b_cols) {
+    const ExactAxis fa = uniform_axis(A.exact_max, k);
+    const ExactAxis fb = uniform_axis(B.exact_max, k);
+    std::vector<ExactAxis> rows(static_cast<std::size_t>(m)), cols(static_cast<std::size_t>(n));
+    // rows are independent: split them over host threads; column summaries
+    // are merged per thread then reduced
+    unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    if (static_cast<int64_t>(nt) > m) nt = static_cast<unsigned>(m);
+    std::vector<std::vector<ExactAxis>> col_parts(nt, std::vector<ExactAxis>(static_cast<std::size_t>(n)));
+    std::vector<I256> maxima(nt);
+    std::vector<std::thread> pool;
+    for (unsigned t = 0; t < nt; ++t) {
+      pool.emplace_back([&, t]() {
+        const int64_t r0 = m * t / nt, r1 = m * (t + 1) / nt;
+        for (int64_t r = r0; r < r1; ++r) {
+          const ExactAxis& a = a_rows ? A.exact_rows[r] : fa;
+          for (int64_t c = 0; c < n; ++c) {
+            const ExactAxis& b = b_cols ? B.exact_cols[c] : fb;
+            const I256 cell = axis_product_bound(a, b, k);
+            maxima[t] = imax(maxima[t], cell);
+            rows[r].max_magnitude = imax(rows[r].max_magnitude, cell);
+            rows[r].absolute_sum = rows[r].absolute_sum + cell;
+            ExactAxis& cc = col_parts[t][c];
+            cc.max_magnitude = imax(cc.max_magnitude, cell);
+            cc.absolute_sum = cc.absolute_sum + cell;
+          }
+        }
+      });
+    }
+    for (auto& th : pool) th.join();
+    I256 maximum;
+    for (unsigned t = 0; t < nt; ++t) {
+      maximum = imax(maximum, maxima[t]);
+      for (int64_t c = 0; c < n; ++c) {
+        cols[c].max_magnitude = imax(cols[c].max_magnitude, col_parts[t][c].max_magnitude);
+        cols[c].absolute_sum = cols[c].absolute_sum + col_parts[t][c].absolute_sum;
+      }
+    }
+    bound = imin(bound, maximum);
+    if (out_rows) out_rows->swap(rows);
+    if (out_cols) out_cols->swap(cols);
+  }
+  return exact_range_fits(plan.desc.semantics, bound, plan.product) ? RNS8_SUCCESS : RNS8_RANGE_ERROR;
+}
+
+// ---- shared validation --------------------------------------------------------
+
+rns8_status check_plan_ctx_ws(const rns8_context& ctx, const rns8_plan& plan, const rns8_workspace& ws) {
+  if (plan.backend != ctx.backend || ws.backend != plan.backend) return RNS8_INVALID_ARGUMENT;
+  if (ws.semantics != plan.desc.semantics || ws.bound_kind != plan.desc.bound_kind) return RNS8_INVALID_ARGUMENT;
+  if (ws.m != plan.desc.m || ws.n != plan.desc.n || ws.k != plan.desc.k || ws.prefix != plan.prefix)
+    return RNS8_WORKSPACE_TOO_SMALL;
+  if (plan.splitk_bytes > ws.splitk_bytes) return RNS8_WORKSPACE_TOO_SMALL;
+  if (plan.device_id != ctx.device_id || ws.device_id != ctx.device_id) return RNS8_INVALID_ARGUMENT;
+  return RNS8_SUCCESS;
+}
+
+// reference api_gemm.cpp:50-111
+rns8_status check_rns_operands(const rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& A,
+                               const rns8_matrix& B, const rns8_matrix& C) {
+  if (!uses_rns_storage(plan.desc.semantics) || plan.prefix == 0) return RNS8_INVALID_ARGUMENT;
+  if (A.backend != plan.backend || B.backend != plan.backend || C.backend != plan.backend)
+    return RNS8_INVALID_ARGUMENT;
+  if (A.device_id != ctx.device_id || B.device_id != ctx.device_id || C.device_id != ctx.device_id)
+    return RNS8_INVALID_ARGUMENT;
+  const uint32_t sp = storage_prefix(plan);
+  const rns8_bound_kind bk = storage_bound_kind(plan);
+  if (!matrix_matches(A, plan.desc.semantics, bk, plan.desc.m, plan.desc.k, sp) ||
+      !matrix_matches(B, plan.desc.semantics, bk, plan.desc.k, plan.desc.n, sp) ||
+      !matrix_matches(C, plan.desc.semantics, bk, plan.desc.m, plan.desc.n, sp))
+    return RNS8_INVALID_ARGUMENT;
+  if (!A.device_current || !B.device_current) return RNS8_INVALID_ARGUMENT;
+  // C is written while A and B are read by other workgroups: no aliasing
+  if (&A == &C || &B == &C) return RNS8_INVALID_ARGUMENT;
+  return RNS8_SUCCESS;
+}
+
+// reference api_gemm.cpp:113-160
+rns8_status check_finite_operands(const rns8_context& ctx, const rns8_plan& plan, uint16_t modulus,
+                                  const rns8_matrix& A, const rns8_matrix& B, const rns8_matrix& C) {
+  if (!uses_finite_storage(plan.desc.semantics) || !valid_finite_modulus(plan.desc.semantics, modulus) ||
+      plan.desc.finite_modulus != modulus)
+    return RNS8_INVALID_ARGUMENT;
+  if (A.backend != plan.backend || B.backend != plan.backend || C.backend != plan.backend)
+    return RNS8_INVALID_ARGUMENT;
+  if (A.device_id != ctx.device_id || B.device_id != ctx.device_id || C.device_id != ctx.device_id)
+    return RNS8_INVALID_ARGUMENT;
+  if (!matrix_matches(A, plan.desc.semantics, RNS8_BOUND_NONE, plan.desc.m, plan.desc.k, 0) ||
+      !matrix_matches(B, plan.desc.semantics, RNS8_BOUND_NONE, plan.desc.k, plan.desc.n, 0) ||
+      !matrix_matches(C, plan.desc.semantics, RNS8_BOUND_NONE, plan.desc.m, plan.desc.n, 0))
+    return RNS8_INVALID_ARGUMENT;
+  if (!A.device_current || !B.device_current || A.finite_modulus != modulus || B.finite_modulus != modulus)
+    return RNS8_INVALID_ARGUMENT;
+  if (&A == &C || &B == &C) return RNS8_INVALID_ARGUMENT;
+  return RNS8_SUCCESS;
+}
+
+// reference api_export.cpp:5-53
+rns8_status check_export(const rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& C,
+                         rns8_semantics semantics) {
+  if (plan.backend != ctx.backend || C.backend != plan.backend || plan.desc.semantics != semantics)
+    return RNS8_INVALID_ARGUMENT;
+  if (C.device_id != ctx.device_id || plan.device_id != ctx.device_id) return RNS8_INVALID_ARGUMENT;
+  if (!matrix_matches(C, semantics, storage_bound_kind(plan), plan.desc.m, plan.desc.n, storage_prefix(plan)))
+    return RNS8_INVALID_ARGUMENT;
+  if (!C.device_current) return RNS8_INVALID_ARGUMENT;
+  if (exact_wide(semantics) && C.exact_prefix != 0 &&
+      (C.exact_prefix < plan.prefix || !exact_range_fits(semantics, C.exact_max, plan.product)))
+    return RNS8_RANGE_ERROR;
+  return RNS8_SUCCESS;
+}
+
+rns8_status check_finite_export(const rns8_context& ctx, const rns8_plan& plan, uint16_t modulus,
+                                const rns8_matrix& C) {
+  if (!uses_finite_storage(plan.desc.semantics) || plan.desc.finite_modulus != modulus ||
+      !valid_finite_modulus(plan.desc.semantics, modulus))
+    return RNS8_INVALID_ARGUMENT;
+  if (plan.backend != ctx.backend || C.backend != plan.backend || C.device_id != ctx.device_id)
+    return RNS8_INVALID_ARGUMENT;
+  if (!matrix_matches(C, plan.desc.semantics, RNS8_BOUND_NONE, plan.desc.m, plan.desc.n, 0))
+    return RNS8_INVALID_ARGUMENT;
+  if (!C.device_current || C.finite_modulus != modulus) return RNS8_INVALID_ARGUMENT;
+  return RNS8_SUCCESS;
+}
+
+rns8_status sync(hipStream_t s) { return hipStreamSynchronize(s) == hipSuccess ? RNS8_SUCCESS : RNS8_BACKEND_FAILURE; }
+
+// ---- pack ------------------------------------------------------------------------
+
+enum class Source { Host, Device };
+
+template <typename T>
+rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, int64_t ld, uint64_t sv, Source where,
+                        void* stream_arg) {
+  constexpr bool is_signed = std::is_same<T, int64_t>::value;
+  if (!ctx || !matrix || !src || !valid_access(matrix->desc.rows, matrix->desc.cols, ld))
+    return RNS8_INVALID_ARGUMENT;
+  const rns8_semantics bounded = is_signed ? RNS8_BOUNDED_I64 : RNS8_BOUNDED_U64;
+  const rns8_semantics wide = is_signed ? RNS8_EXACT_WIDE_SIGNED : RNS8_EXACT_WIDE_UNSIGNED;
+  if (matrix->desc.semantics != bounded && matrix->desc.semantics != wide) return RNS8_INVALID_ARGUMENT;
+  if (ctx->backend != matrix->backend || matrix->device_id != ctx->device_id) return RNS8_INVALID_ARGUMENT;
+  const int64_t rows = matrix->desc.rows, cols = matrix->desc.cols;
+  const bool same_source = sv != 0 && matrix->source_version == sv && matrix->device_current;
+  const hipStream_t stream = pick_stream(*ctx, stream_arg);
+  if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+
+  // exact-wide proof (api_pack.cpp:47-65); kept when the source is unchanged
+  I256 proof_max;
+  std::vector<ExactAxis> proof_rows, proof_cols;
+  const bool is_wide = matrix->desc.semantics == wide;
+  if (is_wide) {
+    if (same_source) {
+      proof_max = matrix->exact_max;
+    } else if (where == Source::Host) {
+      native_exact_ranges(src, rows, cols, ld, proof_max, proof_rows, proof_cols);
+    } else {
+      if (!matrix->scratch64 && hipMalloc(reinterpret_cast<void**>(&matrix->scratch64), 16) != hipSuccess)
+        return RNS8_BACKEND_FAILURE;
+      unsigned long long host_max = 0;
+      if (launch_zero_words(reinterpret_cast<uint32_t*>(matrix->scratch64), 2, stream) != hipSuccess ||
+          launch_max_magnitude(src, rows, cols, ld, is_signed ? NativeKind::I64 : NativeKind::U64,
+                               reinterpret_cast<unsigned long long*>(matrix->scratch64), stream) != hipSuccess ||
+          hipMemcpyAsync(&host_max, matrix->scratch64, sizeof(host_max), hipMemcpyDeviceToHost, stream) !=
+              hipSuccess ||
+          hipStreamSynchronize(stream) != hipSuccess)
+        return RNS8_BACKEND_FAILURE;
+      proof_max = I256::from_u64(host_max);
+    }
+    if (!exact_range_fits(matrix->desc.semantics, proof_max, modulus_product(matrix->prefix))) return RNS8_RANGE_ERROR;
+  }
+  if (same_source) return RNS8_SUCCESS;
+
+  const void* dsrc = src;
+  int64_t dld = ld;
+  if (where == Source::Host) {
+    const std::size_t bytes = static_cast<std::size_t>(rows) * cols * sizeof(T);
+    rns8_status st = ensure_device_buffer(ctx->device_id, &matrix->upload, &matrix->upload_bytes, bytes);
+    if (st != RNS8_SUCCESS) return st;
+    if (hipMemcpy2DAsync(matrix->upload, cols * sizeof(T), src, ld * sizeof(T), cols * sizeof(T), rows,
+                         hipMemcpyHostToDevice, stream) != hipSuccess)
+      return RNS8_BACKEND_FAILURE;
+    dsrc = matrix->upload;
+    dld = cols;
+  }
+  PackArgs args{dsrc,
+                rows,
+                cols,
+                dld,
+                matrix->planes,
+                matrix->plane_ld,
+                matrix->plane_pitch,
+                matrix->prefix,
+                is_signed ? NativeKind::I64 : NativeKind::U64};
+  if (launch_pack_native(args, make_ladder_plane_consts(matrix->prefix), stream) != hipSuccess)
+    return RNS8_BACKEND_FAILURE;
+  if (where == Source::Host) {
+    const rns8_status st = sync(stream);
+    if (st != RNS8_SUCCESS) return st;
+  }
+  matrix->device_current = true;
+  matrix->source_version = sv;
+  if (is_wide) {
+    matrix->exact_max = proof_max;
+    matrix->exact_rows.swap(proof_rows);
+    matrix->exact_cols.swap(proof_cols);
+    matrix->exact_prefix = matrix->prefix;
+  }
+  return RNS8_SUCCESS;
+}
+
+rns8_status pack_u8(rns8_context* ctx, rns8_matrix* matrix, uint16_t modulus, const uint8_t* src, int64_t ld,
+                    uint64_t sv, Source where, void* stream_arg) {
+  if (!ctx || !matrix || !src || !valid_access(matrix->desc.rows, matrix->desc.cols, ld)) return RNS8_INVALID_ARGUMENT;
+  if (!uses_finite_storage(matrix->desc.semantics) || !valid_finite_modulus(matrix->desc.semantics, modulus))
+    return RNS8_INVALID_ARGUMENT;
+  if (ctx->backend != matrix->backend || matrix->device_id != ctx->device_id) return RNS8_INVALID_ARGUMENT;
+  if (sv != 0 && matrix->source_version == sv && matrix->finite_modulus == modulus && matrix->device_current)
+    return RNS8_SUCCESS;
+  const int64_t rows = matrix->desc.rows, cols = matrix->desc.cols;
+  const hipStream_t stream = pick_stream(*ctx, stream_arg);
+  if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  const uint8_t* dsrc = src;
+  int64_t dld = ld;
+  if (where == Source::Host) {
+    const std::size_t bytes = static_cast<std::size_t>(rows) * cols;
+    rns8_status st = ensure_device_buffer(ctx->device_id, &matrix->upload, &matrix->upload_bytes, bytes);
+    if (st != RNS8_SUCCESS) return st;
+    if (hipMemcpy2DAsync(matrix->upload, cols, src, ld, cols, rows, hipMemcpyHostToDevice, stream) != hipSuccess)
+      return RNS8_BACKEND_FAILURE;
+    dsrc = static_cast<const uint8_t*>(matrix->upload);
+    dld = cols;
+  }
+  PackU8Args args{dsrc, rows, cols, dld, matrix->planes, matrix->plane_ld, modulus};
+  if (launch_pack_u8(args, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  if (where == Source::Host) {
+    const rns8_status st = sync(stream);
+    if (st != RNS8_SUCCESS) return st;
+  }
+  matrix->device_current = true;
+  matrix->source_version = sv;
+  matrix->finite_modulus = modulus;
+  return RNS8_SUCCESS;
+}
+
+// ---- GEMM --------------------------------------------------------------------------
+
+rns8_status run_gemm(rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B,
+                     rns8_matrix& C, rns8_workspace& ws, uint32_t nplanes, const PlaneConsts& consts,
+                     hipStream_t stream) {
+  GemmArgs g{};
+  g.a = A.planes;
+  g.b = B.planes;
+  g.c = C.planes;
+  g.m = plan.desc.m;
+  g.n = plan.desc.n;
+  g.k = plan.desc.k;
+  g.lda = A.plane_ld;
+  g.ldb = B.plane_ld;
+  g.ldc = C.plane_ld;
+  g.pitch_a = A.plane_pitch;
+  g.pitch_b = B.plane_pitch;
+  g.pitch_c = C.plane_pitch;
+  g.nplanes = nplanes;
+  g.slices = plan.splitk_slices;
+  g.splitk_ws = plan.splitk_slices > 1 ? ws.splitk : nullptr;
+  if (hipSetDevice(ctx.device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  const hipError_t e = launch_gemm(g, consts, stream);
+  if (e == hipErrorInvalidValue) return RNS8_UNSUPPORTED_BACKEND;  // shape outside the kernel's limits
+  return e == hipSuccess ? RNS8_SUCCESS : RNS8_BACKEND_FAILURE;
+}
+
+rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* A, const rns8_matrix* B,
+                     rns8_matrix* C, rns8_workspace* ws, void* stream_arg, bool synchronous) {
+  if (!ctx || !plan || !A || !B || !C || !ws) return RNS8_INVALID_ARGUMENT;
+  rns8_status st = check_plan_ctx_ws(*ctx, *plan, *ws);
+  if (st != RNS8_SUCCESS) return st;
+  st = check_rns_operands(*ctx, *plan, *A, *B, *C);
+  if (st != RNS8_SUCCESS) return st;
+  I256 bound;
+  std::vector<ExactAxis> out_rows, out_cols;
+  st = exact_gemm_range(*plan, *A, *B, bound, &out_rows, &out_cols);
+  if (st != RNS8_SUCCESS) return st;
+  const hipStream_t stream = pick_stream(*ctx, stream_arg);
+  C->device_current = false;
+  st = run_gemm(*ctx, *plan, *A, *B, *C, *ws, plan->prefix, make_ladder_plane_consts(plan->prefix), stream);
+  if (st != RNS8_SUCCESS) return st;
+  if (synchronous) {
+    st = sync(stream);
+    if (st != RNS8_SUCCESS) return st;
+  }
+  C->device_current = true;
+  C->source_version = output_source_version(A->source_version, B->source_version);
+  if (exact_wide(plan->desc.semantics)) {
+    C->exact_max = bound;
+    C->exact_rows.swap(out_rows);
+    C->exact_cols.swap(out_cols);
+    C->exact_prefix = plan->prefix;
+  }
+  return RNS8_SUCCESS;
+}
+
+rns8_status gemm_finite(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus, const rns8_matrix* A,
+                        const rns8_matrix* B, rns8_matrix* C, rns8_workspace* ws, void* stream_arg, bool synchronous) {
+  if (!ctx || !plan || !A || !B || !C || !ws) return RNS8_INVALID_ARGUMENT;
+  rns8_status st = check_plan_ctx_ws(*ctx, *plan, *ws);
+  if (st != RNS8_SUCCESS) return st;
+  st = check_finite_operands(*ctx, *plan, modulus, *A, *B, *C);
+  if (st != RNS8_SUCCESS) return st;
+  const hipStream_t stream = pick_stream(*ctx, stream_arg);
+  C->device_current = false;
+  st = run_gemm(*ctx, *plan, *A, *B, *C, *ws, 1, make_single_plane_consts(modulus), stream);
+  if (st != RNS8_SUCCESS) return st;
+  if (synchronous) {
+    st = sync(stream);
+    if (st != RNS8_SUCCESS) return st;
+  }
+  C->device_current = true;
+  C->finite_modulus = modulus;
+  C->source_version = output_source_version(A->source_version, B->source_version);
+  return RNS8_SUCCESS;
+}
+
+// ---- export ------------------------------------------------------------------------
+
+struct ExportRequest {
+  ExportKind kind;
+  rns8_semantics semantics;
+  uint32_t limbs;
+};
+
+// Host export: reconstruct into a compact device staging buffer, read the
+// status word, and copy to `dst` only when every cell is in range, so a
+// RANGE_ERROR leaves the caller's buffer untouched (api_export.cpp:365-414,
+// hip_backend_export_bounded.inc:55-67).
+rns8_status export_host(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* C, void* dst, int64_t ld,
+                        const ExportRequest& req) {
+  rns8_status st = check_export(*ctx, *plan, *C, req.semantics);
+  if (st != RNS8_SUCCESS) return st;
+  auto* mc = const_cast<rns8_matrix*>(C);
+  const int64_t m = plan->desc.m, n = plan->desc.n;
+  const std::size_t elem = sizeof(uint64_t) * req.limbs;
+  const std::size_t bytes = static_cast<std::size_t>(m) * n * elem;
+  if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  st = ensure_device_buffer(ctx->device_id, &mc->staging, &mc->staging_bytes, bytes);
+  if (st != RNS8_SUCCESS) return st;
+  if (!mc->status && hipMalloc(reinterpret_cast<void**>(&mc->status), 64) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  const hipStream_t stream = ctx->stream;
+  if (launch_zero_words(mc->status, 1, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  ExportArgs a{C->planes, m, n, C->plane_ld, C->plane_pitch, mc->staging, n, req.limbs, req.kind, plan->desc.bound,
+               mc->status};
+  if (launch_export(a, make_garner_consts(plan->prefix), stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  uint32_t status = 0;
+  if (hipMemcpyAsync(&status, mc->status, sizeof(status), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess)
+    return RNS8_BACKEND_FAILURE;
+  if (status != 0) return RNS8_RANGE_ERROR;
+  if (hipMemcpy2DAsync(dst, ld * elem, mc->staging, n * elem, n * elem, m, hipMemcpyDeviceToHost, stream) !=
+          hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess)
+    return RNS8_BACKEND_FAILURE;
+  return RNS8_SUCCESS;
+}
+
+rns8_status export_device(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* C, void* d_dst, int64_t ld,
+                          uint32_t* d_status, void* stream_arg, const ExportRequest& req) {
+  if (!d_status) return RNS8_INVALID_ARGUMENT;
+  rns8_status st = check_export(*ctx, *plan, *C, req.semantics);
+  if (st != RNS8_SUCCESS) return st;
+  if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  ExportArgs a{C->planes,  plan->desc.m, plan->desc.n,     C->plane_ld, C->plane_pitch, d_dst,
+               ld,         req.limbs,    req.kind,         plan->desc.bound, d_status};
+  return launch_export(a, make_garner_consts(plan->prefix), pick_stream(*ctx, stream_arg)) == hipSuccess
+             ? RNS8_SUCCESS
+             : RNS8_BACKEND_FAILURE;
+}
+
+rns8_status export_finite(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus, const rns8_matrix* C,
+                          uint8_t* dst, int64_t ld, Source where, void* stream_arg) {
+  if (!ctx || !plan || !C || !dst || !valid_access(plan->desc.m, plan->desc.n, ld)) return RNS8_INVALID_ARGUMENT;
+  rns8_status st = check_finite_export(*ctx, *plan, modulus, *C);
+  if (st != RNS8_SUCCESS) return st;
+  auto* mc = const_cast<rns8_matrix*>(C);
+  const int64_t m = plan->desc.m, n = plan->desc.n;
+  if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  const hipStream_t stream = pick_stream(*ctx, stream_arg);
+  if (where == Source::Device) {
+    ExportU8Args a{C->planes, m, n, C->plane_ld, dst, ld, modulus};
+    return launch_export_u8(a, stream) == hipSuccess ? RNS8_SUCCESS : RNS8_BACKEND_FAILURE;
+  }
+  st = ensure_device_buffer(ctx->device_id, &mc->staging, &mc->staging_bytes, static_cast<std::size_t>(m) * n);
+  if (st != RNS8_SUCCESS) return st;
+  ExportU8Args a{C->planes, m, n, C->plane_ld, static_cast<uint8_t*>(mc->staging), n, modulus};
+  if (launch_export_u8(a, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  if (hipMemcpy2DAsync(dst, ld, mc->staging, n, n, m, hipMemcpyDeviceToHost, stream) != hipSuccess)
+    return RNS8_BACKEND_FAILURE;
+  return sync(stream);
+}
+
+// ---- one-shot (api_oneshot.cpp) -----------------------------------------------------
+
+struct OneshotState {
+  rns8_plan* plan = nullptr;
+  rns8_matrix* A = nullptr;
+  rns8_matrix* B = nullptr;
+  rns8_matrix* C = nullptr;
+  rns8_workspace* ws = nullptr;
+  ~OneshotState() {
+    rns8_destroy_workspace(ws);
+    rns8_destroy_matrix(C);
+    rns8_destroy_matrix(B);
+    rns8_destroy_matrix(A);
+    rns8_destroy_plan(plan);
+  }
+};
+
+rns8_matrix_desc make_matrix_desc(int64_t rows, int64_t cols, rns8_semantics s, rns8_bound_kind bk, uint32_t prefix,
+                                  uint32_t tile_m, uint32_t tile_n) {
+  rns8_matrix_desc d{};
+  d.struct_size = sizeof(d);
+  d.abi_version = RNS8_ABI_VERSION;
+  d.rows = rows;
+  d.cols = cols;
+  d.logical_ld = cols;
+  d.semantics = s;
+  d.logical_layout = RNS8_LAYOUT_ROW_MAJOR;
+  d.bound_kind = bk;
+  d.tile_m = tile_m;
+  d.tile_n = tile_n;
+  d.max_prefix = prefix;
+  return d;
+}
+
+rns8_status create_oneshot(rns8_context* ctx, const rns8_gemm_desc& desc, OneshotState& s) {
+  rns8_status st = rns8_create_plan(ctx, &desc, &s.plan);
+  if (st != RNS8_SUCCESS) return st;
+  const rns8_bound_kind bk = storage_bound_kind(*s.plan);
+  const uint32_t sp = storage_prefix(*s.plan);
+  const uint32_t tm = s.plan->desc.tile_m, tn = s.plan->desc.tile_n;
+  const rns8_matrix_desc ad = make_matrix_desc(desc.m, desc.k, desc.semantics, bk, sp, tm, tn);
+  const rns8_matrix_desc bd = make_matrix_desc(desc.k, desc.n, desc.semantics, bk, sp, tm, tn);
+  const rns8_matrix_desc cd = make_matrix_desc(desc.m, desc.n, desc.semantics, bk, sp, tm, tn);
+  st = rns8_create_matrix(ctx, &ad, &s.A);
+  if (st == RNS8_SUCCESS) st = rns8_create_matrix(ctx, &bd, &s.B);
+  if (st == RNS8_SUCCESS) st = rns8_create_matrix(ctx, &cd, &s.C);
+  if (st == RNS8_SUCCESS) st = rns8_create_workspace(ctx, s.plan, &s.ws);
+  return st;
+}
+
+// reference api_oneshot.cpp:440-466
+rns8_status typed_oneshot_contract(const rns8_context& ctx, const rns8_gemm_desc& desc, rns8_semantics expected,
+                                   int64_t lda, int64_t ldb, int64_t ldc) {
+  if (!valid_abi(desc.struct_size, desc.abi_version, sizeof(desc)) || desc.semantics != expected)
+    return RNS8_INVALID_ARGUMENT;
+  const uint32_t budget = desc.max_prefix == 0 ? default_prefix(desc.semantics) : desc.max_prefix;
+  const rns8_status v = validate_gemm_desc(desc, budget);
+  if (v != RNS8_SUCCESS) return v;
+  if (!valid_access(desc.m, desc.k, lda) || !valid_access(desc.k, desc.n, ldb) || !valid_access(desc.m, desc.n, ldc))
+    return RNS8_INVALID_ARGUMENT;
+  if (desc.requested_backend != RNS8_BACKEND_AUTO && desc.requested_backend != ctx.backend)
+    return RNS8_UNSUPPORTED_BACKEND;
+  return RNS8_SUCCESS;
+}
+
+// reference api_oneshot.cpp:78-106
+rns8_status finite_oneshot_contract(const rns8_context& ctx, const rns8_gemm_desc& desc, rns8_semantics expected,
+                                    uint16_t modulus, int64_t lda, int64_t ldb, int64_t ldc) {
+  if (!valid_abi(desc.struct_size, desc.abi_version, sizeof(desc)) || desc.semantics != expected)
+    return RNS8_INVALID_ARGUMENT;
+  const bool tiles_ok = (desc.tile_m == 0 || (desc.tile_m >= 64 && desc.tile_m <= 512 && !(desc.tile_m & (desc.tile_m - 1)))) &&
+                        (desc.tile_n == 0 || (desc.tile_n >= 64 && desc.tile_n <= 512 && !(desc.tile_n & (desc.tile_n - 1))));
+  if (!valid_finite_modulus(expected, modulus) || desc.m <= 0 || desc.n <= 0 || desc.k <= 0 ||
+      desc.bound_kind != RNS8_BOUND_NONE || desc.bound != 0 || desc.max_prefix != 0 || desc.finite_modulus != modulus ||
+      desc.flags != 0 || desc.tile_bounds || desc.tile_bounds_count != 0 || desc.lhs_bound != 0 ||
+      desc.rhs_bound != 0 || !tiles_ok)
+    return RNS8_INVALID_ARGUMENT;
+  if (!valid_access(desc.m, desc.k, lda) || !valid_access(desc.k, desc.n, ldb) || !valid_access(desc.m, desc.n, ldc))
+    return RNS8_INVALID_ARGUMENT;
+  if (desc.requested_backend != RNS8_BACKEND_AUTO && desc.requested_backend != ctx.backend)
+    return RNS8_UNSUPPORTED_BACKEND;
+  return RNS8_SUCCESS;
+}
+
+template <typename T>
+rns8_status bounded_oneshot(rns8_context* ctx, const rns8_gemm_desc* desc, const T* A, int64_t lda, const T* B,
+                            int64_t ldb, T* C, int64_t ldc) {
+  constexpr bool is_signed = std::is_same<T, int64_t>::value;
+  if (!ctx || !desc || !A || !B || !C) return RNS8_INVALID_ARGUMENT;
+  const rns8_status pre =
+      typed_oneshot_contract(*ctx, *desc, is_signed ? RNS8_BOUNDED_I64 : RNS8_BOUNDED_U64, lda, ldb, ldc);
+  if (pre != RNS8_SUCCESS) return pre;
+  OneshotState s;
+  rns8_status st = create_oneshot(ctx, *desc, s);
+  if (st == RNS8_SUCCESS) st = pack_native<T>(ctx, s.A, A, lda, 1, Source::Host, nullptr);
+  if (st == RNS8_SUCCESS) st = pack_native<T>(ctx, s.B, B, ldb, 1, Source::Host, nullptr);
+  if (st == RNS8_SUCCESS) st = gemm_rns(ctx, s.plan, s.A, s.B, s.C, s.ws, nullptr, true);
+  if (st == RNS8_SUCCESS) {
+    if (!valid_access(s.plan->desc.m, s.plan->desc.n, ldc)) return RNS8_INVALID_ARGUMENT;
+    st = export_host(ctx, s.plan, s.C, C, ldc,
+                     ExportRequest{is_signed ? ExportKind::I64 : ExportKind::U64,
+                                   is_signed ? RNS8_BOUNDED_I64 : RNS8_BOUNDED_U64, 1});
+  }
+  return st;
+}
+
+rns8_status finite_oneshot(rns8_context* ctx, const rns8_gemm_desc* desc, rns8_semantics sem, uint16_t modulus,
+                           const uint8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, uint8_t* C, int64_t ldc) {
+  if (!ctx || !desc || !A || !B || !C) return RNS8_INVALID_ARGUMENT;
+  const rns8_status pre = finite_oneshot_contract(*ctx, *desc, sem, modulus, lda, ldb, ldc);
+  if (pre != RNS8_SUCCESS) return pre;
+  OneshotState s;
+  rns8_status st = create_oneshot(ctx, *desc, s);
+  if (st == RNS8_SUCCESS) st = pack_u8(ctx, s.A, modulus, A, lda, 1, Source::Host, nullptr);
+  if (st == RNS8_SUCCESS) st = pack_u8(ctx, s.B, modulus, B, ldb, 2, Source::Host, nullptr);
+  if (st == RNS8_SUCCESS) st = gemm_finite(ctx, s.plan, modulus, s.A, s.B, s.C, s.ws, nullptr, true);
+  if (st == RNS8_SUCCESS) st = export_finite(ctx, s.plan, modulus, s.C, C, ldc, Source::Host, nullptr);
+  return st;
+}
+
+}  // namespace
+}  // namespace rns8x
+
+using namespace rns8x;
+
+// ---- public ABI ------------------------------------------------------------------------
+
+rns8_status rns8_pack_i64(rns8_context* ctx, rns8_matrix* matrix, const int64_t* src, int64_t ld,
+                          uint64_t source_version) {
+  return guard([&] { return pack_native<int64_t>(ctx, matrix, src, ld, source_version, Source::Host, nullptr); });
+}
+
+rns8_status rns8_pack_u64(rns8_context* ctx, rns8_matrix* matrix, const uint64_t* src, int64_t ld,
+                          uint64_t source_version) {
+  return guard([&] { return pack_native<uint64_t>(ctx, matrix, src, ld, source_version, Source::Host, nullptr); });
+}
+
+rns8_status rns8_pack_finite_u8(rns8_context* ctx, rns8_matrix* matrix, uint16_t modulus, const uint8_t* src,
+                                int64_t ld, uint64_t source_version) {
+  return guard([&] { return pack_u8(ctx, matrix, modulus, src, ld, source_version, Source::Host, nullptr); });
+}
+
+rns8_status rns8_gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* A, const rns8_matrix* B,
+                          rns8_matrix* C, rns8_workspace* workspace) {
+  return guard([&] { return gemm_rns(ctx, plan, A, B, C, workspace, nullptr, true); });
+}
+
+rns8_status rns8_gemm_finite_u8(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus, const rns8_matrix* A,
+                                const rns8_matrix* B, rns8_matrix* C, rns8_workspace* workspace) {
+  return guard([&] { return gemm_finite(ctx, plan, modulus, A, B, C, workspace, nullptr, true); });
+}
+
+rns8_status rns8_export_i64(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* C, int64_t* dst, int64_t ld) {
+  return guard([&]() -> rns8_status {
+    if (!ctx || !plan || !C || !dst || !valid_access(plan->desc.m, plan->desc.n, ld)) return RNS8_INVALID_ARGUMENT;
+    return export_host(ctx, plan, C, dst, ld, ExportRequest{ExportKind::I64, RNS8_BOUNDED_I64, 1});
+  });
+}
+
+rns8_status rns8_export_u64(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* C, uint64_t* dst,
+                            int64_t ld) {
+  return guard([&]() -> rns8_status {
+    if (!ctx || !plan || !C || !dst || !valid_access(plan->desc.m, plan->desc.n, ld)) return RNS8_INVALID_ARGUMENT;
+    return export_host(ctx, plan, C, dst, ld, ExportRequest{ExportKind::U64, RNS8_BOUNDED_U64, 1});
+  });
+}
+
+rns8_status rns8_export_exact_wide_signed_limbs(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* C,
+                                                uint64_t* dst, int64_t ld, uint32_t limb_count) {
+  return guard([&]() -> rns8_status {
+    if (!ctx || !plan || !C || !dst || !valid_limb_access(plan->desc.m, plan->desc.n, ld, limb_count))
+      return RNS8_INVALID_ARGUMENT;
+    return export_host(ctx, plan, C, dst, ld,
+                       ExportRequest{ExportKind::WIDE_SIGNED, RNS8_EXACT_WIDE_SIGNED, limb_count});
+  });
+}
+
+rns8_status rns8_export_exact_wide_unsigned_limbs(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* C,
+                                                  uint64_t* dst, int64_t ld, uint32_t limb_count) {
+  return guard([&]() -> rns8_status {
+    if (!ctx || !plan || !C || !dst || !valid_limb_access(plan->desc.m, plan->desc.n, ld, limb_count))
+      return RNS8_INVALID_ARGUMENT;
+    return export_host(ctx, plan, C, dst, ld,
+                       ExportRequest{ExportKind::WIDE_UNSIGNED, RNS8_EXACT_WIDE_UNSIGNED, limb_count});
+  });
+}
+
+rns8_status rns8_export_finite_u8(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus, const rns8_matrix* C,
+                                  uint8_t* dst, int64_t ld) {
+  return guard([&] { return export_finite(ctx, plan, modulus, C, dst, ld, Source::Host, nullptr); });
+}
+
+rns8_status rns8_gemm_i64_oneshot(rns8_context* ctx, const rns8_gemm_desc* desc, const int64_t* A, int64_t lda,
+                                  const int64_t* B, int64_t ldb, int64_t* C, int64_t ldc) {
+  return guard([&] { return bounded_oneshot<int64_t>(ctx, desc, A, lda, B, ldb, C, ldc); });
+}
+
+rns8_status rns8_gemm_u64_oneshot(rns8_context* ctx, const rns8_gemm_desc* desc, const uint64_t* A, int64_t lda,
+                                  const uint64_t* B, int64_t ldb, uint64_t* C, int64_t ldc) {
+  return guard([&] { return bounded_oneshot<uint64_t>(ctx, desc, A, lda, B, ldb, C, ldc); });
+}
+
+rns8_status rns8_gemm_finite_ring_u8_oneshot(rns8_context* ctx, const rns8_gemm_desc* desc, uint16_t modulus,
+                                             const uint8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, uint8_t* C,
+                                             int64_t ldc) {
+  return guard(
+      [&] { return finite_oneshot(ctx, desc, RNS8_FINITE_RING_U8, modulus, A, lda, B, ldb, C, ldc); });
+}
+
+rns8_status rns8_gemm_finite_field_u8_oneshot(rns8_context* ctx, const rns8_gemm_desc* desc, uint16_t modulus,
+                                              const uint8_t* A, int64_t lda, const uint8_t* B, int64_t ldb,
+                                              uint8_t* C, int64_t ldc) {
+  return guard(
+      [&] { return finite_oneshot(ctx, desc, RNS8_FINITE_FIELD_U8, modulus, A, lda, B, ldb, C, ldc); });
+}
+
+// ---- MI355X device-resident extensions ------------------------------------------------
+
+rns8_status rns8_mi355x_pack_i64_device(rns8_context* ctx, rns8_matrix* matrix, const int64_t* d_src, int64_t ld,
+                                        uint64_t source_version, void* stream) {
+  return guard([&] { return pack_native<int64_t>(ctx, matrix, d_src, ld, source_version, Source::Device, stream); });
+}
+
+rns8_status rns8_mi355x_pack_u64_device(rns8_context* ctx, rns8_matrix* matrix, const uint64_t* d_src, int64_t ld,
+                                        uint64_t source_version, void* stream) {
+  return guard([&] { return pack_native<uint64_t>(ctx, matrix, d_src, ld, source_version, Source::Device, stream); });
+}
+
+rns8_status rns8_mi355x_pack_finite_u8_device(rns8_context* ctx, rns8_matrix* matrix, uint16_t modulus,
+                                              const uint8_t* d_src, int64_t ld, uint64_t source_version,
+                                              void* stream) {
+  return guard([&] { return pack_u8(ctx, matrix, modulus, d_src, ld, source_version, Source::Device, stream); });
+}
+
+rns8_status rns8_mi355x_gemm_rns_async(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* A,
+                                       const rns8_matrix* B, rns8_matrix* C, rns8_workspace* workspace,
+                                       void* stream) {
+  return guard([&] { return gemm_rns(ctx, plan, A, B, C, workspace, stream, false); });
+}
+
+rns8_status rns8_mi355x_gemm_finite_u8_async(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus,
+                                             const rns8_matrix* A, const rns8_matrix* B, rns8_matrix* C,
+                                             rns8_workspace* workspace, void* stream) {
+  return guard([&] { return gemm_finite(ctx, plan, modulus, A, B, C, workspace, stream, false); });
+}
+
+rns8_status rns8_mi355x_export_i64_device(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* C,
+                                          int64_t* d_dst, int64_t ld, uint32_t* d_status, void* stream) {
+  return guard([&]() -> rns8_status {
+    if (!ctx || !plan || !C || !d_dst || !valid_access(plan->desc.m, plan->desc.n, ld)) return RNS8_INVALID_ARGUMENT;
+    return export_device(ctx, plan, C, d_dst, ld, d_status, stream,
+                         ExportRequest{ExportKind::I64, RNS8_BOUNDED_I64, 1});
+  });
+}
+
+rns8_status rns8_mi355x_export_u64_device(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* C,
+                                          uint64_t* d_dst, int64_t ld, uint32_t* d_status, void* stream) {
+  return guard([&]() -> rns8_status {
+    if (!ctx || !plan || !C || !d_dst || !valid_access(plan->desc.m, plan->desc.n, ld)) return RNS8_INVALID_ARGUMENT;
+    return export_device(ctx, plan, C, d_dst, ld, d_status, stream,
+                         ExportRequest{ExportKind::U64, RNS8_BOUNDED_U64, 1});
+  });
+}
+
+rns8_status rns8_mi355x_export_exact_wide_signed_limbs_device(rns8_context* ctx, const rns8_plan* plan,
+                                                              const rns8_matrix* C, uint64_t* d_dst, int64_t ld,
+                                                              uint32_t limb_count, uint32_t* d_status, void* stream) {
+  return guard([&]() -> rns8_status {
+    if (!ctx || !plan || !C || !d_dst || !valid_limb_access(plan->desc.m, plan->desc.n, ld, limb_count))
+      return RNS8_INVALID_ARGUMENT;
+    return export_device(ctx, plan, C, d_dst, ld, d_status, stream,
+                         ExportRequest{ExportKind::WIDE_SIGNED, RNS8_EXACT_WIDE_SIGNED, limb_count});
+  });
+}
+
+rns8_status rns8_mi355x_export_exact_wide_unsigned_limbs_device(rns8_context* ctx, const rns8_plan* plan,
+                                                                const rns8_matrix* C, uint64_t* d_dst, int64_t ld,
+                                                                uint32_t limb_count, uint32_t* d_status,
+                                                                void* stream) {
+  return guard([&]() -> rns8_status {
+    if (!ctx || !plan || !C || !d_dst || !valid_limb_access(plan->desc.m, plan->desc.n, ld, limb_count))
+      return RNS8_INVALID_ARGUMENT;
+    return export_device(ctx, plan, C, d_dst, ld, d_status, stream,
+                         ExportRequest{ExportKind::WIDE_UNSIGNED, RNS8_EXACT_WIDE_UNSIGNED, limb_count});
+  });
+}
+
+rns8_status rns8_mi355x_export_finite_u8_device(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus,
+                                                const rns8_matrix* C, uint8_t* d_dst, int64_t ld, void* stream) {
+  return guard([&] { return export_finite(ctx, plan, modulus, C, d_dst, ld, Source::Device, stream); });
+}

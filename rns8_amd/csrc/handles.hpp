@@ -1,0 +1,158 @@
+// Handle state behind the opaque rns8 ABI types, plus shared host helpers.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "rns8/rns8.h"
+#include "rns8_mi355x.h"
+#include "tables.hpp"
+#include "wide_int.hpp"
+
+// Exact-wide per-axis magnitude summary (reference src/core/internal.hpp:72-86
+// rns8_exact_axis_range): used to tighten the output bound of a GEMM.
+struct ExactAxis {
+  rns8x::I256 max_magnitude;
+  rns8x::I256 absolute_sum;
+  rns8x::I256 sum;
+  rns8x::I256 minimum;
+  rns8x::I256 maximum;
+  rns8x::I256 deviation_sum;
+  bool sum_known = false;
+};
+
+struct rns8_context {
+  rns8_backend_kind backend = RNS8_BACKEND_HIP_DIRECT;
+  int device_id = 0;
+  hipStream_t stream = nullptr;
+  rns8_device_info device_info{};
+};
+
+struct rns8_plan {
+  rns8_gemm_desc desc{};  // caller descriptor; max_prefix holds the budget, tiles defaulted to 128
+  rns8_backend_kind backend = RNS8_BACKEND_HIP_DIRECT;
+  int device_id = 0;
+  uint32_t budget = 0;           // max_prefix after defaulting
+  uint32_t prefix = 0;           // selected prefix (0 for finite semantics)
+  uint32_t required_prefix = 0;  // minimum proven prefix
+  uint32_t range_bits = 0;       // bit length of the required CRT range
+  rns8x::I256 product;           // modulus product of the selected prefix
+  uint64_t tile_rows = 0, tile_cols = 0, tile_count = 0;
+  uint32_t splitk_slices = 1;
+  uint64_t splitk_bytes = 0;
+};
+
+struct rns8_matrix {
+  rns8_matrix_desc desc{};
+  rns8_backend_kind backend = RNS8_BACKEND_HIP_DIRECT;
+  int device_id = 0;
+  uint64_t instance_id = 0;
+  uint32_t prefix = 0;  // residue planes held (1 for finite storage)
+  uint16_t finite_modulus = 0;
+  uint64_t source_version = 0;
+  bool device_current = false;
+  // planes in HBM, layout rns8_mi355x_planes_v1 (tables.hpp)
+  int8_t* planes = nullptr;
+  int64_t plane_ld = 0;
+  int64_t plane_pitch = 0;
+  uint64_t plane_bytes = 0;
+  // exact-wide proofs: exact_prefix == 0 means no proof
+  rns8x::I256 exact_max;
+  uint32_t exact_prefix = 0;
+  std::vector<ExactAxis> exact_rows;
+  std::vector<ExactAxis> exact_cols;
+  // cached staging buffers (export is logically const, reference
+  // api_export.cpp:276-287 keeps the same kind of cache on the matrix)
+  void* upload = nullptr;
+  std::size_t upload_bytes = 0;
+  void* staging = nullptr;
+  std::size_t staging_bytes = 0;
+  uint32_t* status = nullptr;
+  uint64_t* scratch64 = nullptr;
+};
+
+struct rns8_workspace {
+  rns8_backend_kind backend = RNS8_BACKEND_HIP_DIRECT;
+  rns8_semantics semantics = RNS8_BOUNDED_I64;
+  rns8_bound_kind bound_kind = RNS8_BOUND_NONE;
+  int64_t m = 0, n = 0, k = 0;
+  uint32_t prefix = 0;
+  uint32_t finite_modulus = 0;
+  int device_id = 0;
+  int32_t* splitk = nullptr;
+  uint64_t splitk_bytes = 0;
+};
+
+// Handles for entry points this library does not execute; never created.
+struct rns8_sparse_matrix {
+  int unused;
+};
+struct rns8_prepack_cache {
+  int unused;
+};
+struct rns8_result_cache {
+  int unused;
+};
+
+namespace rns8x {
+
+template <typename F>
+rns8_status guard(F&& f) {
+  try {
+    return f();
+  } catch (...) {
+    return RNS8_INTERNAL_ERROR;
+  }
+}
+
+inline bool valid_abi(uint64_t struct_size, uint32_t abi_version, std::size_t expected) {
+  return abi_version == RNS8_ABI_VERSION && struct_size >= expected;
+}
+
+void copy_text(char* dst, std::size_t size, const std::string& src);
+
+// out-struct helper: keep caller's size/version, zero the rest
+template <typename T>
+void reset_out(T& out) {
+  const uint64_t size = out.struct_size;
+  const uint32_t version = out.abi_version;
+  out = T{};
+  out.struct_size = size;
+  out.abi_version = version;
+}
+
+bool uses_rns_storage(rns8_semantics s);
+bool uses_finite_storage(rns8_semantics s);
+bool exact_wide(rns8_semantics s);
+uint32_t default_prefix(rns8_semantics s);
+I256 modulus_product(uint32_t prefix);
+uint32_t required_prefix_for_range(const I256& range);
+bool valid_finite_modulus(rns8_semantics s, uint32_t modulus);
+
+// reference moduli.cpp:295-387 (validate_gemm_desc)
+rns8_status validate_gemm_desc(const rns8_gemm_desc& d, uint32_t prefix);
+// reference moduli.cpp:389-448 (validate_matrix_desc)
+rns8_status validate_matrix_desc(const rns8_matrix_desc& d, uint32_t prefix);
+// reference moduli.cpp:234-293 (validate_bound_contract)
+rns8_status validate_bound_contract(rns8_semantics s, rns8_bound_kind bk, uint64_t bound, uint32_t prefix);
+// validation + prefix selection shared by plan creation and select_prefix
+rns8_status plan_prefix(const rns8_gemm_desc& d, uint32_t& budget, uint32_t& selected, uint32_t& required,
+                        uint32_t& range_bits, uint64_t& effective_bound);
+
+// HIP helpers
+rns8_status hip_status(hipError_t e);
+rns8_status ensure_device_buffer(int device, void** ptr, std::size_t* have, std::size_t need);
+void free_device(void* p);
+hipStream_t pick_stream(const rns8_context& ctx, void* stream);
+
+// matrix storage: storage prefix / bound kind a plan expects of its operands
+uint32_t storage_prefix(const rns8_plan& p);
+rns8_bound_kind storage_bound_kind(const rns8_plan& p);
+bool matrix_matches(const rns8_matrix& m, rns8_semantics s, rns8_bound_kind bk, int64_t rows, int64_t cols,
+                    uint32_t prefix);
+
+}  // namespace rns8x

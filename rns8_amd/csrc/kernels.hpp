@@ -1,0 +1,100 @@
+// Host-side launchers for the gfx950 kernels (defined in the .hip files).
+//
+// Every launcher checks that the shapes it receives match what its grid and
+// index arithmetic assume (non-negative sizes, 16-byte padded pitches,
+// prefix <= 20) and returns hipErrorInvalidValue otherwise, so no kernel is
+// launched with a geometry that could index outside its buffers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "tables.hpp"
+
+namespace rns8x {
+
+// ---- pack: native operand -> centered int8 residue planes ------------------
+enum class NativeKind : uint32_t { I64 = 0, U64 = 1 };
+
+struct PackArgs {
+  const void* src;  // device, rows x cols elements at row stride `ld`
+  int64_t rows;
+  int64_t cols;
+  int64_t ld;       // elements
+  int8_t* planes;   // device, `nplanes` planes
+  int64_t plane_ld; // padded_ld(cols)
+  int64_t plane_pitch;
+  uint32_t nplanes;
+  NativeKind kind;
+};
+hipError_t launch_pack_native(const PackArgs& args, const PlaneConsts& consts, hipStream_t stream);
+
+// Maximum |x| over a rows x cols native matrix (row stride ld elements),
+// combined into *out with an atomic max. *out must be zero on entry.
+hipError_t launch_max_magnitude(const void* src, int64_t rows, int64_t cols, int64_t ld, NativeKind kind,
+                                unsigned long long* out, hipStream_t stream);
+
+struct PackU8Args {
+  const uint8_t* src;
+  int64_t rows;
+  int64_t cols;
+  int64_t ld;
+  int8_t* plane;
+  int64_t plane_ld;
+  uint32_t modulus;
+};
+hipError_t launch_pack_u8(const PackU8Args& args, hipStream_t stream);
+
+// ---- plane GEMM: C_p = center(A_p x B_p mod m_p) ---------------------------
+struct GemmArgs {
+  const int8_t* a;  // [planes][m][lda]
+  const int8_t* b;  // [planes][k][ldb]
+  int8_t* c;        // [planes][m][ldc]
+  int64_t m, n, k;
+  int64_t lda, ldb, ldc;  // padded pitches (bytes, multiples of 16)
+  int64_t pitch_a, pitch_b, pitch_c;
+  uint32_t nplanes;
+  // split-K: int32 accumulation buffer [planes][m][ldc] (zero on entry,
+  // left zero on exit) and the number of K slices; slices == 1 disables it.
+  int32_t* splitk_ws;
+  uint32_t slices;
+};
+hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream);
+// Number of K slices the launcher would pick for this shape (1 = no split).
+uint32_t choose_splitk_slices(int64_t m, int64_t n, int64_t k, uint32_t nplanes);
+// Bytes of int32 split-K workspace needed for this shape (0 when slices == 1).
+uint64_t splitk_workspace_bytes(int64_t m, int64_t n, int64_t k, uint32_t nplanes);
+
+// ---- export ------------------------------------------------------------------
+enum class ExportKind : uint32_t { I64 = 0, U64 = 1, WIDE_SIGNED = 2, WIDE_UNSIGNED = 3 };
+
+struct ExportArgs {
+  const int8_t* c;  // [prefix][m][ldc] residue planes
+  int64_t m, n;
+  int64_t ldc;
+  int64_t pitch_c;
+  void* dst;        // device, element (r, col) at dst[(r*ld + col) * limbs]
+  int64_t ld;       // elements
+  uint32_t limbs;   // 64-bit limbs per element (1 for i64/u64)
+  ExportKind kind;
+  uint64_t bound;   // bounded kinds
+  uint32_t* status; // device word; set nonzero on any range violation
+};
+hipError_t launch_export(const ExportArgs& args, const GarnerConsts& g, hipStream_t stream);
+
+struct ExportU8Args {
+  const int8_t* c;
+  int64_t m, n;
+  int64_t ldc;
+  uint8_t* dst;
+  int64_t ld;
+  uint32_t modulus;
+};
+hipError_t launch_export_u8(const ExportU8Args& args, hipStream_t stream);
+
+// Fill `words` 32-bit words with zero (used instead of hipMemsetAsync so the
+// call sequence stays valid under stream capture).
+hipError_t launch_zero_words(uint32_t* dst, uint64_t words, hipStream_t stream);
+
+}  // namespace rns8x

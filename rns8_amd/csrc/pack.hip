@@ -1,0 +1,185 @@
+// Pack kernels: native operands -> modulus-major centered int8 residue planes.
+//
+// Reference semantics: src/cpu/cpu_reference.cpp:53-130 (res[p][r][c] =
+// centered(src[r*ld + c] mod m_p), threshold (m+1)/2).
+//
+// HBM-bound design: each thread owns 16 consecutive columns of one row, reads
+// the 64-bit inputs once and writes one aligned 16-byte run per plane, so the
+// input is read a single time for all planes (the reference's large-matrix
+// path re-reads it once per plane, hip_backend_pack.inc:44-58).
+//
+// Residue of a 64-bit value without 64-bit division (tables.hpp): split u into
+// bytes, s = dot(lo bytes, 2^(8b) mod m) + dot(hi bytes, 2^(32+8b) mod m) + off
+// with two v_dot4_u32_u8 (s < 2^19), then one exact umulhi quotient. Signed
+// inputs are biased by 2^63 (flip the top bit) and the bias is folded into
+// `off`, so int64 and uint64 share the same arithmetic.
+#include "kernels.hpp"
+
+namespace rns8x {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int32_t residue_of_halves(uint32_t lo, uint32_t hi, uint32_t pow_lo, uint32_t pow_hi,
+                                                     uint32_t off, uint32_t recip, uint32_t m, uint32_t half) {
+  uint32_t s = __builtin_amdgcn_udot4(lo, pow_lo, off, false);
+  s = __builtin_amdgcn_udot4(hi, pow_hi, s, false);
+  const uint32_t q = __umulhi(s, recip);
+  return static_cast<int32_t>(s - q * m) - static_cast<int32_t>(half);
+}
+
+__device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {
+  return (static_cast<uint32_t>(a) & 0xFFu) | ((static_cast<uint32_t>(b) & 0xFFu) << 8) |
+         ((static_cast<uint32_t>(c) & 0xFFu) << 16) | (static_cast<uint32_t>(d) << 24);
+}
+
+template <bool Signed, bool Vec>
+__global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConsts pc, int64_t chunks_per_row,
+                                                          int64_t total_chunks) {
+  const uint64_t* const src = static_cast<const uint64_t*>(a.src);
+  for (int64_t ch = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; ch < total_chunks;
+       ch += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t row = ch / chunks_per_row;
+    const int64_t c0 = (ch - row * chunks_per_row) * 16;
+    const uint64_t* const rp = src + row * a.ld;
+    uint32_t lo[16], hi[16];
+    if (Vec && c0 + 16 <= a.cols) {
+      // row start is 16-byte aligned (checked by the launcher) and c0 is even
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) {
+        const v2u64 v = *reinterpret_cast<const v2u64*>(rp + c0 + e);
+        lo[e] = static_cast<uint32_t>(v[0]);
+        hi[e] = static_cast<uint32_t>(v[0] >> 32);
+        lo[e + 1] = static_cast<uint32_t>(v[1]);
+        hi[e + 1] = static_cast<uint32_t>(v[1] >> 32);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint64_t x = (c0 + e < a.cols) ? rp[c0 + e] : 0ull;  // padding packs as 0
+        lo[e] = static_cast<uint32_t>(x);
+        hi[e] = static_cast<uint32_t>(x >> 32);
+      }
+    }
+    if (Signed) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) hi[e] ^= 0x80000000u;
+    }
+    int8_t* const out = a.planes + row * a.plane_ld + c0;
+    for (uint32_t p = 0; p < a.nplanes; ++p) {
+      const ModulusConsts mc = pc.mod[p];
+      const uint32_t off = Signed ? mc.off_i64 : mc.off_u64;
+      int32_t r[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        r[e] = residue_of_halves(lo[e], hi[e], mc.pow_lo, mc.pow_hi, off, mc.recip, mc.m, mc.half);
+      const v4i w = {static_cast<int>(pack4(r[0], r[1], r[2], r[3])), static_cast<int>(pack4(r[4], r[5], r[6], r[7])),
+                     static_cast<int>(pack4(r[8], r[9], r[10], r[11])),
+                     static_cast<int>(pack4(r[12], r[13], r[14], r[15]))};
+      *reinterpret_cast<v4i*>(out + static_cast<int64_t>(p) * a.plane_pitch) = w;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void pack_u8_kernel(PackU8Args a, ModulusConsts mc, int64_t chunks_per_row,
+                                                      int64_t total_chunks) {
+  for (int64_t ch = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; ch < total_chunks;
+       ch += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t row = ch / chunks_per_row;
+    const int64_t c0 = (ch - row * chunks_per_row) * 16;
+    const uint8_t* const rp = a.src + row * a.ld;
+    int32_t r[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t x = (c0 + e < a.cols) ? rp[c0 + e] : 0u;
+      const uint32_t s = x + mc.half;  // < 2^9
+      const uint32_t q = __umulhi(s, mc.recip);
+      r[e] = static_cast<int32_t>(s - q * mc.m) - static_cast<int32_t>(mc.half);
+    }
+    const v4i w = {static_cast<int>(pack4(r[0], r[1], r[2], r[3])), static_cast<int>(pack4(r[4], r[5], r[6], r[7])),
+                   static_cast<int>(pack4(r[8], r[9], r[10], r[11])),
+                   static_cast<int>(pack4(r[12], r[13], r[14], r[15]))};
+    *reinterpret_cast<v4i*>(a.plane + row * a.plane_ld + c0) = w;
+  }
+}
+
+template <bool Signed>
+__global__ __launch_bounds__(256) void max_magnitude_kernel(const uint64_t* src, int64_t rows, int64_t cols,
+                                                            int64_t ld, unsigned long long* out) {
+  const int64_t total = rows * cols;
+  unsigned long long best = 0;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / cols;
+    const uint64_t x = src[r * ld + (i - r * cols)];
+    // |INT64_MIN| = 2^63 is representable as an unsigned magnitude
+    const unsigned long long mag =
+        Signed ? (static_cast<int64_t>(x) < 0 ? 0ull - x : x) : static_cast<unsigned long long>(x);
+    best = mag > best ? mag : best;
+  }
+  // wave reduction, then one atomic per wave
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    const unsigned long long other = __shfl_down(best, offset, 64);
+    best = other > best ? other : best;
+  }
+  if ((threadIdx.x & 63) == 0 && best != 0) atomicMax(out, best);
+}
+
+unsigned grid_for(int64_t items) {
+  const int64_t blocks = (items + 255) / 256;
+  return static_cast<unsigned>(blocks < 16384 ? (blocks > 0 ? blocks : 1) : 16384);
+}
+
+}  // namespace
+
+hipError_t launch_pack_native(const PackArgs& a, const PlaneConsts& consts, hipStream_t stream) {
+  if (!a.src || !a.planes || a.rows <= 0 || a.cols <= 0 || a.ld < a.cols) return hipErrorInvalidValue;
+  if (a.nplanes == 0 || a.nplanes > kMaxPrefix) return hipErrorInvalidValue;
+  if (a.plane_ld != padded_ld(a.cols) || a.plane_pitch < a.rows * a.plane_ld || (a.plane_pitch % 16) != 0)
+    return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(a.planes) & 15u) != 0) return hipErrorInvalidValue;
+  const int64_t chunks_per_row = a.plane_ld / 16;
+  const int64_t total = chunks_per_row * a.rows;
+  const bool vec = (reinterpret_cast<uintptr_t>(a.src) & 15u) == 0 && (a.ld % 2) == 0;
+  const dim3 grid(grid_for(total));
+  if (a.kind == NativeKind::I64) {
+    if (vec)
+      hipLaunchKernelGGL((pack_native_kernel<true, true>), grid, dim3(256), 0, stream, a, consts, chunks_per_row, total);
+    else
+      hipLaunchKernelGGL((pack_native_kernel<true, false>), grid, dim3(256), 0, stream, a, consts, chunks_per_row, total);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((pack_native_kernel<false, true>), grid, dim3(256), 0, stream, a, consts, chunks_per_row, total);
+    else
+      hipLaunchKernelGGL((pack_native_kernel<false, false>), grid, dim3(256), 0, stream, a, consts, chunks_per_row,
+                         total);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_max_magnitude(const void* src, int64_t rows, int64_t cols, int64_t ld, NativeKind kind,
+                                unsigned long long* out, hipStream_t stream) {
+  if (!src || !out || rows <= 0 || cols <= 0 || ld < cols) return hipErrorInvalidValue;
+  const dim3 grid(grid_for(rows * cols) < 2048 ? grid_for(rows * cols) : 2048);
+  if (kind == NativeKind::I64)
+    hipLaunchKernelGGL(max_magnitude_kernel<true>, grid, dim3(256), 0, stream, static_cast<const uint64_t*>(src), rows,
+                       cols, ld, out);
+  else
+    hipLaunchKernelGGL(max_magnitude_kernel<false>, grid, dim3(256), 0, stream, static_cast<const uint64_t*>(src),
+                       rows, cols, ld, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_u8(const PackU8Args& a, hipStream_t stream) {
+  if (!a.src || !a.plane || a.rows <= 0 || a.cols <= 0 || a.ld < a.cols) return hipErrorInvalidValue;
+  if (a.modulus < 2 || a.modulus > 256) return hipErrorInvalidValue;
+  if (a.plane_ld != padded_ld(a.cols) || (reinterpret_cast<uintptr_t>(a.plane) & 15u) != 0) return hipErrorInvalidValue;
+  const int64_t chunks_per_row = a.plane_ld / 16;
+  const int64_t total = chunks_per_row * a.rows;
+  hipLaunchKernelGGL(pack_u8_kernel, dim3(grid_for(total)), dim3(256), 0, stream, a, make_modulus_consts(a.modulus),
+                     chunks_per_row, total);
+  return hipGetLastError();
+}
+
+}  // namespace rns8x

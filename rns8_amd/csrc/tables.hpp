@@ -1,0 +1,208 @@
+// Constant tables shared by the host runtime and the gfx950 kernels.
+//
+// Everything the kernels need per modulus is precomputed here on the host and
+// passed by value as kernel arguments (uniform values land in SGPRs). The
+// arithmetic identities behind each table are stated next to it; tests in
+// tests/test_tables.py check them exhaustively on the CPU.
+#pragma once
+
+#include <cstdint>
+
+namespace rns8x {
+
+// Modulus ladder (reference src/core/internal.hpp:328-330): 28 pairwise-coprime
+// moduli <= 256; prefixes of at most 20 are used.
+constexpr uint32_t kLadderSize = 28;
+constexpr uint32_t kMaxPrefix = 20;
+constexpr uint16_t kLadder[kLadderSize] = {256, 255, 253, 251, 247, 239, 233, 229, 227, 223,
+                                           217, 211, 199, 197, 193, 191, 181, 179, 173, 167,
+                                           163, 157, 151, 149, 139, 137, 131, 127};
+
+// int8 x int8 products are at most 2^14 in magnitude, so 65536 of them plus a
+// carried centered residue fit in int32 (reference residue_dot.hpp:18-19).
+constexpr int64_t kSafeKBlock = 65536;
+
+// ---- exact small-modulus reduction ---------------------------------------
+//
+// For 2 <= m <= 256 let R = ceil(2^32 / m) and e = R*m - 2^32 (0 <= e < m).
+// For 0 <= s < 2^21, floor(s*R / 2^32) == floor(s / m) because s*e < 2^29 <
+// 2^32 keeps the error term below 1/m. So q = umulhi(s, R), r = s - q*m.
+//
+// Centering: with H = floor(m/2), centered(x) = ((x + H) mod m) - H equals the
+// reference rule "r >= (m+1)/2 ? r - m : r" (cpu_reference.cpp:26-32) for
+// every m >= 2. H is folded into the additive offsets below.
+struct ModulusConsts {
+  uint32_t m;
+  uint32_t half;    // H = floor(m/2)
+  uint32_t recip;   // R = ceil(2^32 / m)
+  uint32_t pow_lo;  // bytes [2^0, 2^8, 2^16, 2^24] mod m, packed little-endian
+  uint32_t pow_hi;  // bytes [2^32, 2^40, 2^48, 2^56] mod m
+  uint32_t off_i64; // H + (-2^63 mod m): int64 x read as u = x ^ 2^63
+  uint32_t off_u64; // H
+  uint32_t off_i32; // H + (-2^31 mod m): int32 acc read as u = acc ^ 2^31
+};
+
+inline ModulusConsts make_modulus_consts(uint32_t m) {
+  ModulusConsts c{};
+  c.m = m;
+  c.half = m / 2u;
+  c.recip = static_cast<uint32_t>(((uint64_t{1} << 32) + m - 1u) / m);
+  uint32_t lo = 0, hi = 0;
+  for (uint32_t b = 0; b < 4; ++b) {
+    const uint64_t plo = (uint64_t{1} << (8u * b)) % m;
+    // 2^(32+8b) mod m computed without overflow
+    uint64_t phi = (uint64_t{1} << 32) % m;
+    phi = (phi * ((uint64_t{1} << (8u * b)) % m)) % m;
+    lo |= static_cast<uint32_t>(plo) << (8u * b);
+    hi |= static_cast<uint32_t>(phi) << (8u * b);
+  }
+  c.pow_lo = lo;
+  c.pow_hi = hi;
+  const uint64_t two63_mod = (uint64_t{1} << 63) % m;
+  const uint64_t two31_mod = (uint64_t{1} << 31) % m;
+  c.off_i64 = c.half + static_cast<uint32_t>((m - two63_mod) % m);
+  c.off_u64 = c.half;
+  c.off_i32 = c.half + static_cast<uint32_t>((m - two31_mod) % m);
+  return c;
+}
+
+// Up to kMaxPrefix planes of modulus constants, passed by value to kernels.
+struct PlaneConsts {
+  ModulusConsts mod[kMaxPrefix];
+};
+
+inline PlaneConsts make_ladder_plane_consts(uint32_t prefix) {
+  PlaneConsts pc{};
+  for (uint32_t p = 0; p < prefix && p < kMaxPrefix; ++p) pc.mod[p] = make_modulus_consts(kLadder[p]);
+  return pc;
+}
+
+inline PlaneConsts make_single_plane_consts(uint32_t modulus) {
+  PlaneConsts pc{};
+  pc.mod[0] = make_modulus_consts(modulus);
+  return pc;
+}
+
+// ---- Garner reconstruction ---------------------------------------------------
+//
+// Mixed-radix digits v_i in [0, m_i) with x = sum_i v_i * P_i, P_i = prod_{t<i} m_t:
+//   v_i = (r_i * I_i + sum_{j<i} v_j * W[j][i]) mod m_i
+// where r_i is the centered residue, I_i = P_i^{-1} mod m_i and
+// W[j][i] = (-P_j * I_i) mod m_i. This is Garner's recurrence
+// v_i = (r_i - x_i) * P_i^{-1} mod m_i with x_i mod m_i expanded over the
+// earlier digits, so each digit costs one reduction. Digits are kept packed
+// four per dword, so the inner sum is a byte dot product (v_dot4_u32_u8) against
+// wpack[i][q] = bytes W[4q..4q+3][i]. The sum stays below 2^21 (r_i*I_i + bias
+// <= 2^16, 19 * 255 * 255 < 2^21), inside the exact range of the reduction
+// above.
+//
+// The integer x is then rebuilt by Horner's rule x = (..(v_{P-1} m_{P-2} +
+// v_{P-2}) m_{P-3} + ..) m_0 + v_0 in 24-bit limbs (v_mad_u32_u24 keeps every
+// step exact in 32 bits).
+constexpr uint32_t kGarnerDigitWords = (kMaxPrefix + 3) / 4;  // 5
+constexpr uint32_t kWideLimbs = 7;                            // 7 * 24 = 168 >= 154.85 bits
+
+struct GarnerConsts {
+  uint32_t prefix;
+  uint32_t m[kMaxPrefix];
+  uint32_t recip[kMaxPrefix];
+  uint32_t inv[kMaxPrefix];   // I_i
+  uint32_t bias[kMaxPrefix];  // multiple of m_i >= 128 * I_i (keeps r_i*I_i + bias >= 0)
+  uint32_t wpack[kMaxPrefix][kGarnerDigitWords];
+  uint32_t half_ceil[kWideLimbs];  // ceil(P/2) = (P+1)/2 in 24-bit limbs
+  uint32_t product[kWideLimbs];    // P in 24-bit limbs
+};
+
+// Simple multiprecision helper on 24-bit limbs used only to build the tables.
+struct Limbs24 {
+  uint32_t w[kWideLimbs] = {};
+  void mul_add(uint32_t mul, uint32_t add) {
+    uint64_t carry = add;
+    for (uint32_t i = 0; i < kWideLimbs; ++i) {
+      const uint64_t t = static_cast<uint64_t>(w[i]) * mul + carry;
+      w[i] = static_cast<uint32_t>(t & 0xFFFFFFu);
+      carry = t >> 24;
+    }
+  }
+  uint32_t mod_small(uint32_t m) const {
+    uint64_t r = 0;
+    for (int i = static_cast<int>(kWideLimbs) - 1; i >= 0; --i) r = ((r << 24) | w[i]) % m;
+    return static_cast<uint32_t>(r);
+  }
+};
+
+inline uint32_t inverse_mod(uint32_t a, uint32_t m) {
+  // extended Euclid; a and m coprime
+  int64_t t = 0, nt = 1, r = m, nr = a % m;
+  while (nr != 0) {
+    const int64_t q = r / nr;
+    const int64_t tt = t - q * nt;
+    t = nt;
+    nt = tt;
+    const int64_t rr = r - q * nr;
+    r = nr;
+    nr = rr;
+  }
+  if (r != 1) return 0;
+  if (t < 0) t += m;
+  return static_cast<uint32_t>(t);
+}
+
+inline GarnerConsts make_garner_consts(uint32_t prefix) {
+  GarnerConsts g{};
+  g.prefix = prefix;
+  Limbs24 pj[kMaxPrefix + 1];
+  pj[0].w[0] = 1;
+  for (uint32_t j = 0; j < prefix; ++j) {
+    pj[j + 1] = pj[j];
+    pj[j + 1].mul_add(kLadder[j], 0);
+  }
+  for (uint32_t i = 0; i < prefix; ++i) {
+    const uint32_t m = kLadder[i];
+    g.m[i] = m;
+    g.recip[i] = static_cast<uint32_t>(((uint64_t{1} << 32) + m - 1u) / m);
+    const uint32_t inv = i == 0 ? 1u : inverse_mod(pj[i].mod_small(m), m);
+    g.inv[i] = inv;
+    g.bias[i] = m * ((128u * inv + m - 1u) / m);
+    for (uint32_t j = 0; j < i; ++j) {
+      const uint32_t pm = pj[j].mod_small(m);
+      const uint32_t w = (m - static_cast<uint32_t>((static_cast<uint64_t>(pm) * inv) % m)) % m;
+      g.wpack[i][j / 4] |= w << (8u * (j % 4));
+    }
+  }
+  // P and ceil(P/2) = (P + 1) >> 1
+  Limbs24 p = pj[prefix];
+  for (uint32_t i = 0; i < kWideLimbs; ++i) g.product[i] = p.w[i];
+  Limbs24 h = p;
+  h.mul_add(1, 1);
+  for (uint32_t i = 0; i < kWideLimbs; ++i) {
+    const uint32_t next = i + 1 < kWideLimbs ? h.w[i + 1] : 0u;
+    g.half_ceil[i] = (h.w[i] >> 1) | ((next & 1u) << 23);
+  }
+  return g;
+}
+
+// 64-bit value as 24-bit limbs.
+inline void u64_to_limbs24(uint64_t v, uint32_t out[kWideLimbs]) {
+  for (uint32_t i = 0; i < kWideLimbs; ++i) {
+    out[i] = i < 3 ? static_cast<uint32_t>((v >> (24u * i)) & 0xFFFFFFu) : 0u;
+  }
+}
+
+// ---- byte-matrix planes in HBM -------------------------------------------------
+//
+// Resident layout "rns8_mi355x_planes_v1": plane p of a rows x cols matrix is
+// row-major int8 with a row pitch padded to 16 bytes (zero filled) and a plane
+// pitch padded to 256 bytes. Padding keeps every 16-byte vector access of the
+// GEMM and pack kernels aligned; the zero columns contribute nothing to any
+// product, so GEMM tiles may read them freely.
+constexpr int64_t kRowAlign = 16;
+constexpr int64_t kPlaneAlign = 256;
+
+inline int64_t padded_ld(int64_t cols) { return (cols + kRowAlign - 1) / kRowAlign * kRowAlign; }
+inline int64_t plane_pitch(int64_t rows, int64_t cols) {
+  const int64_t bytes = rows * padded_ld(cols);
+  return (bytes + kPlaneAlign - 1) / kPlaneAlign * kPlaneAlign;
+}
+
+}  // namespace rns8x
