@@ -56,13 +56,16 @@ struct Tile {
   static constexpr int kBGroups = kBRows / 16;                     // 16-row groups per wave
 };
 
+// XOR swizzle of the 16-byte chunk index by row bits 1-5. With BK = 64 (four
+// chunks per row) it keeps every LDS access pattern of the kernel free of
+// bank conflicts for both 32-bank/8-lane and 64-bank/16-lane ds_*_b128
+// servicing: fragment reads (32 consecutive rows, one chunk), A staging writes
+// (16 rows x 4 chunks) and the rotated B staging writes (rows 4*lane + (j +
+// lane) % 4, one chunk); checked by an exhaustive model on the host.
 template <int BK>
 __device__ __forceinline__ int swizzle_chunk(int row, int chunk) {
-  if constexpr (BK == 64) {
-    return chunk ^ (((row >> 1) ^ (row >> 3)) & 3);
-  } else {
-    return chunk ^ ((row ^ (row >> 3)) & 7);
-  }
+  static_assert(BK == 64, "swizzle derived for 4 chunks per row");
+  return chunk ^ (((row >> 1) & 3) ^ (((row >> 3) & 1) * 3) ^ ((row >> 4) & 3));
 }
 
 // Exact centered residue of an int32 (see tables.hpp): u = acc + 2^31 read as
@@ -167,13 +170,16 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
   const uint32_t b_voff = static_cast<uint32_t>(wave * T::kBRows * args.ldb) +
                           (b_col < args.ldb ? static_cast<uint32_t>(b_col) : 0x80000000u);
 
-  auto load_tile = [&](int t) {
+  auto load_a = [&](int t) {
     const int64_t k0 = kbeg + static_cast<int64_t>(t) * BK;
 #pragma unroll
     for (int i = 0; i < T::kALoads; ++i) {
       const uint32_t uni = static_cast<uint32_t>(k0 + static_cast<int64_t>(i) * T::kARowStep * args.lda);
       a_stage[i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, static_cast<int>(a_voff + uni), 0, 0);
     }
+  };
+  auto load_b = [&](int t) {
+    const int64_t k0 = kbeg + static_cast<int64_t>(t) * BK;
     const int64_t rows_left = kend - k0;
     const int64_t b_rows = rows_left < BK ? (rows_left > 0 ? rows_left : 0) : BK;
     const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B + k0 * args.ldb, b_rows * args.ldb);
@@ -184,34 +190,54 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
           static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(b_rsrc, static_cast<int>(b_voff + uni), 0, 0));
     }
   };
+  auto load_tile = [&](int t) {
+    load_a(t);
+    load_b(t);
+  };
 
   // ---- register -> LDS (3-buffer ring; B transposed to K-contiguous rows) --
-  auto store_tile = [&](int buf) {
+  auto store_a = [&](int buf) {
     int8_t* const la = lds + buf * (T::kBufA + T::kBufB);
-    int8_t* const lb = la + T::kBufA;
 #pragma unroll
     for (int i = 0; i < T::kALoads; ++i) {
       const int r = a_row0 + i * T::kARowStep;
       *reinterpret_cast<v4i*>(la + r * BK + swizzle_chunk<BK>(r, a_chunk) * 16) = a_stage[i];
     }
+  };
+  auto store_b = [&](int buf) {
+    int8_t* const lb = lds + buf * (T::kBufA + T::kBufB) + T::kBufA;
+    // Each lane holds a 16-row x 4-column byte block of B. The block is
+    // transposed to 4 columns x 16 K bytes; the 4 output columns are emitted in
+    // an order rotated by (lane & 3) so the rows one write instruction touches
+    // cover all residues mod 4 (rows 4*lane + (j + lane) % 4), which keeps the
+    // writes bank-conflict free. The rotation is a per-lane byte rotate of each
+    // input dword before the fixed 4x4 transpose.
+    const uint32_t rot = static_cast<uint32_t>(lane & 3);
 #pragma unroll
     for (int g = 0; g < T::kBGroups; ++g) {
       uint32_t y[4][4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int base = 16 * g + 4 * q;
-        transpose4x4(b_stage[base], b_stage[base + 1], b_stage[base + 2], b_stage[base + 3], y[q][0], y[q][1],
-                     y[q][2], y[q][3]);
+        const uint32_t x0 = __builtin_amdgcn_alignbyte(b_stage[base], b_stage[base], rot);
+        const uint32_t x1 = __builtin_amdgcn_alignbyte(b_stage[base + 1], b_stage[base + 1], rot);
+        const uint32_t x2 = __builtin_amdgcn_alignbyte(b_stage[base + 2], b_stage[base + 2], rot);
+        const uint32_t x3 = __builtin_amdgcn_alignbyte(b_stage[base + 3], b_stage[base + 3], rot);
+        transpose4x4(x0, x1, x2, x3, y[q][0], y[q][1], y[q][2], y[q][3]);
       }
       const int chunk = (wave * T::kBRows) / 16 + g;
 #pragma unroll
-      for (int col = 0; col < 4; ++col) {
-        const int r = 4 * lane + col;
-        const v4i v = {static_cast<int>(y[0][col]), static_cast<int>(y[1][col]), static_cast<int>(y[2][col]),
-                       static_cast<int>(y[3][col])};
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * lane + ((j + static_cast<int>(rot)) & 3);
+        const v4i v = {static_cast<int>(y[0][j]), static_cast<int>(y[1][j]), static_cast<int>(y[2][j]),
+                       static_cast<int>(y[3][j])};
         *reinterpret_cast<v4i*>(lb + r * BK + swizzle_chunk<BK>(r, chunk) * 16) = v;
       }
     }
+  };
+  auto store_tile = [&](int buf) {
+    store_a(buf);
+    store_b(buf);
   };
 
   // ---- fragments -------------------------------------------------------------
@@ -243,9 +269,9 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v16i{};
 
-  auto mfma_step = [&](const Frags& f) {
+  auto mfma_rows = [&](const Frags& f, int i0, int i1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = i0; i < i1; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
   };
@@ -274,26 +300,41 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
   for (int kt = 0; kt < ktiles; ++kt) {
     const int buf1 = buf == 2 ? 0 : buf + 1;
     const int buf2 = buf1 == 2 ? 0 : buf1 + 1;
-    store_tile(buf2);
-    load_tile(kt + 3);
+    // Region 1: sub-step-1 fragment reads issued first (consumed in region 3),
+    // half of the sub-step-0 MFMAs, A staging store + next A loads.
     read_frags(buf, 1, f1);
-    mfma_step(f0);
+    mfma_rows(f0, 0, 2);
+    store_a(buf2);
+    load_a(kt + 3);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x080, 2, 1);  // DS
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // VMEM read
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);  // VALU
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Region 2: rest of sub-step 0; B transpose + store + next B loads.
+    mfma_rows(f0, 2, 4);
+    store_b(buf2);
+    load_b(kt + 3);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 2);  // VALU (rotate, transpose, offsets)
+      __builtin_amdgcn_sched_group_barrier(0x080, 1, 2);  // DS write
+      __builtin_amdgcn_sched_group_barrier(0x020, 2, 2);  // VMEM read
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Region 3: sub-step 1; prefetch of the next tile's first fragments.
     read_frags(buf1, 0, f0n);
-    mfma_step(f1);
-    // Interleave the staging work into the shadow of the MFMAs.
+    mfma_rows(f1, 0, 4);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU (transposes, offsets)
-      __builtin_amdgcn_sched_group_barrier(0x080, 1, 0);  // DS write / read
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 3);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 3);  // DS read
     }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (next fragments)
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-    }
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     f0 = f0n;
     buf = buf1;
