@@ -8,18 +8,17 @@
 //   * workgroup = 256 threads (4 wave64s) owning a 256x256 output tile of one
 //     plane (and one K slice when split-K is on); waves form a 2x2 grid of
 //     128x128 wave tiles.
-//   * K is consumed in BK-byte steps. A tile (256 x BK, K-contiguous rows) and
-//     B tile (BK x 256, N-contiguous rows) are staged global -> VGPR -> LDS with
-//     LDS double buffering: the global loads for step t+1 are issued before the
-//     MFMAs of step t and written to the other LDS buffer after them, so one
-//     barrier per step suffices.
-//   * B arrives N-contiguous but the MFMA wants 16 K-contiguous bytes per lane,
-//     so each thread loads BK/4 rows x 4 columns with dword loads (a wave reads
-//     whole 256-byte rows, fully coalesced) and transposes 4x4 byte blocks with
-//     v_perm_b32 before writing 16-byte K runs to LDS.
-//   * LDS rows are BK bytes; 16-byte chunks are XOR-swizzled by row so that the
-//     ds_read_b128 fragment loads of 8 (32-bank) or 16 (64-bank) consecutive
-//     rows touch distinct banks.
+//   * K is consumed in BK = 64 byte steps through a 4-stage LDS ring. Both
+//     operands go global -> LDS by buffer-load DMA (no VGPR staging): A tiles
+//     (256 x 64, K-contiguous rows) and B tiles (64 x 256, N-contiguous rows,
+//     the layout they have in HBM). The DMA of step t+3 is in flight while
+//     step t computes; one barrier per step.
+//   * A fragments are ds_read_b128 of 16 K-contiguous bytes; B fragments are
+//     gathered K-contiguous from the N-contiguous stage by ds_read_b64_tr_b8
+//     (LDS transpose read), so no transpose runs on the VALU.
+//   * Stage rows are XOR-swizzled in 16-byte chunks (swizzle applied on the
+//     global-address side of the DMA) so every fragment read is bank-conflict
+//     free.
 //   * MFMA: v_mfma_i32_32x32x32_i8 with the B^T fragment as src0 and the A
 //     fragment as src1, so each lane ends with 4 consecutive output columns
 //     of one row per register group -> one packed dword store per group.
@@ -36,6 +35,22 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+
+__device__ __forceinline__ lds_v2i* as_lds_v2i(const int8_t* p) {
+  return (lds_v2i*)(const_cast<int8_t*>(p));  // generic -> LDS address space
+}
+__device__ __forceinline__ uint32_t lds_address(const int8_t* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t*)(const_cast<int8_t*>(p))));
+}
+
+// s_waitcnt immediates "vmcnt <= n" leaving expcnt and lgkmcnt unconstrained
+// (gfx9 encoding: vmcnt[3:0] bits 3:0, expcnt bits 6:4, lgkmcnt bits 11:8,
+// vmcnt[5:4] bits 15:14).
+constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kWaitVm[9] = {wait_vm(0), wait_vm(1), wait_vm(2), wait_vm(3), wait_vm(4),
+                            wait_vm(5), wait_vm(6), wait_vm(7), wait_vm(8)};
 
 constexpr int kBM = 256;
 constexpr int kBN = 256;
@@ -46,26 +61,30 @@ constexpr int kBufferFlags = 0x00020000;
 
 template <int BK>
 struct Tile {
-  static constexpr int kChunks = BK / 16;                          // 16-byte chunks per LDS row
-  static constexpr int kBufA = kBM * BK;                           // bytes per A buffer
-  static constexpr int kBufB = kBN * BK;                           // bytes per B buffer
-  static constexpr int kLds = 3 * (kBufA + kBufB);                 // 3-buffer ring
-  static constexpr int kARowStep = kThreads / kChunks;             // rows covered per A load round
-  static constexpr int kALoads = kBM * kChunks / kThreads;         // 16-byte A loads per thread
-  static constexpr int kBRows = BK / 4;                            // B k-rows per wave (4 waves)
-  static constexpr int kBGroups = kBRows / 16;                     // 16-row groups per wave
+  static constexpr int kBufA = kBM * BK;              // A stage: 256 rows x BK bytes
+  static constexpr int kBufB = kBN * BK;              // B stage: BK k-rows x 256 bytes
+  static constexpr int kStage = kBufA + kBufB;
+  static constexpr int kStages = 4;
+  static constexpr int kLds = kStages * kStage;       // 128 KB of the 160 KB LDS
+  static constexpr int kDma = kBufA / 1024 / 4;       // 1 KB DMA blocks per wave, per operand
 };
 
-// XOR swizzle of the 16-byte chunk index by row bits 1-5. With BK = 64 (four
-// chunks per row) it keeps every LDS access pattern of the kernel free of
-// bank conflicts for both 32-bank/8-lane and 64-bank/16-lane ds_*_b128
-// servicing: fragment reads (32 consecutive rows, one chunk), A staging writes
-// (16 rows x 4 chunks) and the rotated B staging writes (rows 4*lane + (j +
-// lane) % 4, one chunk); checked by an exhaustive model on the host.
-template <int BK>
-__device__ __forceinline__ int swizzle_chunk(int row, int chunk) {
-  static_assert(BK == 64, "swizzle derived for 4 chunks per row");
+// A stage: row-major 256 x 64 bytes. The 16-byte chunk index is XORed with
+// row bits 1-5 so the ds_read_b128 fragment loads (32 consecutive rows, one
+// chunk) are bank-conflict free for both 32-bank/8-lane and 64-bank/16-lane
+// servicing (exhaustive host model).
+__device__ __forceinline__ int swizzle_a(int row, int chunk) {
   return chunk ^ (((row >> 1) & 3) ^ (((row >> 3) & 1) * 3) ^ ((row >> 4) & 3));
+}
+
+// B stage: row-major 64 (k) x 256 (n) bytes, N-contiguous as in global
+// memory. The 16-byte chunk index is XORed with f(k & 7), f(x) = 2x mod 16 +
+// x / 4: a 16-lane transpose read touches 8 consecutive k rows of one chunk,
+// and f sends them to 8 (32-bank model) resp., with the neighbouring group,
+// 16 (64-bank model) distinct bank quads (exhaustive host model).
+__device__ __forceinline__ int swizzle_b(int k, int chunk) {
+  const int x = k & 7;
+  return chunk ^ (((2 * x) & 15) | (x >> 2));
 }
 
 // Exact centered residue of an int32 (see tables.hpp): u = acc + 2^31 read as
@@ -90,24 +109,33 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64
   return __builtin_amdgcn_make_buffer_rsrc(base, static_cast<short>(0), n, kBufferFlags);
 }
 
+// The same resource as four wave-uniform dwords, for the DMA asm below.
+__device__ __forceinline__ v4i buffer_rsrc(const void* p, int64_t bytes) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(p);
+  return v4i{__builtin_amdgcn_readfirstlane(static_cast<int>(addr)),
+             __builtin_amdgcn_readfirstlane(static_cast<int>(addr >> 32)),
+             __builtin_amdgcn_readfirstlane(static_cast<int>(bytes)), kBufferFlags};
+}
+
+// 16 bytes per lane from a raw buffer straight into LDS: lane l's bytes land
+// at lds_addr + 16*l (M0 = lds_addr, wave-uniform). Written as asm so the
+// compiler does not track the LDS write (it would otherwise wait for every
+// outstanding DMA before each LDS read); callers order the DMA against LDS
+// reads with explicit vmcnt waits and barriers. M0 is a reserved register the
+// compiler re-initialises before any use of its own.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(uint32_t lds_addr, uint32_t voffset, v4i rsrc) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc)
+               : "m0");
+}
+#pragma clang diagnostic pop
+
 __device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {
   return (static_cast<uint32_t>(a) & 0xFFu) | ((static_cast<uint32_t>(b) & 0xFFu) << 8) |
          ((static_cast<uint32_t>(c) & 0xFFu) << 16) | (static_cast<uint32_t>(d) << 24);
-}
-
-// 4x4 byte transpose: x_r holds bytes (row r, cols 0..3); y_c gets bytes
-// (rows 0..3, col c). v_perm_b32(s0, s1, sel): selector 0-3 picks s1 bytes,
-// 4-7 picks s0 bytes.
-__device__ __forceinline__ void transpose4x4(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3, uint32_t& y0,
-                                             uint32_t& y1, uint32_t& y2, uint32_t& y3) {
-  const uint32_t t0 = __builtin_amdgcn_perm(x1, x0, 0x06020400u);  // x0.b0 x1.b0 x0.b2 x1.b2
-  const uint32_t t1 = __builtin_amdgcn_perm(x1, x0, 0x07030501u);  // x0.b1 x1.b1 x0.b3 x1.b3
-  const uint32_t t2 = __builtin_amdgcn_perm(x3, x2, 0x06020400u);
-  const uint32_t t3 = __builtin_amdgcn_perm(x3, x2, 0x07030501u);
-  y0 = __builtin_amdgcn_perm(t2, t0, 0x05040100u);  // t0.b0 t0.b1 t2.b0 t2.b1
-  y2 = __builtin_amdgcn_perm(t2, t0, 0x07060302u);  // t0.b2 t0.b3 t2.b2 t2.b3
-  y1 = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-  y3 = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
 template <int BK>
@@ -120,7 +148,7 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wave_m = wave >> 1;
   const int wave_n = wave & 1;
 
@@ -151,116 +179,89 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
   const int64_t kend = min(k_stop, kbeg + k_slice);
   const int ktiles = kend > kbeg ? static_cast<int>((kend - kbeg + BK - 1) / BK) : 0;
 
-  // ---- global -> register staging -----------------------------------------
-  // Global loads go through raw buffer resources: every offset that needs a
-  // range check is in the per-lane VGPR offset, which the hardware compares
-  // with num_records and answers with zero when out of range. A's resource
-  // covers the valid rows of this tile's row panel (rows >= M read as zero);
-  // B's resource is rebuilt per K step to cover only rows [k0, min(k0+BK,
-  // kend)), so rows past the slice or past K read as zero. Columns past the
-  // padded pitch get an offset beyond num_records.
-  const int a_chunk = tid % T::kChunks;
-  const int a_row0 = tid / T::kChunks;
-  v4i a_stage[T::kALoads];
-  uint32_t b_stage[T::kBRows];
+  // ---- global -> LDS by DMA ------------------------------------------------
+  // buffer_load_dwordx4 ... lds writes lane l's 16 bytes to M0 + 16*l, so one
+  // wave instruction fills a contiguous 1 KB block of a stage; each lane loads
+  // the global bytes that belong in its slot (the LDS swizzle is applied on
+  // the global side). Range checks come from the buffer resources and read
+  // zero when out of range: A's covers the valid rows of this tile's row panel
+  // from the current K offset on, B's the k rows [k0, min(k0 + BK, kend)).
+  // B columns past the padded pitch get an offset beyond num_records.
   const int64_t a_rows = min(static_cast<int64_t>(kBM), args.m - m0);
-  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(A + m0 * args.lda, a_rows * args.lda);
-  const uint32_t a_voff = static_cast<uint32_t>(a_row0 * args.lda + 16 * a_chunk);
-  const int64_t b_col = n0 + 4 * lane;
-  const uint32_t b_voff = static_cast<uint32_t>(wave * T::kBRows * args.ldb) +
-                          (b_col < args.ldb ? static_cast<uint32_t>(b_col) : 0x80000000u);
-
-  auto load_a = [&](int t) {
-    const int64_t k0 = kbeg + static_cast<int64_t>(t) * BK;
+  const int8_t* const a_panel = A + m0 * args.lda;
+  uint32_t a_voff[T::kDma];  // wave w fills A rows 64w .. 64w+63 (4 blocks of 16 rows)
+  uint32_t b_voff[T::kDma];  // wave w fills B k rows 16w .. 16w+15 (4 blocks of 4 rows)
 #pragma unroll
-    for (int i = 0; i < T::kALoads; ++i) {
-      const uint32_t uni = static_cast<uint32_t>(k0 + static_cast<int64_t>(i) * T::kARowStep * args.lda);
-      a_stage[i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, static_cast<int>(a_voff + uni), 0, 0);
-    }
+  for (int i = 0; i < T::kDma; ++i) {
+    const int blk = wave * T::kDma + i;
+    const int row = 16 * blk + (lane >> 2);
+    a_voff[i] = static_cast<uint32_t>(row * args.lda + 16 * swizzle_a(row, lane & 3));
+    const int k = 4 * blk + (lane >> 4);
+    const int64_t col = n0 + 16 * swizzle_b(k, lane & 15);
+    b_voff[i] = static_cast<uint32_t>(k * args.ldb) + (col < args.ldb ? static_cast<uint32_t>(col) : 0x80000000u);
+  }
+  const uint32_t lds_base = lds_address(lds) + static_cast<uint32_t>(wave * T::kDma * 1024);
+
+  struct TileSrc {
+    v4i a, b;  // buffer resources of one K tile
   };
-  auto load_b = [&](int t) {
+  auto tile_src = [&](int t) {
     const int64_t k0 = kbeg + static_cast<int64_t>(t) * BK;
+    const int64_t a_bytes = a_rows * args.lda - k0;
     const int64_t rows_left = kend - k0;
     const int64_t b_rows = rows_left < BK ? (rows_left > 0 ? rows_left : 0) : BK;
-    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B + k0 * args.ldb, b_rows * args.ldb);
-#pragma unroll
-    for (int i = 0; i < T::kBRows; ++i) {
-      const uint32_t uni = static_cast<uint32_t>(i * args.ldb);
-      b_stage[i] =
-          static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(b_rsrc, static_cast<int>(b_voff + uni), 0, 0));
-    }
+    return TileSrc{buffer_rsrc(a_panel + k0, a_bytes > 0 ? a_bytes : 0), buffer_rsrc(B + k0 * args.ldb, b_rows * args.ldb)};
   };
-  auto load_tile = [&](int t) {
-    load_a(t);
-    load_b(t);
+  auto dma_a = [&](const TileSrc& src, int stage, int i) {
+    dma16(lds_base + static_cast<uint32_t>(stage * T::kStage + 1024 * i), a_voff[i], src.a);
   };
-
-  // ---- register -> LDS (3-buffer ring; B transposed to K-contiguous rows) --
-  auto store_a = [&](int buf) {
-    int8_t* const la = lds + buf * (T::kBufA + T::kBufB);
-#pragma unroll
-    for (int i = 0; i < T::kALoads; ++i) {
-      const int r = a_row0 + i * T::kARowStep;
-      *reinterpret_cast<v4i*>(la + r * BK + swizzle_chunk<BK>(r, a_chunk) * 16) = a_stage[i];
-    }
+  auto dma_b = [&](const TileSrc& src, int stage, int i) {
+    dma16(lds_base + static_cast<uint32_t>(stage * T::kStage + T::kBufA + 1024 * i), b_voff[i], src.b);
   };
-  auto store_b = [&](int buf) {
-    int8_t* const lb = lds + buf * (T::kBufA + T::kBufB) + T::kBufA;
-    // Each lane holds a 16-row x 4-column byte block of B. The block is
-    // transposed to 4 columns x 16 K bytes; the 4 output columns are emitted in
-    // an order rotated by (lane & 3) so the rows one write instruction touches
-    // cover all residues mod 4 (rows 4*lane + (j + lane) % 4), which keeps the
-    // writes bank-conflict free. The rotation is a per-lane byte rotate of each
-    // input dword before the fixed 4x4 transpose.
-    const uint32_t rot = static_cast<uint32_t>(lane & 3);
+  auto issue_tile = [&](int t, int stage) {
+    const TileSrc src = tile_src(t);
 #pragma unroll
-    for (int g = 0; g < T::kBGroups; ++g) {
-      uint32_t y[4][4];
+    for (int i = 0; i < T::kDma; ++i) dma_a(src, stage, i);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int base = 16 * g + 4 * q;
-        const uint32_t x0 = __builtin_amdgcn_alignbyte(b_stage[base], b_stage[base], rot);
-        const uint32_t x1 = __builtin_amdgcn_alignbyte(b_stage[base + 1], b_stage[base + 1], rot);
-        const uint32_t x2 = __builtin_amdgcn_alignbyte(b_stage[base + 2], b_stage[base + 2], rot);
-        const uint32_t x3 = __builtin_amdgcn_alignbyte(b_stage[base + 3], b_stage[base + 3], rot);
-        transpose4x4(x0, x1, x2, x3, y[q][0], y[q][1], y[q][2], y[q][3]);
-      }
-      const int chunk = (wave * T::kBRows) / 16 + g;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 4 * lane + ((j + static_cast<int>(rot)) & 3);
-        const v4i v = {static_cast<int>(y[0][j]), static_cast<int>(y[1][j]), static_cast<int>(y[2][j]),
-                       static_cast<int>(y[3][j])};
-        *reinterpret_cast<v4i*>(lb + r * BK + swizzle_chunk<BK>(r, chunk) * 16) = v;
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-    store_a(buf);
-    store_b(buf);
+    for (int i = 0; i < T::kDma; ++i) dma_b(src, stage, i);
   };
 
   // ---- fragments -------------------------------------------------------------
+  // K sub-step s covers k = 32s .. 32s+31 of a stage; lane l takes the 16 k
+  // values 32s + 16*(l >> 5) + 0..15 for both operands.
+  // A (MFMA src1): lane l holds row l & 31 of a 32-row block: one ds_read_b128.
+  // B (MFMA src0): lane l holds column l & 31 of a 32-column block, gathered
+  // by two ds_read_b64_tr_b8. In each 16-lane group, lane j addresses the
+  // 8-byte row segment (k = base + (j >> 1), columns 8*(j & 1) .. +7 of the
+  // group's 16 columns) and lane i receives byte i & 7 of the segments of
+  // lanes 2b + (i >> 3), b = 0..7: its column across 8 consecutive k.
   const int frag_row = lane & 31;
   const int frag_half = lane >> 5;
+  const int tr_j = lane & 15;
+  const int tr_g = lane >> 4;
   struct Frags {
     v4i a[4];
     v4i b[4];
   };
-  auto read_frags = [&](int buf, int s, Frags& f) {
-    const int8_t* const la = lds + buf * (T::kBufA + T::kBufB);
-    const int8_t* const lb = la + T::kBufA;
-    const int c = 2 * s + frag_half;
+  auto read_a = [&](int stage, int s, int i) {
+    const int r = wave_m * 128 + 32 * i + frag_row;
+    return *reinterpret_cast<const v4i*>(lds + stage * T::kStage + r * BK + swizzle_a(r, 2 * s + frag_half) * 16);
+  };
+  auto read_b = [&](int stage, int s, int j) {
+    const int8_t* const sb = lds + stage * T::kStage + T::kBufA;
+    const int ncol = wave_n * 128 + 32 * j + 16 * (tr_g & 1) + 8 * (tr_j & 1);
+    const int k = 32 * s + 16 * (tr_g >> 1) + (tr_j >> 1);
+    const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        as_lds_v2i(sb + k * kBN + swizzle_b(k, ncol >> 4) * 16 + (ncol & 8)));
+    const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        as_lds_v2i(sb + (k + 8) * kBN + swizzle_b(k + 8, ncol >> 4) * 16 + (ncol & 8)));
+    return v4i{lo[0], lo[1], hi[0], hi[1]};
+  };
+  auto read_frags = [&](int stage, int s, Frags& f) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = wave_m * 128 + 32 * i + frag_row;
-      f.a[i] = *reinterpret_cast<const v4i*>(la + r * BK + swizzle_chunk<BK>(r, c) * 16);
-    }
+    for (int i = 0; i < 4; ++i) f.a[i] = read_a(stage, s, i);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = wave_n * 128 + 32 * j + frag_row;
-      f.b[j] = *reinterpret_cast<const v4i*>(lb + r * BK + swizzle_chunk<BK>(r, c) * 16);
-    }
+    for (int j = 0; j < 4; ++j) f.b[j] = read_b(stage, s, j);
   };
 
   v16i acc[4][4];
@@ -277,68 +278,61 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
   };
 
   // ---- pipeline ----------------------------------------------------------------
-  // Three LDS ring buffers. Step t computes tile t from buffer t%3 while
-  //   * tile t+2 (loaded into registers during step t-1) is transposed and
-  //     written to buffer (t+2)%3, last read in step t-1;
-  //   * the global loads of tile t+3 are issued (consumed in step t+1, so a
-  //     whole step hides their latency);
-  //   * the first fragments of tile t+1 are prefetched from buffer (t+1)%3,
-  //     complete since the barrier that ended step t-1.
-  // The barrier ending step t publishes tile t+2 and retires all reads of
-  // buffer t%3. Past the end of K the loads return zeros and land in buffers
-  // no later step reads, so the body has no branches and is one scheduling
-  // region.
+  // Four LDS stages. Step t computes tile t from stage t%4 while the DMA of
+  // tile t+3 into stage (t+3)%4 (last read in step t-1) is in flight and the
+  // first fragments of tile t+1 are prefetched. Before the barrier that ends
+  // step t each wave waits until only its tile t+3 DMAs are outstanding, so
+  // the barrier publishes tile t+2 (first read in step t+1) and retires every
+  // read of stage t%4. Past the end of K the DMAs read zeros into stages no
+  // later step reads, so the body has no branches. The DMAs are issued from
+  // inline asm, so the compiler tracks no LDS write for them and adds no
+  // waits before the fragment reads: the explicit vmcnt waits below are
+  // what orders them.
   Frags f0, f1, f0n;
-  load_tile(0);
-  store_tile(0);
-  load_tile(1);
-  store_tile(1);
-  load_tile(2);
+  issue_tile(0, 0);
+  issue_tile(1, 1);
+  issue_tile(2, 2);
+  __builtin_amdgcn_s_waitcnt(kWaitVm[2 * T::kDma]);  // tiles 0 and 1 landed
   __syncthreads();
   read_frags(0, 0, f0);
-  int buf = 0;
+  int stage = 0;
   for (int kt = 0; kt < ktiles; ++kt) {
-    const int buf1 = buf == 2 ? 0 : buf + 1;
-    const int buf2 = buf1 == 2 ? 0 : buf1 + 1;
-    // Region 1: sub-step-1 fragment reads issued first (consumed in region 3),
-    // half of the sub-step-0 MFMAs, A staging store + next A loads.
-    read_frags(buf, 1, f1);
-    mfma_rows(f0, 0, 2);
-    store_a(buf2);
-    load_a(kt + 3);
+    const int stage1 = (stage + 1) & 3;
+    const int stage3 = (stage + 3) & 3;
+    // Region 1: sub-step 0 MFMAs; tile t+3 DMAs interleaved (in source order)
+    // with the sub-step 1 fragment reads.
+    const TileSrc src = tile_src(kt + 3);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
+      dma_a(src, stage3, i);
+      f1.a[i] = read_a(stage, 1, i);
+      dma_b(src, stage3, i);
+      f1.b[i] = read_b(stage, 1, i);
+    }
+    mfma_rows(f0, 0, 4);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x080, 2, 1);  // DS
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // VMEM read
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // DS read
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
     __builtin_amdgcn_sched_barrier(0);
-    // Region 2: rest of sub-step 0; B transpose + store + next B loads.
-    mfma_rows(f0, 2, 4);
-    store_b(buf2);
-    load_b(kt + 3);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 8, 2);  // VALU (rotate, transpose, offsets)
-      __builtin_amdgcn_sched_group_barrier(0x080, 1, 2);  // DS write
-      __builtin_amdgcn_sched_group_barrier(0x020, 2, 2);  // VMEM read
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // Region 3: sub-step 1; prefetch of the next tile's first fragments.
-    read_frags(buf1, 0, f0n);
+    // Region 2: sub-step 1 MFMAs; first fragments of tile t+1.
+    read_frags(stage1, 0, f0n);
     mfma_rows(f1, 0, 4);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 3);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 3);  // DS read
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);  // DS read
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm[2 * T::kDma]);  // only tile t+3 outstanding
     __syncthreads();
     f0 = f0n;
-    buf = buf1;
+    stage = stage1;
   }
+  __builtin_amdgcn_s_waitcnt(kWaitVm[0]);  // no DMA outlives the workgroup's LDS
 
   // ---- epilogue ---------------------------------------------------------------
   // acc[i][j] register 4g+e holds C[row][col] with
