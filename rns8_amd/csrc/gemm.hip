@@ -23,11 +23,17 @@
 //     fragment as src1, so each lane ends with 4 consecutive output columns
 //     of one row per register group -> one packed dword store per group.
 //   * Exactness: |a*b| <= 2^14, so <= 65536 products plus a carried residue
-//     fit int32. Accumulators are reduced to centered residues in registers
-//     every 65536 K and in the epilogue.
+//     fit int32. One launch covers at most 65536 K; the host issues longer K
+//     as consecutive launches whose epilogues add the residue already in C.
+//   * Epilogue: accumulators start at 2^31, so each holds the biased sum the
+//     reduction reads; reduction is a byte dot product plus a 24-bit
+//     reciprocal quotient (full-rate VALU only), and 4 residues are packed per
+//     dword store.
 //   * Split-K (tall-skinny K): each slice reduces (when K > 65536) and
 //     atomically adds its partial into an int32 workspace; a finalize kernel
 //     reduces to int8 and clears the workspace.
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace rns8x {
@@ -87,15 +93,46 @@ __device__ __forceinline__ int swizzle_b(int k, int chunk) {
   return chunk ^ (((2 * x) & 15) | (x >> 2));
 }
 
-// Exact centered residue of an int32 (see tables.hpp): u = acc + 2^31 read as
-// bytes, s = dot(bytes, 2^(8b) mod m) + (H - 2^31 mod m) < 2^18,
-// q = umulhi(s, ceil(2^32/m)) = floor(s/m), result = s - q*m - H.
-__device__ __forceinline__ int32_t reduce_centered(int32_t acc, uint32_t m, uint32_t half, uint32_t recip,
-                                                   uint32_t pow_lo, uint32_t off) {
-  const uint32_t u = static_cast<uint32_t>(acc) ^ 0x80000000u;
-  const uint32_t s = __builtin_amdgcn_udot4(u, pow_lo, off, false);
-  const uint32_t q = __umulhi(s, recip);
-  return static_cast<int32_t>(s - q * m) - static_cast<int32_t>(half);
+// Accumulator start value: the MFMAs then produce u = 2^31 + sum (mod 2^32),
+// the biased form the reduction reads (|sum| < 2^31).
+constexpr int kAccBias = static_cast<int>(0x80000000u);
+
+// hi32(lo24(x) * lo24(y)): v_mul_hi_u32_u24, full rate.
+__device__ __forceinline__ uint32_t mulhi_u24(uint32_t x, uint32_t y) {
+  return static_cast<uint32_t>((static_cast<uint64_t>(x & 0xFFFFFFu) * (y & 0xFFFFFFu)) >> 32);
+}
+
+// lo24(a) * lo24(b) + c (mod 2^32) as v_mad_u32_u24 (full rate), b uniform.
+// Written as asm: the compiler lowers the same expression in C to a
+// quarter-rate 32- or 64-bit multiply-add.
+__device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t d;
+  asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(b), "v"(c));
+  return d;
+}
+
+// For u = x + 2^31 (x an int32 sum), returns a value whose low byte is
+// (x + H) mod m, H = floor(m/2): s = dot(bytes(u), 2^(8b) mod m) + off_i32 is
+// congruent to x + H and at most s_max, q = floor(s / m) by the 24-bit
+// quotient of tables.hpp, and s + q*(256 - m) is congruent to s - q*m modulo
+// 256. m_comp = 256 - m.
+__device__ __forceinline__ uint32_t residue_plus_half(uint32_t u, const ModulusConsts& mc, uint32_t m_comp) {
+  const uint32_t s = __builtin_amdgcn_udot4(u, mc.pow_lo, mc.off_i32, false);
+  const uint32_t q = mulhi_u24(s << mc.q_shift, mc.q_recip);
+  return mad_u24(q, m_comp, s);
+}
+
+// Packs (r_e - H) mod 256 for e = 0..3 (low bytes of r_e, see
+// residue_plus_half) into one little-endian dword: the centered residues as
+// int8. half2 = H * 0x10001. v_perm_b32(s0, s1, sel) takes result byte k
+// from byte sel_k of s1 (0-3) or of s0 (4-7), or 0 for selector 0x0c.
+__device__ __forceinline__ uint32_t pack_centered(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3,
+                                                  uint32_t half2) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 h = __builtin_bit_cast(u16x2, half2);
+  const u16x2 p01 = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(r1, r0, 0x0c040c00u)) - h;
+  const u16x2 p23 = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(r3, r2, 0x0c040c00u)) - h;
+  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, p23), __builtin_bit_cast(uint32_t, p01), 0x06040200u);
 }
 
 // Raw buffer resource over [p, p + bytes). The inputs are wave-uniform; they
@@ -132,11 +169,6 @@ __device__ __forceinline__ void dma16(uint32_t lds_addr, uint32_t voffset, v4i r
                : "m0");
 }
 #pragma clang diagnostic pop
-
-__device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {
-  return (static_cast<uint32_t>(a) & 0xFFu) | ((static_cast<uint32_t>(b) & 0xFFu) << 8) |
-         ((static_cast<uint32_t>(c) & 0xFFu) << 16) | (static_cast<uint32_t>(d) << 24);
-}
 
 template <int BK>
 __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, PlaneConsts pc, uint32_t tiles_m,
@@ -268,7 +300,7 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v16i{};
+    for (int j = 0; j < 4; ++j) acc[i][j] = v16i{} + kAccBias;
 
   auto mfma_rows = [&](const Frags& f, int i0, int i1) {
 #pragma unroll
@@ -335,69 +367,115 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
   __builtin_amdgcn_s_waitcnt(kWaitVm[0]);  // no DMA outlives the workgroup's LDS
 
   // ---- epilogue ---------------------------------------------------------------
-  // acc[i][j] register 4g+e holds C[row][col] with
+  // acc[i][j] register 4g+e holds u = 2^31 + C[row][col] (mod 2^32; the
+  // accumulators start at 2^31) with
   //   row = m0 + wave_m*128 + 32i + (lane & 31)
-  //   col = n0 + wave_n*128 + 32j + 8g + 4*(lane >> 5) + e
+  //   col = n0 + wave_n*128 + 32j + 8g + 4*(lane >> 5) + e.
+  // Stores go through a buffer resource over this tile's rows, so rows >= M
+  // are dropped by the range check; columns past the padded pitch (only in
+  // the last tile column) get an offset beyond num_records.
   const ModulusConsts mc = pc.mod[plane];
+  const int64_t tile_rows = min(static_cast<int64_t>(kBM), args.m - m0);
+  const uint32_t lane_off =
+      static_cast<uint32_t>((wave_m * 128 + frag_row) * args.ldc + wave_n * 128 + 4 * frag_half);
+  const uint32_t row_step = static_cast<uint32_t>(32 * args.ldc);
+  const bool full_cols = n0 + kBN <= args.ldc;
+  const int col_room = static_cast<int>(args.ldc - n0) - (wave_n * 128 + 4 * frag_half);
+  auto col_off = [&](uint32_t off, int col) {  // col = 32j + 8g within the lane's wave tile
+    return (full_cols || col < col_room) ? off + static_cast<uint32_t>(col) : 0x80000000u;
+  };
   if (args.slices <= 1) {
-    int8_t* const C = args.c + static_cast<int64_t>(plane) * args.pitch_c;
+    int8_t* const C = args.c + static_cast<int64_t>(plane) * args.pitch_c + m0 * args.ldc + n0;
+    const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(C, tile_rows * args.ldc - n0);
+    const uint32_t m_comp = 256u - mc.m;
+    const uint32_t half2 = mc.half * 0x00010001u;
+    // The packed residues of each wave's 128 x 128 block go through LDS (free
+    // once every wave's last DMA has landed) so the global stores are
+    // row-contiguous 16-byte chunks: 8 full 128-byte lines per instruction.
+    // LDS block layout: row-major, 128-byte rows, 16-byte chunk c of row r at
+    // chunk position c ^ ((r >> 1) & 7) (2-way bank conflicts at most).
+    __syncthreads();
+    int8_t* const ep = lds + wave * (128 * 128);
+    auto reduce = [&](auto carry) {
+      constexpr bool kCarry = decltype(carry)::value;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = m0 + wave_m * 128 + 32 * i + frag_row;
-      const bool row_ok = row < args.m;
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t off = lane_off + static_cast<uint32_t>(i) * row_step;
+        uint32_t prev[4][4];
+        if constexpr (kCarry) {
+          // later K block: add the centered residue carried in C (|.| <= 128)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int64_t col = n0 + wave_n * 128 + 32 * j + 8 * g + 4 * frag_half;
-          const bool ok = row_ok && col < args.ldc;
-          uint32_t* const dst = reinterpret_cast<uint32_t*>(C + row * args.ldc + col);
-          int32_t v0 = acc[i][j][4 * g + 0], v1 = acc[i][j][4 * g + 1];
-          int32_t v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
-          if (accumulate && ok) {
-            // later K block: add the centered residue carried in C (|.| <= 128)
-            const uint32_t prev = *dst;
-            v0 += static_cast<int8_t>(prev);
-            v1 += static_cast<int8_t>(prev >> 8);
-            v2 += static_cast<int8_t>(prev >> 16);
-            v3 += static_cast<int8_t>(prev >> 24);
-          }
-          const int32_t r0 = reduce_centered(v0, mc.m, mc.half, mc.recip, mc.pow_lo, mc.off_i32);
-          const int32_t r1 = reduce_centered(v1, mc.m, mc.half, mc.recip, mc.pow_lo, mc.off_i32);
-          const int32_t r2 = reduce_centered(v2, mc.m, mc.half, mc.recip, mc.pow_lo, mc.off_i32);
-          const int32_t r3 = reduce_centered(v3, mc.m, mc.half, mc.recip, mc.pow_lo, mc.off_i32);
-          if (ok) *dst = pack4(r0, r1, r2, r3);
+            for (int g = 0; g < 4; ++g)
+              prev[j][g] = static_cast<uint32_t>(
+                  __builtin_amdgcn_raw_buffer_load_b32(c_rsrc, static_cast<int>(off + 32 * j + 8 * g), 0, 0));
         }
-        __builtin_amdgcn_sched_barrier(0);
+        const int r = 32 * i + frag_row;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            uint32_t res[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              uint32_t u = static_cast<uint32_t>(acc[i][j][4 * g + e]);
+              if constexpr (kCarry)
+                u += static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev[j][g] >> (8 * e))));
+              res[e] = residue_plus_half(u, mc, m_comp);
+            }
+            const int c = 2 * j + (g >> 1);
+            *reinterpret_cast<uint32_t*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + 8 * (g & 1) +
+                                         4 * frag_half) = pack_centered(res[0], res[1], res[2], res[3], half2);
+          }
+        }
       }
+    };
+    if (accumulate)
+      reduce(std::true_type{});
+    else
+      reduce(std::false_type{});
+    // Read back row-contiguous: lane l takes chunk l & 7 of rows 8q + (l >> 3).
+    const int rrow = lane >> 3;
+    const int rchunk = lane & 7;
+    const bool chunk_ok = full_cols || wave_n * 128 + 16 * rchunk < static_cast<int>(args.ldc - n0);
+    const uint32_t goff =
+        static_cast<uint32_t>((wave_m * 128 + rrow) * args.ldc + wave_n * 128 + 16 * rchunk);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int row = 8 * q + rrow;
+      const v4i v = *reinterpret_cast<const v4i*>(ep + row * 128 + ((rchunk ^ ((row >> 1) & 7)) << 4));
+      const uint32_t o = goff + static_cast<uint32_t>(8 * q) * static_cast<uint32_t>(args.ldc);
+      __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(chunk_ok ? o : 0x80000000u), 0, 0);
     }
   } else {
-    int32_t* const W = args.splitk_ws + static_cast<int64_t>(plane) * args.m * args.ldc;
+    // Split-K: add this slice's partial sums (u - 2^31) into the int32
+    // workspace [plane][M][ldc] with buffer atomics.
+    int32_t* const W = args.splitk_ws + (static_cast<int64_t>(plane) * args.m + m0) * args.ldc + n0;
+    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(W, 4 * (tile_rows * args.ldc - n0));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t row = m0 + wave_m * 128 + 32 * i + frag_row;
-      const bool row_ok = row < args.m;
+      const uint32_t off = lane_off + static_cast<uint32_t>(i) * row_step;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int64_t col = n0 + wave_n * 128 + 32 * j + 8 * g + 4 * frag_half;
-          if (row_ok && col < args.ldc) {
+          const uint32_t o = col_off(off, 32 * j + 8 * g);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) atomicAdd(W + row * args.ldc + col + e, acc[i][j][4 * g + e]);
-          }
+          for (int e = 0; e < 4; ++e)
+            __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(acc[i][j][4 * g + e] ^ kAccBias, w_rsrc,
+                                                       static_cast<int>(o == 0x80000000u ? o : 4 * (o + e)), 0, 0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-      }
     }
   }
 }
 
 // Reduce the summed split-K partials to int8 residues and clear the workspace.
+// One thread per 4 consecutive cells of a plane row (ldc is a multiple of 16).
 __global__ __launch_bounds__(256) void splitk_finalize_kernel(int32_t* ws, int8_t* c, int64_t m, int64_t ldc,
                                                               int64_t pitch_c, uint32_t nplanes, PlaneConsts pc,
                                                               uint32_t accumulate) {
-  const int64_t words_per_plane = m * ldc / 4;  // ldc is a multiple of 16
+  const int64_t words_per_plane = m * ldc / 4;
   const int64_t total = words_per_plane * nplanes;
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < total;
        w += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -405,24 +483,21 @@ __global__ __launch_bounds__(256) void splitk_finalize_kernel(int32_t* ws, int8_
     const int64_t in_plane = w - static_cast<int64_t>(plane) * words_per_plane;
     const ModulusConsts mc = pc.mod[plane];
     v4i* const src = reinterpret_cast<v4i*>(ws + static_cast<int64_t>(plane) * m * ldc) + in_plane;
-    v4i v = *src;
+    const v4i v = *src;
     *src = v4i{0, 0, 0, 0};
     const int64_t elem = in_plane * 4;
     const int64_t row = elem / ldc;
     const int64_t col = elem - row * ldc;
     uint32_t* const dst = reinterpret_cast<uint32_t*>(c + static_cast<int64_t>(plane) * pitch_c + row * ldc + col);
-    if (accumulate) {
-      const uint32_t prev = *dst;
-      v[0] += static_cast<int8_t>(prev);
-      v[1] += static_cast<int8_t>(prev >> 8);
-      v[2] += static_cast<int8_t>(prev >> 16);
-      v[3] += static_cast<int8_t>(prev >> 24);
+    const uint32_t prev = accumulate ? *dst : 0u;
+    uint32_t r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t u = (static_cast<uint32_t>(v[e]) ^ 0x80000000u) +
+                         static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev >> (8 * e))));
+      r[e] = residue_plus_half(u, mc, 256u - mc.m);
     }
-    const int32_t r0 = reduce_centered(v[0], mc.m, mc.half, mc.recip, mc.pow_lo, mc.off_i32);
-    const int32_t r1 = reduce_centered(v[1], mc.m, mc.half, mc.recip, mc.pow_lo, mc.off_i32);
-    const int32_t r2 = reduce_centered(v[2], mc.m, mc.half, mc.recip, mc.pow_lo, mc.off_i32);
-    const int32_t r3 = reduce_centered(v[3], mc.m, mc.half, mc.recip, mc.pow_lo, mc.off_i32);
-    *dst = pack4(r0, r1, r2, r3);
+    *dst = pack_centered(r[0], r[1], r[2], r[3], mc.half * 0x00010001u);
   }
 }
 
@@ -433,6 +508,7 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* dst, uint64_t
 }
 
 constexpr int kGemmBK = 64;
+constexpr int64_t kSplitMaxLd = int64_t{1} << 21;
 
 bool gemm_shape_ok(const GemmArgs& a) {
   if (a.m <= 0 || a.n <= 0 || a.k <= 0) return false;
@@ -446,6 +522,8 @@ bool gemm_shape_ok(const GemmArgs& a) {
   if (!a.a || !a.b || !a.c) return false;
   if (a.slices == 0) return false;
   if (a.slices > 1 && !a.splitk_ws) return false;
+  // split-K workspace offsets are byte offsets of int32 cells in a 256-row tile
+  if (a.slices > 1 && a.ldc >= kSplitMaxLd) return false;
   return true;
 }
 
@@ -456,7 +534,7 @@ uint32_t choose_splitk_slices(int64_t m, int64_t n, int64_t k, uint32_t nplanes)
   // 2048 K so each slice still runs a long MFMA main loop.
   const int64_t tiles = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN) * static_cast<int64_t>(nplanes);
   const int64_t target = 512;
-  if (tiles >= target / 2 || k < 4096) return 1;
+  if (tiles >= target / 2 || k < 4096 || padded_ld(n) >= kSplitMaxLd) return 1;
   int64_t slices = (target + tiles - 1) / tiles;
   const int64_t max_by_k = k / 2048;
   if (slices > max_by_k) slices = max_by_k;

@@ -39,8 +39,31 @@ struct ModulusConsts {
   uint32_t pow_hi;  // bytes [2^32, 2^40, 2^48, 2^56] mod m
   uint32_t off_i64; // H + (-2^63 mod m): int64 x read as u = x ^ 2^63
   uint32_t off_u64; // H
-  uint32_t off_i32; // H + (-2^31 mod m): int32 acc read as u = acc ^ 2^31
+  uint32_t off_i32; // H + (-2^31 mod m): int32 acc read as u = acc + 2^31
+  // Full-rate quotient for the int32 reduction: s = dot(bytes(u), pow_lo) +
+  // off_i32 never exceeds s_max = 255 * (sum of pow_lo bytes) + off_i32, and
+  // floor(s / m) = mulhi_u24(s << q_shift, q_recip) (make_quot24).
+  uint32_t q_shift;
+  uint32_t q_recip;
 };
+
+// Shift and reciprocal for floor(s / m) = hi32((s << a) * R) over 0 <= s <=
+// s_max < 2^24, with both factors below 2^24 so v_mul_hi_u32_u24 (full rate)
+// computes it. a is the largest shift with s_max * 2^a < 2^24 and
+// R = ceil(2^k / m), k = 32 - a. Writing e = R*m - 2^k (0 <= e < m) and
+// s = q*m + r: s*R / 2^k = q + (r + s*e / 2^k) / m, and s*e < s_max * m <=
+// 2^k because s_max * 2^a * m < 2^24 * 2^8. So the floor is q. R stays below
+// 2^24: maximality of a gives 2^k <= 2^9 * s_max, so R <= 2^9 * s_max / m + 1.
+struct Quot24 {
+  uint32_t shift;
+  uint32_t recip;
+};
+inline Quot24 make_quot24(uint32_t m, uint32_t s_max) {
+  uint32_t a = 0;
+  while ((uint64_t{s_max} << (a + 1)) < (uint64_t{1} << 24)) ++a;
+  const uint64_t k = uint64_t{1} << (32 - a);
+  return Quot24{a, static_cast<uint32_t>((k + m - 1) / m)};
+}
 
 inline ModulusConsts make_modulus_consts(uint32_t m) {
   ModulusConsts c{};
@@ -63,6 +86,11 @@ inline ModulusConsts make_modulus_consts(uint32_t m) {
   c.off_i64 = c.half + static_cast<uint32_t>((m - two63_mod) % m);
   c.off_u64 = c.half;
   c.off_i32 = c.half + static_cast<uint32_t>((m - two31_mod) % m);
+  uint32_t byte_sum = 0;
+  for (uint32_t b = 0; b < 4; ++b) byte_sum += (lo >> (8u * b)) & 0xFFu;
+  const Quot24 q = make_quot24(m, 255u * byte_sum + c.off_i32);
+  c.q_shift = q.shift;
+  c.q_recip = q.recip;
   return c;
 }
 
