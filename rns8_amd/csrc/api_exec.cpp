@@ -486,7 +486,7 @@ rns8_status export_host(rns8_context* ctx, const rns8_plan* plan, const rns8_mat
   if (launch_zero_words(mc->status, 1, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
   ExportArgs a{C->planes, m, n, C->plane_ld, C->plane_pitch, mc->staging, n, req.limbs, req.kind, plan->desc.bound,
                mc->status};
-  if (launch_export(a, make_garner_consts(plan->prefix), stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  if (launch_export(a, plan->prefix, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
   uint32_t status = 0;
   if (hipMemcpyAsync(&status, mc->status, sizeof(status), hipMemcpyDeviceToHost, stream) != hipSuccess ||
       hipStreamSynchronize(stream) != hipSuccess)
@@ -507,7 +507,7 @@ rns8_status export_device(rns8_context* ctx, const rns8_plan* plan, const rns8_m
   if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
   ExportArgs a{C->planes,  plan->desc.m, plan->desc.n,     C->plane_ld, C->plane_pitch, d_dst,
                ld,         req.limbs,    req.kind,         plan->desc.bound, d_status};
-  return launch_export(a, make_garner_consts(plan->prefix), pick_stream(*ctx, stream_arg)) == hipSuccess
+  return launch_export(a, plan->prefix, pick_stream(*ctx, stream_arg)) == hipSuccess
              ? RNS8_SUCCESS
              : RNS8_BACKEND_FAILURE;
 }

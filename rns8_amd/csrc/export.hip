@@ -6,10 +6,15 @@
 // (finite u8 canonical export).
 //
 // Per cell: P residue bytes -> mixed-radix digits with one exact reduction
-// per digit (tables.hpp, GarnerConsts) -> integer by Horner's rule in 24-bit
-// limbs -> sign/range decisions as limb comparisons against host-computed
-// constants -> native output. Each thread handles 4 consecutive cells of a
-// row so every plane contributes one dword load.
+// per digit -> integer by Horner's rule in 24-bit limbs -> sign/range
+// decisions as limb comparisons -> native output. The kernels are
+// instantiated per prefix P, so the Garner tables are compile-time constants
+// (evaluated from the modulus ladder) and every loop over digits and limbs is
+// fully unrolled with exactly the limbs each Horner step can occupy. Each
+// thread handles 4 consecutive cells of a row, so every plane contributes one
+// dword load; a 2-D grid (column groups x rows) needs no index division.
+#include <utility>
+
 #include "kernels.hpp"
 
 namespace rns8x {
@@ -21,8 +26,86 @@ struct ExportLimits {
   uint32_t check;                // 0: every representable value is admissible
 };
 
-// a <= b where a has L 24-bit limbs and b has kWideLimbs (b's upper limbs may
-// be nonzero, in which case b exceeds every L-limb value).
+// ---- compile-time tables --------------------------------------------------------
+//
+// Digit i of the mixed-radix form is v_i = s mod m_i with
+//   s = r_i * I_i + bias_i + sum_{j<i} v_j * W[j][i]       (GarnerConsts)
+// and 0 <= s <= s_max_i (r_i >= -128, v_j <= 255), so the quotient comes from
+// the full-rate 24-bit reciprocal of make_quot24 and v_i is the low byte of
+// s + q*(256 - m_i) (congruent to s - q*m_i modulo 256, and s - q*m_i < 256).
+template <uint32_t P>
+struct GarnerTable {
+  static constexpr uint32_t kWords = (P + 3) / 4;
+  uint32_t m[P];
+  int32_t inv[P];
+  int32_t bias[P];
+  uint32_t wpack[P][kWords == 0 ? 1 : kWords];
+  uint32_t qshift[P];
+  uint32_t qrecip[P];
+  uint32_t active[P];  // 24-bit limbs of prod_{k >= i} m_k (Horner step i)
+  uint32_t product[kWideLimbs];
+  uint32_t half_ceil[kWideLimbs];
+  uint32_t limbs;      // limbs of P itself
+};
+
+template <uint32_t P>
+constexpr GarnerTable<P> make_garner_table() {
+  const GarnerConsts g = make_garner_consts(P);
+  GarnerTable<P> t{};
+  for (uint32_t i = 0; i < P; ++i) {
+    t.m[i] = g.m[i];
+    t.inv[i] = static_cast<int32_t>(g.inv[i]);
+    t.bias[i] = static_cast<int32_t>(g.bias[i]);
+    uint32_t s_max = 127u * g.inv[i] + g.bias[i];
+    for (uint32_t q = 0; q < GarnerTable<P>::kWords; ++q) {
+      t.wpack[i][q] = g.wpack[i][q];
+      for (uint32_t b = 0; b < 4; ++b) s_max += 255u * ((g.wpack[i][q] >> (8 * b)) & 0xFFu);
+    }
+    const Quot24 qq = make_quot24(g.m[i], s_max);
+    t.qshift[i] = qq.shift;
+    t.qrecip[i] = qq.recip;
+    Limbs24 tail;
+    tail.w[0] = 1;
+    for (uint32_t k = i; k < P; ++k) tail.mul_add(g.m[k], 0);
+    uint32_t n = 1;
+    for (uint32_t l = 0; l < kWideLimbs; ++l)
+      if (tail.w[l] != 0) n = l + 1;
+    t.active[i] = n;
+  }
+  t.limbs = 1;
+  for (uint32_t l = 0; l < kWideLimbs; ++l) {
+    t.product[l] = g.product[l];
+    t.half_ceil[l] = g.half_ceil[l];
+    if (g.product[l] != 0) t.limbs = l + 1;
+  }
+  return t;
+}
+
+// ---- arithmetic helpers ---------------------------------------------------------
+
+__device__ __forceinline__ uint32_t mulhi_u24(uint32_t x, uint32_t y) {
+  return static_cast<uint32_t>((static_cast<uint64_t>(x & 0xFFFFFFu) * (y & 0xFFFFFFu)) >> 32);
+}
+
+// lo24(a) * lo24(b) + c (mod 2^32) as v_mad_u32_u24 (full rate); b uniform.
+// Written as asm because the compiler lowers the same C expression to a
+// quarter-rate 32- or 64-bit multiply-add.
+__device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t d;
+  asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(b), "v"(c));
+  return d;
+}
+
+// Byte 0 of `byte_src` inserted at byte k of `word` (v_perm_b32: selector
+// 0-3 picks bytes of the second operand, 4-7 of the first).
+template <int K>
+__device__ __forceinline__ uint32_t insert_byte(uint32_t word, uint32_t byte_src) {
+  constexpr uint32_t sel = (K == 0 ? 0x03020104u : K == 1 ? 0x03020400u : K == 2 ? 0x03040100u : 0x04020100u);
+  return __builtin_amdgcn_perm(byte_src, word, sel);
+}
+
+// a <= b for L-limb a against a kWideLimbs-limb b (b's upper limbs nonzero
+// means b exceeds every L-limb value).
 template <int L>
 __device__ __forceinline__ bool limbs_le(const uint32_t (&a)[L], const uint32_t* b) {
   uint32_t upper = 0;
@@ -31,128 +114,155 @@ __device__ __forceinline__ bool limbs_le(const uint32_t (&a)[L], const uint32_t*
   if (upper != 0) return true;
   uint32_t borrow = 0;
 #pragma unroll
-  for (int l = 0; l < L; ++l) {
-    const uint32_t d = b[l] - a[l] - borrow;
-    borrow = d >> 31;
-  }
+  for (int l = 0; l < L; ++l) borrow = (b[l] - a[l] - borrow) >> 31;
   return borrow == 0;
 }
 
-template <int L, ExportKind Kind>
-__global__ __launch_bounds__(256) void export_kernel(ExportArgs a, GarnerConsts g, ExportLimits lim,
-                                                     int64_t groups_per_row, int64_t total_groups) {
-  const uint32_t P = g.prefix;
-  for (int64_t gi = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; gi < total_groups;
-       gi += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t row = gi / groups_per_row;
-    const int64_t c0 = (gi - row * groups_per_row) * 4;
+// One cell: centered residue bytes r_i (byte E of words[i]) -> sign and
+// magnitude d (L 24-bit limbs) of the reconstructed value.
+template <uint32_t P, int L, int E, bool Signed>
+__device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], uint32_t (&d)[L], bool& negative) {
+  constexpr GarnerTable<P> T = make_garner_table<P>();
+  static_assert(T.m[0] == 256, "digit 0 is the raw residue byte only for modulus 256");
+  constexpr uint32_t W = GarnerTable<P>::kWords;
+  // ---- mixed-radix digits, packed 4 per dword ----
+  uint32_t vp[W];
+#pragma unroll
+  for (uint32_t q = 0; q < W; ++q) vp[q] = 0u;
+  // m_0 = 256: v_0 = r_0 mod 256 is the residue byte itself
+  vp[0] = (words[0] >> (8 * E)) & 0xFFu;
+#pragma unroll
+  for (uint32_t i = 1; i < P; ++i) {
+    const int32_t r = static_cast<int32_t>(static_cast<int8_t>(words[i] >> (8 * E)));
+    uint32_t s = static_cast<uint32_t>(r * T.inv[i] + T.bias[i]);
+#pragma unroll
+    for (uint32_t q = 0; q < (i + 3) / 4; ++q) s = __builtin_amdgcn_udot4(vp[q], T.wpack[i][q], s, false);
+    const uint32_t qt = mulhi_u24(s << T.qshift[i], T.qrecip[i]);
+    const uint32_t t = mad_u24(qt, 256u - T.m[i], s);
+    switch (i % 4) {
+      case 0: vp[i / 4] = insert_byte<0>(vp[i / 4], t); break;
+      case 1: vp[i / 4] = insert_byte<1>(vp[i / 4], t); break;
+      case 2: vp[i / 4] = insert_byte<2>(vp[i / 4], t); break;
+      default: vp[i / 4] = insert_byte<3>(vp[i / 4], t); break;
+    }
+  }
+  // ---- Horner: x = (..(v_{P-1} m_{P-2} + v_{P-2}) ..) m_0 + v_0 ----
+  uint32_t x[L];
+#pragma unroll
+  for (int l = 0; l < L; ++l) x[l] = 0u;
+  x[0] = (vp[(P - 1) / 4] >> (8 * ((P - 1) % 4))) & 0xFFu;
+#pragma unroll
+  for (int i = static_cast<int>(P) - 2; i >= 0; --i) {
+    uint32_t carry = (vp[i / 4] >> (8 * (i % 4))) & 0xFFu;
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+      if (static_cast<uint32_t>(l) < T.active[i]) {
+        const uint32_t t = mad_u24(x[l], T.m[i], carry);
+        x[l] = t & 0xFFFFFFu;
+        carry = t >> 24;
+      }
+    }
+  }
+  // ---- sign and magnitude ----
+  if constexpr (Signed) {
+    uint32_t borrow = 0;
+#pragma unroll
+    for (int l = 0; l < L; ++l) borrow = (x[l] - T.half_ceil[l] - borrow) >> 31;
+    negative = borrow == 0;  // x >= ceil(P/2): the value is x - P
+    borrow = 0;
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+      const uint32_t t = T.product[l] - x[l] - borrow;
+      borrow = t >> 31;
+      d[l] = negative ? (t & 0xFFFFFFu) : x[l];
+    }
+  } else {
+    negative = false;
+#pragma unroll
+    for (int l = 0; l < L; ++l) d[l] = x[l];
+  }
+}
+
+template <uint32_t P, int L, ExportKind Kind>
+__global__ __launch_bounds__(256) void export_kernel(ExportArgs a, ExportLimits lim, uint32_t groups_per_row,
+                                                     uint32_t vec_store) {
+  constexpr bool kSigned = Kind == ExportKind::I64 || Kind == ExportKind::WIDE_SIGNED;
+  const uint32_t gc = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gc >= groups_per_row) return;
+  const int64_t c0 = static_cast<int64_t>(gc) * 4;
+  bool violation = false;
+  for (int64_t row = blockIdx.y; row < a.m; row += gridDim.y) {
     const int8_t* const cell = a.c + row * a.ldc + c0;
-    uint32_t words[kMaxPrefix];
+    uint32_t words[P];
 #pragma unroll
-    for (uint32_t i = 0; i < kMaxPrefix; ++i)
-      words[i] = i < P ? *reinterpret_cast<const uint32_t*>(cell + static_cast<int64_t>(i) * a.pitch_c) : 0u;
-    bool violation = false;
+    for (uint32_t i = 0; i < P; ++i)
+      words[i] = *reinterpret_cast<const uint32_t*>(cell + static_cast<int64_t>(i) * a.pitch_c);
+    uint32_t d[4][L];
+    bool neg[4];
+    reconstruct<P, L, 0, kSigned>(words, d[0], neg[0]);
+    reconstruct<P, L, 1, kSigned>(words, d[1], neg[1]);
+    reconstruct<P, L, 2, kSigned>(words, d[2], neg[2]);
+    reconstruct<P, L, 3, kSigned>(words, d[3], neg[3]);
+    const int64_t cells = a.n - c0 < 4 ? a.n - c0 : 4;
+    if (lim.check) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t col = c0 + e;
-      // ---- mixed-radix digits ----
-      uint32_t vp[kGarnerDigitWords] = {0u, 0u, 0u, 0u, 0u};
+      for (int e = 0; e < 4; ++e)
+        if (e < cells && !limbs_le<L>(d[e], neg[e] ? lim.lim_neg : lim.lim_pos)) violation = true;
+    }
+    if constexpr (Kind == ExportKind::I64 || Kind == ExportKind::U64) {
+      uint64_t w[4];
 #pragma unroll
-      for (uint32_t i = 0; i < kMaxPrefix; ++i) {
-        if (i < P) {
-          const int32_t r = static_cast<int32_t>(static_cast<int8_t>(words[i] >> (8 * e)));
-          uint32_t s = static_cast<uint32_t>(r * static_cast<int32_t>(g.inv[i]) + static_cast<int32_t>(g.bias[i]));
-#pragma unroll
-          for (uint32_t q = 0; q < (i + 3) / 4; ++q) s = __builtin_amdgcn_udot4(vp[q], g.wpack[i][q], s, false);
-          const uint32_t v = s - __umulhi(s, g.recip[i]) * g.m[i];
-          vp[i / 4] |= v << (8 * (i % 4));
-        }
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t mag = static_cast<uint64_t>(d[e][0]) | (static_cast<uint64_t>(d[e][1]) << 24) |
+                             (static_cast<uint64_t>(d[e][2]) << 48);
+        w[e] = neg[e] ? (0ull - mag) : mag;
       }
-      // ---- Horner: x = (..(v_{P-1} m_{P-2} + v_{P-2}) ..) m_0 + v_0 ----
-      uint32_t x[L];
-#pragma unroll
-      for (int l = 0; l < L; ++l) x[l] = 0u;
-#pragma unroll
-      for (int i = static_cast<int>(kMaxPrefix) - 1; i >= 0; --i) {
-        if (static_cast<uint32_t>(i) < P) {
-          const uint32_t v = (vp[i / 4] >> (8 * (i % 4))) & 0xFFu;
-          const uint32_t mul = static_cast<uint32_t>(i) + 1u < P ? g.m[i] : 0u;  // top digit starts x
-          uint32_t carry = v;
-#pragma unroll
-          for (int l = 0; l < L; ++l) {
-            const uint32_t t = __umul24(x[l], mul) + carry;
-            x[l] = t & 0xFFFFFFu;
-            carry = t >> 24;
-          }
-        }
-      }
-      // ---- sign and magnitude ----
-      bool negative = false;
-      uint32_t d[L];
-      if (Kind == ExportKind::I64 || Kind == ExportKind::WIDE_SIGNED) {
-        uint32_t borrow = 0;
-#pragma unroll
-        for (int l = 0; l < L; ++l) {
-          const uint32_t t = x[l] - g.half_ceil[l] - borrow;
-          borrow = t >> 31;
-        }
-        negative = borrow == 0;  // x >= ceil(P/2)
-        borrow = 0;
-#pragma unroll
-        for (int l = 0; l < L; ++l) {
-          const uint32_t t = g.product[l] - x[l] - borrow;  // P - x when negative
-          borrow = t >> 31;
-          d[l] = negative ? (t & 0xFFFFFFu) : x[l];
-        }
+      uint64_t* const out = static_cast<uint64_t*>(a.dst) + row * a.ld + c0;
+      if (vec_store && cells == 4) {
+        typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+        reinterpret_cast<u64x2*>(out)[0] = u64x2{w[0], w[1]};
+        reinterpret_cast<u64x2*>(out)[1] = u64x2{w[2], w[3]};
       } else {
 #pragma unroll
-        for (int l = 0; l < L; ++l) d[l] = x[l];
+        for (int e = 0; e < 4; ++e)
+          if (e < cells) out[e] = w[e];
       }
-      const bool in_row = col < a.n;
-      if (lim.check && in_row) {
-        if (!limbs_le<L>(d, negative ? lim.lim_neg : lim.lim_pos)) violation = true;
-      }
-      if (!in_row) continue;
-      // ---- 64-bit words of the magnitude ----
-      uint64_t w0 = static_cast<uint64_t>(d[0]) | (static_cast<uint64_t>(d[1]) << 24) |
-                    (static_cast<uint64_t>(d[2]) << 48);
-      if (Kind == ExportKind::I64) {
-        static_cast<int64_t*>(a.dst)[row * a.ld + col] = static_cast<int64_t>(negative ? (0ull - w0) : w0);
-      } else if (Kind == ExportKind::U64) {
-        static_cast<uint64_t*>(a.dst)[row * a.ld + col] = w0;
-      } else {
-        // bits 64..167 of the magnitude (24-bit limb l covers bits 24l..24l+23)
-        uint64_t w[3] = {w0, static_cast<uint64_t>(d[2]) >> 16, 0ull};
-        if (L > 3) {
-          w[1] |= (static_cast<uint64_t>(d[3]) << 8) | (static_cast<uint64_t>(d[4]) << 32) |
-                  (static_cast<uint64_t>(d[5]) << 56);
-          w[2] = (static_cast<uint64_t>(d[5]) >> 8) | (static_cast<uint64_t>(d[L > 6 ? 6 : 0]) << 16);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (e >= cells) continue;
+        // 64-bit words of the magnitude (24-bit limb l covers bits 24l..24l+23)
+        uint64_t w3[3] = {static_cast<uint64_t>(d[e][0]) | (static_cast<uint64_t>(d[e][1]) << 24) |
+                              (static_cast<uint64_t>(d[e][2]) << 48),
+                          static_cast<uint64_t>(d[e][2]) >> 16, 0ull};
+        if constexpr (L > 3) {
+          w3[1] |= (static_cast<uint64_t>(d[e][3]) << 8) | (static_cast<uint64_t>(d[e][4]) << 32) |
+                   (static_cast<uint64_t>(d[e][5]) << 56);
+          w3[2] = (static_cast<uint64_t>(d[e][5]) >> 8) | (static_cast<uint64_t>(d[e][6]) << 16);
         }
-        uint64_t* const out = static_cast<uint64_t*>(a.dst) + (row * a.ld + col) * a.limbs;
-        if (Kind == ExportKind::WIDE_SIGNED && negative) {
-          // two's complement of the magnitude over limbs*64 bits
+        uint64_t* const out = static_cast<uint64_t*>(a.dst) + (row * a.ld + c0 + e) * a.limbs;
+        if (Kind == ExportKind::WIDE_SIGNED && neg[e]) {
+          // two's complement of the magnitude over limbs * 64 bits
           uint64_t carry = 1;
           for (uint32_t l = 0; l < a.limbs; ++l) {
-            const uint64_t word = l < 3 ? w[l] : 0ull;
-            const uint64_t inv = ~word;
-            const uint64_t s = inv + carry;
+            const uint64_t s = ~(l < 3 ? w3[l] : 0ull) + carry;
             carry = (carry && s == 0) ? 1ull : 0ull;
             out[l] = s;
           }
         } else {
-          for (uint32_t l = 0; l < a.limbs; ++l) out[l] = l < 3 ? w[l] : 0ull;
+          for (uint32_t l = 0; l < a.limbs; ++l) out[l] = l < 3 ? w3[l] : 0ull;
         }
       }
     }
-    if (violation) atomicOr(a.status, 1u);
   }
+  if (violation) atomicOr(a.status, 1u);
 }
 
-__global__ __launch_bounds__(256) void export_u8_kernel(ExportU8Args a, int64_t groups_per_row, int64_t total) {
-  for (int64_t gi = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; gi < total;
-       gi += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t row = gi / groups_per_row;
-    const int64_t c0 = (gi - row * groups_per_row) * 4;
+__global__ __launch_bounds__(256) void export_u8_kernel(ExportU8Args a, uint32_t groups_per_row) {
+  const uint32_t gc = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gc >= groups_per_row) return;
+  const int64_t c0 = static_cast<int64_t>(gc) * 4;
+  for (int64_t row = blockIdx.y; row < a.m; row += gridDim.y) {
     const uint32_t word = *reinterpret_cast<const uint32_t*>(a.c + row * a.ldc + c0);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -164,9 +274,12 @@ __global__ __launch_bounds__(256) void export_u8_kernel(ExportU8Args a, int64_t 
   }
 }
 
-unsigned grid_for(int64_t items) {
-  const int64_t blocks = (items + 255) / 256;
-  return static_cast<unsigned>(blocks < 16384 ? (blocks > 0 ? blocks : 1) : 16384);
+// Column groups of 4 cells x rows; rows beyond the grid's y extent are
+// covered by the row loop.
+dim3 grid_2d(uint32_t groups_per_row, int64_t rows) {
+  const uint32_t gx = (groups_per_row + 255u) / 256u;
+  const int64_t gy = rows < 65535 ? rows : 65535;
+  return dim3(gx, static_cast<uint32_t>(gy > 0 ? gy : 1));
 }
 
 void set_limit_u64(uint32_t (&out)[kWideLimbs], uint64_t v) { u64_to_limbs24(v, out); }
@@ -181,39 +294,50 @@ void set_limit_pow2_minus1(uint32_t (&out)[kWideLimbs], uint32_t bits) {
   }
 }
 
-template <int L>
-hipError_t launch_export_l(const ExportArgs& a, const GarnerConsts& g, const ExportLimits& lim, hipStream_t stream) {
-  const int64_t groups_per_row = a.ldc / 4;
-  const int64_t total = groups_per_row * a.m;
-  const dim3 grid(grid_for(total));
+template <uint32_t P>
+hipError_t launch_export_p(const ExportArgs& a, const ExportLimits& lim, hipStream_t stream) {
+  constexpr int L = P <= 9 ? 3 : 7;  // 24-bit limbs holding P: 9 moduli < 2^72, 20 < 2^168
+  static_assert(make_garner_table<P>().limbs <= static_cast<uint32_t>(L), "limb count too small for P");
+  const uint32_t groups_per_row = static_cast<uint32_t>(a.ldc / 4);
+  const dim3 grid = grid_2d(groups_per_row, a.m);
+  const uint32_t vec = (reinterpret_cast<uintptr_t>(a.dst) % 16 == 0 && a.ld % 2 == 0) ? 1u : 0u;
   switch (a.kind) {
     case ExportKind::I64:
-      hipLaunchKernelGGL((export_kernel<L, ExportKind::I64>), grid, dim3(256), 0, stream, a, g, lim, groups_per_row,
-                         total);
+      hipLaunchKernelGGL((export_kernel<P, L, ExportKind::I64>), grid, dim3(256), 0, stream, a, lim, groups_per_row,
+                         vec);
       break;
     case ExportKind::U64:
-      hipLaunchKernelGGL((export_kernel<L, ExportKind::U64>), grid, dim3(256), 0, stream, a, g, lim, groups_per_row,
-                         total);
+      hipLaunchKernelGGL((export_kernel<P, L, ExportKind::U64>), grid, dim3(256), 0, stream, a, lim, groups_per_row,
+                         vec);
       break;
     case ExportKind::WIDE_SIGNED:
-      hipLaunchKernelGGL((export_kernel<L, ExportKind::WIDE_SIGNED>), grid, dim3(256), 0, stream, a, g, lim,
-                         groups_per_row, total);
+      hipLaunchKernelGGL((export_kernel<P, L, ExportKind::WIDE_SIGNED>), grid, dim3(256), 0, stream, a, lim,
+                         groups_per_row, vec);
       break;
     case ExportKind::WIDE_UNSIGNED:
-      hipLaunchKernelGGL((export_kernel<L, ExportKind::WIDE_UNSIGNED>), grid, dim3(256), 0, stream, a, g, lim,
-                         groups_per_row, total);
+      hipLaunchKernelGGL((export_kernel<P, L, ExportKind::WIDE_UNSIGNED>), grid, dim3(256), 0, stream, a, lim,
+                         groups_per_row, vec);
       break;
   }
   return hipGetLastError();
 }
 
+template <uint32_t... Ps>
+hipError_t dispatch_prefix(uint32_t prefix, const ExportArgs& a, const ExportLimits& lim, hipStream_t stream,
+                           std::integer_sequence<uint32_t, Ps...>) {
+  hipError_t err = hipErrorInvalidValue;
+  ((prefix == Ps + 1 ? (err = launch_export_p<Ps + 1>(a, lim, stream), 0) : 0), ...);
+  return err;
+}
+
 }  // namespace
 
-hipError_t launch_export(const ExportArgs& a, const GarnerConsts& g, hipStream_t stream) {
+hipError_t launch_export(const ExportArgs& a, uint32_t prefix, hipStream_t stream) {
   if (!a.c || !a.dst || !a.status || a.m <= 0 || a.n <= 0 || a.ld < a.n) return hipErrorInvalidValue;
-  if (g.prefix == 0 || g.prefix > kMaxPrefix) return hipErrorInvalidValue;
+  if (prefix == 0 || prefix > kMaxPrefix) return hipErrorInvalidValue;
   if (a.ldc != padded_ld(a.n) || a.pitch_c < a.m * a.ldc || (a.pitch_c % 4) != 0) return hipErrorInvalidValue;
   if ((reinterpret_cast<uintptr_t>(a.c) & 3u) != 0) return hipErrorInvalidValue;
+  if (a.ldc / 4 > 0xFFFFFFFFll) return hipErrorInvalidValue;
   if (a.limbs == 0 || a.limbs > 32) return hipErrorInvalidValue;
   if ((a.kind == ExportKind::I64 || a.kind == ExportKind::U64) && a.limbs != 1) return hipErrorInvalidValue;
   ExportLimits lim{};
@@ -255,17 +379,15 @@ hipError_t launch_export(const ExportArgs& a, const GarnerConsts& g, hipStream_t
       }
       break;
   }
-  if (g.prefix <= 9) return launch_export_l<3>(a, g, lim, stream);
-  return launch_export_l<7>(a, g, lim, stream);
+  return dispatch_prefix(prefix, a, lim, stream, std::make_integer_sequence<uint32_t, kMaxPrefix>{});
 }
 
 hipError_t launch_export_u8(const ExportU8Args& a, hipStream_t stream) {
   if (!a.c || !a.dst || a.m <= 0 || a.n <= 0 || a.ld < a.n) return hipErrorInvalidValue;
   if (a.ldc != padded_ld(a.n) || (reinterpret_cast<uintptr_t>(a.c) & 3u) != 0) return hipErrorInvalidValue;
   if (a.modulus < 2 || a.modulus > 256) return hipErrorInvalidValue;
-  const int64_t groups_per_row = a.ldc / 4;
-  const int64_t total = groups_per_row * a.m;
-  hipLaunchKernelGGL(export_u8_kernel, dim3(grid_for(total)), dim3(256), 0, stream, a, groups_per_row, total);
+  const uint32_t groups_per_row = static_cast<uint32_t>(a.ldc / 4);
+  hipLaunchKernelGGL(export_u8_kernel, grid_2d(groups_per_row, a.m), dim3(256), 0, stream, a, groups_per_row);
   return hipGetLastError();
 }
 

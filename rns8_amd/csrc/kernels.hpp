@@ -81,7 +81,7 @@ struct ExportArgs {
   uint64_t bound;   // bounded kinds
   uint32_t* status; // device word; set nonzero on any range violation
 };
-hipError_t launch_export(const ExportArgs& args, const GarnerConsts& g, hipStream_t stream);
+hipError_t launch_export(const ExportArgs& args, uint32_t prefix, hipStream_t stream);
 
 struct ExportU8Args {
   const int8_t* c;

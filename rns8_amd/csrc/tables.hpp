@@ -58,7 +58,7 @@ struct Quot24 {
   uint32_t shift;
   uint32_t recip;
 };
-inline Quot24 make_quot24(uint32_t m, uint32_t s_max) {
+constexpr Quot24 make_quot24(uint32_t m, uint32_t s_max) {
   uint32_t a = 0;
   while ((uint64_t{s_max} << (a + 1)) < (uint64_t{1} << 24)) ++a;
   const uint64_t k = uint64_t{1} << (32 - a);
@@ -144,7 +144,7 @@ struct GarnerConsts {
 // Simple multiprecision helper on 24-bit limbs used only to build the tables.
 struct Limbs24 {
   uint32_t w[kWideLimbs] = {};
-  void mul_add(uint32_t mul, uint32_t add) {
+  constexpr void mul_add(uint32_t mul, uint32_t add) {
     uint64_t carry = add;
     for (uint32_t i = 0; i < kWideLimbs; ++i) {
       const uint64_t t = static_cast<uint64_t>(w[i]) * mul + carry;
@@ -152,14 +152,14 @@ struct Limbs24 {
       carry = t >> 24;
     }
   }
-  uint32_t mod_small(uint32_t m) const {
+  constexpr uint32_t mod_small(uint32_t m) const {
     uint64_t r = 0;
     for (int i = static_cast<int>(kWideLimbs) - 1; i >= 0; --i) r = ((r << 24) | w[i]) % m;
     return static_cast<uint32_t>(r);
   }
 };
 
-inline uint32_t inverse_mod(uint32_t a, uint32_t m) {
+constexpr uint32_t inverse_mod(uint32_t a, uint32_t m) {
   // extended Euclid; a and m coprime
   int64_t t = 0, nt = 1, r = m, nr = a % m;
   while (nr != 0) {
@@ -176,7 +176,7 @@ inline uint32_t inverse_mod(uint32_t a, uint32_t m) {
   return static_cast<uint32_t>(t);
 }
 
-inline GarnerConsts make_garner_consts(uint32_t prefix) {
+constexpr GarnerConsts make_garner_consts(uint32_t prefix) {
   GarnerConsts g{};
   g.prefix = prefix;
   Limbs24 pj[kMaxPrefix + 1];
