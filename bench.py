@@ -53,11 +53,15 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--oneshot", action="store_true",
+                    help="time the host-buffer oneshot entry point instead (PCIe transfers included)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a device copy of BYTES (counter calibration) and exit")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration, max(args.steps, 1))
+    if args.oneshot:
+        return oneshot_rate(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
               "(the path shards by output row blocks; see DESIGN.md)", file=sys.stderr)
@@ -283,6 +287,40 @@ def copy_calibration(nbytes: int, reps: int) -> int:
     dt = (time.perf_counter() - t0) / reps
     print(json.dumps({"copy_bytes": nbytes, "reps": reps, "ms_per_copy": round(dt * 1e3, 4),
                       "GBps_read_plus_write": round(2 * nbytes / dt / 1e9, 1)}))
+    return 0
+
+
+def oneshot_rate(args) -> int:
+    """rns8_gemm_i64_oneshot / rns8_gemm_u64_oneshot on host arrays: H2D of A
+    and B, pack, GEMM, export and D2H of C per call (the reference's oneshot
+    contract, api_oneshot.cpp:510-586). Prints one JSON line; this rate is
+    reported beside the HBM-resident figure, never as `value`."""
+    import rns8_amd as r
+    from rns8_amd import inputs
+
+    sem, M, N, K, bits, bound, budget, forced = CONFIGS[args.config]
+    signed = sem == "i64"
+    gen = inputs.int_range if signed else inputs.uint_range
+    A = gen(inputs.operand_seed(args.seed, "A"), (M, K), bits)
+    B = gen(inputs.operand_seed(args.seed, "B"), (K, N), bits)
+    desc = r.gemm_desc(r.BOUNDED_I64 if signed else r.BOUNDED_U64,
+                       r.BOUND_GLOBAL_MAX_ABS if signed else r.BOUND_GLOBAL_MAX_UNSIGNED, M, N, K, bound=bound,
+                       max_prefix=budget, flags=r.PLAN_FORCE_FIXED_PREFIX if forced else 0)
+    fn = r.gemm_i64_oneshot if signed else r.gemm_u64_oneshot
+    C = np.zeros((M, N), dtype=np.int64 if signed else np.uint64)
+    with r.Context() as ctx:
+        for _ in range(max(args.warmup, 1)):
+            st, _ = fn(ctx, desc, A, B, C)
+            r.check(st, "oneshot")
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            st, _ = fn(ctx, desc, A, B, C)
+        dt = (time.perf_counter() - t0) / args.steps
+        r.check(st, "oneshot")
+    print(json.dumps({"mode": "oneshot (host buffers, PCIe included)", "config": args.config, "m": M, "n": N,
+                      "k": K, "ms_per_call": round(dt * 1e3, 3),
+                      "effective_TOPS": round(2.0 * M * N * K / dt / 1e12, 3),
+                      "host_bytes_moved": int(A.nbytes + B.nbytes + C.nbytes)}))
     return 0
 
 
