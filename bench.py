@@ -163,7 +163,7 @@ def main() -> int:
     achieved = gemm_ops / (stage[2] * 1e-3) / 1e12
 
     result = {
-        "metric": "exact int64 GEMM effective TOPS (2MNK/s) at 4096^3 prefix 9; % int8 MFMA peak",
+        "metric": "exact int64 GEMM effective TOPS (2MNK/s) at 4096\u00b3 prefix 9; % int8 MFMA peak",
         "value": round(value, 3),
         "unit": "TOPS",
         "n_gpus": 1,
