@@ -15,6 +15,7 @@
 // dword load; a 2-D grid (column groups x rows) needs no index division.
 #include <utility>
 
+#include "int_ops.hpp"
 #include "kernels.hpp"
 
 namespace rns8x {
@@ -26,75 +27,7 @@ struct ExportLimits {
   uint32_t check;                // 0: every representable value is admissible
 };
 
-// ---- compile-time tables --------------------------------------------------------
-//
-// Digit i of the mixed-radix form is v_i = s mod m_i with
-//   s = r_i * I_i + bias_i + sum_{j<i} v_j * W[j][i]       (GarnerConsts)
-// and 0 <= s <= s_max_i (r_i >= -128, v_j <= 255), so the quotient comes from
-// the full-rate 24-bit reciprocal of make_quot24 and v_i is the low byte of
-// s + q*(256 - m_i) (congruent to s - q*m_i modulo 256, and s - q*m_i < 256).
-template <uint32_t P>
-struct GarnerTable {
-  static constexpr uint32_t kWords = (P + 3) / 4;
-  uint32_t m[P];
-  int32_t inv[P];
-  int32_t bias[P];
-  uint32_t wpack[P][kWords == 0 ? 1 : kWords];
-  uint32_t qshift[P];
-  uint32_t qrecip[P];
-  uint32_t active[P];  // 24-bit limbs of prod_{k >= i} m_k (Horner step i)
-  uint32_t product[kWideLimbs];
-  uint32_t half_ceil[kWideLimbs];
-  uint32_t limbs;      // limbs of P itself
-};
-
-template <uint32_t P>
-constexpr GarnerTable<P> make_garner_table() {
-  const GarnerConsts g = make_garner_consts(P);
-  GarnerTable<P> t{};
-  for (uint32_t i = 0; i < P; ++i) {
-    t.m[i] = g.m[i];
-    t.inv[i] = static_cast<int32_t>(g.inv[i]);
-    t.bias[i] = static_cast<int32_t>(g.bias[i]);
-    uint32_t s_max = 127u * g.inv[i] + g.bias[i];
-    for (uint32_t q = 0; q < GarnerTable<P>::kWords; ++q) {
-      t.wpack[i][q] = g.wpack[i][q];
-      for (uint32_t b = 0; b < 4; ++b) s_max += 255u * ((g.wpack[i][q] >> (8 * b)) & 0xFFu);
-    }
-    const Quot24 qq = make_quot24(g.m[i], s_max);
-    t.qshift[i] = qq.shift;
-    t.qrecip[i] = qq.recip;
-    Limbs24 tail;
-    tail.w[0] = 1;
-    for (uint32_t k = i; k < P; ++k) tail.mul_add(g.m[k], 0);
-    uint32_t n = 1;
-    for (uint32_t l = 0; l < kWideLimbs; ++l)
-      if (tail.w[l] != 0) n = l + 1;
-    t.active[i] = n;
-  }
-  t.limbs = 1;
-  for (uint32_t l = 0; l < kWideLimbs; ++l) {
-    t.product[l] = g.product[l];
-    t.half_ceil[l] = g.half_ceil[l];
-    if (g.product[l] != 0) t.limbs = l + 1;
-  }
-  return t;
-}
-
 // ---- arithmetic helpers ---------------------------------------------------------
-
-__device__ __forceinline__ uint32_t mulhi_u24(uint32_t x, uint32_t y) {
-  return static_cast<uint32_t>((static_cast<uint64_t>(x & 0xFFFFFFu) * (y & 0xFFFFFFu)) >> 32);
-}
-
-// lo24(a) * lo24(b) + c (mod 2^32) as v_mad_u32_u24 (full rate); b uniform.
-// Written as asm because the compiler lowers the same C expression to a
-// quarter-rate 32- or 64-bit multiply-add.
-__device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
-  uint32_t d;
-  asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(b), "v"(c));
-  return d;
-}
 
 // Byte 0 of `byte_src` inserted at byte k of `word` (v_perm_b32: selector
 // 0-3 picks bytes of the second operand, 4-7 of the first).
@@ -137,8 +70,7 @@ __device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], uint32_t
     uint32_t s = static_cast<uint32_t>(r * T.inv[i] + T.bias[i]);
 #pragma unroll
     for (uint32_t q = 0; q < (i + 3) / 4; ++q) s = __builtin_amdgcn_udot4(vp[q], T.wpack[i][q], s, false);
-    const uint32_t qt = mulhi_u24(s << T.qshift[i], T.qrecip[i]);
-    const uint32_t t = mad_u24(qt, 256u - T.m[i], s);
+    const uint32_t t = mod_low_byte(s, T.qshift[i], T.qrecip[i], 256u - T.m[i]);
     switch (i % 4) {
       case 0: vp[i / 4] = insert_byte<0>(vp[i / 4], t); break;
       case 1: vp[i / 4] = insert_byte<1>(vp[i / 4], t); break;

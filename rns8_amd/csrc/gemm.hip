@@ -34,6 +34,7 @@
 //     reduces to int8 and clears the workspace.
 #include <type_traits>
 
+#include "int_ops.hpp"
 #include "kernels.hpp"
 
 namespace rns8x {
@@ -97,42 +98,13 @@ __device__ __forceinline__ int swizzle_b(int k, int chunk) {
 // the biased form the reduction reads (|sum| < 2^31).
 constexpr int kAccBias = static_cast<int>(0x80000000u);
 
-// hi32(lo24(x) * lo24(y)): v_mul_hi_u32_u24, full rate.
-__device__ __forceinline__ uint32_t mulhi_u24(uint32_t x, uint32_t y) {
-  return static_cast<uint32_t>((static_cast<uint64_t>(x & 0xFFFFFFu) * (y & 0xFFFFFFu)) >> 32);
-}
-
-// lo24(a) * lo24(b) + c (mod 2^32) as v_mad_u32_u24 (full rate), b uniform.
-// Written as asm: the compiler lowers the same expression in C to a
-// quarter-rate 32- or 64-bit multiply-add.
-__device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
-  uint32_t d;
-  asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(b), "v"(c));
-  return d;
-}
-
 // For u = x + 2^31 (x an int32 sum), returns a value whose low byte is
 // (x + H) mod m, H = floor(m/2): s = dot(bytes(u), 2^(8b) mod m) + off_i32 is
 // congruent to x + H and at most s_max, q = floor(s / m) by the 24-bit
 // quotient of tables.hpp, and s + q*(256 - m) is congruent to s - q*m modulo
 // 256. m_comp = 256 - m.
 __device__ __forceinline__ uint32_t residue_plus_half(uint32_t u, const ModulusConsts& mc, uint32_t m_comp) {
-  const uint32_t s = __builtin_amdgcn_udot4(u, mc.pow_lo, mc.off_i32, false);
-  const uint32_t q = mulhi_u24(s << mc.q_shift, mc.q_recip);
-  return mad_u24(q, m_comp, s);
-}
-
-// Packs (r_e - H) mod 256 for e = 0..3 (low bytes of r_e, see
-// residue_plus_half) into one little-endian dword: the centered residues as
-// int8. half2 = H * 0x10001. v_perm_b32(s0, s1, sel) takes result byte k
-// from byte sel_k of s1 (0-3) or of s0 (4-7), or 0 for selector 0x0c.
-__device__ __forceinline__ uint32_t pack_centered(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3,
-                                                  uint32_t half2) {
-  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  const u16x2 h = __builtin_bit_cast(u16x2, half2);
-  const u16x2 p01 = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(r1, r0, 0x0c040c00u)) - h;
-  const u16x2 p23 = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(r3, r2, 0x0c040c00u)) - h;
-  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, p23), __builtin_bit_cast(uint32_t, p01), 0x06040200u);
+  return mod_low_byte(__builtin_amdgcn_udot4(u, mc.pow_lo, mc.off_i32, false), mc.q_shift, mc.q_recip, m_comp);
 }
 
 // Raw buffer resource over [p, p + bytes). The inputs are wave-uniform; they
@@ -331,15 +303,16 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
   for (int kt = 0; kt < ktiles; ++kt) {
     const int stage1 = (stage + 1) & 3;
     const int stage3 = (stage + 3) & 3;
-    // Region 1: sub-step 0 MFMAs; tile t+3 DMAs interleaved (in source order)
-    // with the sub-step 1 fragment reads.
+    // Region 1: sub-step 0 MFMAs; the sub-step 1 fragment reads with the A
+    // DMAs of tile t+3 between them (source order fixes their placement).
+    // The DMAs are spread over the whole step: each one occupies the texture
+    // path for a while, and bunching all of a step's DMAs stalls MFMA issue.
     const TileSrc src = tile_src(kt + 3);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      dma_a(src, stage3, i);
       f1.a[i] = read_a(stage, 1, i);
-      dma_b(src, stage3, i);
       f1.b[i] = read_b(stage, 1, i);
+      dma_a(src, stage3, i);
     }
     mfma_rows(f0, 0, 4);
 #pragma unroll
@@ -349,8 +322,14 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
     __builtin_amdgcn_sched_barrier(0);
-    // Region 2: sub-step 1 MFMAs; first fragments of tile t+1.
-    read_frags(stage1, 0, f0n);
+    // Region 2: sub-step 1 MFMAs; first fragments of tile t+1 with the B DMAs
+    // of tile t+3 between them.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f0n.a[i] = read_a(stage1, 0, i);
+      f0n.b[i] = read_b(stage1, 0, i);
+      dma_b(src, stage3, i);
+    }
     mfma_rows(f1, 0, 4);
 #pragma unroll
     for (int i = 0; i < 12; ++i) {

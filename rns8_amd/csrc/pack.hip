@@ -10,9 +10,10 @@
 //
 // Residue of a 64-bit value without 64-bit division (tables.hpp): split u into
 // bytes, s = dot(lo bytes, 2^(8b) mod m) + dot(hi bytes, 2^(32+8b) mod m) + off
-// with two v_dot4_u32_u8 (s < 2^19), then one exact umulhi quotient. Signed
-// inputs are biased by 2^63 (flip the top bit) and the bias is folded into
-// `off`, so int64 and uint64 share the same arithmetic.
+// with two v_dot4_u32_u8 (s < 2^19), then the full-rate 24-bit quotient.
+// Signed inputs are biased by 2^63 (flip the top bit) and the bias is folded
+// into `off`, so int64 and uint64 share the same arithmetic.
+#include "int_ops.hpp"
 #include "kernels.hpp"
 
 namespace rns8x {
@@ -21,28 +22,16 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ int32_t residue_of_halves(uint32_t lo, uint32_t hi, uint32_t pow_lo, uint32_t pow_hi,
-                                                     uint32_t off, uint32_t recip, uint32_t m, uint32_t half) {
-  uint32_t s = __builtin_amdgcn_udot4(lo, pow_lo, off, false);
-  s = __builtin_amdgcn_udot4(hi, pow_hi, s, false);
-  const uint32_t q = __umulhi(s, recip);
-  return static_cast<int32_t>(s - q * m) - static_cast<int32_t>(half);
-}
-
-__device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {
-  return (static_cast<uint32_t>(a) & 0xFFu) | ((static_cast<uint32_t>(b) & 0xFFu) << 8) |
-         ((static_cast<uint32_t>(c) & 0xFFu) << 16) | (static_cast<uint32_t>(d) << 24);
-}
-
+// Grid-stride over 16-column chunks with 32-bit indices (the launchers reject
+// matrices with 2^32 chunks or more).
 template <bool Signed, bool Vec>
-__global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConsts pc, int64_t chunks_per_row,
-                                                          int64_t total_chunks) {
+__global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConsts pc, uint32_t chunks_per_row,
+                                                          uint32_t total_chunks) {
   const uint64_t* const src = static_cast<const uint64_t*>(a.src);
-  for (int64_t ch = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; ch < total_chunks;
-       ch += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t row = ch / chunks_per_row;
-    const int64_t c0 = (ch - row * chunks_per_row) * 16;
-    const uint64_t* const rp = src + row * a.ld;
+  for (uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x; ch < total_chunks; ch += gridDim.x * blockDim.x) {
+    const uint32_t row = ch / chunks_per_row;
+    const int64_t c0 = static_cast<int64_t>(ch - row * chunks_per_row) * 16;
+    const uint64_t* const rp = src + static_cast<int64_t>(row) * a.ld;
     uint32_t lo[16], hi[16];
     if (Vec && c0 + 16 <= a.cols) {
       // row start is 16-byte aligned (checked by the launcher) and c0 is even
@@ -66,41 +55,48 @@ __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConst
 #pragma unroll
       for (int e = 0; e < 16; ++e) hi[e] ^= 0x80000000u;
     }
-    int8_t* const out = a.planes + row * a.plane_ld + c0;
+    int8_t* const out = a.planes + static_cast<int64_t>(row) * a.plane_ld + c0;
     for (uint32_t p = 0; p < a.nplanes; ++p) {
       const ModulusConsts mc = pc.mod[p];
       const uint32_t off = Signed ? mc.off_i64 : mc.off_u64;
-      int32_t r[16];
+      const uint32_t m_comp = 256u - mc.m;
+      const uint32_t half2 = mc.half * 0x00010001u;
+      uint32_t r[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        r[e] = residue_of_halves(lo[e], hi[e], mc.pow_lo, mc.pow_hi, off, mc.recip, mc.m, mc.half);
-      const v4i w = {static_cast<int>(pack4(r[0], r[1], r[2], r[3])), static_cast<int>(pack4(r[4], r[5], r[6], r[7])),
-                     static_cast<int>(pack4(r[8], r[9], r[10], r[11])),
-                     static_cast<int>(pack4(r[12], r[13], r[14], r[15]))};
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t t = __builtin_amdgcn_udot4(lo[e], mc.pow_lo, off, false);
+        r[e] = mod_low_byte(__builtin_amdgcn_udot4(hi[e], mc.pow_hi, t, false), mc.pq_shift, mc.pq_recip, m_comp);
+      }
+      const v4i w = {static_cast<int>(pack_centered(r[0], r[1], r[2], r[3], half2)),
+                     static_cast<int>(pack_centered(r[4], r[5], r[6], r[7], half2)),
+                     static_cast<int>(pack_centered(r[8], r[9], r[10], r[11], half2)),
+                     static_cast<int>(pack_centered(r[12], r[13], r[14], r[15], half2))};
       *reinterpret_cast<v4i*>(out + static_cast<int64_t>(p) * a.plane_pitch) = w;
     }
   }
 }
 
-__global__ __launch_bounds__(256) void pack_u8_kernel(PackU8Args a, ModulusConsts mc, int64_t chunks_per_row,
-                                                      int64_t total_chunks) {
-  for (int64_t ch = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; ch < total_chunks;
-       ch += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t row = ch / chunks_per_row;
-    const int64_t c0 = (ch - row * chunks_per_row) * 16;
-    const uint8_t* const rp = a.src + row * a.ld;
-    int32_t r[16];
+// Finite u8: x < 256, s = x + H < 2^9 is inside the range of the int32
+// reduction constants (their s_max is at least 255 + H).
+__global__ __launch_bounds__(256) void pack_u8_kernel(PackU8Args a, ModulusConsts mc, uint32_t chunks_per_row,
+                                                      uint32_t total_chunks) {
+  const uint32_t m_comp = 256u - mc.m;
+  const uint32_t half2 = mc.half * 0x00010001u;
+  for (uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x; ch < total_chunks; ch += gridDim.x * blockDim.x) {
+    const uint32_t row = ch / chunks_per_row;
+    const int64_t c0 = static_cast<int64_t>(ch - row * chunks_per_row) * 16;
+    const uint8_t* const rp = a.src + static_cast<int64_t>(row) * a.ld;
+    uint32_t r[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const uint32_t x = (c0 + e < a.cols) ? rp[c0 + e] : 0u;
-      const uint32_t s = x + mc.half;  // < 2^9
-      const uint32_t q = __umulhi(s, mc.recip);
-      r[e] = static_cast<int32_t>(s - q * mc.m) - static_cast<int32_t>(mc.half);
+      r[e] = mod_low_byte(x + mc.half, mc.q_shift, mc.q_recip, m_comp);
     }
-    const v4i w = {static_cast<int>(pack4(r[0], r[1], r[2], r[3])), static_cast<int>(pack4(r[4], r[5], r[6], r[7])),
-                   static_cast<int>(pack4(r[8], r[9], r[10], r[11])),
-                   static_cast<int>(pack4(r[12], r[13], r[14], r[15]))};
-    *reinterpret_cast<v4i*>(a.plane + row * a.plane_ld + c0) = w;
+    const v4i w = {static_cast<int>(pack_centered(r[0], r[1], r[2], r[3], half2)),
+                   static_cast<int>(pack_centered(r[4], r[5], r[6], r[7], half2)),
+                   static_cast<int>(pack_centered(r[8], r[9], r[10], r[11], half2)),
+                   static_cast<int>(pack_centered(r[12], r[13], r[14], r[15], half2))};
+    *reinterpret_cast<v4i*>(a.plane + static_cast<int64_t>(row) * a.plane_ld + c0) = w;
   }
 }
 
@@ -141,19 +137,20 @@ hipError_t launch_pack_native(const PackArgs& a, const PlaneConsts& consts, hipS
   if ((reinterpret_cast<uintptr_t>(a.planes) & 15u) != 0) return hipErrorInvalidValue;
   const int64_t chunks_per_row = a.plane_ld / 16;
   const int64_t total = chunks_per_row * a.rows;
+  if (total >= (int64_t{1} << 32)) return hipErrorInvalidValue;
   const bool vec = (reinterpret_cast<uintptr_t>(a.src) & 15u) == 0 && (a.ld % 2) == 0;
   const dim3 grid(grid_for(total));
   if (a.kind == NativeKind::I64) {
     if (vec)
-      hipLaunchKernelGGL((pack_native_kernel<true, true>), grid, dim3(256), 0, stream, a, consts, chunks_per_row, total);
+      hipLaunchKernelGGL((pack_native_kernel<true, true>), grid, dim3(256), 0, stream, a, consts, static_cast<uint32_t>(chunks_per_row), static_cast<uint32_t>(total));
     else
-      hipLaunchKernelGGL((pack_native_kernel<true, false>), grid, dim3(256), 0, stream, a, consts, chunks_per_row, total);
+      hipLaunchKernelGGL((pack_native_kernel<true, false>), grid, dim3(256), 0, stream, a, consts, static_cast<uint32_t>(chunks_per_row), static_cast<uint32_t>(total));
   } else {
     if (vec)
-      hipLaunchKernelGGL((pack_native_kernel<false, true>), grid, dim3(256), 0, stream, a, consts, chunks_per_row, total);
+      hipLaunchKernelGGL((pack_native_kernel<false, true>), grid, dim3(256), 0, stream, a, consts, static_cast<uint32_t>(chunks_per_row), static_cast<uint32_t>(total));
     else
-      hipLaunchKernelGGL((pack_native_kernel<false, false>), grid, dim3(256), 0, stream, a, consts, chunks_per_row,
-                         total);
+      hipLaunchKernelGGL((pack_native_kernel<false, false>), grid, dim3(256), 0, stream, a, consts, static_cast<uint32_t>(chunks_per_row),
+                         static_cast<uint32_t>(total));
   }
   return hipGetLastError();
 }
@@ -177,8 +174,9 @@ hipError_t launch_pack_u8(const PackU8Args& a, hipStream_t stream) {
   if (a.plane_ld != padded_ld(a.cols) || (reinterpret_cast<uintptr_t>(a.plane) & 15u) != 0) return hipErrorInvalidValue;
   const int64_t chunks_per_row = a.plane_ld / 16;
   const int64_t total = chunks_per_row * a.rows;
+  if (total >= (int64_t{1} << 32)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(pack_u8_kernel, dim3(grid_for(total)), dim3(256), 0, stream, a, make_modulus_consts(a.modulus),
-                     chunks_per_row, total);
+                     static_cast<uint32_t>(chunks_per_row), static_cast<uint32_t>(total));
   return hipGetLastError();
 }
 

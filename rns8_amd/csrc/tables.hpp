@@ -45,6 +45,11 @@ struct ModulusConsts {
   // floor(s / m) = mulhi_u24(s << q_shift, q_recip) (make_quot24).
   uint32_t q_shift;
   uint32_t q_recip;
+  // Same for the pack reduction of a 64-bit value: s = dot(lo bytes, pow_lo)
+  // + dot(hi bytes, pow_hi) + off (off_i64 or off_u64) is at most
+  // 255 * (sum of pow_lo and pow_hi bytes) + max(off_i64, off_u64) < 2^19.
+  uint32_t pq_shift;
+  uint32_t pq_recip;
 };
 
 // Shift and reciprocal for floor(s / m) = hi32((s << a) * R) over 0 <= s <=
@@ -91,6 +96,12 @@ inline ModulusConsts make_modulus_consts(uint32_t m) {
   const Quot24 q = make_quot24(m, 255u * byte_sum + c.off_i32);
   c.q_shift = q.shift;
   c.q_recip = q.recip;
+  uint32_t hi_sum = 0;
+  for (uint32_t b = 0; b < 4; ++b) hi_sum += (hi >> (8u * b)) & 0xFFu;
+  const uint32_t off_max = c.off_i64 > c.off_u64 ? c.off_i64 : c.off_u64;
+  const Quot24 pq = make_quot24(m, 255u * (byte_sum + hi_sum) + off_max);
+  c.pq_shift = pq.shift;
+  c.pq_recip = pq.recip;
   return c;
 }
 
@@ -208,6 +219,61 @@ constexpr GarnerConsts make_garner_consts(uint32_t prefix) {
     g.half_ceil[i] = (h.w[i] >> 1) | ((next & 1u) << 23);
   }
   return g;
+}
+
+// ---- per-prefix Garner tables for the export kernels ----------------------------
+//
+// Digit i of the mixed-radix form is v_i = s mod m_i with
+//   s = r_i * I_i + bias_i + sum_{j<i} v_j * W[j][i]       (GarnerConsts)
+// and 0 <= s <= s_max_i (r_i >= -128, v_j <= 255), so the quotient comes from
+// the full-rate 24-bit reciprocal of make_quot24 and v_i is the low byte of
+// s + q*(256 - m_i) (congruent to s - q*m_i modulo 256, and s - q*m_i < 256).
+template <uint32_t P>
+struct GarnerTable {
+  static constexpr uint32_t kWords = (P + 3) / 4;
+  uint32_t m[P];
+  int32_t inv[P];
+  int32_t bias[P];
+  uint32_t wpack[P][kWords == 0 ? 1 : kWords];
+  uint32_t qshift[P];
+  uint32_t qrecip[P];
+  uint32_t active[P];  // 24-bit limbs of prod_{k >= i} m_k (Horner step i)
+  uint32_t product[kWideLimbs];
+  uint32_t half_ceil[kWideLimbs];
+  uint32_t limbs;      // limbs of P itself
+};
+
+template <uint32_t P>
+constexpr GarnerTable<P> make_garner_table() {
+  const GarnerConsts g = make_garner_consts(P);
+  GarnerTable<P> t{};
+  for (uint32_t i = 0; i < P; ++i) {
+    t.m[i] = g.m[i];
+    t.inv[i] = static_cast<int32_t>(g.inv[i]);
+    t.bias[i] = static_cast<int32_t>(g.bias[i]);
+    uint32_t s_max = 127u * g.inv[i] + g.bias[i];
+    for (uint32_t q = 0; q < GarnerTable<P>::kWords; ++q) {
+      t.wpack[i][q] = g.wpack[i][q];
+      for (uint32_t b = 0; b < 4; ++b) s_max += 255u * ((g.wpack[i][q] >> (8 * b)) & 0xFFu);
+    }
+    const Quot24 qq = make_quot24(g.m[i], s_max);
+    t.qshift[i] = qq.shift;
+    t.qrecip[i] = qq.recip;
+    Limbs24 tail;
+    tail.w[0] = 1;
+    for (uint32_t k = i; k < P; ++k) tail.mul_add(g.m[k], 0);
+    uint32_t n = 1;
+    for (uint32_t l = 0; l < kWideLimbs; ++l)
+      if (tail.w[l] != 0) n = l + 1;
+    t.active[i] = n;
+  }
+  t.limbs = 1;
+  for (uint32_t l = 0; l < kWideLimbs; ++l) {
+    t.product[l] = g.product[l];
+    t.half_ceil[l] = g.half_ceil[l];
+    if (g.product[l] != 0) t.limbs = l + 1;
+  }
+  return t;
 }
 
 // 64-bit value as 24-bit limbs.

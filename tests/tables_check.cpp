@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <utility>
 #include <vector>
 
 #include "tables.hpp"
@@ -95,7 +96,21 @@ void check_quot() {
     if (c.q_recip >= (1u << 24)) fail("recip24", m, c.q_recip, 0, 0);
     for (uint32_t s = 0; s <= smax; ++s, ++checks)
       if (mulhi_u24(s << c.q_shift, c.q_recip) != s / m) fail("quot24", m, s, mulhi_u24(s << c.q_shift, c.q_recip), s / m);
-    // 32-bit reciprocal used by the pack and export kernels: exact below 2^21
+    // byte weights, computed independently
+    for (uint32_t b = 0; b < 4; ++b) {
+      const uint64_t lo = (uint64_t{1} << (8 * b)) % m;
+      const uint64_t hi = static_cast<uint64_t>((static_cast<unsigned __int128>(1) << (32 + 8 * b)) % m);
+      if (((c.pow_lo >> (8 * b)) & 0xFFu) != lo) fail("pow_lo", m, b, c.pow_lo, lo);
+      if (((c.pow_hi >> (8 * b)) & 0xFFu) != hi) fail("pow_hi", m, b, c.pow_hi, hi);
+    }
+    // pack reduction of a 64-bit value: two byte dot products plus an offset
+    uint32_t hbytes = 0;
+    for (int k = 0; k < 4; ++k) hbytes += ((c.pow_lo >> (8 * k)) & 0xFFu) + ((c.pow_hi >> (8 * k)) & 0xFFu);
+    const uint32_t pmax = 255u * hbytes + (c.off_i64 > c.off_u64 ? c.off_i64 : c.off_u64);
+    if ((uint64_t{pmax} << c.pq_shift) >= (1u << 24) || c.pq_recip >= (1u << 24)) fail("pack quot range", m, pmax, 0, 0);
+    for (uint32_t s = 0; s <= pmax; ++s, ++checks)
+      if (mulhi_u24(s << c.pq_shift, c.pq_recip) != s / m) fail("pack quot24", m, s, 0, 0);
+    // 32-bit reciprocal kept for host use: exact below 2^21
     for (uint32_t s = 0; s < (1u << 21); ++s, ++checks)
       if (umulhi(s, c.recip) != s / m) fail("quot32", m, s, umulhi(s, c.recip), s / m);
   }
@@ -109,7 +124,7 @@ int8_t epilogue_byte(int32_t x, const ModulusConsts& c) {
   const uint32_t q = mulhi_u24(s << c.q_shift, c.q_recip);
   return static_cast<int8_t>(mad_u24(q, 256u - c.m, s));  // low byte (x + H) mod m, H not yet subtracted
 }
-uint32_t pack_centered(const uint32_t r[4], uint32_t half2) {
+uint32_t pack_centered(const uint32_t r[4], uint32_t half2) {  // v_perm + packed u16 subtract
   const uint32_t p01 = pk_sub_u16(perm(r[1], r[0], 0x0c040c00u), half2);
   const uint32_t p23 = pk_sub_u16(perm(r[3], r[2], 0x0c040c00u), half2);
   return perm(p23, p01, 0x06040200u);
@@ -144,81 +159,131 @@ void check_reduce32() {
   std::printf("reduce32 checks %" PRIu64 "\n", checks);
 }
 
+uint32_t pack_byte64(uint64_t u, uint32_t off, const ModulusConsts& c) {
+  uint32_t s = udot4(static_cast<uint32_t>(u), c.pow_lo, off);
+  s = udot4(static_cast<uint32_t>(u >> 32), c.pow_hi, s);
+  return mad_u24(mulhi_u24(s << c.pq_shift, c.pq_recip), 256u - c.m, s);
+}
+
 void check_pack64() {
   std::vector<int64_t> xs = {INT64_MIN, INT64_MIN + 1, -1, 0, 1, INT64_MAX, INT64_MAX - 1,
                              int64_t{1} << 62, -(int64_t{1} << 62), int64_t{1} << 32, -(int64_t{1} << 32)};
   Rng rng{777};
   for (int i = 0; i < 50000; ++i) xs.push_back(static_cast<int64_t>(rng.next()));
+  while (xs.size() % 4) xs.push_back(0);
   uint64_t checks = 0;
   for (uint32_t m = 2; m <= 256; ++m) {
     const ModulusConsts c = make_modulus_consts(m);
-    for (int64_t x : xs) {
-      // signed: u = x ^ 2^63, halves of u, offset off_i64
-      const uint64_t u = static_cast<uint64_t>(x) ^ 0x8000000000000000ull;
-      uint32_t s = udot4(static_cast<uint32_t>(u), c.pow_lo, c.off_i64);
-      s = udot4(static_cast<uint32_t>(u >> 32), c.pow_hi, s);
-      if (s >= (1u << 21)) fail("pack64 range", m, x, s, 0);
-      const int64_t got = static_cast<int64_t>(s - umulhi(s, c.recip) * m) - c.half;
-      const int64_t want = centered_ref(x, m);
-      if (got != want) fail("pack i64", m, x, got, want);
-      // unsigned: the same bits read as uint64, offset off_u64
-      const uint64_t v = static_cast<uint64_t>(x);
-      uint32_t t = udot4(static_cast<uint32_t>(v), c.pow_lo, c.off_u64);
-      t = udot4(static_cast<uint32_t>(v >> 32), c.pow_hi, t);
-      const int64_t got_u = static_cast<int64_t>(t - umulhi(t, c.recip) * m) - c.half;
-      const int64_t want_u = centered_ref(static_cast<__int128>(v), m);
-      if (got_u != want_u) fail("pack u64", m, x, got_u, want_u);
-      checks += 2;
+    const uint32_t half2 = c.half * 0x00010001u;
+    for (size_t i = 0; i < xs.size(); i += 4) {
+      uint32_t rs[4], ru[4];
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t v = static_cast<uint64_t>(xs[i + e]);
+        rs[e] = pack_byte64(v ^ 0x8000000000000000ull, c.off_i64, c);  // signed: bias 2^63
+        ru[e] = pack_byte64(v, c.off_u64, c);                          // unsigned
+      }
+      const uint32_t ws = pack_centered(rs, half2), wu = pack_centered(ru, half2);
+      for (int e = 0; e < 4; ++e, checks += 2) {
+        const int64_t want_s = centered_ref(xs[i + e], m);
+        const int64_t want_u = centered_ref(static_cast<__int128>(static_cast<uint64_t>(xs[i + e])), m);
+        if (static_cast<int8_t>(ws >> (8 * e)) != want_s) fail("pack i64", m, xs[i + e], static_cast<int8_t>(ws >> (8 * e)), want_s);
+        if (static_cast<int8_t>(wu >> (8 * e)) != want_u) fail("pack u64", m, xs[i + e], static_cast<int8_t>(wu >> (8 * e)), want_u);
+      }
+    }
+    // finite pack: every byte value
+    for (uint32_t x0 = 0; x0 < 256; x0 += 4) {
+      uint32_t r[4];
+      for (int e = 0; e < 4; ++e) r[e] = mad_u24(mulhi_u24((x0 + e + c.half) << c.q_shift, c.q_recip), 256u - m, x0 + e + c.half);
+      const uint32_t w = pack_centered(r, half2);
+      for (int e = 0; e < 4; ++e, ++checks)
+        if (static_cast<int8_t>(w >> (8 * e)) != centered_ref(x0 + e, m)) fail("pack u8", m, x0 + e, 0, 0);
     }
   }
   std::printf("pack64 checks %" PRIu64 "\n", checks);
 }
 
-// Prints the Garner tables and, for random centered residue vectors, the
-// digits the export kernel's recurrence produces (emulated), for a big-int
-// check of x = sum v_i P_i against every residue.
-void garner_dump() {
-  Rng rng{4242};
-  for (uint32_t prefix = 1; prefix <= kMaxPrefix; ++prefix) {
-    const GarnerConsts g = make_garner_consts(prefix);
-    std::printf("prefix %u\n", prefix);
-    std::printf("m");
-    for (uint32_t i = 0; i < prefix; ++i) std::printf(" %u", g.m[i]);
-    std::printf("\ninv");
-    for (uint32_t i = 0; i < prefix; ++i) std::printf(" %u", g.inv[i]);
-    std::printf("\nbias");
-    for (uint32_t i = 0; i < prefix; ++i) std::printf(" %u", g.bias[i]);
-    std::printf("\nw");
-    for (uint32_t i = 0; i < prefix; ++i)
-      for (uint32_t j = 0; j < i; ++j) std::printf(" %u", (g.wpack[i][j / 4] >> (8 * (j % 4))) & 0xFFu);
-    std::printf("\nproduct");
-    for (uint32_t l = 0; l < kWideLimbs; ++l) std::printf(" %u", g.product[l]);
-    std::printf("\nhalf_ceil");
-    for (uint32_t l = 0; l < kWideLimbs; ++l) std::printf(" %u", g.half_ceil[l]);
-    std::printf("\n");
-    for (int t = 0; t < 64; ++t) {
-      int32_t r[kMaxPrefix];
-      uint32_t v[kMaxPrefix] = {};
-      uint32_t vp[kGarnerDigitWords] = {};
-      for (uint32_t i = 0; i < prefix; ++i) {
-        const int32_t h = static_cast<int32_t>(g.m[i] / 2);
-        // extremes first, then random centered residues
-        r[i] = t == 0 ? -h : t == 1 ? static_cast<int32_t>(g.m[i]) - 1 - h
-                                    : static_cast<int32_t>(rng.next() % g.m[i]) - h;
-        uint32_t s = static_cast<uint32_t>(r[i] * static_cast<int32_t>(g.inv[i]) + static_cast<int32_t>(g.bias[i]));
-        for (uint32_t q = 0; q < (i + 3) / 4; ++q) s = udot4(vp[q], g.wpack[i][q], s);
-        if (s >= (1u << 21)) fail("garner range", g.m[i], s, i, prefix);
-        v[i] = s - umulhi(s, g.recip[i]) * g.m[i];
-        vp[i / 4] |= v[i] << (8 * (i % 4));
-      }
-      std::printf("case");
-      for (uint32_t i = 0; i < prefix; ++i) std::printf(" %d", r[i]);
-      std::printf(" |");
-      for (uint32_t i = 0; i < prefix; ++i) std::printf(" %u", v[i]);
-      std::printf("\n");
+// Prints, for every prefix, the Garner tables and the export kernel's
+// reconstruction (emulated step by step from GarnerTable<P>: digits with the
+// 24-bit quotient, Horner in 24-bit limbs over the compile-time active limb
+// counts, sign and magnitude) for random centered residue vectors, so the
+// Python side can check them with big integers.
+template <uint32_t P>
+void garner_dump_p(Rng& rng) {
+  constexpr GarnerTable<P> T = make_garner_table<P>();
+  const GarnerConsts g = make_garner_consts(P);
+  std::printf("prefix %u\n", P);
+  std::printf("m");
+  for (uint32_t i = 0; i < P; ++i) std::printf(" %u", g.m[i]);
+  std::printf("\ninv");
+  for (uint32_t i = 0; i < P; ++i) std::printf(" %u", g.inv[i]);
+  std::printf("\nbias");
+  for (uint32_t i = 0; i < P; ++i) std::printf(" %u", g.bias[i]);
+  std::printf("\nw");
+  for (uint32_t i = 0; i < P; ++i)
+    for (uint32_t j = 0; j < i; ++j) std::printf(" %u", (g.wpack[i][j / 4] >> (8 * (j % 4))) & 0xFFu);
+  std::printf("\nproduct");
+  for (uint32_t l = 0; l < kWideLimbs; ++l) std::printf(" %u", T.product[l]);
+  std::printf("\nhalf_ceil");
+  for (uint32_t l = 0; l < kWideLimbs; ++l) std::printf(" %u", T.half_ceil[l]);
+  std::printf("\n");
+  for (int t = 0; t < 64; ++t) {
+    int32_t r[kMaxPrefix];
+    uint32_t vp[kGarnerDigitWords] = {};
+    for (uint32_t i = 0; i < P; ++i) {
+      const int32_t h = static_cast<int32_t>(T.m[i] / 2);
+      r[i] = t == 0 ? -h : t == 1 ? static_cast<int32_t>(T.m[i]) - 1 - h
+                                  : static_cast<int32_t>(rng.next() % T.m[i]) - h;
     }
+    // digits (digit 0: the raw residue byte, m_0 = 256)
+    vp[0] = static_cast<uint32_t>(r[0]) & 0xFFu;
+    for (uint32_t i = 1; i < P; ++i) {
+      uint32_t s = static_cast<uint32_t>(r[i] * T.inv[i] + T.bias[i]);
+      for (uint32_t q = 0; q < (i + 3) / 4; ++q) s = udot4(vp[q], T.wpack[i][q], s);
+      const uint32_t v = mad_u24(mulhi_u24(s << T.qshift[i], T.qrecip[i]), 256u - T.m[i], s) & 0xFFu;
+      vp[i / 4] |= v << (8 * (i % 4));
+    }
+    // Horner over the active limbs of each step
+    uint32_t x[kWideLimbs] = {};
+    x[0] = (vp[(P - 1) / 4] >> (8 * ((P - 1) % 4))) & 0xFFu;
+    for (int i = static_cast<int>(P) - 2; i >= 0; --i) {
+      uint32_t carry = (vp[i / 4] >> (8 * (i % 4))) & 0xFFu;
+      for (uint32_t l = 0; l < T.active[i]; ++l) {
+        const uint32_t u = mad_u24(x[l], T.m[i], carry);
+        x[l] = u & 0xFFFFFFu;
+        carry = u >> 24;
+      }
+      if (carry != 0) fail("horner carry out", P, i, carry, 0);
+    }
+    // sign and magnitude as the kernel computes them
+    uint32_t borrow = 0;
+    for (uint32_t l = 0; l < kWideLimbs; ++l) borrow = (x[l] - T.half_ceil[l] - borrow) >> 31;
+    const bool negative = borrow == 0;
+    uint32_t d[kWideLimbs];
+    borrow = 0;
+    for (uint32_t l = 0; l < kWideLimbs; ++l) {
+      const uint32_t u = T.product[l] - x[l] - borrow;
+      borrow = u >> 31;
+      d[l] = negative ? (u & 0xFFFFFFu) : x[l];
+    }
+    std::printf("case");
+    for (uint32_t i = 0; i < P; ++i) std::printf(" %d", r[i]);
+    std::printf(" |");
+    for (uint32_t i = 0; i < P; ++i) std::printf(" %u", (vp[i / 4] >> (8 * (i % 4))) & 0xFFu);
+    std::printf(" | %d |", negative ? 1 : 0);
+    for (uint32_t l = 0; l < kWideLimbs; ++l) std::printf(" %u", d[l]);
+    std::printf(" |");
+    for (uint32_t l = 0; l < kWideLimbs; ++l) std::printf(" %u", x[l]);
+    std::printf("\n");
   }
 }
+
+template <uint32_t... Ps>
+void garner_dump_all(std::integer_sequence<uint32_t, Ps...>) {
+  Rng rng{4242};
+  (garner_dump_p<Ps + 1>(rng), ...);
+}
+
+void garner_dump() { garner_dump_all(std::make_integer_sequence<uint32_t, kMaxPrefix>{}); }
 
 }  // namespace
 

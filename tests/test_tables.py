@@ -62,10 +62,12 @@ def _limbs(vals: list[int]) -> int:
 
 
 def test_garner_tables_and_digits(checker):
-    """Garner tables for prefixes 1..20 and the digit recurrence: the mixed-radix
-    number sum v_i * P_i must reproduce every residue (Chinese remainder
-    property), digits must be in range, and P / ceil(P/2) limbs must match the
-    big-integer product."""
+    """Garner tables for prefixes 1..20 and the export kernel's reconstruction
+    (emulated from the same compile-time tables): the mixed-radix number
+    sum v_i * P_i must reproduce every residue (Chinese remainder property),
+    digits must be in range, Horner over the active limbs must equal it, the
+    sign must follow the centered threshold ceil(P/2), the magnitude must be
+    P - x or x, and the P / ceil(P/2) limbs must match the big-integer product."""
     out = _run(checker, "garner").splitlines()
     prefix = None
     cases = 0
@@ -102,14 +104,20 @@ def test_garner_tables_and_digits(checker):
             assert all(0 <= x < (1 << 24) for x in limbs)
             assert _limbs(limbs) == (P[prefix] + 1) // 2
         elif key == "case":
-            bar = rest.index("|")
-            r = [int(x) for x in rest[:bar]]
-            v = [int(x) for x in rest[bar + 1:]]
+            parts = " ".join(rest).split("|")
+            r = [int(x) for x in parts[0].split()]
+            v = [int(x) for x in parts[1].split()]
+            negative = int(parts[2]) == 1
+            d = _limbs([int(x) for x in parts[3].split()])
+            horner = _limbs([int(x) for x in parts[4].split()])
             x = sum(v[i] * P[i] for i in range(prefix))
             assert 0 <= x < P[prefix]
             for i in range(prefix):
                 assert 0 <= v[i] < m[i]
-                assert (x - r[i]) % m[i] == 0
+                assert (x - r[i]) % m[i] == 0          # Chinese remainder property
+            assert horner == x                          # Horner over the active limbs
+            assert negative == (x >= (P[prefix] + 1) // 2)
+            assert d == (P[prefix] - x if negative else x)
             cases += 1
         elif key == "ok":
             pass
