@@ -314,8 +314,7 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
     const std::size_t bytes = static_cast<std::size_t>(rows) * cols * sizeof(T);
     rns8_status st = ensure_device_buffer(ctx->device_id, &matrix->upload, &matrix->upload_bytes, bytes);
     if (st != RNS8_SUCCESS) return st;
-    if (hipMemcpy2DAsync(matrix->upload, cols * sizeof(T), src, ld * sizeof(T), cols * sizeof(T), rows,
-                         hipMemcpyHostToDevice, stream) != hipSuccess)
+    if (ctx->host.to_device(matrix->upload, src, cols * sizeof(T), ld * sizeof(T), rows, stream) != hipSuccess)
       return RNS8_BACKEND_FAILURE;
     dsrc = matrix->upload;
     dld = cols;
@@ -363,8 +362,7 @@ rns8_status pack_u8(rns8_context* ctx, rns8_matrix* matrix, uint16_t modulus, co
     const std::size_t bytes = static_cast<std::size_t>(rows) * cols;
     rns8_status st = ensure_device_buffer(ctx->device_id, &matrix->upload, &matrix->upload_bytes, bytes);
     if (st != RNS8_SUCCESS) return st;
-    if (hipMemcpy2DAsync(matrix->upload, cols, src, ld, cols, rows, hipMemcpyHostToDevice, stream) != hipSuccess)
-      return RNS8_BACKEND_FAILURE;
+    if (ctx->host.to_device(matrix->upload, src, cols, ld, rows, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
     dsrc = static_cast<const uint8_t*>(matrix->upload);
     dld = cols;
   }
@@ -492,10 +490,7 @@ rns8_status export_host(rns8_context* ctx, const rns8_plan* plan, const rns8_mat
       hipStreamSynchronize(stream) != hipSuccess)
     return RNS8_BACKEND_FAILURE;
   if (status != 0) return RNS8_RANGE_ERROR;
-  if (hipMemcpy2DAsync(dst, ld * elem, mc->staging, n * elem, n * elem, m, hipMemcpyDeviceToHost, stream) !=
-          hipSuccess ||
-      hipStreamSynchronize(stream) != hipSuccess)
-    return RNS8_BACKEND_FAILURE;
+  if (ctx->host.to_host(dst, ld * elem, mc->staging, n * elem, m, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
   return RNS8_SUCCESS;
 }
 
@@ -529,9 +524,7 @@ rns8_status export_finite(rns8_context* ctx, const rns8_plan* plan, uint16_t mod
   if (st != RNS8_SUCCESS) return st;
   ExportU8Args a{C->planes, m, n, C->plane_ld, static_cast<uint8_t*>(mc->staging), n, modulus};
   if (launch_export_u8(a, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
-  if (hipMemcpy2DAsync(dst, ld, mc->staging, n, n, m, hipMemcpyDeviceToHost, stream) != hipSuccess)
-    return RNS8_BACKEND_FAILURE;
-  return sync(stream);
+  return ctx->host.to_host(dst, ld, mc->staging, n, m, stream) == hipSuccess ? RNS8_SUCCESS : RNS8_BACKEND_FAILURE;
 }
 
 // ---- one-shot (api_oneshot.cpp) -----------------------------------------------------

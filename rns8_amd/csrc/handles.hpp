@@ -10,6 +10,7 @@
 
 #include "rns8/rns8.h"
 #include "rns8_mi355x.h"
+#include "host_copy.hpp"
 #include "tables.hpp"
 #include "wide_int.hpp"
 
@@ -30,6 +31,7 @@ struct rns8_context {
   int device_id = 0;
   hipStream_t stream = nullptr;
   rns8_device_info device_info{};
+  rns8x::HostStaging host;  // pinned staging for host-memory operands and results
 };
 
 struct rns8_plan {

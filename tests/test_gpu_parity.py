@@ -3,6 +3,8 @@
 Every comparison is bit-exact: residue planes byte for byte, exports value for
 value and status for status, on the same seeded inputs.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -221,3 +223,38 @@ def test_exact_wide_signed_limbs_match_oracle(gpu_ctx, prefix, limbs):
                 assert oracle.limbs_to_int(out[i, limbs * j:limbs * j + limbs], True) == v
     else:
         assert (out == 0xA5A5).all()
+
+
+def test_host_staging_multi_chunk_strided(gpu_ctx):
+    """Host operands and results larger than one 16 MB staging chunk, with row
+    strides above the row length on both sides (C = A x I round trip)."""
+    rows, cols, ld = 2100, 1100, 1111
+    full = rand_i64(77, (rows, ld), bits=40)
+    n = cols
+    B = np.eye(cols, dtype=np.int64)
+    desc = r.gemm_desc(r.BOUNDED_I64, r.BOUND_GLOBAL_MAX_ABS, rows, n, cols, bound=1 << 40, max_prefix=9,
+                       flags=r.PLAN_FORCE_FIXED_PREFIX)
+    plan = r.Plan(gpu_ctx, desc)
+    Am = bounded_matrix(gpu_ctx, rows, cols, r.BOUNDED_I64, 9)
+    Bm = bounded_matrix(gpu_ctx, cols, n, r.BOUNDED_I64, 9)
+    Cm = bounded_matrix(gpu_ctx, rows, n, r.BOUNDED_I64, 9)
+    ws = r.Workspace(gpu_ctx, plan)
+    r.check(r.pack_i64(gpu_ctx, Am, full, 1, ld=ld), "pack A")
+    A = np.ascontiguousarray(full[:, :cols])
+    np.testing.assert_array_equal(Am.read_residues(9)[:, ::97], oracle.pack_i64(A, 9)[:, ::97])
+    r.check(r.pack_i64(gpu_ctx, Bm, B, 2), "pack B")
+    r.check(r.gemm_rns(gpu_ctx, plan, Am, Bm, Cm, ws), "gemm")
+    out = np.full((rows, n + 7), 5, dtype=np.int64)
+    st = r.lib().rns8_export_i64(gpu_ctx.ptr, plan.ptr, Cm.ptr, out.ctypes.data_as(ctypes.c_void_p), n + 7)
+    assert st == r.SUCCESS
+    np.testing.assert_array_equal(out[:, :n], A)
+    assert (out[:, n:] == 5).all()  # padding columns of dst untouched
+
+
+def test_host_staging_row_longer_than_chunk(gpu_ctx):
+    """One row of 17.6 MB: the staging splits inside the row."""
+    cols = 2_200_000
+    src = rand_i64(78, (1, cols))
+    m = bounded_matrix(gpu_ctx, 1, cols, r.BOUNDED_I64, 3)
+    r.check(r.pack_i64(gpu_ctx, m, src, 1), "pack")
+    np.testing.assert_array_equal(m.read_residues(3), oracle.pack_i64(src, 3))
