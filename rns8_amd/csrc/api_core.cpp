@@ -540,9 +540,9 @@ rns8_status rns8_create_plan(rns8_context* ctx, const rns8_gemm_desc* desc, rns8
     plan->tile_cols = (static_cast<uint64_t>(desc->n) + plan->desc.tile_n - 1) / plan->desc.tile_n;
     plan->tile_count = plan->tile_rows * plan->tile_cols;
     const uint32_t planes = uses_finite_storage(desc->semantics) ? 1u : selected;
-    plan->splitk_slices = choose_splitk_slices(desc->m, desc->n, desc->k > kSafeKBlock ? kSafeKBlock : desc->k,
-                                               planes);
-    plan->splitk_bytes = plan->splitk_slices > 1 ? static_cast<uint64_t>(planes) * desc->m * padded_ld(desc->n) * 4u : 0u;
+    const int64_t kblock = desc->k > kSafeKBlock ? kSafeKBlock : desc->k;
+    plan->splitk_slices = choose_splitk_slices(desc->m, desc->n, kblock, planes);
+    plan->splitk_bytes = splitk_workspace_bytes(desc->m, desc->n, kblock, planes);
     *out = plan;
     return RNS8_SUCCESS;
   });
@@ -626,8 +626,10 @@ rns8_status rns8_get_plan_backend_info(const rns8_plan* plan, rns8_plan_backend_
     out->exact_differential_validated = 1;
     out->workspace_required_bytes = plan->splitk_bytes;
     copy_text(out->selected_kernel, sizeof(out->selected_kernel),
-              plan->splitk_slices > 1 ? "plane_gemm_kernel<64> split-K + splitk_finalize_kernel"
-                                      : "plane_gemm_kernel<64> (256x256 tile, 3-stage LDS ring)");
+              plan->splitk_slices > 1 ? "plane_gemm_kernel 128x128 split-K + splitk_finalize_kernel"
+              : choose_gemm_shape(plan->desc.m, plan->desc.n, plan->desc.k, plan->prefix ? plan->prefix : 1u).tile == 256
+                  ? "plane_gemm_kernel 256x256 tile, 4-stage LDS DMA ring"
+                  : "plane_gemm_kernel 128x128 tile, 4-stage LDS DMA ring");
     copy_text(out->accelerator_library, sizeof(out->accelerator_library), "none (hand-written HIP)");
     copy_text(out->capability_status, sizeof(out->capability_status), "available");
     copy_text(out->epilogue_mode, sizeof(out->epilogue_mode), "in_register_centered_reduction");

@@ -5,12 +5,14 @@
 // ring GEMM with int32 accumulation reduced at least every 65536 K).
 //
 // Work decomposition
-//   * workgroup = 256 threads (4 wave64s) owning a 256x256 output tile of one
-//     plane (and one K slice when split-K is on); waves form a 2x2 grid of
-//     128x128 wave tiles.
+//   * workgroup = 256 threads (4 wave64s) owning an output tile of one plane
+//     (and one K slice when split-K is on); waves form a 2x2 grid. Two tile
+//     configurations: 256x256 (128x128 per wave, 16 MFMA accumulators, one
+//     workgroup per CU) for large outputs and 128x128 (64x64 per wave, two
+//     workgroups per CU) when 256x256 tiles would leave CUs idle.
 //   * K is consumed in BK = 64 byte steps through a 4-stage LDS ring. Both
 //     operands go global -> LDS by buffer-load DMA (no VGPR staging): A tiles
-//     (256 x 64, K-contiguous rows) and B tiles (64 x 256, N-contiguous rows,
+//     (BM x 64, K-contiguous rows) and B tiles (64 x BN, N-contiguous rows,
 //     the layout they have in HBM). The DMA of step t+3 is in flight while
 //     step t computes; one barrier per step.
 //   * A fragments are ds_read_b128 of 16 K-contiguous bytes; B fragments are
@@ -29,9 +31,9 @@
 //     reduction reads; reduction is a byte dot product plus a 24-bit
 //     reciprocal quotient (full-rate VALU only), and 4 residues are packed per
 //     dword store.
-//   * Split-K (tall-skinny K): each slice reduces (when K > 65536) and
-//     atomically adds its partial into an int32 workspace; a finalize kernel
-//     reduces to int8 and clears the workspace.
+//   * Split-K (tall-skinny K, 128x128 tiles): each slice stores its int32
+//     partial tile to its own workspace slot; a finalize kernel adds the
+//     slices, reduces to int8 and writes C (deterministic, no atomics).
 #include <type_traits>
 
 #include "int_ops.hpp"
@@ -59,44 +61,58 @@ constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (
 constexpr int kWaitVm[9] = {wait_vm(0), wait_vm(1), wait_vm(2), wait_vm(3), wait_vm(4),
                             wait_vm(5), wait_vm(6), wait_vm(7), wait_vm(8)};
 
-constexpr int kBM = 256;
-constexpr int kBN = 256;
 constexpr int kThreads = 256;
 constexpr int kGroupM = 4;  // tile rows per L2 reuse group
 // Buffer resource word 3 for gfx9-family raw buffers (32-bit data format).
 constexpr int kBufferFlags = 0x00020000;
+// Accumulator start value: the MFMAs then produce u = 2^31 + sum (mod 2^32),
+// the biased form the reduction reads (|sum| < 2^31).
+constexpr int kAccBias = static_cast<int>(0x80000000u);
 
-template <int BK>
-struct Tile {
-  static constexpr int kBufA = kBM * BK;              // A stage: 256 rows x BK bytes
-  static constexpr int kBufB = kBN * BK;              // B stage: BK k-rows x 256 bytes
+// Tile configuration: each of the 4 waves (a 2 x 2 grid) owns WM x WN blocks
+// of 32 x 32 outputs, so a workgroup tile is (64 WM) x (64 WN). K steps are 64
+// bytes through 4 LDS stages.
+template <int WM, int WN>
+struct Cfg {
+  static constexpr int kWM = WM, kWN = WN;
+  static constexpr int BM = 64 * WM, BN = 64 * WN, BK = 64;
+  static constexpr int kBufA = BM * BK;               // A stage: BM rows x 64 bytes
+  static constexpr int kBufB = BK * BN;               // B stage: 64 k-rows x BN bytes
   static constexpr int kStage = kBufA + kBufB;
   static constexpr int kStages = 4;
-  static constexpr int kLds = kStages * kStage;       // 128 KB of the 160 KB LDS
-  static constexpr int kDma = kBufA / 1024 / 4;       // 1 KB DMA blocks per wave, per operand
+  static constexpr int kLds = kStages * kStage;
+  static constexpr int kDmaA = kBufA / 4096;          // 1 KB DMA blocks per wave (4 waves)
+  static constexpr int kDmaB = kBufB / 4096;
+  static constexpr int kChunksB = BN / 16;            // 16-byte chunks per B stage row
+  static constexpr int kRowsPerBlockB = 1024 / BN;    // k rows per 1 KB B block
+  static constexpr int kEpiRow = 32 * WN;             // bytes of one wave's output row
+  static constexpr int kEpiChunks = kEpiRow / 16;
+  static constexpr int kEpiRowsPerStore = 64 / kEpiChunks;
+  static constexpr int kEpiBytes = 32 * WM * kEpiRow; // one wave's output block
+  static_assert(kDmaA >= 1 && kDmaB >= 1 && 4 * kEpiBytes <= kLds, "tile config");
 };
 
-// A stage: row-major 256 x 64 bytes. The 16-byte chunk index is XORed with
-// row bits 1-5 so the ds_read_b128 fragment loads (32 consecutive rows, one
-// chunk) are bank-conflict free for both 32-bank/8-lane and 64-bank/16-lane
+// A stage: row-major BM x 64 bytes. The 16-byte chunk index is XORed with row
+// bits 1-5 so the ds_read_b128 fragment loads (32 consecutive rows, one chunk)
+// are bank-conflict free for both 32-bank/8-lane and 64-bank/16-lane
 // servicing (exhaustive host model).
 __device__ __forceinline__ int swizzle_a(int row, int chunk) {
   return chunk ^ (((row >> 1) & 3) ^ (((row >> 3) & 1) * 3) ^ ((row >> 4) & 3));
 }
 
-// B stage: row-major 64 (k) x 256 (n) bytes, N-contiguous as in global
-// memory. The 16-byte chunk index is XORed with f(k & 7), f(x) = 2x mod 16 +
-// x / 4: a 16-lane transpose read touches 8 consecutive k rows of one chunk,
-// and f sends them to 8 (32-bank model) resp., with the neighbouring group,
-// 16 (64-bank model) distinct bank quads (exhaustive host model).
+// B stage: row-major 64 (k) x BN bytes, N-contiguous as in global memory. A
+// 16-lane transpose read touches 8 consecutive k rows of one chunk; the chunk
+// index is XORed with f(k & 7) so those rows (and, in the 64-bank model, the
+// neighbouring group's) land in distinct bank quads: f(x) = 2x mod 16 + x / 4
+// for 16-chunk rows, f(x) = x for 8-chunk rows (exhaustive host model).
+template <int BN>
 __device__ __forceinline__ int swizzle_b(int k, int chunk) {
   const int x = k & 7;
-  return chunk ^ (((2 * x) & 15) | (x >> 2));
+  if constexpr (BN == 256)
+    return chunk ^ (((2 * x) & 15) | (x >> 2));
+  else
+    return chunk ^ x;
 }
-
-// Accumulator start value: the MFMAs then produce u = 2^31 + sum (mod 2^32),
-// the biased form the reduction reads (|sum| < 2^31).
-constexpr int kAccBias = static_cast<int>(0x80000000u);
 
 // For u = x + 2^31 (x an int32 sum), returns a value whose low byte is
 // (x + H) mod m, H = floor(m/2): s = dot(bytes(u), 2^(8b) mod m) + off_i32 is
@@ -142,13 +158,26 @@ __device__ __forceinline__ void dma16(uint32_t lds_addr, uint32_t voffset, v4i r
 }
 #pragma clang diagnostic pop
 
-template <int BK>
-__global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, PlaneConsts pc, uint32_t tiles_m,
-                                                                  uint32_t tiles_n, int64_t k_begin, int64_t k_stop,
-                                                                  int64_t k_slice, uint32_t accumulate) {
-  using T = Tile<BK>;
-  static_assert(BK == 64, "fragment schedule below assumes two k32 sub-steps per K step");
-  __shared__ __attribute__((aligned(16))) int8_t lds[T::kLds];
+// Scheduling slots of a K sub-step region: slot Q is one MFMA followed by up
+// to kPerSlot of the region's kReads LDS fragment reads.
+template <int kId, int Q, int kSlots, int kPerSlot, int kReads>
+__device__ __forceinline__ void sched_slots() {
+  if constexpr (Q < kSlots) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, kId);  // MFMA
+    constexpr int kLeft = kReads - Q * kPerSlot;
+    constexpr int kNum = kLeft < kPerSlot ? kLeft : kPerSlot;
+    if constexpr (kNum > 0) __builtin_amdgcn_sched_group_barrier(0x100, kNum, kId);  // DS read
+    sched_slots<kId, Q + 1, kSlots, kPerSlot, kReads>();
+  }
+}
+
+template <typename C, int kMinBlocks>
+__global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmArgs args, PlaneConsts pc,
+                                                                           uint32_t tiles_m, uint32_t tiles_n,
+                                                                           int64_t k_begin, int64_t k_stop,
+                                                                           int64_t k_slice, uint32_t accumulate) {
+  constexpr int WM = C::kWM, WN = C::kWN, BM = C::BM, BN = C::BN, BK = C::BK;
+  __shared__ __attribute__((aligned(16))) int8_t lds[C::kLds];
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
@@ -177,8 +206,8 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
 
   const int8_t* const A = args.a + static_cast<int64_t>(plane) * args.pitch_a;
   const int8_t* const B = args.b + static_cast<int64_t>(plane) * args.pitch_b;
-  const int64_t m0 = static_cast<int64_t>(tm) * kBM;
-  const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM;
+  const int64_t n0 = static_cast<int64_t>(tn) * BN;
   const int64_t kbeg = k_begin + static_cast<int64_t>(slice) * k_slice;
   const int64_t kend = min(k_stop, kbeg + k_slice);
   const int ktiles = kend > kbeg ? static_cast<int>((kend - kbeg + BK - 1) / BK) : 0;
@@ -191,20 +220,23 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
   // zero when out of range: A's covers the valid rows of this tile's row panel
   // from the current K offset on, B's the k rows [k0, min(k0 + BK, kend)).
   // B columns past the padded pitch get an offset beyond num_records.
-  const int64_t a_rows = min(static_cast<int64_t>(kBM), args.m - m0);
+  const int64_t a_rows = min(static_cast<int64_t>(BM), args.m - m0);
   const int8_t* const a_panel = A + m0 * args.lda;
-  uint32_t a_voff[T::kDma];  // wave w fills A rows 64w .. 64w+63 (4 blocks of 16 rows)
-  uint32_t b_voff[T::kDma];  // wave w fills B k rows 16w .. 16w+15 (4 blocks of 4 rows)
+  uint32_t a_voff[C::kDmaA];  // wave w fills A rows [16 kDmaA w, 16 kDmaA (w + 1))
+  uint32_t b_voff[C::kDmaB];  // wave w fills B k rows [kRowsPerBlockB kDmaB w, ...)
 #pragma unroll
-  for (int i = 0; i < T::kDma; ++i) {
-    const int blk = wave * T::kDma + i;
-    const int row = 16 * blk + (lane >> 2);
+  for (int i = 0; i < C::kDmaA; ++i) {
+    const int row = 16 * (wave * C::kDmaA + i) + (lane >> 2);
     a_voff[i] = static_cast<uint32_t>(row * args.lda + 16 * swizzle_a(row, lane & 3));
-    const int k = 4 * blk + (lane >> 4);
-    const int64_t col = n0 + 16 * swizzle_b(k, lane & 15);
+  }
+#pragma unroll
+  for (int i = 0; i < C::kDmaB; ++i) {
+    const int k = C::kRowsPerBlockB * (wave * C::kDmaB + i) + lane / C::kChunksB;
+    const int64_t col = n0 + 16 * swizzle_b<BN>(k, lane % C::kChunksB);
     b_voff[i] = static_cast<uint32_t>(k * args.ldb) + (col < args.ldb ? static_cast<uint32_t>(col) : 0x80000000u);
   }
-  const uint32_t lds_base = lds_address(lds) + static_cast<uint32_t>(wave * T::kDma * 1024);
+  const uint32_t lds_a = lds_address(lds) + static_cast<uint32_t>(wave * C::kDmaA * 1024);
+  const uint32_t lds_b = lds_address(lds) + static_cast<uint32_t>(C::kBufA + wave * C::kDmaB * 1024);
 
   struct TileSrc {
     v4i a, b;  // buffer resources of one K tile
@@ -217,17 +249,17 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
     return TileSrc{buffer_rsrc(a_panel + k0, a_bytes > 0 ? a_bytes : 0), buffer_rsrc(B + k0 * args.ldb, b_rows * args.ldb)};
   };
   auto dma_a = [&](const TileSrc& src, int stage, int i) {
-    dma16(lds_base + static_cast<uint32_t>(stage * T::kStage + 1024 * i), a_voff[i], src.a);
+    dma16(lds_a + static_cast<uint32_t>(stage * C::kStage + 1024 * i), a_voff[i], src.a);
   };
   auto dma_b = [&](const TileSrc& src, int stage, int i) {
-    dma16(lds_base + static_cast<uint32_t>(stage * T::kStage + T::kBufA + 1024 * i), b_voff[i], src.b);
+    dma16(lds_b + static_cast<uint32_t>(stage * C::kStage + 1024 * i), b_voff[i], src.b);
   };
   auto issue_tile = [&](int t, int stage) {
     const TileSrc src = tile_src(t);
 #pragma unroll
-    for (int i = 0; i < T::kDma; ++i) dma_a(src, stage, i);
+    for (int i = 0; i < C::kDmaA; ++i) dma_a(src, stage, i);
 #pragma unroll
-    for (int i = 0; i < T::kDma; ++i) dma_b(src, stage, i);
+    for (int i = 0; i < C::kDmaB; ++i) dma_b(src, stage, i);
   };
 
   // ---- fragments -------------------------------------------------------------
@@ -244,42 +276,55 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
   const int tr_j = lane & 15;
   const int tr_g = lane >> 4;
   struct Frags {
-    v4i a[4];
-    v4i b[4];
+    v4i a[WM];
+    v4i b[WN];
   };
   auto read_a = [&](int stage, int s, int i) {
-    const int r = wave_m * 128 + 32 * i + frag_row;
-    return *reinterpret_cast<const v4i*>(lds + stage * T::kStage + r * BK + swizzle_a(r, 2 * s + frag_half) * 16);
+    const int r = wave_m * (32 * WM) + 32 * i + frag_row;
+    return *reinterpret_cast<const v4i*>(lds + stage * C::kStage + r * BK + swizzle_a(r, 2 * s + frag_half) * 16);
   };
   auto read_b = [&](int stage, int s, int j) {
-    const int8_t* const sb = lds + stage * T::kStage + T::kBufA;
-    const int ncol = wave_n * 128 + 32 * j + 16 * (tr_g & 1) + 8 * (tr_j & 1);
+    const int8_t* const sb = lds + stage * C::kStage + C::kBufA;
+    const int ncol = wave_n * (32 * WN) + 32 * j + 16 * (tr_g & 1) + 8 * (tr_j & 1);
     const int k = 32 * s + 16 * (tr_g >> 1) + (tr_j >> 1);
     const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-        as_lds_v2i(sb + k * kBN + swizzle_b(k, ncol >> 4) * 16 + (ncol & 8)));
+        as_lds_v2i(sb + k * BN + swizzle_b<BN>(k, ncol >> 4) * 16 + (ncol & 8)));
     const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-        as_lds_v2i(sb + (k + 8) * kBN + swizzle_b(k + 8, ncol >> 4) * 16 + (ncol & 8)));
+        as_lds_v2i(sb + (k + 8) * BN + swizzle_b<BN>(k + 8, ncol >> 4) * 16 + (ncol & 8)));
     return v4i{lo[0], lo[1], hi[0], hi[1]};
   };
   auto read_frags = [&](int stage, int s, Frags& f) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f.a[i] = read_a(stage, s, i);
+    for (int i = 0; i < WM; ++i) f.a[i] = read_a(stage, s, i);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f.b[j] = read_b(stage, s, j);
+    for (int j = 0; j < WN; ++j) f.b[j] = read_b(stage, s, j);
   };
 
-  v16i acc[4][4];
+  v16i acc[WM][WN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v16i{} + kAccBias;
+    for (int j = 0; j < WN; ++j) acc[i][j] = v16i{} + kAccBias;
 
-  auto mfma_rows = [&](const Frags& f, int i0, int i1) {
+  auto mfma_all = [&](const Frags& f) {
 #pragma unroll
-    for (int i = i0; i < i1; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
   };
+  // Interleave a region's WM*WN MFMAs with its WM + 2*WN fragment reads: the
+  // reads go between the first three quarters of the MFMAs.
+  constexpr int kMfma = WM * WN;
+  constexpr int kReads = WM + 2 * WN;
+  constexpr int kSlots = kMfma - kMfma / 4;
+  constexpr int kPerSlot = (kReads + kSlots - 1) / kSlots;
+  auto schedule_region = [&](auto id) {
+    constexpr int kId = decltype(id)::value;
+    sched_slots<kId, 0, kSlots, kPerSlot, kReads>();
+    __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kSlots, kId);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  constexpr int kRegionLen = (WM > WN ? WM : WN) > C::kDmaA ? (WM > WN ? WM : WN) : C::kDmaA;
 
   // ---- pipeline ----------------------------------------------------------------
   // Four LDS stages. Step t computes tile t from stage t%4 while the DMA of
@@ -291,54 +336,41 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
   // later step reads, so the body has no branches. The DMAs are issued from
   // inline asm, so the compiler tracks no LDS write for them and adds no
   // waits before the fragment reads: the explicit vmcnt waits below are
-  // what orders them.
+  // what orders them. They are spread over the whole step (A DMAs in the
+  // first half, B DMAs in the second): each one holds the texture path for a
+  // while, and bunching a step's DMAs stalls MFMA issue.
+  constexpr int kDmaPerTile = C::kDmaA + C::kDmaB;
   Frags f0, f1, f0n;
   issue_tile(0, 0);
   issue_tile(1, 1);
   issue_tile(2, 2);
-  __builtin_amdgcn_s_waitcnt(kWaitVm[2 * T::kDma]);  // tiles 0 and 1 landed
+  __builtin_amdgcn_s_waitcnt(kWaitVm[kDmaPerTile]);  // tiles 0 and 1 landed
   __syncthreads();
   read_frags(0, 0, f0);
   int stage = 0;
   for (int kt = 0; kt < ktiles; ++kt) {
     const int stage1 = (stage + 1) & 3;
     const int stage3 = (stage + 3) & 3;
-    // Region 1: sub-step 0 MFMAs; the sub-step 1 fragment reads with the A
-    // DMAs of tile t+3 between them (source order fixes their placement).
-    // The DMAs are spread over the whole step: each one occupies the texture
-    // path for a while, and bunching all of a step's DMAs stalls MFMA issue.
     const TileSrc src = tile_src(kt + 3);
+    // Region 1: sub-step 0 MFMAs; sub-step 1 fragment reads and the A DMAs.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f1.a[i] = read_a(stage, 1, i);
-      f1.b[i] = read_b(stage, 1, i);
-      dma_a(src, stage3, i);
+    for (int t = 0; t < kRegionLen; ++t) {
+      if (t < WM) f1.a[t] = read_a(stage, 1, t);
+      if (t < WN) f1.b[t] = read_b(stage, 1, t);
+      if (t < C::kDmaA) dma_a(src, stage3, t);
     }
-    mfma_rows(f0, 0, 4);
+    mfma_all(f0);
+    schedule_region(std::integral_constant<int, 1>{});
+    // Region 2: sub-step 1 MFMAs; first fragments of tile t+1 and the B DMAs.
 #pragma unroll
-    for (int i = 0; i < 12; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // DS read
+    for (int t = 0; t < kRegionLen; ++t) {
+      if (t < WM) f0n.a[t] = read_a(stage1, 0, t);
+      if (t < WN) f0n.b[t] = read_b(stage1, 0, t);
+      if (t < C::kDmaB) dma_b(src, stage3, t);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    // Region 2: sub-step 1 MFMAs; first fragments of tile t+1 with the B DMAs
-    // of tile t+3 between them.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f0n.a[i] = read_a(stage1, 0, i);
-      f0n.b[i] = read_b(stage1, 0, i);
-      dma_b(src, stage3, i);
-    }
-    mfma_rows(f1, 0, 4);
-#pragma unroll
-    for (int i = 0; i < 12; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);  // DS read
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(kWaitVm[2 * T::kDma]);  // only tile t+3 outstanding
+    mfma_all(f1);
+    schedule_region(std::integral_constant<int, 2>{});
+    __builtin_amdgcn_s_waitcnt(kWaitVm[kDmaPerTile]);  // only tile t+3 outstanding
     __syncthreads();
     f0 = f0n;
     stage = stage1;
@@ -348,43 +380,43 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
   // ---- epilogue ---------------------------------------------------------------
   // acc[i][j] register 4g+e holds u = 2^31 + C[row][col] (mod 2^32; the
   // accumulators start at 2^31) with
-  //   row = m0 + wave_m*128 + 32i + (lane & 31)
-  //   col = n0 + wave_n*128 + 32j + 8g + 4*(lane >> 5) + e.
+  //   row = m0 + wave_m*32*WM + 32i + (lane & 31)
+  //   col = n0 + wave_n*32*WN + 32j + 8g + 4*(lane >> 5) + e.
   // Stores go through a buffer resource over this tile's rows, so rows >= M
   // are dropped by the range check; columns past the padded pitch (only in
   // the last tile column) get an offset beyond num_records.
   const ModulusConsts mc = pc.mod[plane];
-  const int64_t tile_rows = min(static_cast<int64_t>(kBM), args.m - m0);
+  const int64_t tile_rows = min(static_cast<int64_t>(BM), args.m - m0);
   const uint32_t lane_off =
-      static_cast<uint32_t>((wave_m * 128 + frag_row) * args.ldc + wave_n * 128 + 4 * frag_half);
+      static_cast<uint32_t>((wave_m * (32 * WM) + frag_row) * args.ldc + wave_n * (32 * WN) + 4 * frag_half);
   const uint32_t row_step = static_cast<uint32_t>(32 * args.ldc);
-  const bool full_cols = n0 + kBN <= args.ldc;
-  const int col_room = static_cast<int>(args.ldc - n0) - (wave_n * 128 + 4 * frag_half);
+  const bool full_cols = n0 + BN <= args.ldc;
+  const int col_room = static_cast<int>(args.ldc - n0) - (wave_n * (32 * WN) + 4 * frag_half);
   auto col_off = [&](uint32_t off, int col) {  // col = 32j + 8g within the lane's wave tile
     return (full_cols || col < col_room) ? off + static_cast<uint32_t>(col) : 0x80000000u;
   };
   if (args.slices <= 1) {
-    int8_t* const C = args.c + static_cast<int64_t>(plane) * args.pitch_c + m0 * args.ldc + n0;
-    const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(C, tile_rows * args.ldc - n0);
+    int8_t* const Cp = args.c + static_cast<int64_t>(plane) * args.pitch_c + m0 * args.ldc + n0;
+    const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(Cp, tile_rows * args.ldc - n0);
     const uint32_t m_comp = 256u - mc.m;
     const uint32_t half2 = mc.half * 0x00010001u;
-    // The packed residues of each wave's 128 x 128 block go through LDS (free
-    // once every wave's last DMA has landed) so the global stores are
-    // row-contiguous 16-byte chunks: 8 full 128-byte lines per instruction.
-    // LDS block layout: row-major, 128-byte rows, 16-byte chunk c of row r at
-    // chunk position c ^ ((r >> 1) & 7) (2-way bank conflicts at most).
+    // The packed residues of each wave's block go through LDS (free once
+    // every wave's last DMA has landed) so the global stores are row-contiguous
+    // 16-byte chunks. LDS block layout: row-major kEpiRow-byte rows, 16-byte
+    // chunk c of row r at chunk position c ^ ((r >> 1) & (kEpiChunks - 1)).
     __syncthreads();
-    int8_t* const ep = lds + wave * (128 * 128);
+    int8_t* const ep = lds + wave * C::kEpiBytes;
+    auto epi_swz = [](int r) { return (r >> 1) & (C::kEpiChunks - 1); };
     auto reduce = [&](auto carry) {
       constexpr bool kCarry = decltype(carry)::value;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < WM; ++i) {
         const uint32_t off = lane_off + static_cast<uint32_t>(i) * row_step;
-        uint32_t prev[4][4];
+        uint32_t prev[WN][4];
         if constexpr (kCarry) {
           // later K block: add the centered residue carried in C (|.| <= 128)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < WN; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g)
               prev[j][g] = static_cast<uint32_t>(
@@ -392,7 +424,7 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
         }
         const int r = 32 * i + frag_row;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < WN; ++j) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             uint32_t res[4];
@@ -404,7 +436,7 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
               res[e] = residue_plus_half(u, mc, m_comp);
             }
             const int c = 2 * j + (g >> 1);
-            *reinterpret_cast<uint32_t*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + 8 * (g & 1) +
+            *reinterpret_cast<uint32_t*>(ep + r * C::kEpiRow + ((c ^ epi_swz(r)) << 4) + 8 * (g & 1) +
                                          4 * frag_half) = pack_centered(res[0], res[1], res[2], res[3], half2);
           }
         }
@@ -414,56 +446,63 @@ __global__ __launch_bounds__(kThreads, 1) void plane_gemm_kernel(GemmArgs args, 
       reduce(std::true_type{});
     else
       reduce(std::false_type{});
-    // Read back row-contiguous: lane l takes chunk l & 7 of rows 8q + (l >> 3).
-    const int rrow = lane >> 3;
-    const int rchunk = lane & 7;
-    const bool chunk_ok = full_cols || wave_n * 128 + 16 * rchunk < static_cast<int>(args.ldc - n0);
+    // Read back row-contiguous: lane l takes chunk l % kEpiChunks of rows
+    // q * kEpiRowsPerStore + l / kEpiChunks.
+    const int rrow = lane / C::kEpiChunks;
+    const int rchunk = lane % C::kEpiChunks;
+    const bool chunk_ok = full_cols || wave_n * (32 * WN) + 16 * rchunk < static_cast<int>(args.ldc - n0);
     const uint32_t goff =
-        static_cast<uint32_t>((wave_m * 128 + rrow) * args.ldc + wave_n * 128 + 16 * rchunk);
+        static_cast<uint32_t>((wave_m * (32 * WM) + rrow) * args.ldc + wave_n * (32 * WN) + 16 * rchunk);
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int row = 8 * q + rrow;
-      const v4i v = *reinterpret_cast<const v4i*>(ep + row * 128 + ((rchunk ^ ((row >> 1) & 7)) << 4));
-      const uint32_t o = goff + static_cast<uint32_t>(8 * q) * static_cast<uint32_t>(args.ldc);
+    for (int q = 0; q < 32 * WM / C::kEpiRowsPerStore; ++q) {
+      const int row = C::kEpiRowsPerStore * q + rrow;
+      const v4i v = *reinterpret_cast<const v4i*>(ep + row * C::kEpiRow + ((rchunk ^ epi_swz(row)) << 4));
+      const uint32_t o = goff + static_cast<uint32_t>(C::kEpiRowsPerStore * q) * static_cast<uint32_t>(args.ldc);
       __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(chunk_ok ? o : 0x80000000u), 0, 0);
     }
   } else {
-    // Split-K: add this slice's partial sums (u - 2^31) into the int32
-    // workspace [plane][M][ldc] with buffer atomics.
-    int32_t* const W = args.splitk_ws + (static_cast<int64_t>(plane) * args.m + m0) * args.ldc + n0;
+    // Split-K: this slice's partial sums (u - 2^31) go, as plain int32 stores,
+    // to its own slot of the workspace [slice][plane][M][ldc]; the finalize
+    // kernel adds the slices. No atomics, no zeroing, deterministic.
+    int32_t* const W =
+        args.splitk_ws + ((static_cast<int64_t>(slice) * args.nplanes + plane) * args.m + m0) * args.ldc + n0;
     const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(W, 4 * (tile_rows * args.ldc - n0));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < WM; ++i) {
       const uint32_t off = lane_off + static_cast<uint32_t>(i) * row_step;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < WN; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const uint32_t o = col_off(off, 32 * j + 8 * g);
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(acc[i][j][4 * g + e] ^ kAccBias, w_rsrc,
-                                                       static_cast<int>(o == 0x80000000u ? o : 4 * (o + e)), 0, 0);
+          const v4i v = {acc[i][j][4 * g] ^ kAccBias, acc[i][j][4 * g + 1] ^ kAccBias,
+                         acc[i][j][4 * g + 2] ^ kAccBias, acc[i][j][4 * g + 3] ^ kAccBias};
+          __builtin_amdgcn_raw_buffer_store_b128(v, w_rsrc, static_cast<int>(o == 0x80000000u ? o : 4 * o), 0, 0);
         }
     }
   }
 }
 
-// Reduce the summed split-K partials to int8 residues and clear the workspace.
-// One thread per 4 consecutive cells of a plane row (ldc is a multiple of 16).
-__global__ __launch_bounds__(256) void splitk_finalize_kernel(int32_t* ws, int8_t* c, int64_t m, int64_t ldc,
-                                                              int64_t pitch_c, uint32_t nplanes, PlaneConsts pc,
-                                                              uint32_t accumulate) {
+// Sums the split-K partials of `slices` slices, adds the residue already in C
+// for later K blocks, and writes centered int8 residues. One thread per 4
+// consecutive cells of a plane row (ldc is a multiple of 16).
+__global__ __launch_bounds__(256) void splitk_finalize_kernel(const int32_t* ws, int8_t* c, int64_t m, int64_t ldc,
+                                                              int64_t pitch_c, uint32_t nplanes, uint32_t slices,
+                                                              PlaneConsts pc, uint32_t accumulate) {
   const int64_t words_per_plane = m * ldc / 4;
   const int64_t total = words_per_plane * nplanes;
+  const int64_t slice_stride = static_cast<int64_t>(nplanes) * m * ldc;  // int32 elements
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < total;
        w += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const uint32_t plane = static_cast<uint32_t>(w / words_per_plane);
     const int64_t in_plane = w - static_cast<int64_t>(plane) * words_per_plane;
     const ModulusConsts mc = pc.mod[plane];
-    v4i* const src = reinterpret_cast<v4i*>(ws + static_cast<int64_t>(plane) * m * ldc) + in_plane;
-    const v4i v = *src;
-    *src = v4i{0, 0, 0, 0};
+    const v4i* src = reinterpret_cast<const v4i*>(ws + static_cast<int64_t>(plane) * m * ldc) + in_plane;
+    v4i sum = *src;
+    for (uint32_t s = 1; s < slices; ++s) {
+      src += slice_stride / 4;
+      sum += *src;
+    }
     const int64_t elem = in_plane * 4;
     const int64_t row = elem / ldc;
     const int64_t col = elem - row * ldc;
@@ -472,7 +511,7 @@ __global__ __launch_bounds__(256) void splitk_finalize_kernel(int32_t* ws, int8_
     uint32_t r[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t u = (static_cast<uint32_t>(v[e]) ^ 0x80000000u) +
+      const uint32_t u = (static_cast<uint32_t>(sum[e]) ^ 0x80000000u) +
                          static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev >> (8 * e))));
       r[e] = residue_plus_half(u, mc, 256u - mc.m);
     }
@@ -486,46 +525,57 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* dst, uint64_t
     dst[w] = 0u;
 }
 
-constexpr int kGemmBK = 64;
 constexpr int64_t kSplitMaxLd = int64_t{1} << 21;
+using CfgLarge = Cfg<4, 4>;  // 256 x 256 tiles, one workgroup per CU (all 512 registers per lane)
+using CfgSmall = Cfg<2, 2>;  // 128 x 128 tiles, two workgroups per CU
 
 bool gemm_shape_ok(const GemmArgs& a) {
   if (a.m <= 0 || a.n <= 0 || a.k <= 0) return false;
   if (a.nplanes == 0 || a.nplanes > kMaxPrefix) return false;
   if (a.lda % 16 || a.ldb % 16 || a.ldc % 16) return false;
   if (a.lda < a.k || a.ldb < a.n || a.ldc < a.n) return false;
-  // 32-bit buffer offsets: a 256-row panel and a BK-row slab must stay below 2^31
+  // 32-bit buffer offsets: a 256-row panel and a 64-row slab must stay below 2^31
   if (a.lda >= (int64_t{1} << 23) || a.ldb >= (int64_t{1} << 23)) return false;
   if (a.ldc != a.ldb) return false;  // C columns == B columns: same padded pitch
   if (a.pitch_a < a.m * a.lda || a.pitch_b < a.k * a.ldb || a.pitch_c < a.m * a.ldc) return false;
   if (!a.a || !a.b || !a.c) return false;
   if (a.slices == 0) return false;
   if (a.slices > 1 && !a.splitk_ws) return false;
-  // split-K workspace offsets are byte offsets of int32 cells in a 256-row tile
+  // split-K workspace offsets are byte offsets of int32 cells in one tile
   if (a.slices > 1 && a.ldc >= kSplitMaxLd) return false;
   return true;
 }
 
+template <typename Cf>
+int64_t tile_count(int64_t m, int64_t n, uint32_t nplanes) {
+  return ((m + Cf::BM - 1) / Cf::BM) * ((n + Cf::BN - 1) / Cf::BN) * static_cast<int64_t>(nplanes);
+}
+
 }  // namespace
 
-uint32_t choose_splitk_slices(int64_t m, int64_t n, int64_t k, uint32_t nplanes) {
-  // Enough workgroups to cover the 256 CUs at least twice; slices of at least
-  // 2048 K so each slice still runs a long MFMA main loop.
-  const int64_t tiles = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN) * static_cast<int64_t>(nplanes);
-  const int64_t target = 512;
-  if (tiles >= target / 2 || k < 4096 || padded_ld(n) >= kSplitMaxLd) return 1;
-  int64_t slices = (target + tiles - 1) / tiles;
-  const int64_t max_by_k = k / 2048;
-  if (slices > max_by_k) slices = max_by_k;
+GemmShape choose_gemm_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes) {
+  // 256 x 256 tiles when they already give every CU at least one; otherwise
+  // 128 x 128 tiles (two per CU), and split K when even those leave the chip
+  // under-filled: slices of at least 1024 K until ~512 workgroups.
+  const int64_t kblock = k < kSafeKBlock ? k : kSafeKBlock;
+  if (tile_count<CfgLarge>(m, n, nplanes) >= 256) return GemmShape{256, 1};
+  const int64_t tiles = tile_count<CfgSmall>(m, n, nplanes);
+  if (tiles >= 256 || kblock < 2048 || padded_ld(n) >= kSplitMaxLd) return GemmShape{128, 1};
+  int64_t slices = (512 + tiles - 1) / tiles;
+  if (slices > kblock / 1024) slices = kblock / 1024;
+  if (slices > 64) slices = 64;
   if (slices < 1) slices = 1;
-  if (slices > 256) slices = 256;
-  return static_cast<uint32_t>(slices);
+  return GemmShape{128, static_cast<uint32_t>(slices)};
+}
+
+uint32_t choose_splitk_slices(int64_t m, int64_t n, int64_t k, uint32_t nplanes) {
+  return choose_gemm_shape(m, n, k, nplanes).slices;
 }
 
 uint64_t splitk_workspace_bytes(int64_t m, int64_t n, int64_t k, uint32_t nplanes) {
-  if (choose_splitk_slices(m, n, k, nplanes) <= 1) return 0;
-  const int64_t ldc = padded_ld(n);
-  return static_cast<uint64_t>(nplanes) * static_cast<uint64_t>(m) * static_cast<uint64_t>(ldc) * 4u;
+  const uint32_t slices = choose_splitk_slices(m, n, k, nplanes);
+  if (slices <= 1) return 0;
+  return static_cast<uint64_t>(slices) * nplanes * static_cast<uint64_t>(m) * static_cast<uint64_t>(padded_ld(n)) * 4u;
 }
 
 hipError_t launch_zero_words(uint32_t* dst, uint64_t words, hipStream_t stream) {
@@ -537,10 +587,12 @@ hipError_t launch_zero_words(uint32_t* dst, uint64_t words, hipStream_t stream) 
   return hipGetLastError();
 }
 
-hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream) {
-  if (!gemm_shape_ok(args)) return hipErrorInvalidValue;
-  const uint32_t tiles_m = static_cast<uint32_t>((args.m + kBM - 1) / kBM);
-  const uint32_t tiles_n = static_cast<uint32_t>((args.ldc + kBN - 1) / kBN);
+namespace {
+
+template <typename Cf, int kMinBlocks>
+hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream) {
+  const uint32_t tiles_m = static_cast<uint32_t>((args.m + Cf::BM - 1) / Cf::BM);
+  const uint32_t tiles_n = static_cast<uint32_t>((args.ldc + Cf::BN - 1) / Cf::BN);
   const uint64_t words = static_cast<uint64_t>(args.nplanes) * args.m * args.ldc / 4;
   // K is processed in int32-safe blocks of 65536; a later block adds its sum
   // to the centered residue already in C (reference cpu_reference.cpp:160-175).
@@ -551,25 +603,36 @@ hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStrea
     uint32_t used_slices = 1;
     if (args.slices > 1) {
       k_slice = (k_slice + args.slices - 1) / args.slices;
-      k_slice = (k_slice + kGemmBK - 1) / kGemmBK * kGemmBK;
+      k_slice = (k_slice + Cf::BK - 1) / Cf::BK * Cf::BK;
       used_slices = static_cast<uint32_t>((kstop - kb + k_slice - 1) / k_slice);
     }
     const uint64_t blocks = static_cast<uint64_t>(tiles_m) * tiles_n * args.nplanes * used_slices;
     if (blocks == 0 || blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(plane_gemm_kernel<kGemmBK>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream,
-                       args, consts, tiles_m, tiles_n, kb, kstop, k_slice, accumulate);
+    hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                       stream, args, consts, tiles_m, tiles_n, kb, kstop, k_slice, accumulate);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     if (args.slices > 1) {
       const uint64_t fblocks = (words + 255) / 256;
       const unsigned grid = static_cast<unsigned>(fblocks < 8192 ? fblocks : 8192);
       hipLaunchKernelGGL(splitk_finalize_kernel, dim3(grid), dim3(256), 0, stream, args.splitk_ws, args.c, args.m,
-                         args.ldc, args.pitch_c, args.nplanes, consts, accumulate);
+                         args.ldc, args.pitch_c, args.nplanes, used_slices, consts, accumulate);
       err = hipGetLastError();
       if (err != hipSuccess) return err;
     }
   }
   return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream) {
+  if (!gemm_shape_ok(args)) return hipErrorInvalidValue;
+  const GemmShape shape = choose_gemm_shape(args.m, args.n, args.k, args.nplanes);
+  // the workspace was sized for the plan's slice count: never use more
+  if (args.slices > 1 && args.slices != shape.slices) return hipErrorInvalidValue;
+  if (shape.tile == 256) return launch_gemm_cfg<CfgLarge, 1>(args, consts, stream);
+  return launch_gemm_cfg<CfgSmall, 2>(args, consts, stream);
 }
 
 }  // namespace rns8x

@@ -61,9 +61,17 @@ struct GemmArgs {
   uint32_t slices;
 };
 hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream);
+// Tile edge (256 or 128) and K slices the launcher uses for this shape
+// (k is the K of one launch block, at most 65536).
+struct GemmShape {
+  int tile;
+  uint32_t slices;
+};
+GemmShape choose_gemm_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes);
 // Number of K slices the launcher would pick for this shape (1 = no split).
 uint32_t choose_splitk_slices(int64_t m, int64_t n, int64_t k, uint32_t nplanes);
-// Bytes of int32 split-K workspace needed for this shape (0 when slices == 1).
+// Bytes of int32 split-K workspace needed for this shape (0 when slices == 1):
+// one [plane][M][ldc] int32 slot per slice.
 uint64_t splitk_workspace_bytes(int64_t m, int64_t n, int64_t k, uint32_t nplanes);
 
 // ---- export ------------------------------------------------------------------
