@@ -5,16 +5,21 @@
 // ring GEMM with int32 accumulation reduced at least every 65536 K).
 //
 // Work decomposition
-//   * workgroup = 256 threads (4 wave64s) owning an output tile of one plane
-//     (and one K slice when split-K is on); waves form a 2x2 grid. Two tile
-//     configurations: 256x256 (128x128 per wave, 16 MFMA accumulators, one
-//     workgroup per CU) for large outputs and 128x128 (64x64 per wave, two
-//     workgroups per CU) when 256x256 tiles would leave CUs idle.
+//   * unit = one output tile of one plane (and one K slice when split-K is
+//     on). A persistent grid of workgroups (one per resident slot, a
+//     multiple of 8) walks the unit list, each XCD a contiguous share, so the
+//     DMA stream runs on across unit boundaries.
+//   * workgroup = 256 threads (4 wave64s); waves form a 2x2 grid over the
+//     tile. Two tile configurations: 256x256 (128x128 per wave, 16 MFMA
+//     accumulators, one workgroup per CU) for large outputs and 128x128
+//     (64x64 per wave, two workgroups per CU) when 256x256 tiles would leave
+//     CUs idle.
 //   * K is consumed in BK = 64 byte steps through a 4-stage LDS ring. Both
 //     operands go global -> LDS by buffer-load DMA (no VGPR staging): A tiles
 //     (BM x 64, K-contiguous rows) and B tiles (64 x BN, N-contiguous rows,
-//     the layout they have in HBM). The DMA of step t+3 is in flight while
-//     step t computes; one barrier per step.
+//     the layout they have in HBM). The DMA three K steps ahead is in flight
+//     while a step computes, also across the epilogue into the next unit;
+//     one barrier per step.
 //   * A fragments are ds_read_b128 of 16 K-contiguous bytes; B fragments are
 //     gathered K-contiguous from the N-contiguous stage by ds_read_b64_tr_b8
 //     (LDS transpose read), so no transpose runs on the VALU.
@@ -29,8 +34,9 @@
 //     as consecutive launches whose epilogues add the residue already in C.
 //   * Epilogue: accumulators start at 2^31, so each holds the biased sum the
 //     reduction reads; reduction is a byte dot product plus a 24-bit
-//     reciprocal quotient (full-rate VALU only), and 4 residues are packed per
-//     dword store.
+//     reciprocal quotient (full-rate VALU only); 4 residues are packed per
+//     dword and staged through a per-wave LDS region (outside the stage
+//     ring) into row-contiguous 16-byte stores.
 //   * Split-K (tall-skinny K, 128x128 tiles): each slice stores its int32
 //     partial tile to its own workspace slot; a finalize kernel adds the
 //     slices, reduces to int8 and writes C (deterministic, no atomics).
@@ -89,7 +95,12 @@ struct Cfg {
   static constexpr int kEpiChunks = kEpiRow / 16;
   static constexpr int kEpiRowsPerStore = 64 / kEpiChunks;
   static constexpr int kEpiBytes = 32 * WM * kEpiRow; // one wave's output block
-  static_assert(kDmaA >= 1 && kDmaB >= 1 && 4 * kEpiBytes <= kLds, "tile config");
+  // The epilogue stages output through its own LDS region after the stage
+  // ring, in kEpiParts passes (two for 256x256 tiles: 4 waves x 8 KB).
+  static constexpr int kEpiParts = WM >= 4 ? 2 : 1;
+  static constexpr int kEpiLds = 4 * kEpiBytes / kEpiParts;
+  static_assert(kDmaA >= 1 && kDmaB >= 1 && WM % kEpiParts == 0, "tile config");
+  static_assert(kLds + kEpiLds <= 160 * 1024, "LDS per workgroup");
 };
 
 // A stage: row-major BM x 64 bytes. The 16-byte chunk index is XORed with row
@@ -171,13 +182,47 @@ __device__ __forceinline__ void sched_slots() {
   }
 }
 
+// Work list of one launch: units (K slice, plane, output tile) are numbered
+// slice-major, then plane, then tile; tiles run in groups of kGroupM tile
+// rows. The divisors carry host-computed reciprocals (make_div_u31).
+struct UnitMap {
+  uint32_t units;
+  uint32_t tiles_m;
+  DivU31 tiles;   // tiles per plane
+  DivU31 planes;  // planes
+  DivU31 group;   // kGroupM * tiles_n: tiles per group of tile rows
+  DivU31 rows;    // kGroupM: tile rows of a full group
+  DivU31 tail;    // tile rows of the last group (tiles_m - its first row)
+  uint32_t k_begin, k_stop, k_slice;
+};
+
+// Reads accumulator elements 4g .. 4g+3 straight from their AGPRs. The asm
+// keeps the accumulators in AGPRs through the epilogue (the compiler
+// otherwise copies all of them to VGPRs at once) and, being volatile, keeps
+// the reads in program order with the epilogue's LDS stores, so only a few
+// values are live at a time; four per statement leave the scheduler four
+// independent chains to interleave.
+struct Acc4 {
+  uint32_t v[4];
+};
+__device__ __forceinline__ Acc4 acc_read4(const v16i& acc, int g) {
+  Acc4 r;
+  asm volatile(
+      "v_accvgpr_read_b32 %0, %4\n\tv_accvgpr_read_b32 %1, %5\n\t"
+      "v_accvgpr_read_b32 %2, %6\n\tv_accvgpr_read_b32 %3, %7"
+      : "=v"(r.v[0]), "=v"(r.v[1]), "=v"(r.v[2]), "=v"(r.v[3])
+      : "a"(acc[4 * g]), "a"(acc[4 * g + 1]), "a"(acc[4 * g + 2]), "a"(acc[4 * g + 3]));
+  return r;
+}
+
+// floor(n / d) for n < 2^31 (make_div_u31).
+__device__ __forceinline__ uint32_t div_u31(uint32_t n, DivU31 v) { return __umulhi(n << 1, v.mul) >> v.shift; }
+
 template <typename C, int kMinBlocks>
-__global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmArgs args, PlaneConsts pc,
-                                                                           uint32_t tiles_m, uint32_t tiles_n,
-                                                                           int64_t k_begin, int64_t k_stop,
-                                                                           int64_t k_slice, uint32_t accumulate) {
+__global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmArgs args, PlaneConsts pc, UnitMap map,
+                                                                           uint32_t accumulate) {
   constexpr int WM = C::kWM, WN = C::kWN, BM = C::BM, BN = C::BN, BK = C::BK;
-  __shared__ __attribute__((aligned(16))) int8_t lds[C::kLds];
+  __shared__ __attribute__((aligned(16))) int8_t lds[C::kLds + C::kEpiLds];
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
@@ -185,81 +230,126 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
   const int wave_m = wave >> 1;
   const int wave_n = wave & 1;
 
-  // ---- block -> (slice, plane, tile) with XCD-aware ordering --------------
-  // Workgroups are dispatched round-robin over the 8 XCDs; renumber so each
-  // XCD receives a contiguous range of tiles, then order tiles within a
-  // plane in groups of kGroupM tile rows so that concurrently running tiles
-  // share A and B panels in that XCD's L2.
-  const uint32_t total = gridDim.x;
-  uint32_t id = blockIdx.x;
-  if ((total & 7u) == 0u) id = (id & 7u) * (total >> 3) + (id >> 3);
-  const uint32_t tiles = tiles_m * tiles_n;
-  const uint32_t pid = id % tiles;
-  const uint32_t plane_slice = id / tiles;
-  const uint32_t plane = plane_slice % args.nplanes;
-  const uint32_t slice = plane_slice / args.nplanes;
-  const uint32_t group = pid / (kGroupM * tiles_n);
-  const uint32_t first_m = group * kGroupM;
-  const uint32_t group_rows = min(tiles_m - first_m, static_cast<uint32_t>(kGroupM));
-  const uint32_t tm = first_m + (pid % (kGroupM * tiles_n)) % group_rows;
-  const uint32_t tn = (pid % (kGroupM * tiles_n)) / group_rows;
+  // ---- persistent work list ----------------------------------------------------
+  // A unit is one (K slice, plane, output tile). The grid holds a few
+  // workgroups per CU and each walks its units in order, so the DMA stream
+  // runs on across unit boundaries: the next unit's first K tiles land while
+  // the current unit's epilogue runs. Workgroups are dispatched round-robin
+  // over the 8 XCDs; with a grid that is a multiple of 8, XCD x owns the
+  // contiguous unit range [x*units/8, (x+1)*units/8), walked by its
+  // workgroups in lock step, so concurrently running tiles are neighbours and
+  // share A and B panels in that XCD's L2 (tiles are ordered within a plane
+  // in groups of kGroupM tile rows).
+  const uint32_t grid = gridDim.x;
+  uint32_t u_first, u_step, u_end;
+  if ((grid & 7u) == 0u) {
+    const uint32_t xcd = blockIdx.x & 7u;
+    u_first = static_cast<uint32_t>((static_cast<uint64_t>(xcd) * map.units) / 8) + (blockIdx.x >> 3);
+    u_end = static_cast<uint32_t>((static_cast<uint64_t>(xcd + 1) * map.units) / 8);
+    u_step = grid >> 3;
+  } else {
+    u_first = blockIdx.x;
+    u_end = map.units;
+    u_step = grid;
+  }
+  u_first = __builtin_amdgcn_readfirstlane(u_first);
+  u_end = __builtin_amdgcn_readfirstlane(u_end);
 
-  const int8_t* const A = args.a + static_cast<int64_t>(plane) * args.pitch_a;
-  const int8_t* const B = args.b + static_cast<int64_t>(plane) * args.pitch_b;
-  const int64_t m0 = static_cast<int64_t>(tm) * BM;
-  const int64_t n0 = static_cast<int64_t>(tn) * BN;
-  const int64_t kbeg = k_begin + static_cast<int64_t>(slice) * k_slice;
-  const int64_t kend = min(k_stop, kbeg + k_slice);
-  const int ktiles = kend > kbeg ? static_cast<int>((kend - kbeg + BK - 1) / BK) : 0;
+  // Units are decoded on the scalar unit (every value here is uniform) with
+  // the host's reciprocals, branch-free, so the cursor below can advance
+  // every K step without splitting the loop body.
+  struct Unit {
+    uint32_t plane, slice, m0, n0, kbeg, kend, ktiles;
+  };
+  auto decode = [&](uint32_t u) {
+    Unit U;
+    const uint32_t plane_slice = div_u31(u, map.tiles);
+    const uint32_t pid = u - plane_slice * map.tiles.d;
+    U.slice = div_u31(plane_slice, map.planes);
+    U.plane = plane_slice - U.slice * map.planes.d;
+    const uint32_t group = div_u31(pid, map.group);
+    const uint32_t first_m = group * kGroupM;
+    const uint32_t rem = pid - group * map.group.d;
+    const DivU31 rows = first_m + kGroupM <= map.tiles_m ? map.rows : map.tail;
+    const uint32_t tn = div_u31(rem, rows);
+    U.m0 = (first_m + rem - tn * rows.d) * BM;
+    U.n0 = tn * BN;
+    U.kbeg = map.k_begin + U.slice * map.k_slice;
+    U.kend = min(map.k_stop, U.kbeg + map.k_slice);
+    U.ktiles = U.kend > U.kbeg ? (U.kend - U.kbeg + BK - 1) / BK : 0u;
+    return U;
+  };
 
   // ---- global -> LDS by DMA ------------------------------------------------
   // buffer_load_dwordx4 ... lds writes lane l's 16 bytes to M0 + 16*l, so one
   // wave instruction fills a contiguous 1 KB block of a stage; each lane loads
   // the global bytes that belong in its slot (the LDS swizzle is applied on
-  // the global side). Range checks come from the buffer resources and read
-  // zero when out of range: A's covers the valid rows of this tile's row panel
-  // from the current K offset on, B's the k rows [k0, min(k0 + BK, kend)).
-  // B columns past the padded pitch get an offset beyond num_records.
-  const int64_t a_rows = min(static_cast<int64_t>(BM), args.m - m0);
-  const int8_t* const a_panel = A + m0 * args.lda;
+  // the global side). The lane offsets are fixed; the K tile moves the
+  // buffer resources. Range checks come from the resources and read zero when
+  // out of range: A's covers the valid rows of the unit's row panel from the
+  // current K offset on, B's the k rows [k0, min(k0 + BK, kend)) from column
+  // n0 on. B columns past the padded pitch read the next k row (zero past the
+  // resource): they only feed output columns >= ldc, which are never stored.
+  const uint32_t lda = static_cast<uint32_t>(args.lda), ldb = static_cast<uint32_t>(args.ldb);
+  const uint32_t m_rows = static_cast<uint32_t>(args.m);
   uint32_t a_voff[C::kDmaA];  // wave w fills A rows [16 kDmaA w, 16 kDmaA (w + 1))
   uint32_t b_voff[C::kDmaB];  // wave w fills B k rows [kRowsPerBlockB kDmaB w, ...)
 #pragma unroll
   for (int i = 0; i < C::kDmaA; ++i) {
     const int row = 16 * (wave * C::kDmaA + i) + (lane >> 2);
-    a_voff[i] = static_cast<uint32_t>(row * args.lda + 16 * swizzle_a(row, lane & 3));
+    a_voff[i] = static_cast<uint32_t>(row) * lda + static_cast<uint32_t>(16 * swizzle_a(row, lane & 3));
   }
 #pragma unroll
   for (int i = 0; i < C::kDmaB; ++i) {
     const int k = C::kRowsPerBlockB * (wave * C::kDmaB + i) + lane / C::kChunksB;
-    const int64_t col = n0 + 16 * swizzle_b<BN>(k, lane % C::kChunksB);
-    b_voff[i] = static_cast<uint32_t>(k * args.ldb) + (col < args.ldb ? static_cast<uint32_t>(col) : 0x80000000u);
+    b_voff[i] = static_cast<uint32_t>(k) * ldb + static_cast<uint32_t>(16 * swizzle_b<BN>(k, lane % C::kChunksB));
   }
   const uint32_t lds_a = lds_address(lds) + static_cast<uint32_t>(wave * C::kDmaA * 1024);
   const uint32_t lds_b = lds_address(lds) + static_cast<uint32_t>(C::kBufA + wave * C::kDmaB * 1024);
 
+  // DMA cursor: the (unit, K tile) whose DMA is issued next, three K tiles
+  // ahead of the compute position, and nsrc, its buffer resources. Past the
+  // last unit the resources are empty (every lane reads zero), which keeps
+  // the per-step DMA count and therefore the vmcnt bookkeeping uniform.
   struct TileSrc {
-    v4i a, b;  // buffer resources of one K tile
+    v4i a, b;
   };
-  auto tile_src = [&](int t) {
-    const int64_t k0 = kbeg + static_cast<int64_t>(t) * BK;
-    const int64_t a_bytes = a_rows * args.lda - k0;
-    const int64_t rows_left = kend - k0;
-    const int64_t b_rows = rows_left < BK ? (rows_left > 0 ? rows_left : 0) : BK;
-    return TileSrc{buffer_rsrc(a_panel + k0, a_bytes > 0 ? a_bytes : 0), buffer_rsrc(B + k0 * args.ldb, b_rows * args.ldb)};
+  uint32_t du = u_first, dkt = 0;
+  Unit dU = decode(u_first);
+  TileSrc nsrc;
+  auto cursor_load = [&]() {
+    const bool live = du < u_end;
+    const uint32_t k0 = dU.kbeg + dkt * BK;
+    const uint32_t a_rows = min(static_cast<uint32_t>(BM), m_rows - dU.m0);
+    const uint32_t b_rows = min(static_cast<uint32_t>(BK), dU.kend - k0);
+    const int8_t* const a_panel = args.a + static_cast<uint64_t>(dU.plane) * args.pitch_a +
+                                  static_cast<uint64_t>(dU.m0) * lda;
+    const int8_t* const b_slab = args.b + static_cast<uint64_t>(dU.plane) * args.pitch_b +
+                                 static_cast<uint64_t>(k0) * ldb + dU.n0;
+    nsrc = TileSrc{buffer_rsrc(a_panel + k0, live ? a_rows * lda - k0 : 0u),
+                   buffer_rsrc(b_slab, live ? b_rows * ldb - dU.n0 : 0u)};
   };
+  auto cursor_advance = [&]() {
+    const bool next_unit = dkt + 1 >= dU.ktiles;
+    du = next_unit ? min(du + u_step, u_end) : du;
+    dkt = next_unit ? 0u : dkt + 1;
+    const Unit nU = decode(min(du, u_end - 1));
+    if (next_unit) dU = nU;
+    cursor_load();
+  };
+  cursor_load();
   auto dma_a = [&](const TileSrc& src, int stage, int i) {
     dma16(lds_a + static_cast<uint32_t>(stage * C::kStage + 1024 * i), a_voff[i], src.a);
   };
   auto dma_b = [&](const TileSrc& src, int stage, int i) {
     dma16(lds_b + static_cast<uint32_t>(stage * C::kStage + 1024 * i), b_voff[i], src.b);
   };
-  auto issue_tile = [&](int t, int stage) {
-    const TileSrc src = tile_src(t);
+  auto issue_next = [&](int stage) {
 #pragma unroll
-    for (int i = 0; i < C::kDmaA; ++i) dma_a(src, stage, i);
+    for (int i = 0; i < C::kDmaA; ++i) dma_a(nsrc, stage, i);
 #pragma unroll
-    for (int i = 0; i < C::kDmaB; ++i) dma_b(src, stage, i);
+    for (int i = 0; i < C::kDmaB; ++i) dma_b(nsrc, stage, i);
+    cursor_advance();
   };
 
   // ---- fragments -------------------------------------------------------------
@@ -301,11 +391,12 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
   };
 
   v16i acc[WM][WN];
+  auto reset_acc = [&]() {
 #pragma unroll
-  for (int i = 0; i < WM; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < WN; ++j) acc[i][j] = v16i{} + kAccBias;
-
+      for (int j = 0; j < WN; ++j) acc[i][j] = v16i{} + kAccBias;
+  };
   auto mfma_all = [&](const Frags& f) {
 #pragma unroll
     for (int i = 0; i < WM; ++i)
@@ -318,169 +409,213 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
   constexpr int kReads = WM + 2 * WN;
   constexpr int kSlots = kMfma - kMfma / 4;
   constexpr int kPerSlot = (kReads + kSlots - 1) / kSlots;
+  // The MFMA builtins carry no ordering of their own, so instruction
+  // selection may place some of a region's MFMAs after its sched_barrier; an
+  // empty asm statement that takes every accumulator (and is ordered before
+  // the barrier) keeps them all inside the region.
   auto schedule_region = [&](auto id) {
     constexpr int kId = decltype(id)::value;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j) asm volatile("" ::"a"(acc[i][j]));
     sched_slots<kId, 0, kSlots, kPerSlot, kReads>();
     __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kSlots, kId);
     __builtin_amdgcn_sched_barrier(0);
   };
   constexpr int kRegionLen = (WM > WN ? WM : WN) > C::kDmaA ? (WM > WN ? WM : WN) : C::kDmaA;
 
-  // ---- pipeline ----------------------------------------------------------------
-  // Four LDS stages. Step t computes tile t from stage t%4 while the DMA of
-  // tile t+3 into stage (t+3)%4 (last read in step t-1) is in flight and the
-  // first fragments of tile t+1 are prefetched. Before the barrier that ends
-  // step t each wave waits until only its tile t+3 DMAs are outstanding, so
-  // the barrier publishes tile t+2 (first read in step t+1) and retires every
-  // read of stage t%4. Past the end of K the DMAs read zeros into stages no
-  // later step reads, so the body has no branches. The DMAs are issued from
-  // inline asm, so the compiler tracks no LDS write for them and adds no
-  // waits before the fragment reads: the explicit vmcnt waits below are
-  // what orders them. They are spread over the whole step (A DMAs in the
-  // first half, B DMAs in the second): each one holds the texture path for a
-  // while, and bunching a step's DMAs stalls MFMA issue.
-  constexpr int kDmaPerTile = C::kDmaA + C::kDmaB;
-  Frags f0, f1, f0n;
-  issue_tile(0, 0);
-  issue_tile(1, 1);
-  issue_tile(2, 2);
-  __builtin_amdgcn_s_waitcnt(kWaitVm[kDmaPerTile]);  // tiles 0 and 1 landed
-  __syncthreads();
-  read_frags(0, 0, f0);
-  int stage = 0;
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int stage1 = (stage + 1) & 3;
-    const int stage3 = (stage + 3) & 3;
-    const TileSrc src = tile_src(kt + 3);
-    // Region 1: sub-step 0 MFMAs; sub-step 1 fragment reads and the A DMAs.
-#pragma unroll
-    for (int t = 0; t < kRegionLen; ++t) {
-      if (t < WM) f1.a[t] = read_a(stage, 1, t);
-      if (t < WN) f1.b[t] = read_b(stage, 1, t);
-      if (t < C::kDmaA) dma_a(src, stage3, t);
-    }
-    mfma_all(f0);
-    schedule_region(std::integral_constant<int, 1>{});
-    // Region 2: sub-step 1 MFMAs; first fragments of tile t+1 and the B DMAs.
-#pragma unroll
-    for (int t = 0; t < kRegionLen; ++t) {
-      if (t < WM) f0n.a[t] = read_a(stage1, 0, t);
-      if (t < WN) f0n.b[t] = read_b(stage1, 0, t);
-      if (t < C::kDmaB) dma_b(src, stage3, t);
-    }
-    mfma_all(f1);
-    schedule_region(std::integral_constant<int, 2>{});
-    __builtin_amdgcn_s_waitcnt(kWaitVm[kDmaPerTile]);  // only tile t+3 outstanding
-    __syncthreads();
-    f0 = f0n;
-    stage = stage1;
-  }
-  __builtin_amdgcn_s_waitcnt(kWaitVm[0]);  // no DMA outlives the workgroup's LDS
-
   // ---- epilogue ---------------------------------------------------------------
   // acc[i][j] register 4g+e holds u = 2^31 + C[row][col] (mod 2^32; the
   // accumulators start at 2^31) with
   //   row = m0 + wave_m*32*WM + 32i + (lane & 31)
   //   col = n0 + wave_n*32*WN + 32j + 8g + 4*(lane >> 5) + e.
-  // Stores go through a buffer resource over this tile's rows, so rows >= M
-  // are dropped by the range check; columns past the padded pitch (only in
-  // the last tile column) get an offset beyond num_records.
-  const ModulusConsts mc = pc.mod[plane];
-  const int64_t tile_rows = min(static_cast<int64_t>(BM), args.m - m0);
-  const uint32_t lane_off =
-      static_cast<uint32_t>((wave_m * (32 * WM) + frag_row) * args.ldc + wave_n * (32 * WN) + 4 * frag_half);
-  const uint32_t row_step = static_cast<uint32_t>(32 * args.ldc);
-  const bool full_cols = n0 + BN <= args.ldc;
-  const int col_room = static_cast<int>(args.ldc - n0) - (wave_n * (32 * WN) + 4 * frag_half);
-  auto col_off = [&](uint32_t off, int col) {  // col = 32j + 8g within the lane's wave tile
-    return (full_cols || col < col_room) ? off + static_cast<uint32_t>(col) : 0x80000000u;
-  };
-  if (args.slices <= 1) {
-    int8_t* const Cp = args.c + static_cast<int64_t>(plane) * args.pitch_c + m0 * args.ldc + n0;
-    const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(Cp, tile_rows * args.ldc - n0);
-    const uint32_t m_comp = 256u - mc.m;
-    const uint32_t half2 = mc.half * 0x00010001u;
-    // The packed residues of each wave's block go through LDS (free once
-    // every wave's last DMA has landed) so the global stores are row-contiguous
-    // 16-byte chunks. LDS block layout: row-major kEpiRow-byte rows, 16-byte
-    // chunk c of row r at chunk position c ^ ((r >> 1) & (kEpiChunks - 1)).
-    __syncthreads();
-    int8_t* const ep = lds + wave * C::kEpiBytes;
-    auto epi_swz = [](int r) { return (r >> 1) & (C::kEpiChunks - 1); };
-    auto reduce = [&](auto carry) {
-      constexpr bool kCarry = decltype(carry)::value;
+  // Stores go through a buffer resource over the unit's tile rows, so rows
+  // >= M are dropped by the range check; columns past the padded pitch (only
+  // in the last tile column) get an offset beyond num_records.
+  auto epilogue = [&](const Unit& U) {
+    // The accumulator reads below are asm, so the compiler inserts no wait
+    // states after the last MFMA for them: 24 here cover the longest
+    // MFMA-write to v_accvgpr_read dependency.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    const ModulusConsts mc = pc.mod[U.plane];
+    const int64_t tile_rows = min(static_cast<int64_t>(BM), args.m - U.m0);
+    const uint32_t lane_off =
+        static_cast<uint32_t>((wave_m * (32 * WM) + frag_row) * args.ldc + wave_n * (32 * WN) + 4 * frag_half);
+    const uint32_t row_step = static_cast<uint32_t>(32 * args.ldc);
+    const bool full_cols = U.n0 + BN <= args.ldc;
+    const int col_room = static_cast<int>(args.ldc - U.n0) - (wave_n * (32 * WN) + 4 * frag_half);
+    auto col_off = [&](uint32_t off, int col) {  // col = 32j + 8g within the lane's wave tile
+      return (full_cols || col < col_room) ? off + static_cast<uint32_t>(col) : 0x80000000u;
+    };
+    if (args.slices <= 1) {
+      int8_t* const Cp = args.c + static_cast<int64_t>(U.plane) * args.pitch_c + U.m0 * args.ldc + U.n0;
+      const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(Cp, tile_rows * args.ldc - U.n0);
+      const uint32_t m_comp = 256u - mc.m;
+      const uint32_t half2 = mc.half * 0x00010001u;
+      // The packed residues go through this wave's slice of the epilogue LDS
+      // region (outside the stage ring, so the next unit's DMAs keep landing)
+      // so the global stores are row-contiguous 16-byte chunks; kEpiParts
+      // passes of WM / kEpiParts block rows each. Layout: row-major
+      // kEpiRow-byte rows, 16-byte chunk c of row r at c ^ ((r >> 1) &
+      // (kEpiChunks - 1)).
+      int8_t* const ep = lds + C::kLds + wave * (C::kEpiBytes / C::kEpiParts);
+      auto epi_swz = [](int r) { return (r >> 1) & (C::kEpiChunks - 1); };
+      const int rrow = lane / C::kEpiChunks;
+      const int rchunk = lane % C::kEpiChunks;
+      const bool chunk_ok = full_cols || wave_n * (32 * WN) + 16 * rchunk < static_cast<int>(args.ldc - U.n0);
+      constexpr int kPartRows = WM / C::kEpiParts;  // 32-row blocks per pass
+#pragma unroll
+      for (int part = 0; part < C::kEpiParts; ++part) {
+        auto reduce = [&](auto carry) {
+          constexpr bool kCarry = decltype(carry)::value;
+#pragma unroll
+          for (int ii = 0; ii < kPartRows; ++ii) {
+            const int i = part * kPartRows + ii;
+            const uint32_t off = lane_off + static_cast<uint32_t>(i) * row_step;
+            uint32_t prev[WN][4];
+            if constexpr (kCarry) {
+              // later K block: add the centered residue carried in C (|.| <= 128)
+#pragma unroll
+              for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                  prev[j][g] = static_cast<uint32_t>(
+                      __builtin_amdgcn_raw_buffer_load_b32(c_rsrc, static_cast<int>(off + 32 * j + 8 * g), 0, 0));
+            }
+            const int r = 32 * ii + frag_row;
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+#pragma unroll
+              for (int g = 0; g < 4; ++g) {
+                uint32_t res[4];
+                const Acc4 a4 = acc_read4(acc[i][j], g);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  uint32_t u = a4.v[e];
+                  if constexpr (kCarry)
+                    u += static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev[j][g] >> (8 * e))));
+                  res[e] = residue_plus_half(u, mc, m_comp);
+                }
+                const int c = 2 * j + (g >> 1);
+                *reinterpret_cast<uint32_t*>(ep + r * C::kEpiRow + ((c ^ epi_swz(r)) << 4) + 8 * (g & 1) +
+                                             4 * frag_half) = pack_centered(res[0], res[1], res[2], res[3], half2);
+              }
+            }
+          }
+        };
+        if (accumulate)
+          reduce(std::true_type{});
+        else
+          reduce(std::false_type{});
+        // Read back row-contiguous: lane l takes chunk l % kEpiChunks of rows
+        // q * kEpiRowsPerStore + l / kEpiChunks of this pass.
+        const uint32_t goff = static_cast<uint32_t>((wave_m * (32 * WM) + 32 * kPartRows * part + rrow) * args.ldc +
+                                                    wave_n * (32 * WN) + 16 * rchunk);
+#pragma unroll
+        for (int q = 0; q < 32 * kPartRows / C::kEpiRowsPerStore; ++q) {
+          const int row = C::kEpiRowsPerStore * q + rrow;
+          const v4i v = *reinterpret_cast<const v4i*>(ep + row * C::kEpiRow + ((rchunk ^ epi_swz(row)) << 4));
+          const uint32_t o = goff + static_cast<uint32_t>(C::kEpiRowsPerStore * q) * static_cast<uint32_t>(args.ldc);
+          __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(chunk_ok ? o : 0x80000000u), 0, 0);
+        }
+      }
+    } else {
+      // Split-K: this slice's partial sums (u - 2^31) go, as plain int32
+      // stores, to its own slot of the workspace [slice][plane][M][ldc]; the
+      // finalize kernel adds the slices. No atomics, no zeroing, deterministic.
+      int32_t* const W =
+          args.splitk_ws + ((static_cast<int64_t>(U.slice) * args.nplanes + U.plane) * args.m + U.m0) * args.ldc + U.n0;
+      const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(W, 4 * (tile_rows * args.ldc - U.n0));
 #pragma unroll
       for (int i = 0; i < WM; ++i) {
         const uint32_t off = lane_off + static_cast<uint32_t>(i) * row_step;
-        uint32_t prev[WN][4];
-        if constexpr (kCarry) {
-          // later K block: add the centered residue carried in C (|.| <= 128)
 #pragma unroll
-          for (int j = 0; j < WN; ++j)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-              prev[j][g] = static_cast<uint32_t>(
-                  __builtin_amdgcn_raw_buffer_load_b32(c_rsrc, static_cast<int>(off + 32 * j + 8 * g), 0, 0));
-        }
-        const int r = 32 * i + frag_row;
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
+        for (int j = 0; j < WN; ++j)
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            uint32_t res[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              uint32_t u = static_cast<uint32_t>(acc[i][j][4 * g + e]);
-              if constexpr (kCarry)
-                u += static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev[j][g] >> (8 * e))));
-              res[e] = residue_plus_half(u, mc, m_comp);
-            }
-            const int c = 2 * j + (g >> 1);
-            *reinterpret_cast<uint32_t*>(ep + r * C::kEpiRow + ((c ^ epi_swz(r)) << 4) + 8 * (g & 1) +
-                                         4 * frag_half) = pack_centered(res[0], res[1], res[2], res[3], half2);
+            const uint32_t o = col_off(off, 32 * j + 8 * g);
+            const Acc4 a4 = acc_read4(acc[i][j], g);
+            const v4i v = {static_cast<int32_t>(a4.v[0] ^ kAccBias), static_cast<int32_t>(a4.v[1] ^ kAccBias),
+                           static_cast<int32_t>(a4.v[2] ^ kAccBias), static_cast<int32_t>(a4.v[3] ^ kAccBias)};
+            __builtin_amdgcn_raw_buffer_store_b128(v, w_rsrc, static_cast<int>(o == 0x80000000u ? o : 4 * o), 0, 0);
           }
-        }
       }
-    };
-    if (accumulate)
-      reduce(std::true_type{});
-    else
-      reduce(std::false_type{});
-    // Read back row-contiguous: lane l takes chunk l % kEpiChunks of rows
-    // q * kEpiRowsPerStore + l / kEpiChunks.
-    const int rrow = lane / C::kEpiChunks;
-    const int rchunk = lane % C::kEpiChunks;
-    const bool chunk_ok = full_cols || wave_n * (32 * WN) + 16 * rchunk < static_cast<int>(args.ldc - n0);
-    const uint32_t goff =
-        static_cast<uint32_t>((wave_m * (32 * WM) + rrow) * args.ldc + wave_n * (32 * WN) + 16 * rchunk);
-#pragma unroll
-    for (int q = 0; q < 32 * WM / C::kEpiRowsPerStore; ++q) {
-      const int row = C::kEpiRowsPerStore * q + rrow;
-      const v4i v = *reinterpret_cast<const v4i*>(ep + row * C::kEpiRow + ((rchunk ^ epi_swz(row)) << 4));
-      const uint32_t o = goff + static_cast<uint32_t>(C::kEpiRowsPerStore * q) * static_cast<uint32_t>(args.ldc);
-      __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(chunk_ok ? o : 0x80000000u), 0, 0);
     }
-  } else {
-    // Split-K: this slice's partial sums (u - 2^31) go, as plain int32 stores,
-    // to its own slot of the workspace [slice][plane][M][ldc]; the finalize
-    // kernel adds the slices. No atomics, no zeroing, deterministic.
-    int32_t* const W =
-        args.splitk_ws + ((static_cast<int64_t>(slice) * args.nplanes + plane) * args.m + m0) * args.ldc + n0;
-    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(W, 4 * (tile_rows * args.ldc - n0));
+  };
+
+  // ---- pipeline ----------------------------------------------------------------
+  // Four LDS stages. Stream position s (the s-th K tile of this workgroup's
+  // work list, across unit boundaries) is computed from stage s%4 while the
+  // DMA of position s+3 into stage (s+3)%4 (last read at position s-1) is in
+  // flight and the first fragments of position s+1 are prefetched. Before the
+  // barrier that ends position s each wave waits until only its position s+3
+  // DMAs are outstanding (older VMEM operations, the previous epilogue's
+  // stores included, complete in order before them), so the barrier publishes
+  // position s+2 and retires every read of stage s%4. The DMAs are issued
+  // from inline asm, so the compiler tracks no LDS write for them and adds no
+  // waits before the fragment reads: the explicit vmcnt waits below are what
+  // orders them. They are spread over the whole step (A DMAs in the first
+  // half, B DMAs in the second): each one holds the texture path for a while,
+  // and bunching a step's DMAs stalls MFMA issue.
+  if (u_first >= u_end) return;
+  constexpr int kDmaPerTile = C::kDmaA + C::kDmaB;
+  Frags f0, f1, f0n;
+  issue_next(0);
+  issue_next(1);
+  issue_next(2);
+  __builtin_amdgcn_s_waitcnt(kWaitVm[kDmaPerTile]);  // positions 0 and 1 landed
+  __syncthreads();
+  read_frags(0, 0, f0);
+  int stage = 0;
+  for (uint32_t u = u_first; u < u_end; u += u_step) {
+    const Unit U = decode(u);
+    reset_acc();
+    // every unit has at least one K tile (the host sizes slices so)
+    uint32_t kt = 0;
+    do {
+      const int stage1 = (stage + 1) & 3;
+      const int stage3 = (stage + 3) & 3;
+      const TileSrc src = nsrc;
+      // Region 1: sub-step 0 MFMAs; sub-step 1 fragment reads and the A DMAs.
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
-      const uint32_t off = lane_off + static_cast<uint32_t>(i) * row_step;
+      for (int t = 0; t < kRegionLen; ++t) {
+        if (t < WM) f1.a[t] = read_a(stage, 1, t);
+        if (t < WN) f1.b[t] = read_b(stage, 1, t);
+        if (t < C::kDmaA) dma_a(src, stage3, t);
+      }
+      mfma_all(f0);
+      schedule_region(std::integral_constant<int, 1>{});
+      // Region 2: sub-step 1 MFMAs; first fragments of position s+1 and the B
+      // DMAs.
 #pragma unroll
-      for (int j = 0; j < WN; ++j)
+      for (int t = 0; t < kRegionLen; ++t) {
+        if (t < WM) f0n.a[t] = read_a(stage1, 0, t);
+        if (t < WN) f0n.b[t] = read_b(stage1, 0, t);
+        if (t < C::kDmaB) dma_b(src, stage3, t);
+      }
+      mfma_all(f1);
+      schedule_region(std::integral_constant<int, 2>{});
+      // the next position's fragments stay in this step (not sunk past the
+      // cursor's branch)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const uint32_t o = col_off(off, 32 * j + 8 * g);
-          const v4i v = {acc[i][j][4 * g] ^ kAccBias, acc[i][j][4 * g + 1] ^ kAccBias,
-                         acc[i][j][4 * g + 2] ^ kAccBias, acc[i][j][4 * g + 3] ^ kAccBias};
-          __builtin_amdgcn_raw_buffer_store_b128(v, w_rsrc, static_cast<int>(o == 0x80000000u ? o : 4 * o), 0, 0);
-        }
-    }
+      for (int i = 0; i < WM; ++i) asm volatile("" ::"v"(f0n.a[i]));
+#pragma unroll
+      for (int j = 0; j < WN; ++j) asm volatile("" ::"v"(f0n.b[j]));
+      cursor_advance();
+      __builtin_amdgcn_s_waitcnt(kWaitVm[kDmaPerTile]);  // only position s+3 outstanding
+      __syncthreads();
+      f0 = f0n;
+      stage = stage1;
+    } while (++kt < U.ktiles);
+    epilogue(U);
+    // The first fragments of the next unit are read again here rather than
+    // kept from the last step: holding them through the epilogue costs
+    // registers the epilogue needs. The stage stays valid: its next DMA is
+    // issued only in the next step.
+    read_frags(stage, 0, f0);
   }
+  __builtin_amdgcn_s_waitcnt(kWaitVm[0]);  // no DMA outlives the workgroup's LDS
 }
 
 // Sums the split-K partials of `slices` slices, adds the residue already in C
@@ -536,6 +671,8 @@ bool gemm_shape_ok(const GemmArgs& a) {
   if (a.lda < a.k || a.ldb < a.n || a.ldc < a.n) return false;
   // 32-bit buffer offsets: a 256-row panel and a 64-row slab must stay below 2^31
   if (a.lda >= (int64_t{1} << 23) || a.ldb >= (int64_t{1} << 23)) return false;
+  // unit decode runs in 32 bits: rows and tile origins below 2^31
+  if (a.m >= (int64_t{1} << 31)) return false;
   if (a.ldc != a.ldb) return false;  // C columns == B columns: same padded pitch
   if (a.pitch_a < a.m * a.lda || a.pitch_b < a.k * a.ldb || a.pitch_c < a.m * a.ldc) return false;
   if (!a.a || !a.b || !a.c) return false;
@@ -589,11 +726,25 @@ hipError_t launch_zero_words(uint32_t* dst, uint64_t words, hipStream_t stream) 
 
 namespace {
 
+// Compute units of the current device (cached per device id).
+int device_cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 template <typename Cf, int kMinBlocks>
 hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream) {
   const uint32_t tiles_m = static_cast<uint32_t>((args.m + Cf::BM - 1) / Cf::BM);
   const uint32_t tiles_n = static_cast<uint32_t>((args.ldc + Cf::BN - 1) / Cf::BN);
   const uint64_t words = static_cast<uint64_t>(args.nplanes) * args.m * args.ldc / 4;
+  const uint64_t slots = static_cast<uint64_t>(device_cu_count()) * kMinBlocks;
   // K is processed in int32-safe blocks of 65536; a later block adds its sum
   // to the centered residue already in C (reference cpu_reference.cpp:160-175).
   for (int64_t kb = 0; kb < args.k; kb += kSafeKBlock) {
@@ -606,16 +757,31 @@ hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipS
       k_slice = (k_slice + Cf::BK - 1) / Cf::BK * Cf::BK;
       used_slices = static_cast<uint32_t>((kstop - kb + k_slice - 1) / k_slice);
     }
-    const uint64_t blocks = static_cast<uint64_t>(tiles_m) * tiles_n * args.nplanes * used_slices;
-    if (blocks == 0 || blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                       stream, args, consts, tiles_m, tiles_n, kb, kstop, k_slice, accumulate);
+    const uint64_t units = static_cast<uint64_t>(tiles_m) * tiles_n * args.nplanes * used_slices;
+    if (units == 0 || units > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    UnitMap map{};
+    map.units = static_cast<uint32_t>(units);
+    map.tiles_m = tiles_m;
+    map.tiles = make_div_u31(tiles_m * tiles_n);
+    map.planes = make_div_u31(args.nplanes);
+    map.group = make_div_u31(static_cast<uint32_t>(kGroupM) * tiles_n);
+    map.rows = make_div_u31(kGroupM);
+    map.tail = make_div_u31(tiles_m - (tiles_m - 1) / kGroupM * kGroupM);
+    map.k_begin = static_cast<uint32_t>(kb);
+    map.k_stop = static_cast<uint32_t>(kstop);
+    map.k_slice = static_cast<uint32_t>(k_slice);
+    // persistent grid: one workgroup per resident slot, a multiple of 8 (one
+    // share per XCD) when there are at least 8 units
+    uint64_t grid = units < slots ? units : slots;
+    if (grid >= 8) grid -= grid % 8;
+    hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
+                       stream, args, consts, map, accumulate);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     if (args.slices > 1) {
       const uint64_t fblocks = (words + 255) / 256;
-      const unsigned grid = static_cast<unsigned>(fblocks < 8192 ? fblocks : 8192);
-      hipLaunchKernelGGL(splitk_finalize_kernel, dim3(grid), dim3(256), 0, stream, args.splitk_ws, args.c, args.m,
+      const unsigned fgrid = static_cast<unsigned>(fblocks < 8192 ? fblocks : 8192);
+      hipLaunchKernelGGL(splitk_finalize_kernel, dim3(fgrid), dim3(256), 0, stream, args.splitk_ws, args.c, args.m,
                          args.ldc, args.pitch_c, args.nplanes, used_slices, consts, accumulate);
       err = hipGetLastError();
       if (err != hipSuccess) return err;

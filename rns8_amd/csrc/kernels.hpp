@@ -55,8 +55,9 @@ struct GemmArgs {
   int64_t lda, ldb, ldc;  // padded pitches (bytes, multiples of 16)
   int64_t pitch_a, pitch_b, pitch_c;
   uint32_t nplanes;
-  // split-K: int32 accumulation buffer [planes][m][ldc] (zero on entry,
-  // left zero on exit) and the number of K slices; slices == 1 disables it.
+  // split-K: int32 partial sums [slices][planes][m][ldc] (each slice writes
+  // its own slot; no zeroing needed) and the number of K slices; slices == 1
+  // disables it.
   int32_t* splitk_ws;
   uint32_t slices;
 };

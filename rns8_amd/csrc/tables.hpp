@@ -70,6 +70,29 @@ constexpr Quot24 make_quot24(uint32_t m, uint32_t s_max) {
   return Quot24{a, static_cast<uint32_t>((k + m - 1) / m)};
 }
 
+// Division by a runtime divisor d >= 1 of any n < 2^31 with one 32-bit
+// high multiply (uniform values: the scalar unit's s_mul_hi_u32), no special
+// cases. With s = ceil(log2 d), mul = ceil(2^(31+s) / d) <= 2^31 for d = 2^s
+// and < 2^32 otherwise (d > 2^(s-1)); e = mul*d - 2^(31+s) < d gives
+// n*mul / 2^(31+s) = n/d + n*e / (d 2^(31+s)) with an error term below
+// n / 2^(31+s) < 2^-s <= 1/d, so floor(n / d) = floor(n*mul / 2^(31+s))
+// = hi32(2n * mul) >> s (2n < 2^32; nested floors by powers of two compose).
+struct DivU31 {
+  uint32_t d;
+  uint32_t mul;
+  uint32_t shift;
+};
+constexpr DivU31 make_div_u31(uint32_t d) {
+  if (d == 0) d = 1;
+  uint32_t s = 0;
+  while ((uint64_t{1} << s) < d) ++s;
+  const uint64_t mul = ((uint64_t{1} << (31 + s)) + d - 1) / d;
+  return DivU31{d, static_cast<uint32_t>(mul), s};
+}
+constexpr uint32_t div_u31_host(uint32_t n, DivU31 v) {
+  return static_cast<uint32_t>((static_cast<uint64_t>(n << 1) * v.mul) >> 32) >> v.shift;
+}
+
 inline ModulusConsts make_modulus_consts(uint32_t m) {
   ModulusConsts c{};
   c.m = m;

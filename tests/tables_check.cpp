@@ -12,6 +12,7 @@
 //   reduce32  int32 accumulator -> packed centered int8 (GEMM epilogue)
 //   pack64    int64 / uint64 -> centered residue (pack kernel)
 //   garner    prints Garner tables and digit vectors for a big-int check
+//   div       unit-index division: make_div_u31 over n < 2^31
 // Exit status 0 and a final "ok" line when every check passes.
 #include <cinttypes>
 #include <cstdint>
@@ -285,6 +286,49 @@ void garner_dump_all(std::integer_sequence<uint32_t, Ps...>) {
 
 void garner_dump() { garner_dump_all(std::make_integer_sequence<uint32_t, kMaxPrefix>{}); }
 
+void check_div_case(uint32_t n, uint32_t d, const DivU31& v) {
+  const uint32_t got = div_u31_host(n, v);
+  if (got != n / d) {
+    if (++failures < 10) std::printf("div %u / %u: got %u\n", n, d, got);
+  }
+}
+
+void check_div() {
+  Rng rng{777};
+  std::vector<uint32_t> divisors;
+  for (uint32_t d = 1; d <= 5000; ++d) divisors.push_back(d);
+  for (uint32_t s = 12; s < 31; ++s) {
+    divisors.push_back(1u << s);
+    divisors.push_back((1u << s) - 1);
+    divisors.push_back((1u << s) + 1);
+  }
+  divisors.push_back(0x7FFFFFFFu);
+  for (int i = 0; i < 2000; ++i) divisors.push_back(1u + static_cast<uint32_t>(rng.next() % 0x7FFFFFFFu));
+  uint64_t cases = 0;
+  for (const uint32_t d : divisors) {
+    const DivU31 v = make_div_u31(d);
+    if (v.shift > 31 || v.d != d || (d > 1 && v.mul <= 0x7FFFFFFFu)) ++failures;
+    const uint32_t top = 0x7FFFFFFFu;
+    // edges: 0, around every multiple of d near 0 and near 2^31, and random n
+    for (uint32_t n = 0; n < 64; ++n) check_div_case(n, d, v);
+    for (uint32_t q = 1; q < 64; ++q) {
+      const uint64_t base = uint64_t{q} * d;
+      if (base > top) break;
+      for (int dn = -1; dn <= 1; ++dn)
+        if (base + dn <= top) check_div_case(static_cast<uint32_t>(base + dn), d, v);
+    }
+    const uint32_t qtop = top / d;
+    for (uint32_t q = qtop > 64 ? qtop - 64 : 0; q <= qtop; ++q) {
+      const uint64_t base = uint64_t{q} * d;
+      for (int dn = -1; dn <= 1; ++dn)
+        if (base + dn <= top) check_div_case(static_cast<uint32_t>(base + dn), d, v);
+    }
+    for (int i = 0; i < 2000; ++i) check_div_case(static_cast<uint32_t>(rng.next() & top), d, v);
+    cases += 2200;
+  }
+  std::printf("div checks %" PRIu64 " divisors %zu\n", cases, divisors.size());
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -293,6 +337,7 @@ int main(int argc, char** argv) {
   else if (!std::strcmp(argv[1], "reduce32")) check_reduce32();
   else if (!std::strcmp(argv[1], "pack64")) check_pack64();
   else if (!std::strcmp(argv[1], "garner")) garner_dump();
+  else if (!std::strcmp(argv[1], "div")) check_div();
   else return 2;
   if (failures) {
     std::printf("failures %d\n", failures);

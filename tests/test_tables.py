@@ -57,6 +57,13 @@ def test_pack_reduction_int64(checker):
     _run(checker, "pack64")
 
 
+def test_unit_index_division(checker):
+    """Reciprocal division of unit indices (n < 2^31) by every divisor up to
+    5000, powers of two and their neighbours, 2^31 - 1 and random divisors."""
+    out = _run(checker, "div")
+    assert "div checks" in out
+
+
 def _limbs(vals: list[int]) -> int:
     return sum(v << (24 * i) for i, v in enumerate(vals))
 
