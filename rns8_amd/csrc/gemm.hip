@@ -467,8 +467,9 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
       constexpr int kPartRows = WM / C::kEpiParts;  // 32-row blocks per pass
 #pragma unroll
       for (int part = 0; part < C::kEpiParts; ++part) {
-        auto reduce = [&](auto carry) {
+        auto reduce = [&](auto carry, auto low_byte) {
           constexpr bool kCarry = decltype(carry)::value;
+          constexpr bool kLowByte = decltype(low_byte)::value;  // m = 256: the residue is the low byte
 #pragma unroll
           for (int ii = 0; ii < kPartRows; ++ii) {
             const int i = part * kPartRows + ii;
@@ -490,24 +491,33 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
               for (int g = 0; g < 4; ++g) {
                 uint32_t res[4];
                 const Acc4 a4 = acc_read4(acc[i][j], g);
+                uint32_t packed;
+                if constexpr (kLowByte) {
+                  // 2^31 is 0 mod 256, so u's low byte is C's, read as int8 its centered residue
+                  packed = pack_low_bytes(a4.v[0], a4.v[1], a4.v[2], a4.v[3]);
+                } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  uint32_t u = a4.v[e];
-                  if constexpr (kCarry)
-                    u += static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev[j][g] >> (8 * e))));
-                  res[e] = residue_plus_half(u, mc, m_comp);
+                  for (int e = 0; e < 4; ++e) {
+                    uint32_t u = a4.v[e];
+                    if constexpr (kCarry)
+                      u += static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev[j][g] >> (8 * e))));
+                    res[e] = residue_plus_half(u, mc, m_comp);
+                  }
+                  packed = pack_centered(res[0], res[1], res[2], res[3], half2);
                 }
                 const int c = 2 * j + (g >> 1);
                 *reinterpret_cast<uint32_t*>(ep + r * C::kEpiRow + ((c ^ epi_swz(r)) << 4) + 8 * (g & 1) +
-                                             4 * frag_half) = pack_centered(res[0], res[1], res[2], res[3], half2);
+                                             4 * frag_half) = packed;
               }
             }
           }
         };
         if (accumulate)
-          reduce(std::true_type{});
+          reduce(std::true_type{}, std::false_type{});
+        else if (mc.m == 256u)
+          reduce(std::false_type{}, std::true_type{});
         else
-          reduce(std::false_type{});
+          reduce(std::false_type{}, std::false_type{});
         // Read back row-contiguous: lane l takes chunk l % kEpiChunks of rows
         // q * kEpiRowsPerStore + l / kEpiChunks of this pass.
         const uint32_t goff = static_cast<uint32_t>((wave_m * (32 * WM) + 32 * kPartRows * part + rrow) * args.ldc +

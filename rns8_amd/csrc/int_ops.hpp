@@ -48,4 +48,9 @@ __device__ __forceinline__ uint32_t pack_centered(uint32_t r0, uint32_t r1, uint
   return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, p23), __builtin_bit_cast(uint32_t, p01), 0x06040200u);
 }
 
+// The low bytes of r0..r3 as one little-endian dword.
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3) {
+  return __builtin_amdgcn_perm(r1, r0, 0x0c0c0400u) | __builtin_amdgcn_perm(r3, r2, 0x04000c0cu);
+}
+
 }  // namespace rns8x

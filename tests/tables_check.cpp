@@ -200,6 +200,19 @@ void check_pack64() {
         if (static_cast<int8_t>(w >> (8 * e)) != centered_ref(x0 + e, m)) fail("pack u8", m, x0 + e, 0, 0);
     }
   }
+  // m = 256 planes: the kernels pack the low byte of x (pack_low_bytes), whose
+  // int8 value must be the centered residue for int64 and uint64 alike
+  for (size_t i = 0; i < xs.size(); i += 4) {
+    uint32_t lo[4];
+    for (int e = 0; e < 4; ++e) lo[e] = static_cast<uint32_t>(static_cast<uint64_t>(xs[i + e]));
+    const uint32_t w = perm(lo[1], lo[0], 0x0c0c0400u) | perm(lo[3], lo[2], 0x04000c0cu);
+    for (int e = 0; e < 4; ++e, checks += 2) {
+      const int8_t got = static_cast<int8_t>(w >> (8 * e));
+      if (got != centered_ref(xs[i + e], 256)) fail("pack i64 m=256", 256, xs[i + e], got, 0);
+      if (got != centered_ref(static_cast<__int128>(static_cast<uint64_t>(xs[i + e])), 256))
+        fail("pack u64 m=256", 256, xs[i + e], got, 0);
+    }
+  }
   std::printf("pack64 checks %" PRIu64 "\n", checks);
 }
 
