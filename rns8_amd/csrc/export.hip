@@ -24,6 +24,7 @@ namespace {
 struct ExportLimits {
   uint32_t lim_pos[kWideLimbs];  // largest admissible magnitude for a non-negative result
   uint32_t lim_neg[kWideLimbs];  // largest admissible magnitude for a negative result
+  uint64_t pos64, neg64;         // the same two limits for the 64-bit kinds (neg64 <= 2^63)
   uint32_t check;                // 0: every representable value is admissible
 };
 
@@ -51,10 +52,10 @@ __device__ __forceinline__ bool limbs_le(const uint32_t (&a)[L], const uint32_t*
   return borrow == 0;
 }
 
-// One cell: centered residue bytes r_i (byte E of words[i]) -> sign and
-// magnitude d (L 24-bit limbs) of the reconstructed value.
-template <uint32_t P, int L, int E, bool Signed>
-__device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], uint32_t (&d)[L], bool& negative) {
+// One cell: centered residue bytes r_i (byte E of words[i]) -> the canonical
+// representative x in [0, prod m_i) as L 24-bit limbs.
+template <uint32_t P, int L, int E>
+__device__ __forceinline__ void reconstruct_x(const uint32_t (&words)[P], uint32_t (&x)[L]) {
   constexpr GarnerTable<P> T = make_garner_table<P>();
   static_assert(T.m[0] == 256, "digit 0 is the raw residue byte only for modulus 256");
   constexpr uint32_t W = GarnerTable<P>::kWords;
@@ -79,7 +80,9 @@ __device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], uint32_t
     }
   }
   // ---- Horner: x = (..(v_{P-1} m_{P-2} + v_{P-2}) ..) m_0 + v_0 ----
-  uint32_t x[L];
+  // Limbs are kept unmasked between steps: v_mad_u32_u24 reads only the low
+  // 24 bits of its multiplicand, and the bits above are the carry already
+  // passed on, so each limb is masked once, at the end.
 #pragma unroll
   for (int l = 0; l < L; ++l) x[l] = 0u;
   x[0] = (vp[(P - 1) / 4] >> (8 * ((P - 1) % 4))) & 0xFFu;
@@ -89,19 +92,35 @@ __device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], uint32_t
 #pragma unroll
     for (int l = 0; l < L; ++l) {
       if (static_cast<uint32_t>(l) < T.active[i]) {
-        const uint32_t t = mad_u24(x[l], T.m[i], carry);
-        x[l] = t & 0xFFFFFFu;
-        carry = t >> 24;
+        x[l] = mad_u24(x[l], T.m[i], carry);
+        carry = x[l] >> 24;
       }
     }
   }
-  // ---- sign and magnitude ----
-  if constexpr (Signed) {
-    uint32_t borrow = 0;
 #pragma unroll
-    for (int l = 0; l < L; ++l) borrow = (x[l] - T.half_ceil[l] - borrow) >> 31;
-    negative = borrow == 0;  // x >= ceil(P/2): the value is x - P
-    borrow = 0;
+  for (int l = 0; l < L; ++l) x[l] &= 0xFFFFFFu;
+}
+
+// x >= ceil(P/2): the centered value is x - P (negative).
+template <uint32_t P, int L>
+__device__ __forceinline__ bool centered_negative(const uint32_t (&x)[L]) {
+  constexpr GarnerTable<P> T = make_garner_table<P>();
+  uint32_t borrow = 0;
+#pragma unroll
+  for (int l = 0; l < L; ++l) borrow = (x[l] - T.half_ceil[l] - borrow) >> 31;
+  return borrow == 0;
+}
+
+// One cell -> sign and magnitude d (L 24-bit limbs) of the reconstructed
+// value (the wide exports).
+template <uint32_t P, int L, int E, bool Signed>
+__device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], uint32_t (&d)[L], bool& negative) {
+  constexpr GarnerTable<P> T = make_garner_table<P>();
+  uint32_t x[L];
+  reconstruct_x<P, L, E>(words, x);
+  if constexpr (Signed) {
+    negative = centered_negative<P, L>(x);
+    uint32_t borrow = 0;
 #pragma unroll
     for (int l = 0; l < L; ++l) {
       const uint32_t t = T.product[l] - x[l] - borrow;
@@ -113,6 +132,38 @@ __device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], uint32_t
 #pragma unroll
     for (int l = 0; l < L; ++l) d[l] = x[l];
   }
+}
+
+// One cell for the 64-bit kinds: the low 64 bits of the centered (Signed) or
+// canonical value v, and whether v is admissible. v is formed as a 24L-bit
+// two's complement value (x - P for a negative result); it has a 64-bit
+// representation iff its bits from 64 up repeat its sign, and then its
+// magnitude is -w or w modulo 2^64, except for v = -2^64, whose low 64 bits
+// are zero (caught by testing mag - 1 against the limit). Same decisions and
+// output bits as sign/magnitude with limbs_le.
+template <uint32_t P, int L, int E, bool Signed>
+__device__ __forceinline__ uint64_t value64(const uint32_t (&words)[P], const ExportLimits& lim, bool& ok) {
+  constexpr GarnerTable<P> T = make_garner_table<P>();
+  uint32_t x[L];
+  reconstruct_x<P, L, E>(words, x);
+  const bool neg = Signed && centered_negative<P, L>(x);
+  uint32_t v[L];
+  uint32_t borrow = 0;
+#pragma unroll
+  for (int l = 0; l < L; ++l) {
+    const uint32_t t = x[l] - (neg ? T.product[l] : 0u) - borrow;
+    borrow = t >> 31;
+    v[l] = t & 0xFFFFFFu;
+  }
+  const uint64_t w = static_cast<uint64_t>(v[0] | (v[1] << 24)) |
+                     (static_cast<uint64_t>((v[1] >> 8) | (v[2] << 16)) << 32);
+  const uint32_t ext = neg ? 0xFFFFFFu : 0u;
+  bool fits = (v[2] >> 16) == (ext & 0xFFu);
+#pragma unroll
+  for (int l = 3; l < L; ++l) fits = fits && v[l] == ext;
+  const uint64_t mag = neg ? 0ull - w : w;
+  ok = fits && (neg ? mag - 1ull < lim.neg64 : mag <= lim.pos64);
+  return w;
 }
 
 template <uint32_t P, int L, ExportKind Kind>
@@ -129,26 +180,16 @@ __global__ __launch_bounds__(256) void export_kernel(ExportArgs a, ExportLimits 
 #pragma unroll
     for (uint32_t i = 0; i < P; ++i)
       words[i] = *reinterpret_cast<const uint32_t*>(cell + static_cast<int64_t>(i) * a.pitch_c);
-    uint32_t d[4][L];
-    bool neg[4];
-    reconstruct<P, L, 0, kSigned>(words, d[0], neg[0]);
-    reconstruct<P, L, 1, kSigned>(words, d[1], neg[1]);
-    reconstruct<P, L, 2, kSigned>(words, d[2], neg[2]);
-    reconstruct<P, L, 3, kSigned>(words, d[3], neg[3]);
     const int64_t cells = a.n - c0 < 4 ? a.n - c0 : 4;
-    if (lim.check) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (e < cells && !limbs_le<L>(d[e], neg[e] ? lim.lim_neg : lim.lim_pos)) violation = true;
-    }
     if constexpr (Kind == ExportKind::I64 || Kind == ExportKind::U64) {
       uint64_t w[4];
+      bool ok[4];
+      w[0] = value64<P, L, 0, kSigned>(words, lim, ok[0]);
+      w[1] = value64<P, L, 1, kSigned>(words, lim, ok[1]);
+      w[2] = value64<P, L, 2, kSigned>(words, lim, ok[2]);
+      w[3] = value64<P, L, 3, kSigned>(words, lim, ok[3]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint64_t mag = static_cast<uint64_t>(d[e][0]) | (static_cast<uint64_t>(d[e][1]) << 24) |
-                             (static_cast<uint64_t>(d[e][2]) << 48);
-        w[e] = neg[e] ? (0ull - mag) : mag;
-      }
+      for (int e = 0; e < 4; ++e) violation |= e < cells && !ok[e];
       uint64_t* const out = static_cast<uint64_t*>(a.dst) + row * a.ld + c0;
       if (vec_store && cells == 4) {
         typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
@@ -160,6 +201,17 @@ __global__ __launch_bounds__(256) void export_kernel(ExportArgs a, ExportLimits 
           if (e < cells) out[e] = w[e];
       }
     } else {
+      uint32_t d[4][L];
+      bool neg[4];
+      reconstruct<P, L, 0, kSigned>(words, d[0], neg[0]);
+      reconstruct<P, L, 1, kSigned>(words, d[1], neg[1]);
+      reconstruct<P, L, 2, kSigned>(words, d[2], neg[2]);
+      reconstruct<P, L, 3, kSigned>(words, d[3], neg[3]);
+      if (lim.check) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (e < cells && !limbs_le<L>(d[e], neg[e] ? lim.lim_neg : lim.lim_pos)) violation = true;
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         if (e >= cells) continue;
@@ -279,13 +331,12 @@ hipError_t launch_export(const ExportArgs& a, uint32_t prefix, hipStream_t strea
       // |v| <= bound and v in int64: magnitude <= min(bound, 2^63 - 1) for
       // v >= 0 and <= min(bound, 2^63) for v < 0 (crt.cpp:113-119).
       const uint64_t two63 = 1ull << 63;
-      set_limit_u64(lim.lim_pos, a.bound < two63 - 1 ? a.bound : two63 - 1);
-      set_limit_u64(lim.lim_neg, a.bound < two63 ? a.bound : two63);
+      lim.pos64 = a.bound < two63 - 1 ? a.bound : two63 - 1;
+      lim.neg64 = a.bound < two63 ? a.bound : two63;
       break;
     }
     case ExportKind::U64:
-      set_limit_u64(lim.lim_pos, a.bound);
-      set_limit_u64(lim.lim_neg, a.bound);
+      lim.pos64 = a.bound;  // no negative results
       break;
     case ExportKind::WIDE_SIGNED:
       if (a.limbs >= 3) {

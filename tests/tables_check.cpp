@@ -13,6 +13,8 @@
 //   pack64    int64 / uint64 -> centered residue (pack kernel)
 //   garner    prints Garner tables and digit vectors for a big-int check
 //   div       unit-index division: make_div_u31 over n < 2^31
+//   export64  the int64 / uint64 export tail at every prefix around the
+//             64-bit edges, against __int128 arithmetic
 // Exit status 0 and a final "ok" line when every check passes.
 #include <cinttypes>
 #include <cstdint>
@@ -216,6 +218,35 @@ void check_pack64() {
   std::printf("pack64 checks %" PRIu64 "\n", checks);
 }
 
+// The export kernel's digits and Horner steps (reconstruct_x) for centered
+// residues r: packed digits vp and the canonical value x in 24-bit limbs.
+template <uint32_t P>
+void emulate_x(const int32_t* r, uint32_t (&vp)[kGarnerDigitWords], uint32_t (&x)[kWideLimbs]) {
+  constexpr GarnerTable<P> T = make_garner_table<P>();
+  for (uint32_t q = 0; q < kGarnerDigitWords; ++q) vp[q] = 0;
+  for (uint32_t l = 0; l < kWideLimbs; ++l) x[l] = 0;
+  // digits (digit 0: the raw residue byte, m_0 = 256)
+  vp[0] = static_cast<uint32_t>(r[0]) & 0xFFu;
+  for (uint32_t i = 1; i < P; ++i) {
+    uint32_t s = static_cast<uint32_t>(r[i] * T.inv[i] + T.bias[i]);
+    for (uint32_t q = 0; q < (i + 3) / 4; ++q) s = udot4(vp[q], T.wpack[i][q], s);
+    const uint32_t v = mad_u24(mulhi_u24(s << T.qshift[i], T.qrecip[i]), 256u - T.m[i], s) & 0xFFu;
+    vp[i / 4] |= v << (8 * (i % 4));
+  }
+  // Horner over the active limbs of each step, limbs left unmasked between
+  // steps (mad_u24 reads their low 24 bits) and masked once at the end
+  x[0] = (vp[(P - 1) / 4] >> (8 * ((P - 1) % 4))) & 0xFFu;
+  for (int i = static_cast<int>(P) - 2; i >= 0; --i) {
+    uint32_t carry = (vp[i / 4] >> (8 * (i % 4))) & 0xFFu;
+    for (uint32_t l = 0; l < T.active[i]; ++l) {
+      x[l] = mad_u24(x[l], T.m[i], carry);
+      carry = x[l] >> 24;
+    }
+    if (carry != 0) fail("horner carry out", P, i, carry, 0);
+  }
+  for (uint32_t l = 0; l < kWideLimbs; ++l) x[l] &= 0xFFFFFFu;
+}
+
 // Prints, for every prefix, the Garner tables and the export kernel's
 // reconstruction (emulated step by step from GarnerTable<P>: digits with the
 // 24-bit quotient, Horner in 24-bit limbs over the compile-time active limb
@@ -248,26 +279,8 @@ void garner_dump_p(Rng& rng) {
       r[i] = t == 0 ? -h : t == 1 ? static_cast<int32_t>(T.m[i]) - 1 - h
                                   : static_cast<int32_t>(rng.next() % T.m[i]) - h;
     }
-    // digits (digit 0: the raw residue byte, m_0 = 256)
-    vp[0] = static_cast<uint32_t>(r[0]) & 0xFFu;
-    for (uint32_t i = 1; i < P; ++i) {
-      uint32_t s = static_cast<uint32_t>(r[i] * T.inv[i] + T.bias[i]);
-      for (uint32_t q = 0; q < (i + 3) / 4; ++q) s = udot4(vp[q], T.wpack[i][q], s);
-      const uint32_t v = mad_u24(mulhi_u24(s << T.qshift[i], T.qrecip[i]), 256u - T.m[i], s) & 0xFFu;
-      vp[i / 4] |= v << (8 * (i % 4));
-    }
-    // Horner over the active limbs of each step
-    uint32_t x[kWideLimbs] = {};
-    x[0] = (vp[(P - 1) / 4] >> (8 * ((P - 1) % 4))) & 0xFFu;
-    for (int i = static_cast<int>(P) - 2; i >= 0; --i) {
-      uint32_t carry = (vp[i / 4] >> (8 * (i % 4))) & 0xFFu;
-      for (uint32_t l = 0; l < T.active[i]; ++l) {
-        const uint32_t u = mad_u24(x[l], T.m[i], carry);
-        x[l] = u & 0xFFFFFFu;
-        carry = u >> 24;
-      }
-      if (carry != 0) fail("horner carry out", P, i, carry, 0);
-    }
+    uint32_t x[kWideLimbs];
+    emulate_x<P>(r, vp, x);
     // sign and magnitude as the kernel computes them
     uint32_t borrow = 0;
     for (uint32_t l = 0; l < kWideLimbs; ++l) borrow = (x[l] - T.half_ceil[l] - borrow) >> 31;
@@ -289,6 +302,117 @@ void garner_dump_p(Rng& rng) {
     for (uint32_t l = 0; l < kWideLimbs; ++l) std::printf(" %u", x[l]);
     std::printf("\n");
   }
+}
+
+// The 64-bit export tail (value64): the low 64 bits of the centered
+// (Signed) or canonical value and its admissibility under the limits
+// pos / neg, from x in L = (P <= 9 ? 3 : 7) limbs, as the kernel computes it.
+template <uint32_t P>
+uint64_t emulate_value64(const uint32_t (&x)[kWideLimbs], bool is_signed, uint64_t pos, uint64_t neg_lim, bool& ok) {
+  constexpr GarnerTable<P> T = make_garner_table<P>();
+  constexpr int L = P <= 9 ? 3 : 7;
+  uint32_t borrow = 0;
+  for (int l = 0; l < L; ++l) borrow = (x[l] - T.half_ceil[l] - borrow) >> 31;
+  const bool neg = is_signed && borrow == 0;
+  uint32_t v[L];
+  borrow = 0;
+  for (int l = 0; l < L; ++l) {
+    const uint32_t t = x[l] - (neg ? T.product[l] : 0u) - borrow;
+    borrow = t >> 31;
+    v[l] = t & 0xFFFFFFu;
+  }
+  const uint64_t w = static_cast<uint64_t>(v[0] | (v[1] << 24)) | (static_cast<uint64_t>((v[1] >> 8) | (v[2] << 16)) << 32);
+  const uint32_t ext = neg ? 0xFFFFFFu : 0u;
+  bool fits = (v[2] >> 16) == (ext & 0xFFu);
+  for (int l = 3; l < L; ++l) fits = fits && v[l] == ext;
+  const uint64_t mag = neg ? 0ull - w : w;
+  ok = fits && (neg ? mag - 1ull < neg_lim : mag <= pos);
+  return w;
+}
+
+int32_t centered_i128(__int128 v, uint32_t m) {
+  __int128 r = v % static_cast<__int128>(m);
+  if (r < 0) r += m;
+  return static_cast<int32_t>(r >= (m + 1) / 2 ? r - m : r);
+}
+
+// Values around every 64-bit edge (0, +-2^62, +-2^63, +-2^64, +-2^65 and
+// neighbours, plus random ones) within each prefix's centered / canonical
+// range, through the emulated export for int64 and uint64 at several bounds;
+// expected results from __int128 arithmetic.
+template <uint32_t P>
+void export64_p(Rng& rng, uint64_t& checks) {
+  const GarnerConsts g = make_garner_consts(P);
+  // prod m_i in __int128 where it fits (P <= 15: < 2^120); otherwise every
+  // test value (|v| <= 2^100) is inside the range
+  bool small = P <= 15;
+  __int128 prod = 1;
+  if (small)
+    for (uint32_t i = 0; i < P; ++i) prod *= g.m[i];
+  const __int128 one = 1;
+  std::vector<__int128> base = {0, one << 62, (one << 63) - 1, one << 63, (one << 63) + 1, (one << 64) - 2,
+                                (one << 64) - 1, one << 64, (one << 64) + 1, one << 65, (one << 72) + 5, one << 100};
+  std::vector<__int128> vals;
+  for (const __int128 b : base)
+    for (int d = -2; d <= 2; ++d) {
+      vals.push_back(b + d);
+      vals.push_back(-(b + d));
+    }
+  for (int i = 0; i < 200; ++i) {
+    const int bits = static_cast<int>(rng.next() % 70);
+    __int128 v = static_cast<__int128>(rng.next() >> (64 - (bits > 63 ? 63 : bits + 1)));
+    if (bits > 63) v <<= (bits - 63);
+    vals.push_back(rng.next() & 1 ? -v : v);
+  }
+  if (small) {
+    const __int128 h = (prod + 1) / 2;  // ceil(prod / 2)
+    for (int d = 0; d <= 2; ++d) {
+      vals.push_back(h - 1 - d);
+      vals.push_back(h - prod + d);
+    }
+  }
+  const uint64_t two63 = 1ull << 63;
+  const uint64_t bounds[] = {0, 1, 1ull << 62, two63 - 1, two63, ~0ull};
+  for (const __int128 v : vals) {
+    for (int is_signed = 0; is_signed < 2; ++is_signed) {
+      // representable: centered range [h - prod, h - 1] or canonical [0, prod)
+      if (small) {
+        const __int128 h = (prod + 1) / 2;
+        if (is_signed ? (v < h - prod || v > h - 1) : (v < 0 || v >= prod)) continue;
+      } else if (v < 0 && !is_signed) {
+        continue;
+      }
+      int32_t r[kMaxPrefix];
+      for (uint32_t i = 0; i < P; ++i) r[i] = centered_i128(v, g.m[i]);
+      uint32_t vp[kGarnerDigitWords], x[kWideLimbs];
+      emulate_x<P>(r, vp, x);
+      for (const uint64_t b : bounds) {
+        const uint64_t pos = is_signed ? (b < two63 - 1 ? b : two63 - 1) : b;
+        const uint64_t neg_lim = is_signed ? (b < two63 ? b : two63) : 0;
+        bool ok = false;
+        const uint64_t w = emulate_value64<P>(x, is_signed != 0, pos, neg_lim, ok);
+        const bool want_ok = v >= 0 ? v <= static_cast<__int128>(pos) : -v <= static_cast<__int128>(neg_lim);
+        const uint64_t want_w = static_cast<uint64_t>(v);
+        ++checks;
+        if (w != want_w || ok != want_ok) {
+          if (failures < 20)
+            std::printf("export64 P=%u signed=%d v=%s%016llx%016llx bound=%llu: w %016llx ok %d, want %016llx %d\n", P,
+                        is_signed, v < 0 ? "-" : "", static_cast<unsigned long long>((v < 0 ? -v : v) >> 64),
+                        static_cast<unsigned long long>(v < 0 ? -v : v), static_cast<unsigned long long>(b),
+                        static_cast<unsigned long long>(w), ok, static_cast<unsigned long long>(want_w), want_ok);
+          ++failures;
+        }
+      }
+    }
+  }
+}
+
+template <uint32_t... Ps>
+void export64_all(std::integer_sequence<uint32_t, Ps...>) {
+  Rng rng{9090};
+  uint64_t checks = 0;
+  (export64_p<Ps + 1>(rng, checks), ...);
+  std::printf("export64 checks %" PRIu64 "\n", checks);
 }
 
 template <uint32_t... Ps>
@@ -351,6 +475,7 @@ int main(int argc, char** argv) {
   else if (!std::strcmp(argv[1], "pack64")) check_pack64();
   else if (!std::strcmp(argv[1], "garner")) garner_dump();
   else if (!std::strcmp(argv[1], "div")) check_div();
+  else if (!std::strcmp(argv[1], "export64")) export64_all(std::make_integer_sequence<uint32_t, kMaxPrefix>{});
   else return 2;
   if (failures) {
     std::printf("failures %d\n", failures);

@@ -64,6 +64,14 @@ def test_unit_index_division(checker):
     assert "div checks" in out
 
 
+def test_export64_tail_edges(checker):
+    """int64 / uint64 export tail at every prefix: values at and around 0,
+    +-2^62, +-2^63, +-2^64 (incl. -2^64, whose low 64 bits are 0), +-2^65 and
+    the ends of the centered range, bounds 0 .. 2^64 - 1, against __int128."""
+    out = _run(checker, "export64")
+    assert "export64 checks" in out
+
+
 def _limbs(vals: list[int]) -> int:
     return sum(v << (24 * i) for i, v in enumerate(vals))
 
