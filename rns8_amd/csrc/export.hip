@@ -54,8 +54,11 @@ __device__ __forceinline__ bool limbs_le(const uint32_t (&a)[L], const uint32_t*
 
 // One cell: centered residue bytes r_i (byte E of words[i]) -> the canonical
 // representative x in [0, prod m_i) as L 24-bit limbs.
+// words[i] holds the centered residue bytes of 4 cells for plane i; flipped[i]
+// is words[i] ^ 0x80808080 (each byte + 128, as unsigned bytes).
 template <uint32_t P, int L, int E>
-__device__ __forceinline__ void reconstruct_x(const uint32_t (&words)[P], uint32_t (&x)[L]) {
+__device__ __forceinline__ void reconstruct_x(const uint32_t (&words)[P], const uint32_t (&flipped)[P],
+                                              uint32_t (&x)[L]) {
   constexpr GarnerTable<P> T = make_garner_table<P>();
   static_assert(T.m[0] == 256, "digit 0 is the raw residue byte only for modulus 256");
   constexpr uint32_t W = GarnerTable<P>::kWords;
@@ -67,8 +70,9 @@ __device__ __forceinline__ void reconstruct_x(const uint32_t (&words)[P], uint32
   vp[0] = (words[0] >> (8 * E)) & 0xFFu;
 #pragma unroll
   for (uint32_t i = 1; i < P; ++i) {
-    const int32_t r = static_cast<int32_t>(static_cast<int8_t>(words[i] >> (8 * E)));
-    uint32_t s = static_cast<uint32_t>(r * T.inv[i] + T.bias[i]);
+    // (r_i + 128) * I_i + xbias_i: the flipped residue byte against I_i at
+    // byte E (the other cells' bytes meet zero weights)
+    uint32_t s = __builtin_amdgcn_udot4(flipped[i], T.inv[i] << (8 * E), T.xbias[i], false);
 #pragma unroll
     for (uint32_t q = 0; q < (i + 3) / 4; ++q) s = __builtin_amdgcn_udot4(vp[q], T.wpack[i][q], s, false);
     const uint32_t t = mod_low_byte(s, T.qshift[i], T.qrecip[i], 256u - T.m[i]);
@@ -114,10 +118,11 @@ __device__ __forceinline__ bool centered_negative(const uint32_t (&x)[L]) {
 // One cell -> sign and magnitude d (L 24-bit limbs) of the reconstructed
 // value (the wide exports).
 template <uint32_t P, int L, int E, bool Signed>
-__device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], uint32_t (&d)[L], bool& negative) {
+__device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], const uint32_t (&flipped)[P], uint32_t (&d)[L],
+                                            bool& negative) {
   constexpr GarnerTable<P> T = make_garner_table<P>();
   uint32_t x[L];
-  reconstruct_x<P, L, E>(words, x);
+  reconstruct_x<P, L, E>(words, flipped, x);
   if constexpr (Signed) {
     negative = centered_negative<P, L>(x);
     uint32_t borrow = 0;
@@ -142,10 +147,11 @@ __device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], uint32_t
 // are zero (caught by testing mag - 1 against the limit). Same decisions and
 // output bits as sign/magnitude with limbs_le.
 template <uint32_t P, int L, int E, bool Signed>
-__device__ __forceinline__ uint64_t value64(const uint32_t (&words)[P], const ExportLimits& lim, bool& ok) {
+__device__ __forceinline__ uint64_t value64(const uint32_t (&words)[P], const uint32_t (&flipped)[P],
+                                            const ExportLimits& lim, bool& ok) {
   constexpr GarnerTable<P> T = make_garner_table<P>();
   uint32_t x[L];
-  reconstruct_x<P, L, E>(words, x);
+  reconstruct_x<P, L, E>(words, flipped, x);
   const bool neg = Signed && centered_negative<P, L>(x);
   uint32_t v[L];
   uint32_t borrow = 0;
@@ -157,12 +163,15 @@ __device__ __forceinline__ uint64_t value64(const uint32_t (&words)[P], const Ex
   }
   const uint64_t w = static_cast<uint64_t>(v[0] | (v[1] << 24)) |
                      (static_cast<uint64_t>((v[1] >> 8) | (v[2] << 16)) << 32);
+  // branch-free: every term is evaluated (bitwise & / |, selects)
   const uint32_t ext = neg ? 0xFFFFFFu : 0u;
-  bool fits = (v[2] >> 16) == (ext & 0xFFu);
+  uint32_t diff = (v[2] >> 16) ^ (ext & 0xFFu);
 #pragma unroll
-  for (int l = 3; l < L; ++l) fits = fits && v[l] == ext;
+  for (int l = 3; l < L; ++l) diff |= v[l] ^ ext;
   const uint64_t mag = neg ? 0ull - w : w;
-  ok = fits && (neg ? mag - 1ull < lim.neg64 : mag <= lim.pos64);
+  const bool in_neg = mag - 1ull < lim.neg64;
+  const bool in_pos = mag <= lim.pos64;
+  ok = (diff == 0u) & (neg ? in_neg : in_pos);
   return w;
 }
 
@@ -176,20 +185,22 @@ __global__ __launch_bounds__(256) void export_kernel(ExportArgs a, ExportLimits 
   bool violation = false;
   for (int64_t row = blockIdx.y; row < a.m; row += gridDim.y) {
     const int8_t* const cell = a.c + row * a.ldc + c0;
-    uint32_t words[P];
+    uint32_t words[P], flipped[P];
 #pragma unroll
-    for (uint32_t i = 0; i < P; ++i)
+    for (uint32_t i = 0; i < P; ++i) {
       words[i] = *reinterpret_cast<const uint32_t*>(cell + static_cast<int64_t>(i) * a.pitch_c);
+      flipped[i] = words[i] ^ 0x80808080u;
+    }
     const int64_t cells = a.n - c0 < 4 ? a.n - c0 : 4;
     if constexpr (Kind == ExportKind::I64 || Kind == ExportKind::U64) {
       uint64_t w[4];
       bool ok[4];
-      w[0] = value64<P, L, 0, kSigned>(words, lim, ok[0]);
-      w[1] = value64<P, L, 1, kSigned>(words, lim, ok[1]);
-      w[2] = value64<P, L, 2, kSigned>(words, lim, ok[2]);
-      w[3] = value64<P, L, 3, kSigned>(words, lim, ok[3]);
+      w[0] = value64<P, L, 0, kSigned>(words, flipped, lim, ok[0]);
+      w[1] = value64<P, L, 1, kSigned>(words, flipped, lim, ok[1]);
+      w[2] = value64<P, L, 2, kSigned>(words, flipped, lim, ok[2]);
+      w[3] = value64<P, L, 3, kSigned>(words, flipped, lim, ok[3]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) violation |= e < cells && !ok[e];
+      for (int e = 0; e < 4; ++e) violation |= (e < cells) & !ok[e];
       uint64_t* const out = static_cast<uint64_t*>(a.dst) + row * a.ld + c0;
       if (vec_store && cells == 4) {
         typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
@@ -203,10 +214,10 @@ __global__ __launch_bounds__(256) void export_kernel(ExportArgs a, ExportLimits 
     } else {
       uint32_t d[4][L];
       bool neg[4];
-      reconstruct<P, L, 0, kSigned>(words, d[0], neg[0]);
-      reconstruct<P, L, 1, kSigned>(words, d[1], neg[1]);
-      reconstruct<P, L, 2, kSigned>(words, d[2], neg[2]);
-      reconstruct<P, L, 3, kSigned>(words, d[3], neg[3]);
+      reconstruct<P, L, 0, kSigned>(words, flipped, d[0], neg[0]);
+      reconstruct<P, L, 1, kSigned>(words, flipped, d[1], neg[1]);
+      reconstruct<P, L, 2, kSigned>(words, flipped, d[2], neg[2]);
+      reconstruct<P, L, 3, kSigned>(words, flipped, d[3], neg[3]);
       if (lim.check) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -239,7 +250,13 @@ __global__ __launch_bounds__(256) void export_kernel(ExportArgs a, ExportLimits 
       }
     }
   }
-  if (violation) atomicOr(a.status, 1u);
+  // At most one atomic per wave, and none once the flag is visible: atomics
+  // on the single status word serialize (one per thread took 0.75 ms at
+  // 4096 x 4096 when every cell was out of range).
+  const uint64_t voters = __ballot(violation);
+  if (voters != 0 && (threadIdx.x & 63u) == static_cast<uint32_t>(__ffsll(static_cast<long long>(voters)) - 1) &&
+      __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u)
+    atomicOr(a.status, 1u);
 }
 
 __global__ __launch_bounds__(256) void export_u8_kernel(ExportU8Args a, uint32_t groups_per_row) {

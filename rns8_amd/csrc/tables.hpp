@@ -247,16 +247,19 @@ constexpr GarnerConsts make_garner_consts(uint32_t prefix) {
 // ---- per-prefix Garner tables for the export kernels ----------------------------
 //
 // Digit i of the mixed-radix form is v_i = s mod m_i with
-//   s = r_i * I_i + bias_i + sum_{j<i} v_j * W[j][i]       (GarnerConsts)
-// and 0 <= s <= s_max_i (r_i >= -128, v_j <= 255), so the quotient comes from
-// the full-rate 24-bit reciprocal of make_quot24 and v_i is the low byte of
-// s + q*(256 - m_i) (congruent to s - q*m_i modulo 256, and s - q*m_i < 256).
+//   s = (r_i + 128) * I_i + xbias_i + sum_{j<i} v_j * W[j][i]
+// where r_i + 128 is the residue byte with its top bit flipped (an unsigned
+// byte, so the whole sum is one chain of v_dot4_u32_u8 with I_i placed at the
+// cell's byte) and xbias_i = (-128 I_i) mod m_i restores r_i * I_i. With
+// 0 <= s <= s_max_i the quotient comes from the full-rate 24-bit reciprocal
+// of make_quot24 and v_i is the low byte of s + q*(256 - m_i) (congruent to
+// s - q*m_i modulo 256, and s - q*m_i < 256).
 template <uint32_t P>
 struct GarnerTable {
   static constexpr uint32_t kWords = (P + 3) / 4;
   uint32_t m[P];
-  int32_t inv[P];
-  int32_t bias[P];
+  uint32_t inv[P];    // I_i
+  uint32_t xbias[P];
   uint32_t wpack[P][kWords == 0 ? 1 : kWords];
   uint32_t qshift[P];
   uint32_t qrecip[P];
@@ -272,9 +275,9 @@ constexpr GarnerTable<P> make_garner_table() {
   GarnerTable<P> t{};
   for (uint32_t i = 0; i < P; ++i) {
     t.m[i] = g.m[i];
-    t.inv[i] = static_cast<int32_t>(g.inv[i]);
-    t.bias[i] = static_cast<int32_t>(g.bias[i]);
-    uint32_t s_max = 127u * g.inv[i] + g.bias[i];
+    t.inv[i] = g.inv[i];
+    t.xbias[i] = (g.m[i] - (128u * g.inv[i]) % g.m[i]) % g.m[i];
+    uint32_t s_max = 255u * g.inv[i] + t.xbias[i];
     for (uint32_t q = 0; q < GarnerTable<P>::kWords; ++q) {
       t.wpack[i][q] = g.wpack[i][q];
       for (uint32_t b = 0; b < 4; ++b) s_max += 255u * ((g.wpack[i][q] >> (8 * b)) & 0xFFu);

@@ -228,7 +228,8 @@ void emulate_x(const int32_t* r, uint32_t (&vp)[kGarnerDigitWords], uint32_t (&x
   // digits (digit 0: the raw residue byte, m_0 = 256)
   vp[0] = static_cast<uint32_t>(r[0]) & 0xFFu;
   for (uint32_t i = 1; i < P; ++i) {
-    uint32_t s = static_cast<uint32_t>(r[i] * T.inv[i] + T.bias[i]);
+    // the residue byte with its top bit flipped (r + 128) against I_i
+    uint32_t s = udot4((static_cast<uint32_t>(r[i]) & 0xFFu) ^ 0x80u, T.inv[i], T.xbias[i]);
     for (uint32_t q = 0; q < (i + 3) / 4; ++q) s = udot4(vp[q], T.wpack[i][q], s);
     const uint32_t v = mad_u24(mulhi_u24(s << T.qshift[i], T.qrecip[i]), 256u - T.m[i], s) & 0xFFu;
     vp[i / 4] |= v << (8 * (i % 4));
