@@ -218,7 +218,7 @@ __device__ __forceinline__ Acc4 acc_read4(const v16i& acc, int g) {
 // floor(n / d) for n < 2^31 (make_div_u31).
 __device__ __forceinline__ uint32_t div_u31(uint32_t n, DivU31 v) { return __umulhi(n << 1, v.mul) >> v.shift; }
 
-template <typename C, int kMinBlocks>
+template <typename C, int kMinBlocks, bool kUniform>
 __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmArgs args, PlaneConsts pc, UnitMap map,
                                                                            uint32_t accumulate) {
   constexpr int WM = C::kWM, WN = C::kWN, BM = C::BM, BN = C::BN, BK = C::BK;
@@ -329,14 +329,24 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
     nsrc = TileSrc{buffer_rsrc(a_panel + k0, live ? a_rows * lda - k0 : 0u),
                    buffer_rsrc(b_slab, live ? b_rows * ldb - dU.n0 : 0u)};
   };
-  auto cursor_advance = [&]() {
+  // General advance: decodes the cursor's unit at every step (the prologue,
+  // and launches whose units differ in K tiles). With uniform units
+  // (kUniform) the cursor crosses exactly one unit boundary per compute unit
+  // (it advances one unit's K tiles per unit), so the unit after the
+  // cursor's is decoded once per compute unit (next_du) and the per-step
+  // advance is only selects: decoding at every step cost ~4% of the kernel.
+  Unit nU = dU;
+  auto cursor_advance = [&](auto uniform) {
+    constexpr bool kFast = decltype(uniform)::value;
     const bool next_unit = dkt + 1 >= dU.ktiles;
     du = next_unit ? min(du + u_step, u_end) : du;
     dkt = next_unit ? 0u : dkt + 1;
-    const Unit nU = decode(min(du, u_end - 1));
+    if constexpr (!kFast) nU = decode(min(du, u_end - 1));
     if (next_unit) dU = nU;
     cursor_load();
   };
+  // (past the last unit any decoded unit will do: the resources are empty)
+  auto next_du = [&]() { nU = decode(min(du + u_step, u_end - 1)); };
   cursor_load();
   auto dma_a = [&](const TileSrc& src, int stage, int i) {
     dma16(lds_a + static_cast<uint32_t>(stage * C::kStage + 1024 * i), a_voff[i], src.a);
@@ -349,7 +359,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
     for (int i = 0; i < C::kDmaA; ++i) dma_a(nsrc, stage, i);
 #pragma unroll
     for (int i = 0; i < C::kDmaB; ++i) dma_b(nsrc, stage, i);
-    cursor_advance();
+    cursor_advance(std::false_type{});
   };
 
   // ---- fragments -------------------------------------------------------------
@@ -580,6 +590,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
   int stage = 0;
   for (uint32_t u = u_first; u < u_end; u += u_step) {
     const Unit U = decode(u);
+    if constexpr (kUniform) next_du();
     reset_acc();
     // every unit has at least one K tile (the host sizes slices so)
     uint32_t kt = 0;
@@ -605,6 +616,10 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
         if (t < C::kDmaB) dma_b(src, stage3, t);
       }
       mfma_all(f1);
+      // The cursor's scalar work sits in this region, where it issues in the
+      // shadow of the MFMAs; after the region it would run with the MFMA
+      // pipe idle.
+      if constexpr (kUniform) cursor_advance(std::true_type{});
       schedule_region(std::integral_constant<int, 2>{});
       // the next position's fragments stay in this step (not sunk past the
       // cursor's branch)
@@ -612,7 +627,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
       for (int i = 0; i < WM; ++i) asm volatile("" ::"v"(f0n.a[i]));
 #pragma unroll
       for (int j = 0; j < WN; ++j) asm volatile("" ::"v"(f0n.b[j]));
-      cursor_advance();
+      if constexpr (!kUniform) cursor_advance(std::false_type{});
       __builtin_amdgcn_s_waitcnt(kWaitVm[kDmaPerTile]);  // only position s+3 outstanding
       __syncthreads();
       f0 = f0n;
@@ -784,8 +799,14 @@ hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipS
     // share per XCD) when there are at least 8 units
     uint64_t grid = units < slots ? units : slots;
     if (grid >= 8) grid -= grid % 8;
-    hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
-                       stream, args, consts, map, accumulate);
+    // every unit has the same K tiles when the slices divide the block evenly
+    const bool uniform = (kstop - kb) % k_slice == 0;
+    if (uniform)
+      hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks, true>), dim3(static_cast<unsigned>(grid)), dim3(kThreads),
+                         0, stream, args, consts, map, accumulate);
+    else
+      hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks, false>), dim3(static_cast<unsigned>(grid)), dim3(kThreads),
+                         0, stream, args, consts, map, accumulate);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     if (args.slices > 1) {
