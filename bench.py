@@ -185,7 +185,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "plane_gemm_kernel<64>",
+            "kernel": "plane_gemm_kernel<Cfg<4,4>,1,true> (256x256 tiles, persistent)",
             "achieved": round(achieved, 2),
             "peak": PEAK_INT8_TOPS,
             "unit": "TOP/s",
