@@ -62,9 +62,31 @@ _PROTOS = {
     "orc_fill": (None, [_U64, _U32, _U32, _P, _I64]),
     "orc_checksum_u64": (_U64, [_P, _I64, _I64, _I64, _U32]),
     "orc_checksum_u8": (_U64, [_P, _I64, _I64, _I64]),
+    "orc_tile_schedule": (C.c_int, [_U32, _I64, _I64, _U32, _U32, _P, _U64, _U32, _U32, _P, _P, _P, _P]),
+    "orc_gemm_rns_tiled": (None, [_P, _P, _P, _I64, _I64, _I64, _P, _U64]),
+    "orc_export_i64_tiled": (C.c_int, [_P, _I64, _I64, _U32, _U32, _U32, _P, _P, _U64, _P, _I64]),
+    "orc_export_u64_tiled": (C.c_int, [_P, _I64, _I64, _U32, _U32, _U32, _P, _P, _U64, _P, _I64]),
     "orc_num_threads": (C.c_int, []),
     "orc_set_num_threads": (None, [C.c_int]),
 }
+
+
+
+class TileEntry(C.Structure):
+    """orc_tile_entry (rns8_oracle.h)."""
+    _fields_ = [("flags", _U32), ("tile_row", _U64), ("tile_col", _U64), ("row_offset", _I64),
+                ("col_offset", _I64), ("row_extent", _I64), ("col_extent", _I64), ("required_prefix", _U32),
+                ("selected_prefix", _U32), ("group_index", _U32), ("range_bit_length", _U32)]
+
+
+class ScheduleSummary(C.Structure):
+    """orc_schedule_summary (rns8_oracle.h)."""
+    _fields_ = [("tile_rows", _U64), ("tile_cols", _U64), ("tile_count", _U64), ("min_required", _U32),
+                ("max_required", _U32), ("min_selected", _U32), ("max_selected", _U32), ("group_count", _U32),
+                ("adaptive_prefix", _U32), ("adaptive_skip", _U32), ("range_bits", _U32), ("flags", _U32),
+                ("zero_a_row_count", _U64), ("zero_b_col_count", _U64), ("zero_row_col_product_count", _U64),
+                ("collapsed", _U32)]
+
 
 _lib = None
 _ref = None
@@ -294,3 +316,53 @@ def set_threads(n: int) -> None:
 
 def threads() -> int:
     return int(lib().orc_num_threads())
+
+
+SEM_BOUNDED_I64, SEM_BOUNDED_U64 = 1, 2
+
+
+def tile_schedule(signed: bool, m: int, n: int, tile_m: int, tile_n: int, bounds, budget: int, flags: int = 0,
+                  zero_a_rows=None, zero_b_cols=None):
+    """Per-tile bounded schedule: (status, entries, summary) as ctypes records."""
+    b = np.ascontiguousarray(np.asarray(bounds, dtype=np.uint64))
+    tm = tile_m or 128
+    tn = tile_n or 128
+    count = ((m + tm - 1) // tm) * ((n + tn - 1) // tn)
+    entries = (TileEntry * max(count, 1))()
+    summary = ScheduleSummary()
+    za = None if zero_a_rows is None else np.ascontiguousarray(zero_a_rows, dtype=np.uint8)
+    zb = None if zero_b_cols is None else np.ascontiguousarray(zero_b_cols, dtype=np.uint8)
+    st = lib().orc_tile_schedule(SEM_BOUNDED_I64 if signed else SEM_BOUNDED_U64, m, n, tile_m, tile_n, _p(b), len(b),
+                                 budget, flags, None if za is None else _p(za), None if zb is None else _p(zb),
+                                 C.cast(entries, C.c_void_p), C.byref(summary))
+    return st, list(entries)[:count], summary
+
+
+def _entry_array(entries):
+    arr = (TileEntry * max(len(entries), 1))()
+    for i, e in enumerate(entries):
+        arr[i] = e
+    return arr
+
+
+def gemm_rns_tiled(Ap: np.ndarray, Bp: np.ndarray, Cp: np.ndarray, entries) -> np.ndarray:
+    """Tiled plane GEMM into a copy of Cp (planes beyond a tile's prefix keep Cp's values)."""
+    Ap = np.ascontiguousarray(Ap, dtype=np.int8)
+    Bp = np.ascontiguousarray(Bp, dtype=np.int8)
+    out = np.array(Cp, dtype=np.int8, order="C", copy=True)
+    _, m, k = Ap.shape
+    n = Bp.shape[2]
+    arr = _entry_array(entries)
+    lib().orc_gemm_rns_tiled(_p(Ap), _p(Bp), _p(out), m, n, k, C.cast(arr, C.c_void_p), len(entries))
+    return out
+
+
+def export_tiled(Cp: np.ndarray, tile_m: int, tile_n: int, entries, bounds, signed: bool):
+    Cp = np.ascontiguousarray(Cp, dtype=np.int8)
+    P, m, n = Cp.shape
+    b = np.ascontiguousarray(np.asarray(bounds, dtype=np.uint64))
+    arr = _entry_array(entries)
+    out = np.zeros((m, n), dtype=np.int64 if signed else np.uint64)
+    fn = lib().orc_export_i64_tiled if signed else lib().orc_export_u64_tiled
+    st = fn(_p(Cp), m, n, P, tile_m or 128, tile_n or 128, C.cast(arr, C.c_void_p), _p(b), len(entries), _p(out), n)
+    return st, out

@@ -512,6 +512,200 @@ int orc_export_u64(const int8_t* C, int64_t m, int64_t n, uint32_t prefix, uint6
   return st;
 }
 
+/* ---- per-tile bounded schedules ------------------------------------------- */
+
+#define ORC_TILE_ZERO_OUTPUT 0x1u         /* rns8.h:74 */
+#define ORC_TILE_ZERO_ROW_COL_PRODUCT 0x2u /* rns8.h:75 */
+#define ORC_PLAN_FORCE_FIXED_PREFIX 0x1u
+#define ORC_PLAN_ZERO_TILE_SKIPS 0x2u
+#define ORC_PLAN_ZERO_ROW_COL_SKIPS 0x4u
+
+static uint32_t u256_bit_length(const u256* v) {
+  for (int i = 3; i >= 0; --i)
+    if (v->w[i]) return (uint32_t)(64 * i + 64 - __builtin_clzll(v->w[i]));
+  return 0;
+}
+
+static int mask_has_set(const uint8_t* mask, int64_t begin, int64_t end) {
+  for (int64_t i = begin; i < end; ++i)
+    if (mask[i]) return 1;
+  return 0;
+}
+
+/* api_plan_schedule.inc:54-72 (make_tile_schedule_entry) */
+static orc_tile_entry tile_entry(int64_t m, int64_t n, uint32_t tile_m, uint32_t tile_n, uint64_t tile_cols,
+                                 uint64_t index, uint32_t required, uint32_t selected, uint32_t range_bits,
+                                 uint32_t flags) {
+  orc_tile_entry e;
+  memset(&e, 0, sizeof(e));
+  e.flags = flags;
+  e.tile_row = index / tile_cols;
+  e.tile_col = index % tile_cols;
+  e.row_offset = (int64_t)(e.tile_row * tile_m);
+  e.col_offset = (int64_t)(e.tile_col * tile_n);
+  e.row_extent = (m - e.row_offset) < (int64_t)tile_m ? (m - e.row_offset) : (int64_t)tile_m;
+  e.col_extent = (n - e.col_offset) < (int64_t)tile_n ? (n - e.col_offset) : (int64_t)tile_n;
+  e.required_prefix = required;
+  e.selected_prefix = selected;
+  e.range_bit_length = range_bits;
+  return e;
+}
+
+/* range of a bound: 2 * bound (signed) or bound (api_plan_schedule.inc:35-38) */
+static u256 tile_range(uint32_t semantics, uint64_t bound) {
+  return semantics == SEM_BOUNDED_I64 ? u256_mul_u64(u256_of(bound), 2) : u256_of(bound);
+}
+
+int orc_tile_schedule(uint32_t semantics, int64_t m, int64_t n, uint32_t tile_m, uint32_t tile_n,
+                      const uint64_t* tile_bounds, uint64_t count, uint32_t budget, uint32_t flags,
+                      const uint8_t* zero_a_rows, const uint8_t* zero_b_cols, orc_tile_entry* entries,
+                      orc_schedule_summary* s) {
+  if (semantics != SEM_BOUNDED_I64 && semantics != SEM_BOUNDED_U64) return ORC_INVALID_ARGUMENT;
+  if (m <= 0 || n <= 0 || !s) return ORC_INVALID_ARGUMENT;
+  if (tile_m == 0) tile_m = 128;
+  if (tile_n == 0) tile_n = 128;
+  memset(s, 0, sizeof(*s));
+  s->tile_rows = (uint64_t)((m + tile_m - 1) / tile_m);
+  s->tile_cols = (uint64_t)((n + tile_n - 1) / tile_n);
+  s->tile_count = s->tile_rows * s->tile_cols;
+  const int proofs = (flags & ORC_PLAN_ZERO_ROW_COL_SKIPS) != 0;
+  if (proofs) {
+    if (!zero_a_rows || !zero_b_cols) return ORC_INVALID_ARGUMENT;
+    for (int64_t r = 0; r < m; ++r) s->zero_a_row_count += zero_a_rows[r] != 0;
+    for (int64_t c = 0; c < n; ++c) s->zero_b_col_count += zero_b_cols[c] != 0;
+    s->zero_row_col_product_count =
+        s->zero_a_row_count * (uint64_t)n + ((uint64_t)m - s->zero_a_row_count) * s->zero_b_col_count;
+  }
+  if (!tile_bounds || count != s->tile_count || !entries) return ORC_INVALID_ARGUMENT;
+  const int fixed = (flags & ORC_PLAN_FORCE_FIXED_PREFIX) != 0;
+  const int zero_tiles = (flags & ORC_PLAN_ZERO_TILE_SKIPS) != 0;
+  uint32_t min_req = UINT32_MAX, max_req = 0, min_sel = UINT32_MAX, max_sel = 0, max_bits = 0;
+  uint32_t present[ORC_MAX_PREFIX + 1];
+  memset(present, 0, sizeof(present));
+  for (uint64_t i = 0; i < count; ++i) {
+    const uint64_t bound = tile_bounds[i];
+    if (semantics == SEM_BOUNDED_I64 && bound > (1ull << 63)) return ORC_INVALID_ARGUMENT;
+    const u256 range = tile_range(semantics, bound);
+    const uint32_t bits = u256_bit_length(&range);
+    const uint32_t req = required_prefix(&range);
+    if (req == 0 || req > budget) return ORC_RANGE_ERROR;
+    const uint32_t sel = fixed ? budget : req;
+    min_req = req < min_req ? req : min_req;
+    max_req = req > max_req ? req : max_req;
+    min_sel = sel < min_sel ? sel : min_sel;
+    max_sel = sel > max_sel ? sel : max_sel;
+    max_bits = bits > max_bits ? bits : max_bits;
+    present[sel] = 1;
+    uint32_t ef = zero_tiles && bound == 0 ? ORC_TILE_ZERO_OUTPUT : 0u;
+    orc_tile_entry e = tile_entry(m, n, tile_m, tile_n, s->tile_cols, i, req, sel, bits, 0);
+    if (proofs && (mask_has_set(zero_a_rows, e.row_offset, e.row_offset + e.row_extent) ||
+                   mask_has_set(zero_b_cols, e.col_offset, e.col_offset + e.col_extent)))
+      ef |= ORC_TILE_ZERO_ROW_COL_PRODUCT;
+    e.flags = ef;
+    s->flags |= ef;
+    entries[i] = e;
+  }
+  /* group index = rank of the selected prefix among the distinct ones */
+  uint32_t rank[ORC_MAX_PREFIX + 1];
+  uint32_t groups = 0;
+  for (uint32_t p = 0; p <= ORC_MAX_PREFIX; ++p) {
+    rank[p] = groups;
+    groups += present[p];
+  }
+  for (uint64_t i = 0; i < count; ++i) entries[i].group_index = rank[entries[i].selected_prefix];
+  s->min_required = count ? min_req : 0;
+  s->max_required = max_req;
+  s->min_selected = count ? min_sel : 0;
+  s->max_selected = max_sel;
+  s->group_count = groups;
+  s->range_bits = max_bits;
+  s->adaptive_prefix = groups > 1;
+  s->adaptive_skip = max_sel < budget;
+  s->collapsed = groups == 1 && min_req == budget && max_req == budget && min_sel == budget && max_sel == budget &&
+                 s->flags == 0;
+  if (s->collapsed) {
+    /* api_plan_public_api.inc:141-157: entries rebuilt from the copied bounds */
+    for (uint64_t i = 0; i < count; ++i) {
+      const u256 range = tile_range(semantics, tile_bounds[i]);
+      entries[i] = tile_entry(m, n, tile_m, tile_n, s->tile_cols, i, required_prefix(&range), s->min_selected,
+                              u256_bit_length(&range), 0);
+    }
+  }
+  return ORC_SUCCESS;
+}
+
+void orc_gemm_rns_tiled(const int8_t* A, const int8_t* B, int8_t* C, int64_t m, int64_t n, int64_t k,
+                        const orc_tile_entry* entries, uint64_t count) {
+  for (uint64_t t = 0; t < count; ++t) {
+    const orc_tile_entry* e = &entries[t];
+    for (uint32_t p = 0; p < e->selected_prefix; ++p) {
+      int8_t* c_tile = C + (int64_t)p * m * n + e->row_offset * n + e->col_offset;
+      if (e->flags & ORC_TILE_ZERO_OUTPUT) {
+        for (int64_t r = 0; r < e->row_extent; ++r) memset(c_tile + r * n, 0, (size_t)e->col_extent);
+        continue;
+      }
+      orc_ring_gemm_modulus(A + (int64_t)p * m * k + e->row_offset * k, B + (int64_t)p * k * n + e->col_offset,
+                            c_tile, e->row_extent, e->col_extent, k, k, n, n, kLadder[p]);
+    }
+  }
+}
+
+static const orc_tile_entry* entry_for_cell(const orc_tile_entry* entries, uint64_t count, uint32_t tile_m,
+                                            uint32_t tile_n, int64_t n, int64_t row, int64_t col) {
+  const uint64_t cols = (uint64_t)((n + tile_n - 1) / tile_n);
+  const uint64_t index = (uint64_t)(row / tile_m) * cols + (uint64_t)(col / tile_n);
+  return index < count ? &entries[index] : NULL;
+}
+
+int orc_export_i64_tiled(const int8_t* C, int64_t m, int64_t n, uint32_t storage, uint32_t tile_m, uint32_t tile_n,
+                         const orc_tile_entry* entries, const uint64_t* tile_bounds, uint64_t count, int64_t* dst,
+                         int64_t ld) {
+  const int64_t cells = m * n;
+  int64_t* staged = (int64_t*)calloc((size_t)cells, sizeof(int64_t));
+  int* status = (int*)calloc((size_t)cells, sizeof(int));
+  (void)storage;
+#pragma omp parallel for schedule(static)
+  for (int64_t cell = 0; cell < cells; ++cell) {
+    const int64_t row = cell / n, col = cell % n;
+    const orc_tile_entry* e = entry_for_cell(entries, count, tile_m, tile_n, n, row, col);
+    if (!e) { status[cell] = ORC_INVALID_ARGUMENT; continue; }
+    if (e->flags & ORC_TILE_ZERO_OUTPUT) { staged[cell] = 0; continue; }
+    const uint64_t idx = (uint64_t)(e - entries);
+    status[cell] = reconstruct_signed_strided(C + cell, cells, e->selected_prefix, tile_bounds[idx], &staged[cell]);
+  }
+  const int st = first_failure(status, cells);
+  if (st == ORC_SUCCESS)
+    for (int64_t r = 0; r < m; ++r) memcpy(dst + r * ld, staged + r * n, sizeof(int64_t) * (size_t)n);
+  free(staged);
+  free(status);
+  return st;
+}
+
+int orc_export_u64_tiled(const int8_t* C, int64_t m, int64_t n, uint32_t storage, uint32_t tile_m, uint32_t tile_n,
+                         const orc_tile_entry* entries, const uint64_t* tile_bounds, uint64_t count, uint64_t* dst,
+                         int64_t ld) {
+  const int64_t cells = m * n;
+  uint64_t* staged = (uint64_t*)calloc((size_t)cells, sizeof(uint64_t));
+  int* status = (int*)calloc((size_t)cells, sizeof(int));
+  (void)storage;
+#pragma omp parallel for schedule(static)
+  for (int64_t cell = 0; cell < cells; ++cell) {
+    const int64_t row = cell / n, col = cell % n;
+    const orc_tile_entry* e = entry_for_cell(entries, count, tile_m, tile_n, n, row, col);
+    if (!e) { status[cell] = ORC_INVALID_ARGUMENT; continue; }
+    if (e->flags & ORC_TILE_ZERO_OUTPUT) { staged[cell] = 0; continue; }
+    const uint64_t idx = (uint64_t)(e - entries);
+    status[cell] =
+        reconstruct_unsigned_strided(C + cell, cells, e->selected_prefix, tile_bounds[idx], &staged[cell]);
+  }
+  const int st = first_failure(status, cells);
+  if (st == ORC_SUCCESS)
+    for (int64_t r = 0; r < m; ++r) memcpy(dst + r * ld, staged + r * n, sizeof(uint64_t) * (size_t)n);
+  free(staged);
+  free(status);
+  return st;
+}
+
 static int export_limbs(const int8_t* C, int64_t m, int64_t n, uint32_t prefix, uint64_t* dst, int64_t ld,
                         uint32_t limbs, int is_signed) {
   const int64_t cells = m * n;

@@ -86,6 +86,45 @@ int orc_export_exact_wide_unsigned(const int8_t* C, int64_t m, int64_t n, uint32
                                    int64_t ld, uint32_t limbs);
 void orc_export_finite_u8(const int8_t* C, int64_t m, int64_t n, uint32_t modulus, uint8_t* dst, int64_t ld); /* cpu_reference.cpp:132-153 */
 
+/* ---- per-tile bounded schedules ------------------------------------------- */
+/* One tile of the schedule as rns8_get_plan_tile_schedule reports it
+ * (rns8.h rns8_plan_tile_schedule_entry without the size/version header). */
+typedef struct orc_tile_entry {
+  uint32_t flags;
+  uint64_t tile_row, tile_col;
+  int64_t row_offset, col_offset, row_extent, col_extent;
+  uint32_t required_prefix, selected_prefix, group_index, range_bit_length;
+} orc_tile_entry;
+
+typedef struct orc_schedule_summary {
+  uint64_t tile_rows, tile_cols, tile_count;
+  uint32_t min_required, max_required, min_selected, max_selected;
+  uint32_t group_count, adaptive_prefix, adaptive_skip, range_bits, flags;
+  uint64_t zero_a_row_count, zero_b_col_count, zero_row_col_product_count;
+  uint32_t collapsed; /* 1: every tile runs the plan prefix; execution is the global one */
+} orc_schedule_summary;
+
+/* api_plan_schedule.inc:109-261 (per-tile branch) and
+ * api_plan_public_api.inc:119-160 (entries reported for a collapsed schedule).
+ * semantics: BOUNDED_I64 or BOUNDED_U64; budget = the plan prefix. */
+int orc_tile_schedule(uint32_t semantics, int64_t m, int64_t n, uint32_t tile_m, uint32_t tile_n,
+                      const uint64_t* tile_bounds, uint64_t count, uint32_t budget, uint32_t flags,
+                      const uint8_t* zero_a_rows, const uint8_t* zero_b_cols, orc_tile_entry* entries,
+                      orc_schedule_summary* summary);
+/* cpu_reference.cpp:231-257: planes p < selected prefix of each tile; zero-output
+ * tiles filled with 0; other planes of C left as they are. Compact planes. */
+void orc_gemm_rns_tiled(const int8_t* A, const int8_t* B, int8_t* C, int64_t m, int64_t n, int64_t k,
+                        const orc_tile_entry* entries, uint64_t count);
+/* api_export.cpp:365-410: per cell the tile's selected prefix and bound; 0 for
+ * zero-output tiles; dst untouched on the first failing status. C holds
+ * `storage` compact planes. */
+int orc_export_i64_tiled(const int8_t* C, int64_t m, int64_t n, uint32_t storage, uint32_t tile_m, uint32_t tile_n,
+                         const orc_tile_entry* entries, const uint64_t* tile_bounds, uint64_t count, int64_t* dst,
+                         int64_t ld);
+int orc_export_u64_tiled(const int8_t* C, int64_t m, int64_t n, uint32_t storage, uint32_t tile_m, uint32_t tile_n,
+                         const orc_tile_entry* entries, const uint64_t* tile_bounds, uint64_t count, uint64_t* dst,
+                         int64_t ld);
+
 /* ---- end-to-end CPU_REFERENCE path (api_oneshot.cpp:510-547, CS5) ------- */
 /* pack -> gemm_rns -> export at an explicit prefix; rows [row0, row0+rows)
  * of C only (a bounded sample of a large GEMM uses row0/rows). */
