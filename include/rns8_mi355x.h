@@ -36,6 +36,18 @@ extern "C" {
  * semantics report 0. */
 RNS8_API rns8_status rns8_mi355x_select_prefix(const rns8_gemm_desc* desc, uint32_t* out_prefix);
 
+/* The schedule rns8_create_plan would build for `desc`, without a context or
+ * device: the same results as rns8_get_plan_schedule_info and
+ * rns8_get_plan_tile_schedule on that plan (reference rns8.h:683-691,
+ * api_plan_schedule.inc:109-279, api_plan_public_api.inc:80-160), including
+ * per-tile bounded schedules. `entries` may be NULL to query the count. */
+RNS8_API rns8_status rns8_mi355x_plan_schedule(
+    const rns8_gemm_desc* desc,
+    rns8_plan_schedule_info* info,
+    rns8_plan_tile_schedule_entry* entries,
+    uint64_t capacity,
+    uint64_t* written);
+
 /* Device-source variants of rns8_pack_i64 / rns8_pack_u64 / rns8_pack_finite_u8
  * (reference rns8.h:848-911): `d_src` is device memory, row stride `ld`
  * elements. For exact-wide matrices the magnitude proof is the global

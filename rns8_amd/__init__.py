@@ -60,8 +60,23 @@ def check(status: int, what: str) -> None:
 
 
 def gemm_desc(semantics, bound_kind, m, n, k, bound=0, max_prefix=0, flags=0, finite_modulus=0, lhs_bound=0,
-              rhs_bound=0, requested_backend=BACKEND_AUTO, tile_m=0, tile_n=0) -> abi.GemmDesc:
+              rhs_bound=0, requested_backend=BACKEND_AUTO, tile_m=0, tile_n=0, tile_bounds=None, zero_a_rows=None,
+              zero_b_cols=None) -> abi.GemmDesc:
+    """A gemm descriptor; per-tile bounds and zero proof masks are kept alive on
+    the returned object (the library copies them at plan creation)."""
     d = abi.new_struct(abi.GemmDesc)
+    if tile_bounds is not None:
+        d._tile_bounds = (C.c_uint64 * max(len(tile_bounds), 1))(*[int(b) for b in tile_bounds])
+        d.tile_bounds = C.cast(d._tile_bounds, C.POINTER(C.c_uint64))
+        d.tile_bounds_count = len(tile_bounds)
+    if zero_a_rows is not None:
+        d._zero_a = (C.c_uint8 * max(len(zero_a_rows), 1))(*[int(v) for v in zero_a_rows])
+        d.zero_a_rows = C.cast(d._zero_a, C.POINTER(C.c_uint8))
+        d.zero_a_rows_count = len(zero_a_rows)
+    if zero_b_cols is not None:
+        d._zero_b = (C.c_uint8 * max(len(zero_b_cols), 1))(*[int(v) for v in zero_b_cols])
+        d.zero_b_cols = C.cast(d._zero_b, C.POINTER(C.c_uint8))
+        d.zero_b_cols_count = len(zero_b_cols)
     d.semantics = semantics
     d.bound_kind = bound_kind
     d.requested_backend = requested_backend
@@ -75,13 +90,14 @@ def gemm_desc(semantics, bound_kind, m, n, k, bound=0, max_prefix=0, flags=0, fi
     return d
 
 
-def matrix_desc(rows, cols, semantics, bound_kind, max_prefix=0, logical_ld=0) -> abi.MatrixDesc:
+def matrix_desc(rows, cols, semantics, bound_kind, max_prefix=0, logical_ld=0, tile_m=0, tile_n=0) -> abi.MatrixDesc:
     d = abi.new_struct(abi.MatrixDesc)
     d.rows, d.cols = rows, cols
     d.logical_ld = logical_ld
     d.semantics = semantics
     d.logical_layout = abi.LAYOUT_ROW_MAJOR
     d.bound_kind = bound_kind
+    d.tile_m, d.tile_n = tile_m, tile_n
     d.max_prefix = max_prefix
     return d
 
@@ -91,6 +107,22 @@ def select_prefix(desc: abi.GemmDesc) -> tuple[int, int]:
     out = C.c_uint32(0)
     st = lib().rns8_mi355x_select_prefix(C.byref(desc), C.byref(out))
     return st, out.value
+
+
+def plan_schedule(desc: abi.GemmDesc):
+    """(status, info, entries) of the schedule a plan from `desc` would build (no device needed)."""
+    info = abi.new_struct(abi.PlanScheduleInfo)
+    written = C.c_uint64(0)
+    st = lib().rns8_mi355x_plan_schedule(C.byref(desc), C.byref(info), None, 0, C.byref(written))
+    if st != abi.SUCCESS:
+        return st, None, []
+    entries = (abi.TileScheduleEntry * max(written.value, 1))()
+    for e in entries:
+        e.struct_size = C.sizeof(abi.TileScheduleEntry)
+        e.abi_version = abi.ABI_VERSION
+    st = lib().rns8_mi355x_plan_schedule(C.byref(desc), C.byref(info), C.cast(entries, C.c_void_p), written.value,
+                                         C.byref(written))
+    return st, info, list(entries)[:written.value]
 
 
 def _ptr(a: np.ndarray) -> C.c_void_p:
@@ -146,6 +178,14 @@ class Plan(_Handle):
         info = abi.new_struct(abi.PlanScheduleInfo)
         check(lib().rns8_get_plan_schedule_info(self.ptr, C.byref(info)), "rns8_get_plan_schedule_info")
         return info
+
+    def tile_schedule(self) -> list:
+        written = C.c_uint64(0)
+        check(lib().rns8_get_plan_tile_schedule(self.ptr, None, 0, C.byref(written)), "rns8_get_plan_tile_schedule")
+        entries = (abi.TileScheduleEntry * max(written.value, 1))()
+        check(lib().rns8_get_plan_tile_schedule(self.ptr, C.cast(entries, C.c_void_p), written.value,
+                                                C.byref(written)), "rns8_get_plan_tile_schedule")
+        return list(entries)[:written.value]
 
     @property
     def prefix(self) -> int:

@@ -160,6 +160,24 @@ class PlanScheduleInfo(C.Structure):
     ]
 
 
+class TileScheduleEntry(C.Structure):
+    _fields_ = [
+        ("struct_size", C.c_uint64),
+        ("abi_version", C.c_uint32),
+        ("flags", C.c_uint32),
+        ("tile_row", C.c_uint64),
+        ("tile_col", C.c_uint64),
+        ("row_offset", C.c_int64),
+        ("col_offset", C.c_int64),
+        ("row_extent", C.c_int64),
+        ("col_extent", C.c_int64),
+        ("required_prefix", C.c_uint32),
+        ("selected_prefix", C.c_uint32),
+        ("group_index", C.c_uint32),
+        ("range_bit_length", C.c_uint32),
+    ]
+
+
 class MatrixStorageInfo(C.Structure):
     _fields_ = [
         ("struct_size", C.c_uint64),
@@ -244,6 +262,9 @@ PROTOTYPES = {
     "rns8_gemm_finite_ring_u8_oneshot": (_U32, [_P, C.POINTER(GemmDesc), _U16, _P, _I64, _P, _I64, _P, _I64]),
     "rns8_gemm_finite_field_u8_oneshot": (_U32, [_P, C.POINTER(GemmDesc), _U16, _P, _I64, _P, _I64, _P, _I64]),
     "rns8_mi355x_select_prefix": (_U32, [C.POINTER(GemmDesc), C.POINTER(_U32)]),
+    "rns8_mi355x_plan_schedule": (_U32, [C.POINTER(GemmDesc), C.POINTER(PlanScheduleInfo), _P, _U64,
+                                         C.POINTER(_U64)]),
+    "rns8_get_plan_tile_schedule": (_U32, [_P, _P, _U64, C.POINTER(_U64)]),
     "rns8_mi355x_pack_i64_device": (_U32, [_P, _P, _P, _I64, _U64, _P]),
     "rns8_mi355x_pack_u64_device": (_U32, [_P, _P, _P, _I64, _U64, _P]),
     "rns8_mi355x_pack_finite_u8_device": (_U32, [_P, _P, _U16, _P, _I64, _U64, _P]),

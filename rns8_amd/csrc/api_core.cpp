@@ -7,6 +7,7 @@
 //   src/core/api_plan_public_api.inc   plan creation order of checks
 //   src/core/api_plan_schedule.inc     global-bound prefix schedule
 //   src/core/api_matrix_public_api.inc matrix creation
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstring>
@@ -262,7 +263,16 @@ rns8_status plan_prefix(const rns8_gemm_desc& d, uint32_t& budget, uint32_t& sel
       break;
   }
   range_bits = range.bit_length();
-  if (per_tile(d.bound_kind)) return RNS8_UNSUPPORTED_BACKEND;  // per-tile schedules: not implemented here
+  if (per_tile(d.bound_kind)) {
+    // the plan prefix is the budget; each tile selects its own (build_tile_schedule)
+    TileSchedule sched;
+    const rns8_status st = build_tile_schedule(d, budget, sched);
+    if (st != RNS8_SUCCESS) return st;
+    selected = budget;
+    required = sched.min_required;
+    range_bits = sched.range_bits;
+    return RNS8_SUCCESS;
+  }
   required = required_prefix_for_range(range);
   if (required == 0 || required > budget) return RNS8_RANGE_ERROR;
   selected = (d.flags & RNS8_PLAN_FORCE_FIXED_PREFIX) ? budget : required;
@@ -294,7 +304,131 @@ hipStream_t pick_stream(const rns8_context& ctx, void* stream) {
   return stream ? static_cast<hipStream_t>(stream) : ctx.stream;
 }
 
-uint32_t storage_prefix(const rns8_plan& p) { return uses_finite_storage(p.desc.semantics) ? 0u : p.prefix; }
+bool per_tile_kind(rns8_bound_kind b) { return per_tile(b); }
+
+// reference api_plan_schedule.inc:46-52: a per-tile plan stores only the
+// planes its tiles select
+uint32_t storage_prefix(const rns8_plan& p) {
+  if (uses_finite_storage(p.desc.semantics)) return 0u;
+  if (per_tile(p.desc.bound_kind) && p.schedule.max_selected > 0) return p.schedule.max_selected;
+  return p.prefix;
+}
+
+namespace {
+
+// reference api_plan_schedule.inc:54-72 (make_tile_schedule_entry)
+rns8_plan_tile_schedule_entry tile_entry(int64_t m, int64_t n, uint32_t tile_m, uint32_t tile_n, uint64_t tile_cols,
+                                         uint64_t index, uint32_t required, uint32_t selected, uint32_t range_bits,
+                                         uint32_t flags) {
+  rns8_plan_tile_schedule_entry e{};
+  e.struct_size = sizeof(e);
+  e.abi_version = RNS8_ABI_VERSION;
+  e.flags = flags;
+  e.tile_row = index / tile_cols;
+  e.tile_col = index % tile_cols;
+  e.row_offset = static_cast<int64_t>(e.tile_row * tile_m);
+  e.col_offset = static_cast<int64_t>(e.tile_col * tile_n);
+  e.row_extent = std::min<int64_t>(tile_m, m - e.row_offset);
+  e.col_extent = std::min<int64_t>(tile_n, n - e.col_offset);
+  e.required_prefix = required;
+  e.selected_prefix = selected;
+  e.range_bit_length = range_bits;
+  return e;
+}
+
+// reference api_plan_schedule.inc:35-38
+I256 tile_range(rns8_semantics s, uint64_t bound) {
+  return s == RNS8_BOUNDED_I64 ? I256::from_u64(bound) * I256::from_u64(2) : I256::from_u64(bound);
+}
+
+}  // namespace
+
+rns8_status build_tile_schedule(const rns8_gemm_desc& d, uint32_t budget, TileSchedule& s) {
+  s = TileSchedule{};
+  const uint32_t tm = d.tile_m == 0 ? 128u : d.tile_m;
+  const uint32_t tn = d.tile_n == 0 ? 128u : d.tile_n;
+  const uint64_t rows = (static_cast<uint64_t>(d.m) + tm - 1) / tm;
+  const uint64_t cols = (static_cast<uint64_t>(d.n) + tn - 1) / tn;
+  const uint64_t count = rows * cols;
+  const bool proofs = (d.flags & RNS8_PLAN_ALLOW_PROVEN_ZERO_ROW_COL_SKIPS) != 0;
+  if (proofs) {
+    s.zero_a_rows.assign(d.zero_a_rows, d.zero_a_rows + d.zero_a_rows_count);
+    s.zero_b_cols.assign(d.zero_b_cols, d.zero_b_cols + d.zero_b_cols_count);
+    for (uint8_t v : s.zero_a_rows) s.zero_a_row_count += v != 0;
+    for (uint8_t v : s.zero_b_cols) s.zero_b_col_count += v != 0;
+    s.zero_row_col_product_count = s.zero_a_row_count * static_cast<uint64_t>(d.n) +
+                                   (static_cast<uint64_t>(d.m) - s.zero_a_row_count) * s.zero_b_col_count;
+  }
+  if (!d.tile_bounds || d.tile_bounds_count != count) return RNS8_INVALID_ARGUMENT;
+  s.bounds.assign(d.tile_bounds, d.tile_bounds + count);
+  const bool fixed = (d.flags & RNS8_PLAN_FORCE_FIXED_PREFIX) != 0;
+  const bool zero_tiles = (d.flags & RNS8_PLAN_ALLOW_PROVEN_ZERO_TILE_SKIPS) != 0;
+  uint32_t min_req = UINT32_MAX, max_req = 0, min_sel = UINT32_MAX, max_sel = 0;
+  bool present[kMaxPrefix + 1] = {};
+  s.entries.reserve(count);
+  auto any_set = [](const std::vector<uint8_t>& mask, int64_t begin, int64_t end) {
+    for (int64_t i = begin; i < end; ++i)
+      if (mask[static_cast<std::size_t>(i)]) return true;
+    return false;
+  };
+  for (uint64_t i = 0; i < count; ++i) {
+    const uint64_t bound = s.bounds[i];
+    if (d.semantics == RNS8_BOUNDED_I64 && bound > (uint64_t{1} << 63)) return RNS8_INVALID_ARGUMENT;
+    const I256 range = tile_range(d.semantics, bound);
+    const uint32_t bits = range.bit_length();
+    const uint32_t req = required_prefix_for_range(range);
+    if (req == 0 || req > budget) return RNS8_RANGE_ERROR;
+    const uint32_t sel = fixed ? budget : req;
+    min_req = std::min(min_req, req);
+    max_req = std::max(max_req, req);
+    min_sel = std::min(min_sel, sel);
+    max_sel = std::max(max_sel, sel);
+    s.range_bits = std::max(s.range_bits, bits);
+    present[sel] = true;
+    rns8_plan_tile_schedule_entry e = tile_entry(d.m, d.n, tm, tn, cols, i, req, sel, bits, 0);
+    uint32_t f = zero_tiles && bound == 0 ? RNS8_TILE_SCHEDULE_ZERO_OUTPUT : 0u;
+    if (proofs && (any_set(s.zero_a_rows, e.row_offset, e.row_offset + e.row_extent) ||
+                   any_set(s.zero_b_cols, e.col_offset, e.col_offset + e.col_extent)))
+      f |= RNS8_TILE_SCHEDULE_ZERO_ROW_COL_PRODUCT;
+    e.flags = f;
+    s.flags |= f;
+    s.entries.push_back(e);
+  }
+  uint32_t rank[kMaxPrefix + 1] = {};
+  for (uint32_t p = 0; p <= kMaxPrefix; ++p) {
+    rank[p] = s.groups;
+    s.groups += present[p] ? 1u : 0u;
+  }
+  for (auto& e : s.entries) e.group_index = rank[e.selected_prefix];
+  s.min_required = count ? min_req : 0;
+  s.max_required = max_req;
+  s.min_selected = count ? min_sel : 0;
+  s.max_selected = max_sel;
+  s.adaptive_prefix = s.groups > 1 ? 1u : 0u;
+  s.adaptive_skip = max_sel < budget ? 1u : 0u;
+  if (s.groups == 1 && min_req == budget && max_req == budget && min_sel == budget && max_sel == budget &&
+      s.flags == 0)
+    s.entries.clear();  // every tile runs the plan prefix
+  return RNS8_SUCCESS;
+}
+
+void plan_tile_entries(const rns8_plan& p, rns8_plan_tile_schedule_entry* out) {
+  const bool crt = uses_rns_storage(p.desc.semantics);
+  if (per_tile(p.desc.bound_kind) && !p.schedule.entries.empty()) {
+    std::copy(p.schedule.entries.begin(), p.schedule.entries.end(), out);
+    return;
+  }
+  for (uint64_t index = 0; index < p.tile_count; ++index) {
+    if (per_tile(p.desc.bound_kind) && p.schedule.bounds.size() == p.tile_count) {
+      const I256 range = tile_range(p.desc.semantics, p.schedule.bounds[index]);
+      out[index] = tile_entry(p.desc.m, p.desc.n, p.desc.tile_m, p.desc.tile_n, p.tile_cols, index,
+                              required_prefix_for_range(range), p.schedule.min_selected, range.bit_length(), 0);
+      continue;
+    }
+    out[index] = tile_entry(p.desc.m, p.desc.n, p.desc.tile_m, p.desc.tile_n, p.tile_cols, index,
+                            crt ? p.required_prefix : 0, crt ? p.prefix : 0, p.range_bits, 0);
+  }
+}
 
 rns8_bound_kind storage_bound_kind(const rns8_plan& p) {
   if (p.desc.bound_kind != RNS8_BOUND_INPUT_RANGE_AND_K) return p.desc.bound_kind;
@@ -303,10 +437,12 @@ rns8_bound_kind storage_bound_kind(const rns8_plan& p) {
 
 // reference api_matrix_currentness_storage.inc:1-23
 bool matrix_matches(const rns8_matrix& m, rns8_semantics s, rns8_bound_kind bk, int64_t rows, int64_t cols,
-                    uint32_t prefix) {
+                    uint32_t prefix, uint32_t tile_m, uint32_t tile_n) {
   if (m.desc.semantics != s || m.desc.bound_kind != bk || m.desc.rows != rows || m.desc.cols != cols ||
       m.desc.logical_layout != RNS8_LAYOUT_ROW_MAJOR || m.desc.flags != 0)
     return false;
+  // per-tile matrices carry the schedule's tile grid
+  if (per_tile(bk) && (m.desc.tile_m != tile_m || m.desc.tile_n != tile_n)) return false;
   if (prefix == 0) return m.desc.max_prefix == 0;
   return m.prefix >= prefix && m.desc.max_prefix >= prefix;
 }
@@ -380,6 +516,19 @@ rns8_status rns8_mi355x_select_prefix(const rns8_gemm_desc* desc, uint32_t* out_
     if (desc->semantics == RNS8_WRAP_U64_MOD_2_64) return RNS8_UNSUPPORTED_BACKEND;
     *out_prefix = selected;
     return RNS8_SUCCESS;
+  });
+}
+
+rns8_status rns8_mi355x_plan_schedule(const rns8_gemm_desc* desc, rns8_plan_schedule_info* info,
+                                      rns8_plan_tile_schedule_entry* entries, uint64_t capacity, uint64_t* written) {
+  return guard([&]() -> rns8_status {
+    if (!desc || !info || !written) return RNS8_INVALID_ARGUMENT;
+    rns8_plan plan;
+    const rns8_status st = init_plan(*desc, RNS8_BACKEND_HIP_DIRECT, plan);
+    if (st != RNS8_SUCCESS) return st;
+    const rns8_status si = rns8_get_plan_schedule_info(&plan, info);
+    if (si != RNS8_SUCCESS) return si;
+    return rns8_get_plan_tile_schedule(&plan, entries, capacity, written);
   });
 }
 
@@ -503,61 +652,98 @@ rns8_status rns8_get_backend_capability_info(rns8_backend_kind backend, rns8_bac
 
 // ---- plan ----------------------------------------------------------------------
 
+namespace rns8x {
+
+// Plan state that needs no device: validation, prefix selection, tile grid,
+// per-tile schedule, split-K sizing (reference api_plan_public_api.inc:3-73).
+rns8_status init_plan(const rns8_gemm_desc& d, rns8_backend_kind backend, rns8_plan& plan) {
+  if (!valid_abi(d.struct_size, d.abi_version, sizeof(d))) return RNS8_INVALID_ARGUMENT;
+  const uint32_t budget0 = d.max_prefix == 0 ? default_prefix(d.semantics) : d.max_prefix;
+  const rns8_status v = validate_gemm_desc(d, budget0);
+  if (v != RNS8_SUCCESS) return v;
+  // backend routing (reference api_plan_public_api.inc:19-33)
+  if (d.requested_backend != RNS8_BACKEND_AUTO && d.requested_backend != backend) return RNS8_UNSUPPORTED_BACKEND;
+  if (d.semantics == RNS8_WRAP_U64_MOD_2_64) return RNS8_UNSUPPORTED_BACKEND;
+  uint32_t budget = 0, selected = 0, required = 0, bits = 0;
+  uint64_t eff = 0;
+  const rns8_status st = plan_prefix(d, budget, selected, required, bits, eff);
+  if (st != RNS8_SUCCESS) return st;
+  plan.desc = d;
+  plan.desc.max_prefix = budget;
+  plan.desc.bound = eff;
+  if (plan.desc.tile_m == 0) plan.desc.tile_m = 128;
+  if (plan.desc.tile_n == 0) plan.desc.tile_n = 128;
+  plan.desc.tile_bounds = nullptr;
+  plan.desc.zero_a_rows = nullptr;
+  plan.desc.zero_b_cols = nullptr;
+  plan.backend = backend;
+  plan.budget = budget;
+  plan.prefix = selected;
+  plan.required_prefix = required;
+  plan.range_bits = bits;
+  plan.product = modulus_product(selected);
+  plan.tile_rows = (static_cast<uint64_t>(d.m) + plan.desc.tile_m - 1) / plan.desc.tile_m;
+  plan.tile_cols = (static_cast<uint64_t>(d.n) + plan.desc.tile_n - 1) / plan.desc.tile_n;
+  plan.tile_count = plan.tile_rows * plan.tile_cols;
+  if (per_tile(d.bound_kind)) {
+    // copies the bounds and proof masks: the caller's arrays may change later
+    const rns8_status ss = build_tile_schedule(d, budget, plan.schedule);
+    if (ss != RNS8_SUCCESS) return ss;
+    plan.desc.tile_bounds_count = plan.schedule.bounds.size();
+    plan.desc.zero_a_rows_count = plan.schedule.zero_a_rows.size();
+    plan.desc.zero_b_cols_count = plan.schedule.zero_b_cols.size();
+  }
+  const uint32_t planes = uses_finite_storage(d.semantics) ? 1u : selected;
+  const int64_t kblock = d.k > kSafeKBlock ? kSafeKBlock : d.k;
+  // per-tile plans run the tiled unit list (no K split)
+  if (!per_tile(d.bound_kind)) {
+    plan.splitk_slices = choose_splitk_slices(d.m, d.n, kblock, planes);
+    plan.splitk_bytes = splitk_workspace_bytes(d.m, d.n, kblock, planes);
+  }
+  return RNS8_SUCCESS;
+}
+
+}  // namespace rns8x
+
 rns8_status rns8_create_plan(rns8_context* ctx, const rns8_gemm_desc* desc, rns8_plan** out) {
   return guard([&]() -> rns8_status {
     if (!ctx || !desc || !out) return RNS8_INVALID_ARGUMENT;
     *out = nullptr;
-    if (!valid_abi(desc->struct_size, desc->abi_version, sizeof(*desc))) return RNS8_INVALID_ARGUMENT;
-    const uint32_t budget0 = desc->max_prefix == 0 ? default_prefix(desc->semantics) : desc->max_prefix;
-    const rns8_status v = validate_gemm_desc(*desc, budget0);
-    if (v != RNS8_SUCCESS) return v;
-    // backend routing (reference api_plan_public_api.inc:19-33)
-    if (desc->requested_backend != RNS8_BACKEND_AUTO && desc->requested_backend != ctx->backend)
-      return RNS8_UNSUPPORTED_BACKEND;
-    if (desc->semantics == RNS8_WRAP_U64_MOD_2_64) return RNS8_UNSUPPORTED_BACKEND;
-    uint32_t budget = 0, selected = 0, required = 0, bits = 0;
-    uint64_t eff = 0;
-    const rns8_status st = plan_prefix(*desc, budget, selected, required, bits, eff);
-    if (st != RNS8_SUCCESS) return st;
     auto* plan = new (std::nothrow) rns8_plan();
     if (!plan) return RNS8_INTERNAL_ERROR;
-    plan->desc = *desc;
-    plan->desc.max_prefix = budget;
-    plan->desc.bound = eff;
-    if (plan->desc.tile_m == 0) plan->desc.tile_m = 128;
-    if (plan->desc.tile_n == 0) plan->desc.tile_n = 128;
-    plan->desc.tile_bounds = nullptr;
-    plan->desc.zero_a_rows = nullptr;
-    plan->desc.zero_b_cols = nullptr;
-    plan->backend = ctx->backend;
+    rns8_status st = init_plan(*desc, ctx->backend, *plan);
     plan->device_id = ctx->device_id;
-    plan->budget = budget;
-    plan->prefix = selected;
-    plan->required_prefix = required;
-    plan->range_bits = bits;
-    plan->product = modulus_product(selected);
-    plan->tile_rows = (static_cast<uint64_t>(desc->m) + plan->desc.tile_m - 1) / plan->desc.tile_m;
-    plan->tile_cols = (static_cast<uint64_t>(desc->n) + plan->desc.tile_n - 1) / plan->desc.tile_n;
-    plan->tile_count = plan->tile_rows * plan->tile_cols;
-    const uint32_t planes = uses_finite_storage(desc->semantics) ? 1u : selected;
-    const int64_t kblock = desc->k > kSafeKBlock ? kSafeKBlock : desc->k;
-    plan->splitk_slices = choose_splitk_slices(desc->m, desc->n, kblock, planes);
-    plan->splitk_bytes = splitk_workspace_bytes(desc->m, desc->n, kblock, planes);
+    if (st == RNS8_SUCCESS && per_tile(plan->desc.bound_kind))
+      st = hipSetDevice(ctx->device_id) == hipSuccess ? upload_tile_lists(*plan, ctx->stream) : RNS8_BACKEND_FAILURE;
+    if (st != RNS8_SUCCESS) {
+      free_tile_lists(*plan);
+      delete plan;
+      return st;
+    }
     *out = plan;
     return RNS8_SUCCESS;
   });
 }
 
 rns8_status rns8_destroy_plan(rns8_plan* plan) {
-  delete plan;
-  return RNS8_SUCCESS;
+  return guard([&]() -> rns8_status {
+    if (!plan) return RNS8_SUCCESS;
+    if (plan->units || plan->zero_fills || plan->export_tiles) {
+      (void)hipSetDevice(plan->device_id);
+      free_tile_lists(*plan);
+    }
+    delete plan;
+    return RNS8_SUCCESS;
+  });
 }
 
+// reference api_plan_contract_names.inc:39-51
 static const char* bound_contract_name(const rns8_plan& p) {
-  if (uses_finite_storage(p.desc.semantics)) return "finite_modulus_no_crt";
-  if (exact_wide(p.desc.semantics)) return "exact_wide_k_times_input_range";
-  if (p.desc.bound_kind == RNS8_BOUND_INPUT_RANGE_AND_K) return "input_range_and_k";
-  return p.desc.semantics == RNS8_BOUNDED_I64 ? "global_max_abs" : "global_max_unsigned";
+  if (p.desc.bound_kind == RNS8_BOUND_INPUT_RANGE_AND_K) return "input_range_and_k_derived_output_bound";
+  if (per_tile(p.desc.bound_kind)) return "per_tile_output_bounds";
+  if (p.desc.bound_kind == RNS8_BOUND_GLOBAL_MAX_ABS || p.desc.bound_kind == RNS8_BOUND_GLOBAL_MAX_UNSIGNED)
+    return "global_output_bound";
+  return "not_applicable";
 }
 
 rns8_status rns8_get_plan_schedule_info(const rns8_plan* plan, rns8_plan_schedule_info* out) {
@@ -570,15 +756,31 @@ rns8_status rns8_get_plan_schedule_info(const rns8_plan* plan, rns8_plan_schedul
     out->tile_cols = plan->tile_cols;
     out->tile_count = plan->tile_count;
     const bool crt = uses_rns_storage(plan->desc.semantics);
-    out->min_required_prefix = crt ? plan->required_prefix : 0;
-    out->max_required_prefix = crt ? plan->required_prefix : 0;
-    out->min_selected_prefix = crt ? plan->prefix : 0;
-    out->max_selected_prefix = crt ? plan->prefix : 0;
-    out->prefix_group_count = crt ? 1u : 0u;
-    out->adaptive_prefix_active = 0;
-    out->adaptive_skip_active = (crt && plan->prefix < plan->budget) ? 1u : 0u;
-    out->range_bit_length = plan->range_bits;
-    out->flags = 0;
+    if (per_tile(plan->desc.bound_kind)) {
+      const TileSchedule& sc = plan->schedule;
+      out->min_required_prefix = sc.min_required;
+      out->max_required_prefix = sc.max_required;
+      out->min_selected_prefix = sc.min_selected;
+      out->max_selected_prefix = sc.max_selected;
+      out->prefix_group_count = sc.groups;
+      out->adaptive_prefix_active = sc.adaptive_prefix;
+      out->adaptive_skip_active = sc.adaptive_skip;
+      out->range_bit_length = sc.range_bits;
+      out->flags = sc.flags;
+      out->zero_a_row_count = sc.zero_a_row_count;
+      out->zero_b_col_count = sc.zero_b_col_count;
+      out->zero_row_col_product_count = sc.zero_row_col_product_count;
+    } else {
+      out->min_required_prefix = crt ? plan->required_prefix : 0;
+      out->max_required_prefix = crt ? plan->required_prefix : 0;
+      out->min_selected_prefix = crt ? plan->prefix : 0;
+      out->max_selected_prefix = crt ? plan->prefix : 0;
+      out->prefix_group_count = crt ? 1u : 0u;
+      out->adaptive_prefix_active = 0;
+      out->adaptive_skip_active = (crt && plan->prefix < plan->budget) ? 1u : 0u;
+      out->range_bit_length = plan->range_bits;
+      out->flags = 0;
+    }
     out->bound_kind = plan->desc.bound_kind;
     out->effective_bound = plan->desc.bound;
     out->lhs_bound = plan->desc.lhs_bound;
@@ -595,22 +797,7 @@ rns8_status rns8_get_plan_tile_schedule(const rns8_plan* plan, rns8_plan_tile_sc
     *written = plan->tile_count;
     if (!entries || capacity == 0) return RNS8_SUCCESS;
     if (capacity < plan->tile_count) return RNS8_WORKSPACE_TOO_SMALL;
-    for (uint64_t index = 0; index < plan->tile_count; ++index) {
-      rns8_plan_tile_schedule_entry e{};
-      e.struct_size = sizeof(e);
-      e.abi_version = RNS8_ABI_VERSION;
-      e.tile_row = index / plan->tile_cols;
-      e.tile_col = index % plan->tile_cols;
-      e.row_offset = static_cast<int64_t>(e.tile_row * plan->desc.tile_m);
-      e.col_offset = static_cast<int64_t>(e.tile_col * plan->desc.tile_n);
-      e.row_extent = std::min<int64_t>(plan->desc.tile_m, plan->desc.m - e.row_offset);
-      e.col_extent = std::min<int64_t>(plan->desc.tile_n, plan->desc.n - e.col_offset);
-      e.required_prefix = plan->required_prefix;
-      e.selected_prefix = plan->prefix;
-      e.group_index = 0;
-      e.range_bit_length = plan->range_bits;
-      entries[index] = e;
-    }
+    plan_tile_entries(*plan, entries);
     return RNS8_SUCCESS;
   });
 }
@@ -745,7 +932,6 @@ rns8_status rns8_create_matrix(rns8_context* ctx, const rns8_matrix_desc* desc, 
     const rns8_status v = validate_matrix_desc(*desc, prefix);
     if (v != RNS8_SUCCESS) return v;
     if (desc->semantics == RNS8_WRAP_U64_MOD_2_64) return RNS8_UNSUPPORTED_BACKEND;
-    if (per_tile(desc->bound_kind)) return RNS8_UNSUPPORTED_BACKEND;
     const int64_t pitch = plane_pitch(desc->rows, desc->cols);
     const uint32_t planes = uses_finite_storage(desc->semantics) ? 1u : prefix;
     if (pitch <= 0 || static_cast<uint64_t>(pitch) > std::numeric_limits<uint64_t>::max() / planes)

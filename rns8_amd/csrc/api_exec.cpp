@@ -203,9 +203,10 @@ rns8_status check_rns_operands(const rns8_context& ctx, const rns8_plan& plan, c
     return RNS8_INVALID_ARGUMENT;
   const uint32_t sp = storage_prefix(plan);
   const rns8_bound_kind bk = storage_bound_kind(plan);
-  if (!matrix_matches(A, plan.desc.semantics, bk, plan.desc.m, plan.desc.k, sp) ||
-      !matrix_matches(B, plan.desc.semantics, bk, plan.desc.k, plan.desc.n, sp) ||
-      !matrix_matches(C, plan.desc.semantics, bk, plan.desc.m, plan.desc.n, sp))
+  const uint32_t tm = plan.desc.tile_m, tn = plan.desc.tile_n;
+  if (!matrix_matches(A, plan.desc.semantics, bk, plan.desc.m, plan.desc.k, sp, tm, tn) ||
+      !matrix_matches(B, plan.desc.semantics, bk, plan.desc.k, plan.desc.n, sp, tm, tn) ||
+      !matrix_matches(C, plan.desc.semantics, bk, plan.desc.m, plan.desc.n, sp, tm, tn))
     return RNS8_INVALID_ARGUMENT;
   if (!A.device_current || !B.device_current) return RNS8_INVALID_ARGUMENT;
   // C is written while A and B are read by other workgroups: no aliasing
@@ -239,7 +240,8 @@ rns8_status check_export(const rns8_context& ctx, const rns8_plan& plan, const r
   if (plan.backend != ctx.backend || C.backend != plan.backend || plan.desc.semantics != semantics)
     return RNS8_INVALID_ARGUMENT;
   if (C.device_id != ctx.device_id || plan.device_id != ctx.device_id) return RNS8_INVALID_ARGUMENT;
-  if (!matrix_matches(C, semantics, storage_bound_kind(plan), plan.desc.m, plan.desc.n, storage_prefix(plan)))
+  if (!matrix_matches(C, semantics, storage_bound_kind(plan), plan.desc.m, plan.desc.n, storage_prefix(plan),
+                      plan.desc.tile_m, plan.desc.tile_n))
     return RNS8_INVALID_ARGUMENT;
   if (!C.device_current) return RNS8_INVALID_ARGUMENT;
   if (exact_wide(semantics) && C.exact_prefix != 0 &&
@@ -405,6 +407,34 @@ rns8_status run_gemm(rns8_context& ctx, const rns8_plan& plan, const rns8_matrix
   return e == hipSuccess ? RNS8_SUCCESS : RNS8_BACKEND_FAILURE;
 }
 
+// Per-tile plan whose schedule did not collapse: the listed GEMM over the
+// plan's unit list plus the zero-output fills (the two write disjoint cells).
+rns8_status run_gemm_tiled(rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B,
+                           rns8_matrix& C, hipStream_t stream) {
+  const uint32_t planes = storage_prefix(plan);
+  GemmArgs g{};
+  g.a = A.planes;
+  g.b = B.planes;
+  g.c = C.planes;
+  g.m = plan.desc.m;
+  g.n = plan.desc.n;
+  g.k = plan.desc.k;
+  g.lda = A.plane_ld;
+  g.ldb = B.plane_ld;
+  g.ldc = C.plane_ld;
+  g.pitch_a = A.plane_pitch;
+  g.pitch_b = B.plane_pitch;
+  g.pitch_c = C.plane_pitch;
+  g.nplanes = planes;
+  g.slices = 1;
+  if (hipSetDevice(ctx.device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  hipError_t e = launch_gemm_listed(g, make_ladder_plane_consts(planes), plan.units, plan.unit_count, stream);
+  if (e == hipErrorInvalidValue) return RNS8_UNSUPPORTED_BACKEND;
+  if (e == hipSuccess) e = launch_zero_tiles(C.planes, C.plane_ld, C.plane_pitch, plan.zero_fills,
+                                             plan.zero_fill_count, stream);
+  return e == hipSuccess ? RNS8_SUCCESS : RNS8_BACKEND_FAILURE;
+}
+
 rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* A, const rns8_matrix* B,
                      rns8_matrix* C, rns8_workspace* ws, void* stream_arg, bool synchronous) {
   if (!ctx || !plan || !A || !B || !C || !ws) return RNS8_INVALID_ARGUMENT;
@@ -418,7 +448,10 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
   if (st != RNS8_SUCCESS) return st;
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
   C->device_current = false;
-  st = run_gemm(*ctx, *plan, *A, *B, *C, *ws, plan->prefix, make_ladder_plane_consts(plan->prefix), stream);
+  if (per_tile_kind(plan->desc.bound_kind) && !plan->schedule.entries.empty())
+    st = run_gemm_tiled(*ctx, *plan, *A, *B, *C, stream);
+  else
+    st = run_gemm(*ctx, *plan, *A, *B, *C, *ws, plan->prefix, make_ladder_plane_consts(plan->prefix), stream);
   if (st != RNS8_SUCCESS) return st;
   if (synchronous) {
     st = sync(stream);
@@ -464,6 +497,21 @@ struct ExportRequest {
   uint32_t limbs;
 };
 
+// Global plans: one launch at the plan prefix. Per-tile plans: one launch per
+// prefix group of tiles, each tile with its own bound, and one for the
+// zero-output tiles (reference api_export.cpp:365-410).
+hipError_t launch_plan_export(const rns8_plan& plan, const ExportArgs& a, hipStream_t stream) {
+  if (!per_tile_kind(plan.desc.bound_kind)) return launch_export(a, plan.prefix, stream);
+  for (const auto& g : plan.export_groups) {
+    const TileExport* const t = plan.export_tiles + g.first;
+    const hipError_t e =
+        g.prefix == 0 ? launch_export_zero_tiles(a, t, g.count, plan.desc.tile_m, plan.desc.tile_n, stream)
+                      : launch_export_tiles(a, g.prefix, t, g.count, plan.desc.tile_m, plan.desc.tile_n, stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 // Host export: reconstruct into a compact device staging buffer, read the
 // status word, and copy to `dst` only when every cell is in range, so a
 // RANGE_ERROR leaves the caller's buffer untouched (api_export.cpp:365-414,
@@ -484,7 +532,7 @@ rns8_status export_host(rns8_context* ctx, const rns8_plan* plan, const rns8_mat
   if (launch_zero_words(mc->status, 1, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
   ExportArgs a{C->planes, m, n, C->plane_ld, C->plane_pitch, mc->staging, n, req.limbs, req.kind, plan->desc.bound,
                mc->status};
-  if (launch_export(a, plan->prefix, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  if (launch_plan_export(*plan, a, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
   uint32_t status = 0;
   if (hipMemcpyAsync(&status, mc->status, sizeof(status), hipMemcpyDeviceToHost, stream) != hipSuccess ||
       hipStreamSynchronize(stream) != hipSuccess)
@@ -502,7 +550,7 @@ rns8_status export_device(rns8_context* ctx, const rns8_plan* plan, const rns8_m
   if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
   ExportArgs a{C->planes,  plan->desc.m, plan->desc.n,     C->plane_ld, C->plane_pitch, d_dst,
                ld,         req.limbs,    req.kind,         plan->desc.bound, d_status};
-  return launch_export(a, plan->prefix, pick_stream(*ctx, stream_arg)) == hipSuccess
+  return launch_plan_export(*plan, a, pick_stream(*ctx, stream_arg)) == hipSuccess
              ? RNS8_SUCCESS
              : RNS8_BACKEND_FAILURE;
 }

@@ -259,6 +259,71 @@ __global__ __launch_bounds__(256) void export_kernel(ExportArgs a, ExportLimits 
     atomicOr(a.status, 1u);
 }
 
+// Per-tile bounded export (reference api_export.cpp:365-410 with
+// per_tile_bounds): one workgroup per (tile of this prefix group, pass of
+// rows_per_pass rows); thread t takes 4 cells of row t / gpr, column group
+// t % gpr, with the tile's own 64-bit limits.
+template <uint32_t P, int L, ExportKind Kind>
+__global__ __launch_bounds__(256) void export_tiles_kernel(ExportArgs a, const TileExport* tiles, uint32_t gpr_log2,
+                                                           uint32_t rows_per_pass, uint32_t vec_store) {
+  constexpr bool kSigned = Kind == ExportKind::I64;
+  const TileExport t = tiles[blockIdx.x];
+  const uint32_t r = blockIdx.y * rows_per_pass + (threadIdx.x >> gpr_log2);
+  const uint32_t cg = threadIdx.x & ((1u << gpr_log2) - 1u);
+  bool violation = false;
+  if (r < t.rows && 4u * cg < t.cols) {
+    const int64_t row = static_cast<int64_t>(t.row_off) + r;
+    const int64_t c0 = static_cast<int64_t>(t.col_off) + 4 * cg;
+    const int8_t* const cell = a.c + row * a.ldc + c0;
+    uint32_t words[P], flipped[P];
+#pragma unroll
+    for (uint32_t i = 0; i < P; ++i) {
+      words[i] = *reinterpret_cast<const uint32_t*>(cell + static_cast<int64_t>(i) * a.pitch_c);
+      flipped[i] = words[i] ^ 0x80808080u;
+    }
+    ExportLimits lim{};
+    lim.pos64 = t.pos64;
+    lim.neg64 = t.neg64;
+    const uint32_t cells = t.cols - 4u * cg < 4u ? t.cols - 4u * cg : 4u;
+    uint64_t w[4];
+    bool ok[4];
+    w[0] = value64<P, L, 0, kSigned>(words, flipped, lim, ok[0]);
+    w[1] = value64<P, L, 1, kSigned>(words, flipped, lim, ok[1]);
+    w[2] = value64<P, L, 2, kSigned>(words, flipped, lim, ok[2]);
+    w[3] = value64<P, L, 3, kSigned>(words, flipped, lim, ok[3]);
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e) violation |= (e < cells) & !ok[e];
+    uint64_t* const out = static_cast<uint64_t*>(a.dst) + row * a.ld + c0;
+    if (vec_store && cells == 4) {
+      typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+      reinterpret_cast<u64x2*>(out)[0] = u64x2{w[0], w[1]};
+      reinterpret_cast<u64x2*>(out)[1] = u64x2{w[2], w[3]};
+    } else {
+#pragma unroll
+      for (uint32_t e = 0; e < 4; ++e)
+        if (e < cells) out[e] = w[e];
+    }
+  }
+  const uint64_t voters = __ballot(violation);
+  if (voters != 0 && (threadIdx.x & 63u) == static_cast<uint32_t>(__ffsll(static_cast<long long>(voters)) - 1) &&
+      __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u)
+    atomicOr(a.status, 1u);
+}
+
+// Zero-output tiles: their cells are 0 (reference cpu_reference.cpp:243-246
+// and the export's zero branch); same grid as export_tiles_kernel.
+__global__ __launch_bounds__(256) void export_zero_tiles_kernel(ExportArgs a, const TileExport* tiles,
+                                                                uint32_t gpr_log2, uint32_t rows_per_pass) {
+  const TileExport t = tiles[blockIdx.x];
+  const uint32_t r = blockIdx.y * rows_per_pass + (threadIdx.x >> gpr_log2);
+  const uint32_t cg = threadIdx.x & ((1u << gpr_log2) - 1u);
+  if (r >= t.rows || 4u * cg >= t.cols) return;
+  const uint32_t cells = t.cols - 4u * cg < 4u ? t.cols - 4u * cg : 4u;
+  uint64_t* const out =
+      static_cast<uint64_t*>(a.dst) + (static_cast<int64_t>(t.row_off) + r) * a.ld + t.col_off + 4 * cg;
+  for (uint32_t e = 0; e < cells; ++e) out[e] = 0ull;
+}
+
 __global__ __launch_bounds__(256) void export_u8_kernel(ExportU8Args a, uint32_t groups_per_row) {
   const uint32_t gc = blockIdx.x * blockDim.x + threadIdx.x;
   if (gc >= groups_per_row) return;
@@ -331,7 +396,68 @@ hipError_t dispatch_prefix(uint32_t prefix, const ExportArgs& a, const ExportLim
   return err;
 }
 
+// Tiles of schedule edge tile_m x tile_n (powers of two, 64 .. 512): 4-cell
+// column groups per tile row and the rows one 256-thread pass covers.
+struct TileGrid {
+  uint32_t gpr_log2, rows_per_pass;
+  dim3 grid;
+};
+bool tile_grid(uint32_t tile_m, uint32_t tile_n, uint32_t count, TileGrid& g) {
+  auto pow2 = [](uint32_t v) { return v >= 64 && v <= 512 && (v & (v - 1u)) == 0; };
+  if (!pow2(tile_m) || !pow2(tile_n) || count == 0 || count > 0x7FFFFFFFu) return false;
+  g.gpr_log2 = static_cast<uint32_t>(__builtin_ctz(tile_n / 4u));
+  g.rows_per_pass = 256u >> g.gpr_log2;
+  g.grid = dim3(count, (tile_m + g.rows_per_pass - 1) / g.rows_per_pass);
+  return true;
+}
+
+bool tile_args_ok(const ExportArgs& a) {
+  if (!a.c || !a.dst || a.m <= 0 || a.n <= 0 || a.ld < a.n || a.limbs != 1) return false;
+  if (a.kind != ExportKind::I64 && a.kind != ExportKind::U64) return false;
+  if (a.m >= (int64_t{1} << 31) || a.n >= (int64_t{1} << 31)) return false;
+  if (a.ldc != padded_ld(a.n) || a.pitch_c < a.m * a.ldc || (a.pitch_c % 4) != 0) return false;
+  return (reinterpret_cast<uintptr_t>(a.c) & 3u) == 0;
+}
+
+template <uint32_t P>
+hipError_t launch_export_tiles_p(const ExportArgs& a, const TileExport* tiles, const TileGrid& g, hipStream_t stream) {
+  constexpr int L = P <= 9 ? 3 : 7;
+  const uint32_t vec = (reinterpret_cast<uintptr_t>(a.dst) % 16 == 0 && a.ld % 2 == 0) ? 1u : 0u;
+  if (a.kind == ExportKind::I64)
+    hipLaunchKernelGGL((export_tiles_kernel<P, L, ExportKind::I64>), g.grid, dim3(256), 0, stream, a, tiles,
+                       g.gpr_log2, g.rows_per_pass, vec);
+  else
+    hipLaunchKernelGGL((export_tiles_kernel<P, L, ExportKind::U64>), g.grid, dim3(256), 0, stream, a, tiles,
+                       g.gpr_log2, g.rows_per_pass, vec);
+  return hipGetLastError();
+}
+
+template <uint32_t... Ps>
+hipError_t dispatch_tiles(uint32_t prefix, const ExportArgs& a, const TileExport* tiles, const TileGrid& g,
+                          hipStream_t stream, std::integer_sequence<uint32_t, Ps...>) {
+  hipError_t err = hipErrorInvalidValue;
+  ((prefix == Ps + 1 ? (err = launch_export_tiles_p<Ps + 1>(a, tiles, g, stream), 0) : 0), ...);
+  return err;
+}
+
 }  // namespace
+
+hipError_t launch_export_tiles(const ExportArgs& a, uint32_t prefix, const TileExport* d_tiles, uint32_t count,
+                               uint32_t tile_m, uint32_t tile_n, hipStream_t stream) {
+  TileGrid g;
+  if (!tile_args_ok(a) || !a.status || !d_tiles || !tile_grid(tile_m, tile_n, count, g)) return hipErrorInvalidValue;
+  if (prefix == 0 || prefix > kMaxPrefix) return hipErrorInvalidValue;
+  return dispatch_tiles(prefix, a, d_tiles, g, stream, std::make_integer_sequence<uint32_t, kMaxPrefix>{});
+}
+
+hipError_t launch_export_zero_tiles(const ExportArgs& a, const TileExport* d_tiles, uint32_t count, uint32_t tile_m,
+                                    uint32_t tile_n, hipStream_t stream) {
+  TileGrid g;
+  if (!tile_args_ok(a) || !d_tiles || !tile_grid(tile_m, tile_n, count, g)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(export_zero_tiles_kernel, g.grid, dim3(256), 0, stream, a, d_tiles, g.gpr_log2,
+                     g.rows_per_pass);
+  return hipGetLastError();
+}
 
 hipError_t launch_export(const ExportArgs& a, uint32_t prefix, hipStream_t stream) {
   if (!a.c || !a.dst || !a.status || a.m <= 0 || a.n <= 0 || a.ld < a.n) return hipErrorInvalidValue;

@@ -194,6 +194,9 @@ struct UnitMap {
   DivU31 rows;    // kGroupM: tile rows of a full group
   DivU31 tail;    // tile rows of the last group (tiles_m - its first row)
   uint32_t k_begin, k_stop, k_slice;
+  // listed launches: two words per unit, (plane << 24 | tile row) and
+  // (quadrant mask << 24 | tile column), in place of the arithmetic order
+  const uint32_t* list;
 };
 
 // Reads accumulator elements 4g .. 4g+3 straight from their AGPRs. The asm
@@ -218,7 +221,7 @@ __device__ __forceinline__ Acc4 acc_read4(const v16i& acc, int g) {
 // floor(n / d) for n < 2^31 (make_div_u31).
 __device__ __forceinline__ uint32_t div_u31(uint32_t n, DivU31 v) { return __umulhi(n << 1, v.mul) >> v.shift; }
 
-template <typename C, int kMinBlocks, bool kUniform>
+template <typename C, int kMinBlocks, bool kUniform, bool kListed = false>
 __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmArgs args, PlaneConsts pc, UnitMap map,
                                                                            uint32_t accumulate) {
   constexpr int WM = C::kWM, WN = C::kWN, BM = C::BM, BN = C::BN, BK = C::BK;
@@ -259,10 +262,28 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
   // the host's reciprocals, branch-free, so the cursor below can advance
   // every K step without splitting the loop body.
   struct Unit {
-    uint32_t plane, slice, m0, n0, kbeg, kend, ktiles;
+    uint32_t plane, slice, m0, n0, kbeg, kend, ktiles, quad;
   };
+  // Listed units come from a per-tile schedule: a 128 x 128 tile of one plane
+  // whose four 64 x 64 quadrants (one per wave) are stored only where the
+  // mask has their bit (wave_m * 2 + wave_n); quadrants outside the tiles that
+  // select this plane keep their contents.
+  static_assert(!kListed || (C::kWM == 2 && C::kWN == 2), "quadrant masks assume 64 x 64 wave tiles");
   auto decode = [&](uint32_t u) {
     Unit U;
+    if constexpr (kListed) {
+      const uint32_t w0 = map.list[2u * u], w1 = map.list[2u * u + 1u];
+      U.plane = w0 >> 24;
+      U.slice = 0;
+      U.m0 = (w0 & 0xFFFFFFu) * BM;
+      U.n0 = (w1 & 0xFFFFFFu) * BN;
+      U.quad = w1 >> 24;
+      U.kbeg = map.k_begin;
+      U.kend = map.k_stop;
+      U.ktiles = (U.kend - U.kbeg + BK - 1) / BK;
+      return U;
+    }
+    U.quad = 0xFu;
     const uint32_t plane_slice = div_u31(u, map.tiles);
     const uint32_t pid = u - plane_slice * map.tiles.d;
     U.slice = div_u31(plane_slice, map.planes);
@@ -459,6 +480,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
       return (full_cols || col < col_room) ? off + static_cast<uint32_t>(col) : 0x80000000u;
     };
     if (args.slices <= 1) {
+      // a listed unit's wave stores its quadrant only if the mask selects it
+      if (kListed && ((U.quad >> (wave_m * 2 + wave_n)) & 1u) == 0u) return;
       int8_t* const Cp = args.c + static_cast<int64_t>(U.plane) * args.pitch_c + U.m0 * args.ldc + U.n0;
       const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(Cp, tile_rows * args.ldc - U.n0);
       const uint32_t m_comp = 256u - mc.m;
@@ -679,6 +702,27 @@ __global__ __launch_bounds__(256) void splitk_finalize_kernel(const int32_t* ws,
   }
 }
 
+// Zero-output tiles of a per-tile schedule: planes [0, planes) of each tile's
+// rows and columns are set to 0 (reference cpu_reference.cpp:243-246). Whole
+// 16-byte chunks are written: a tile's column offset is a multiple of 64, and
+// the last tile column's chunks end inside the padded pitch.
+__global__ __launch_bounds__(256) void zero_tiles_kernel(int8_t* c, int64_t ldc, int64_t pitch_c,
+                                                         const TileFill* tiles) {
+  const TileFill t = tiles[blockIdx.x];
+  const uint32_t chunks = (t.cols + 15u) / 16u;
+  const uint64_t per_plane = static_cast<uint64_t>(t.rows) * chunks;
+  const uint64_t total = per_plane * t.planes;
+  for (uint64_t i = threadIdx.x; i < total; i += blockDim.x) {
+    const uint32_t p = static_cast<uint32_t>(i / per_plane);
+    const uint64_t rem = i - static_cast<uint64_t>(p) * per_plane;
+    const uint32_t r = static_cast<uint32_t>(rem / chunks);
+    const uint32_t ch = static_cast<uint32_t>(rem - static_cast<uint64_t>(r) * chunks);
+    int8_t* const dst = c + static_cast<int64_t>(p) * pitch_c + static_cast<int64_t>(t.row_off + r) * ldc + t.col_off +
+                        16 * ch;
+    *reinterpret_cast<v4i*>(dst) = v4i{0, 0, 0, 0};
+  }
+}
+
 __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* dst, uint64_t words) {
   for (uint64_t w = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < words;
        w += static_cast<uint64_t>(gridDim.x) * blockDim.x)
@@ -822,6 +866,39 @@ hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipS
 }
 
 }  // namespace
+
+hipError_t launch_gemm_listed(const GemmArgs& args, const PlaneConsts& consts, const uint32_t* d_units,
+                              uint32_t units, hipStream_t stream) {
+  // the list's entries are checked against the shape where it is built
+  if (!gemm_shape_ok(args) || args.slices != 1 || !d_units || units > 0x7FFFFFFFu) return hipErrorInvalidValue;
+  if (units == 0) return hipSuccess;
+  constexpr int kMinBlocks = 2;
+  const uint64_t slots = static_cast<uint64_t>(device_cu_count()) * kMinBlocks;
+  uint64_t grid = units < slots ? units : slots;
+  if (grid >= 8) grid -= grid % 8;
+  for (int64_t kb = 0; kb < args.k; kb += kSafeKBlock) {
+    const int64_t kstop = min(args.k, kb + kSafeKBlock);
+    UnitMap map{};
+    map.units = units;
+    map.k_begin = static_cast<uint32_t>(kb);
+    map.k_stop = static_cast<uint32_t>(kstop);
+    map.k_slice = static_cast<uint32_t>(kstop - kb);
+    map.list = d_units;
+    hipLaunchKernelGGL((plane_gemm_kernel<CfgSmall, kMinBlocks, true, true>), dim3(static_cast<unsigned>(grid)),
+                       dim3(kThreads), 0, stream, args, consts, map, kb > 0 ? 1u : 0u);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_zero_tiles(int8_t* c, int64_t ldc, int64_t pitch_c, const TileFill* d_tiles, uint32_t count,
+                             hipStream_t stream) {
+  if (count == 0) return hipSuccess;
+  if (!c || !d_tiles || ldc <= 0 || ldc % 16 || pitch_c < ldc || count > 0x7FFFFFFFu) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(zero_tiles_kernel, dim3(count), dim3(256), 0, stream, c, ldc, pitch_c, d_tiles);
+  return hipGetLastError();
+}
 
 hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream) {
   if (!gemm_shape_ok(args)) return hipErrorInvalidValue;

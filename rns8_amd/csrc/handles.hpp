@@ -11,6 +11,7 @@
 #include "rns8/rns8.h"
 #include "rns8_mi355x.h"
 #include "host_copy.hpp"
+#include "kernels.hpp"
 #include "tables.hpp"
 #include "wide_int.hpp"
 
@@ -34,6 +35,20 @@ struct rns8_context {
   rns8x::HostStaging host;  // pinned staging for host-memory operands and results
 };
 
+// Per-tile bounded schedule (reference src/core/internal.hpp:22-70, the
+// rns8_plan schedule_* fields and tile_schedule). For a per-tile plan `entries`
+// lists every tile's prefixes; it is empty when every tile runs the plan
+// prefix without flags (the schedule collapses), and always empty for global
+// plans.
+struct TileSchedule {
+  std::vector<uint64_t> bounds;
+  std::vector<rns8_plan_tile_schedule_entry> entries;
+  std::vector<uint8_t> zero_a_rows, zero_b_cols;
+  uint32_t min_required = 0, max_required = 0, min_selected = 0, max_selected = 0;
+  uint32_t groups = 0, adaptive_prefix = 0, adaptive_skip = 0, range_bits = 0, flags = 0;
+  uint64_t zero_a_row_count = 0, zero_b_col_count = 0, zero_row_col_product_count = 0;
+};
+
 struct rns8_plan {
   rns8_gemm_desc desc{};  // caller descriptor; max_prefix holds the budget, tiles defaulted to 128
   rns8_backend_kind backend = RNS8_BACKEND_HIP_DIRECT;
@@ -46,6 +61,21 @@ struct rns8_plan {
   uint64_t tile_rows = 0, tile_cols = 0, tile_count = 0;
   uint32_t splitk_slices = 1;
   uint64_t splitk_bytes = 0;
+  TileSchedule schedule;  // per-tile bound kinds only
+  // Per-tile plans: device lists the GEMM and export run from, built when the
+  // plan is created and never changed. `units` (two words per unit, see
+  // launch_gemm_listed) is empty when every tile runs the plan prefix; then
+  // the ordinary GEMM runs. `export_tiles` holds one record per tile, ordered
+  // by selected prefix, in `export_groups`; prefix 0 marks zero-output tiles.
+  struct ExportGroup {
+    uint32_t prefix, first, count;
+  };
+  uint32_t* units = nullptr;
+  uint32_t unit_count = 0;
+  rns8x::TileFill* zero_fills = nullptr;
+  uint32_t zero_fill_count = 0;
+  rns8x::TileExport* export_tiles = nullptr;
+  std::vector<ExportGroup> export_groups;
 };
 
 struct rns8_matrix {
@@ -153,8 +183,19 @@ hipStream_t pick_stream(const rns8_context& ctx, void* stream);
 
 // matrix storage: storage prefix / bound kind a plan expects of its operands
 uint32_t storage_prefix(const rns8_plan& p);
+bool per_tile_kind(rns8_bound_kind b);
+// plan state that needs no device (validation, prefixes, tiles, schedule)
+rns8_status init_plan(const rns8_gemm_desc& d, rns8_backend_kind backend, rns8_plan& plan);
+// reference api_plan_schedule.inc:109-261 (per-tile branch)
+rns8_status build_tile_schedule(const rns8_gemm_desc& d, uint32_t budget, TileSchedule& s);
+// rns8_get_plan_tile_schedule's entries for a plan (api_plan_public_api.inc:119-160)
+void plan_tile_entries(const rns8_plan& p, rns8_plan_tile_schedule_entry* out);
+// Builds and uploads a per-tile plan's device lists (no-op for other plans);
+// the current device must be the plan's.
+rns8_status upload_tile_lists(rns8_plan& p, hipStream_t stream);
+void free_tile_lists(rns8_plan& p);
 rns8_bound_kind storage_bound_kind(const rns8_plan& p);
 bool matrix_matches(const rns8_matrix& m, rns8_semantics s, rns8_bound_kind bk, int64_t rows, int64_t cols,
-                    uint32_t prefix);
+                    uint32_t prefix, uint32_t tile_m = 0, uint32_t tile_n = 0);
 
 }  // namespace rns8x

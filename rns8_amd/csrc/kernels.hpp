@@ -62,6 +62,19 @@ struct GemmArgs {
   uint32_t slices;
 };
 hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream);
+// Per-tile schedules: `units` 128 x 128 tile-planes from a device list of two
+// words each, (plane << 24 | tile row) and (quadrant mask << 24 | tile column);
+// bit q = 2 * (row half) + (column half) of the mask enables the stores of that
+// 64 x 64 quadrant. No K split; K beyond 65536 runs as accumulating launches.
+hipError_t launch_gemm_listed(const GemmArgs& args, const PlaneConsts& consts, const uint32_t* d_units,
+                              uint32_t units, hipStream_t stream);
+// Zero-output tiles: planes [0, planes) of each tile set to 0; records are
+// checked against the shape where they are built.
+struct TileFill {
+  uint32_t row_off, col_off, rows, cols, planes;
+};
+hipError_t launch_zero_tiles(int8_t* c, int64_t ldc, int64_t pitch_c, const TileFill* d_tiles, uint32_t count,
+                             hipStream_t stream);
 // Tile edge (256 or 128) and K slices the launcher uses for this shape
 // (k is the K of one launch block, at most 65536).
 struct GemmShape {
@@ -91,6 +104,22 @@ struct ExportArgs {
   uint32_t* status; // device word; set nonzero on any range violation
 };
 hipError_t launch_export(const ExportArgs& args, uint32_t prefix, hipStream_t stream);
+
+// Per-tile export (bounded int64 / uint64): one record per schedule tile,
+// cells [row_off, row_off + rows) x [col_off, col_off + cols), admissible
+// magnitudes pos64 (v >= 0) and neg64 (v < 0). The tiles of one call share
+// the prefix; tile_m / tile_n are the schedule's tile edges (64 .. 512), which
+// every record's extent is within. The records are checked against the shape
+// where they are built.
+struct TileExport {
+  uint32_t row_off, col_off, rows, cols;
+  uint64_t pos64, neg64;
+};
+hipError_t launch_export_tiles(const ExportArgs& a, uint32_t prefix, const TileExport* d_tiles, uint32_t count,
+                               uint32_t tile_m, uint32_t tile_n, hipStream_t stream);
+// Zero-output tiles: their cells of dst set to 0 (a.status is not used).
+hipError_t launch_export_zero_tiles(const ExportArgs& a, const TileExport* d_tiles, uint32_t count, uint32_t tile_m,
+                                    uint32_t tile_n, hipStream_t stream);
 
 struct ExportU8Args {
   const int8_t* c;
