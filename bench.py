@@ -37,7 +37,12 @@ CONFIGS = {
     "c3": ("i64", 4096, 4096, 4096, 25, 1 << 62, 9, True),
     "c1": ("i64", 256, 256, 256, 20, 256 << 40, 0, False),
     "c5": ("u64", 128, 128, 65536, 23, 1 << 62, 0, False),
+    # per-tile bounds (128 x 128 tiles) on C3's shape: A's tile rows cycle
+    # through magnitudes 2^1 .. 2^25, so tiles select prefixes 5 .. 9
+    "tiled": ("i64", 4096, 4096, 4096, 25, 1 << 62, 9, False),
 }
+TILED_EDGE = 128
+TILED_ROW_BITS = [1, 5, 9, 13, 17, 21, 25]
 
 
 def log(msg: str) -> None:
@@ -81,17 +86,30 @@ def main() -> int:
         A = inputs.uint_range(inputs.operand_seed(args.seed, "A"), (M, K), bits)
         B = inputs.uint_range(inputs.operand_seed(args.seed, "B"), (K, N), bits)
 
+    tiled = args.config == "tiled"
     ctx = r.Context()
     semantics = r.BOUNDED_I64 if signed else r.BOUNDED_U64
     bk = r.BOUND_GLOBAL_MAX_ABS if signed else r.BOUND_GLOBAL_MAX_UNSIGNED
-    desc = r.gemm_desc(semantics, bk, M, N, K, bound=bound, max_prefix=budget,
-                       flags=r.PLAN_FORCE_FIXED_PREFIX if forced else 0)
+    tile = 0
+    if tiled:
+        A, tile_bounds = tiled_operands(A, bits, N, K)
+        bk, tile = r.BOUND_PER_TILE_MAX_ABS, TILED_EDGE
+        desc = r.gemm_desc(semantics, bk, M, N, K, max_prefix=budget, tile_m=tile, tile_n=tile,
+                           tile_bounds=tile_bounds)
+    else:
+        desc = r.gemm_desc(semantics, bk, M, N, K, bound=bound, max_prefix=budget,
+                           flags=r.PLAN_FORCE_FIXED_PREFIX if forced else 0)
     plan = r.Plan(ctx, desc)
     P = plan.prefix
-    Am = r.Matrix(ctx, r.matrix_desc(M, K, semantics, bk, P))
-    Bm = r.Matrix(ctx, r.matrix_desc(K, N, semantics, bk, P))
-    Cm = r.Matrix(ctx, r.matrix_desc(M, N, semantics, bk, P))
+    Am = r.Matrix(ctx, r.matrix_desc(M, K, semantics, bk, P, tile_m=tile, tile_n=tile))
+    Bm = r.Matrix(ctx, r.matrix_desc(K, N, semantics, bk, P, tile_m=tile, tile_n=tile))
+    Cm = r.Matrix(ctx, r.matrix_desc(M, N, semantics, bk, P, tile_m=tile, tile_n=tile))
     ws = r.Workspace(ctx, plan)
+    # int8 MFMA ops the GEMM must do: every plane of every cell, or, per tile,
+    # the planes its schedule selects
+    gemm_ops = 2.0 * M * N * K * P
+    if tiled:
+        gemm_ops = sum(2.0 * e.row_extent * e.col_extent * K * e.selected_prefix for e in plan.tile_schedule())
     log(f"[bench] prefix {P}")
 
     dA = hip.malloc(A.nbytes)
@@ -159,8 +177,17 @@ def main() -> int:
     hip.from_device(Cout, dC)
     ops = 2.0 * M * N * K
     value = ops / (ms_per_step * 1e-3) / 1e12
-    gemm_ops = ops * P
     achieved = gemm_ops / (stage[2] * 1e-3) / 1e12
+    if tiled:
+        workload = (f"RNS8_BOUNDED_I64 {M}x{N}x{K}, per-tile bounds ({tile}x{tile} tiles, A tile rows at "
+                    f"2^{TILED_ROW_BITS} cycling, B at 2^{bits}), storage prefix {P}, pack+GEMM+Garner device-resident")
+        kernel = "plane_gemm_kernel<Cfg<4,4>,1,true,true> (listed 256x256 units, persistent)"
+    elif args.config == "c3":
+        workload = f"RNS8_BOUNDED_I64 {M}x{N}x{K} prefix {P} (FORCE_FIXED_PREFIX), pack+GEMM+Garner device-resident"
+        kernel = "plane_gemm_kernel<Cfg<4,4>,1,true> (256x256 tiles, persistent)"
+    else:
+        workload = f"{args.config} {sem} {M}x{N}x{K} prefix {P}"
+        kernel = "plane_gemm_kernel (persistent)"
 
     result = {
         "metric": "exact int64 GEMM effective TOPS (2MNK/s) at 4096\u00b3 prefix 9; % int8 MFMA peak",
@@ -176,16 +203,15 @@ def main() -> int:
         "dtype": "int64 (int8 residue MFMA)",
         "data": "synthetic: SplitMix64 uniform [-2^25, 2^25) int64 operands, resident in HBM",
         "config": {
-            "workload": f"RNS8_BOUNDED_I64 {M}x{N}x{K} prefix {P} (FORCE_FIXED_PREFIX), pack+GEMM+Garner device-resident"
-            if args.config == "c3" else f"{args.config} {sem} {M}x{N}x{K} prefix {P}",
-            "m": M, "n": N, "k": K, "prefix": P, "bound": str(bound),
+            "workload": workload,
+            "m": M, "n": N, "k": K, "prefix": P, "bound": "per tile" if tiled else str(bound),
             "stage_ms": {"pack_a": round(stage[0], 4), "pack_b": round(stage[1], 4), "gemm": round(stage[2], 4),
                          "export": round(stage[3], 4)},
             "range_status": int(status[0]),
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "plane_gemm_kernel<Cfg<4,4>,1,true> (256x256 tiles, persistent)",
+            "kernel": kernel,
             "achieved": round(achieved, 2),
             "peak": PEAK_INT8_TOPS,
             "unit": "TOP/s",
@@ -196,7 +222,13 @@ def main() -> int:
         "cpu_baseline": None,
     }
 
-    if not args.no_cpu:
+    if tiled:
+        # exact in int64 (|C| <= 2^62): sampled rows of every tile row against numpy
+        rows = np.arange(0, M, TILED_EDGE // 2)
+        want = A[rows].astype(np.int64) @ B.astype(np.int64)
+        result["config"]["rows_bit_exact"] = bool(np.array_equal(Cout[rows], want))
+        log(f"[bench] {len(rows)} sampled rows bit-exact: {result['config']['rows_bit_exact']}")
+    elif not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args, A, B, Cout, P, bound, signed)
 
     print(json.dumps(result))
@@ -255,6 +287,20 @@ def cpu_baseline(args, A, B, Cout, P, bound, signed) -> dict:
                   f"{t_cpu:.2f} s per run, {reps} run(s), on {threads} threads of {_cpu_model()}",
         "rows_bit_exact_vs_gpu": match,
     }
+
+
+def tiled_operands(A, bits, N, K):
+    """A with its 128-row blocks scaled to |a| <= 2^TILED_ROW_BITS[i % 7]
+    (arithmetic shift of the 2^bits operand), and the per-tile bounds
+    K * 2^row_bits * 2^bits (|b| <= 2^bits), row-major over 128 x 128 tiles."""
+    A = A.copy()
+    tiles_m, tiles_n = -(-A.shape[0] // TILED_EDGE), -(-N // TILED_EDGE)
+    bounds = []
+    for t in range(tiles_m):
+        row_bits = TILED_ROW_BITS[t % len(TILED_ROW_BITS)]
+        A[t * TILED_EDGE:(t + 1) * TILED_EDGE] >>= bits - row_bits
+        bounds += [K << (row_bits + bits)] * tiles_n
+    return A, bounds
 
 
 def traffic_from_profiles(kernel_prefix: str, workload: str):

@@ -21,6 +21,8 @@ from .abi import (  # noqa: F401  (re-exported constants)
     BOUND_GLOBAL_MAX_UNSIGNED,
     BOUND_INPUT_RANGE_AND_K,
     BOUND_NONE,
+    BOUND_PER_TILE_MAX_ABS,
+    BOUND_PER_TILE_MAX_UNSIGNED,
     BOUNDED_I64,
     BOUNDED_U64,
     EXACT_WIDE_SIGNED,
@@ -28,6 +30,7 @@ from .abi import (  # noqa: F401  (re-exported constants)
     FINITE_FIELD_U8,
     FINITE_RING_U8,
     INVALID_ARGUMENT,
+    PLAN_ALLOW_PROVEN_ZERO_TILE_SKIPS,
     PLAN_FORCE_FIXED_PREFIX,
     RANGE_ERROR,
     SUCCESS,

@@ -428,7 +428,8 @@ rns8_status run_gemm_tiled(rns8_context& ctx, const rns8_plan& plan, const rns8_
   g.nplanes = planes;
   g.slices = 1;
   if (hipSetDevice(ctx.device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
-  hipError_t e = launch_gemm_listed(g, make_ladder_plane_consts(planes), plan.units, plan.unit_count, stream);
+  hipError_t e = launch_gemm_listed(g, make_ladder_plane_consts(planes), plan.units, plan.unit_count,
+                                    plan.unit_edge, stream);
   if (e == hipErrorInvalidValue) return RNS8_UNSUPPORTED_BACKEND;
   if (e == hipSuccess) e = launch_zero_tiles(C.planes, C.plane_ld, C.plane_pitch, plan.zero_fills,
                                              plan.zero_fill_count, stream);

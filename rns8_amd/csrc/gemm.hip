@@ -264,11 +264,11 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
   struct Unit {
     uint32_t plane, slice, m0, n0, kbeg, kend, ktiles, quad;
   };
-  // Listed units come from a per-tile schedule: a 128 x 128 tile of one plane
-  // whose four 64 x 64 quadrants (one per wave) are stored only where the
-  // mask has their bit (wave_m * 2 + wave_n); quadrants outside the tiles that
+  // Listed units come from a per-tile schedule: a BM x BN tile of one plane
+  // whose four quadrants (one per wave, 2 x 2) are stored only where the mask
+  // has their bit (wave_m * 2 + wave_n); quadrants outside the tiles that
   // select this plane keep their contents.
-  static_assert(!kListed || (C::kWM == 2 && C::kWN == 2), "quadrant masks assume 64 x 64 wave tiles");
+  static_assert(kThreads == 256, "quadrant masks assume four waves in a 2 x 2 grid");
   auto decode = [&](uint32_t u) {
     Unit U;
     if constexpr (kListed) {
@@ -867,12 +867,11 @@ hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipS
 
 }  // namespace
 
-hipError_t launch_gemm_listed(const GemmArgs& args, const PlaneConsts& consts, const uint32_t* d_units,
-                              uint32_t units, hipStream_t stream) {
-  // the list's entries are checked against the shape where it is built
-  if (!gemm_shape_ok(args) || args.slices != 1 || !d_units || units > 0x7FFFFFFFu) return hipErrorInvalidValue;
-  if (units == 0) return hipSuccess;
-  constexpr int kMinBlocks = 2;
+namespace {
+
+template <typename Cf, int kMinBlocks>
+hipError_t launch_listed(const GemmArgs& args, const PlaneConsts& consts, const uint32_t* d_units, uint32_t units,
+                         hipStream_t stream) {
   const uint64_t slots = static_cast<uint64_t>(device_cu_count()) * kMinBlocks;
   uint64_t grid = units < slots ? units : slots;
   if (grid >= 8) grid -= grid % 8;
@@ -884,12 +883,24 @@ hipError_t launch_gemm_listed(const GemmArgs& args, const PlaneConsts& consts, c
     map.k_stop = static_cast<uint32_t>(kstop);
     map.k_slice = static_cast<uint32_t>(kstop - kb);
     map.list = d_units;
-    hipLaunchKernelGGL((plane_gemm_kernel<CfgSmall, kMinBlocks, true, true>), dim3(static_cast<unsigned>(grid)),
+    hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks, true, true>), dim3(static_cast<unsigned>(grid)),
                        dim3(kThreads), 0, stream, args, consts, map, kb > 0 ? 1u : 0u);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
   return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_gemm_listed(const GemmArgs& args, const PlaneConsts& consts, const uint32_t* d_units,
+                              uint32_t units, uint32_t edge, hipStream_t stream) {
+  // the list's entries are checked against the shape and edge where it is built
+  if (!gemm_shape_ok(args) || args.slices != 1 || !d_units || units > 0x7FFFFFFFu) return hipErrorInvalidValue;
+  if (units == 0) return hipSuccess;
+  if (edge == 256) return launch_listed<CfgLarge, 1>(args, consts, d_units, units, stream);
+  if (edge == 128) return launch_listed<CfgSmall, 2>(args, consts, d_units, units, stream);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_zero_tiles(int8_t* c, int64_t ldc, int64_t pitch_c, const TileFill* d_tiles, uint32_t count,

@@ -72,6 +72,7 @@ struct rns8_plan {
   };
   uint32_t* units = nullptr;
   uint32_t unit_count = 0;
+  uint32_t unit_edge = 0;  // 256 or 128: output tile edge of a listed unit
   rns8x::TileFill* zero_fills = nullptr;
   uint32_t zero_fill_count = 0;
   rns8x::TileExport* export_tiles = nullptr;

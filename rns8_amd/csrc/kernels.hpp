@@ -62,12 +62,13 @@ struct GemmArgs {
   uint32_t slices;
 };
 hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream);
-// Per-tile schedules: `units` 128 x 128 tile-planes from a device list of two
-// words each, (plane << 24 | tile row) and (quadrant mask << 24 | tile column);
-// bit q = 2 * (row half) + (column half) of the mask enables the stores of that
-// 64 x 64 quadrant. No K split; K beyond 65536 runs as accumulating launches.
+// Per-tile schedules: `units` edge x edge tile-planes (edge 256 or 128) from a
+// device list of two words each, (plane << 24 | tile row) and (quadrant mask
+// << 24 | tile column); bit q = 2 * (row half) + (column half) of the mask
+// enables the stores of that edge/2 x edge/2 quadrant. No K split; K beyond
+// 65536 runs as accumulating launches.
 hipError_t launch_gemm_listed(const GemmArgs& args, const PlaneConsts& consts, const uint32_t* d_units,
-                              uint32_t units, hipStream_t stream);
+                              uint32_t units, uint32_t edge, hipStream_t stream);
 // Zero-output tiles: planes [0, planes) of each tile set to 0; records are
 // checked against the shape where they are built.
 struct TileFill {

@@ -3,10 +3,12 @@
 // GEMM (reference cpu_reference.cpp:231-257, the GEMM over a tile schedule):
 // planes [0, selected) of every tile are computed, zero-output tiles get 0 in
 // those planes, and planes from a tile's selected prefix up are left as they
-// are. The listed GEMM runs 128 x 128 output tiles of one plane, each split
-// into four 64 x 64 quadrants (one per wave); since schedule tiles are powers
-// of two from 64 to 512, every quadrant lies in exactly one schedule tile, and
-// a unit's quadrant mask holds the quadrants whose tile computes that plane.
+// are. The listed GEMM runs output tiles of one plane (256 x 256, or 128 x 128
+// when a schedule tile edge is 64 or the larger units would leave CUs idle),
+// each split into four quadrants, one per wave; since schedule tiles are powers
+// of two from 64 to 512 and at least as large as a quadrant, every quadrant
+// lies in exactly one schedule tile, and a unit's quadrant mask holds the
+// quadrants whose tile computes that plane.
 //
 // Export (reference api_export.cpp:365-410 with per-tile bounds): each tile is
 // reconstructed with its own selected prefix and bound, zero-output tiles
@@ -19,9 +21,8 @@
 namespace rns8x {
 namespace {
 
-constexpr uint32_t kUnitEdge = 128;  // listed GEMM output tile
-constexpr uint32_t kQuadEdge = 64;   // one wave's quadrant of it
 constexpr uint32_t kUnitGroupRows = 4;  // tile rows walked together (neighbours share A / B panels in L2)
+constexpr uint64_t kLargeUnitsMin = 256;  // large units only when every CU gets one
 
 template <typename T>
 rns8_status upload(const std::vector<T>& host, T** dev, hipStream_t stream) {
@@ -85,29 +86,39 @@ rns8_status upload_tile_lists(rns8_plan& p, hipStream_t stream) {
   std::vector<TileFill> fills;
   if (!p.schedule.entries.empty()) {
     const uint32_t planes = storage_prefix(p);
-    const uint32_t tiles_m = static_cast<uint32_t>((m + kUnitEdge - 1) / kUnitEdge);
-    const uint32_t tiles_n = static_cast<uint32_t>((n + kUnitEdge - 1) / kUnitEdge);
-    if (tiles_m >= (1u << 24) || tiles_n >= (1u << 24) || planes > kMaxPrefix) return RNS8_UNSUPPORTED_BACKEND;
-    auto quad_tile = [&](uint32_t tr, uint32_t tc, uint32_t q) -> const rns8_plan_tile_schedule_entry* {
-      const int64_t r0 = int64_t{tr} * kUnitEdge + (q >> 1) * kQuadEdge;
-      const int64_t c0 = int64_t{tc} * kUnitEdge + (q & 1u) * kQuadEdge;
-      if (r0 >= m || c0 >= n) return nullptr;
-      return &entries[static_cast<std::size_t>((r0 / tm) * static_cast<int64_t>(p.tile_cols) + c0 / tn)];
-    };
-    for (uint32_t plane = 0; plane < planes; ++plane)
-      for (uint32_t g0 = 0; g0 < tiles_m; g0 += kUnitGroupRows)
-        for (uint32_t tc = 0; tc < tiles_n; ++tc)
-          for (uint32_t tr = g0; tr < std::min(tiles_m, g0 + kUnitGroupRows); ++tr) {
-            uint32_t mask = 0;
-            for (uint32_t q = 0; q < 4; ++q) {
-              const auto* e = quad_tile(tr, tc, q);
-              if (e && !zero_output(*e) && plane < e->selected_prefix) mask |= 1u << q;
+    if (planes > kMaxPrefix) return RNS8_UNSUPPORTED_BACKEND;
+    auto build_units = [&](uint32_t edge) -> bool {
+      units.clear();
+      const uint32_t quad = edge / 2;
+      const uint32_t tiles_m = static_cast<uint32_t>((m + edge - 1) / edge);
+      const uint32_t tiles_n = static_cast<uint32_t>((n + edge - 1) / edge);
+      if (tiles_m >= (1u << 24) || tiles_n >= (1u << 24)) return false;
+      auto quad_tile = [&](uint32_t tr, uint32_t tc, uint32_t q) -> const rns8_plan_tile_schedule_entry* {
+        const int64_t r0 = int64_t{tr} * edge + (q >> 1) * quad;
+        const int64_t c0 = int64_t{tc} * edge + (q & 1u) * quad;
+        if (r0 >= m || c0 >= n) return nullptr;
+        return &entries[static_cast<std::size_t>((r0 / tm) * static_cast<int64_t>(p.tile_cols) + c0 / tn)];
+      };
+      for (uint32_t plane = 0; plane < planes; ++plane)
+        for (uint32_t g0 = 0; g0 < tiles_m; g0 += kUnitGroupRows)
+          for (uint32_t tc = 0; tc < tiles_n; ++tc)
+            for (uint32_t tr = g0; tr < std::min(tiles_m, g0 + kUnitGroupRows); ++tr) {
+              uint32_t mask = 0;
+              for (uint32_t q = 0; q < 4; ++q) {
+                const auto* e = quad_tile(tr, tc, q);
+                if (e && !zero_output(*e) && plane < e->selected_prefix) mask |= 1u << q;
+              }
+              if (!mask) continue;
+              units.push_back(plane << 24 | tr);
+              units.push_back(mask << 24 | tc);
             }
-            if (!mask) continue;
-            units.push_back(plane << 24 | tr);
-            units.push_back(mask << 24 | tc);
-          }
-    if (units.size() / 2 > 0x7FFFFFFFu) return RNS8_UNSUPPORTED_BACKEND;
+      return units.size() / 2 <= 0x7FFFFFFFu;
+    };
+    // 256 x 256 units (128 x 128 quadrants) run ~1.4x faster per MFMA op than
+    // 128 x 128 ones; they need schedule tiles of at least 128 and enough units
+    p.unit_edge = 128;
+    if (tm >= 128 && tn >= 128 && build_units(256) && units.size() / 2 >= kLargeUnitsMin) p.unit_edge = 256;
+    if (p.unit_edge == 128 && !build_units(128)) return RNS8_UNSUPPORTED_BACKEND;
     for (const auto& e : entries)
       if (zero_output(e))
         fills.push_back(TileFill{static_cast<uint32_t>(e.row_offset), static_cast<uint32_t>(e.col_offset),

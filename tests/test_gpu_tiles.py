@@ -156,6 +156,58 @@ def test_random_tiles_match_oracle(gpu_ctx, tile_m, tile_n, signed):
     np.testing.assert_array_equal(out, oout)
 
 
+def _block_operands(rng, signed, m, n, k, block=64):
+    # magnitudes set per 64-row block of A and per 64-column block of B, so the
+    # quadrants of one GEMM unit need different prefixes; |C| < 24 * 2^56 fits int64
+    dt = np.int64 if signed else np.uint64
+    rb = np.repeat(rng.integers(1, 29, size=-(-m // block)), block)[:m]
+    cb = np.repeat(rng.integers(1, 29, size=-(-n // block)), block)[:n]
+    A = rng.integers(0, 1 << 28, size=(m, k)) >> (28 - rb[:, None])
+    B = rng.integers(0, 1 << 28, size=(k, n)) >> (28 - cb[None, :])
+    if signed:
+        A = A * np.where(rng.random((m, k)) < 0.5, -1, 1)
+    return A.astype(dt), B.astype(dt)
+
+
+def _tile_maxima_np(exact, tile_m, tile_n):
+    mag = np.abs(exact) if exact.dtype == np.int64 else exact
+    rows = np.maximum.reduceat(mag, np.arange(0, mag.shape[0], tile_m), axis=0)
+    return [int(x) for x in np.maximum.reduceat(rows, np.arange(0, mag.shape[1], tile_n), axis=1).reshape(-1)]
+
+
+def _units_at_edge(entries, m, n, tile_m, tile_n, planes, edge):
+    # (plane, edge x edge tile) pairs with some quadrant whose schedule tile selects more than the plane
+    sel = {(e.tile_row, e.tile_col): e.selected_prefix for e in entries}
+    count = 0
+    for p in range(planes):
+        for r0 in range(0, m, edge):
+            for c0 in range(0, n, edge):
+                quads = [(r0 + dr, c0 + dc) for dr in (0, edge // 2) for dc in (0, edge // 2)
+                         if r0 + dr < m and c0 + dc < n]
+                count += any(sel[(qr // tile_m, qc // tile_n)] > p for qr, qc in quads)
+    return count
+
+
+@pytest.mark.parametrize("tile_m,tile_n", [(128, 128), (256, 128), (512, 256)])
+@pytest.mark.parametrize("signed", [True, False])
+def test_large_units_match_oracle(gpu_ctx, tile_m, tile_n, signed):
+    # enough 256 x 256 units that the listed GEMM runs its large configuration
+    rng = np.random.default_rng(100 + tile_m + tile_n + signed)
+    m, n, k = 1900 + int(rng.integers(0, 100)), 1800 + int(rng.integers(0, 100)), int(rng.integers(8, 24))
+    A, B = _block_operands(rng, signed, m, n, k)
+    exact = A @ B
+    bounds = _tile_maxima_np(exact, tile_m, tile_n)
+    st, entries, summary = oracle.tile_schedule(signed, m, n, tile_m, tile_n, bounds, 9, 0)
+    assert st == 0 and summary.group_count > 1
+    assert _units_at_edge(entries, m, n, tile_m, tile_n, summary.max_selected, 256) >= 256
+    gst, est, out, planes, sp = _tile_run(gpu_ctx, signed, A, B, tile_m, tile_n, bounds)
+    assert gst == r.SUCCESS and est == r.SUCCESS
+    np.testing.assert_array_equal(out, exact)
+    Cp, ost, oout, osp = _oracle_planes(signed, A, B, tile_m, tile_n, bounds)
+    assert sp == osp and ost == 0
+    np.testing.assert_array_equal(planes, Cp)
+
+
 @pytest.mark.parametrize("signed", [True, False])
 def test_tile_bound_one_below_maximum_is_range_error(gpu_ctx, signed):
     rng = np.random.default_rng(40 + signed)
