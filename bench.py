@@ -41,6 +41,9 @@ CONFIGS = {
     # through magnitudes 2^1 .. 2^25, so tiles select prefixes 5 .. 9
     "tiled": ("i64", 4096, 4096, 4096, 25, 1 << 62, 9, False),
 }
+# grouped resident GEMM: GROUP_TASKS same-shape int64 tasks per step
+GROUPED = ("i64", 1024, 1024, 1024, 25, 1 << 62, 9, True)
+GROUP_TASKS = 8
 TILED_EDGE = 128
 TILED_ROW_BITS = [1, 5, 9, 13, 17, 21, 25]
 
@@ -54,7 +57,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["grouped"])
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true")
@@ -71,6 +74,8 @@ def main() -> int:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
               "(the path shards by output row blocks; see DESIGN.md)", file=sys.stderr)
         return 2
+    if args.config == "grouped":
+        return grouped_bench(args)
 
     import rns8_amd as r
     from rns8_amd import hip, inputs
@@ -287,6 +292,120 @@ def cpu_baseline(args, A, B, Cout, P, bound, signed) -> dict:
                   f"{t_cpu:.2f} s per run, {reps} run(s), on {threads} threads of {_cpu_model()}",
         "rows_bit_exact_vs_gpu": match,
     }
+
+
+def grouped_bench(args) -> int:
+    """GROUP_TASKS int64 GEMMs of one shape per step: pack every A_i and B_i,
+    one rns8_mi355x_gemm_rns_grouped_async call, export every C_i, all on one
+    stream. Also times the same GEMMs as GROUP_TASKS ungrouped calls."""
+    import rns8_amd as r
+    from rns8_amd import hip, inputs
+
+    _, M, N, K, bits, bound, budget, forced = GROUPED
+    T = GROUP_TASKS
+    log(f"[bench] grouped: {T} x int64 {M}x{N}x{K} bits={bits}")
+    ctx = r.Context()
+    bk = r.BOUND_GLOBAL_MAX_ABS
+    desc = r.gemm_desc(r.BOUNDED_I64, bk, M, N, K, bound=bound, max_prefix=budget,
+                       flags=r.PLAN_FORCE_FIXED_PREFIX if forced else 0)
+    plan = r.Plan(ctx, desc)
+    P = plan.prefix
+    mk = lambda rows, cols: r.Matrix(ctx, r.matrix_desc(rows, cols, r.BOUNDED_I64, bk, P))
+    quads = [(mk(M, K), mk(K, N), mk(M, N), r.Workspace(ctx, plan)) for _ in range(T)]
+    tasks = r.grouped_tasks(quads)
+    host = [(inputs.int_range(inputs.operand_seed(args.seed + i, "A"), (M, K), bits),
+             inputs.int_range(inputs.operand_seed(args.seed + i, "B"), (K, N), bits)) for i in range(T)]
+    dev = []
+    for A, B in host:
+        dA, dB, dC = hip.malloc(A.nbytes), hip.malloc(B.nbytes), hip.malloc(M * N * 8)
+        hip.to_device(dA, A)
+        hip.to_device(dB, B)
+        dev.append((dA, dB, dC))
+    dS = hip.malloc(64)
+    hip.memset(dS, 0, 64)
+    stream = hip.stream_create()
+    L = r.lib()
+    ev = [hip.event_create() for _ in range(4)]
+
+    def step(timed: bool, grouped: bool = True):
+        if timed:
+            hip.event_record(ev[0], stream)
+        for (Am, Bm, _, _), (dA, dB, _) in zip(quads, dev):
+            r.check(L.rns8_mi355x_pack_i64_device(ctx.ptr, Am.ptr, dA, K, 0, stream), "pack A")
+            r.check(L.rns8_mi355x_pack_i64_device(ctx.ptr, Bm.ptr, dB, N, 0, stream), "pack B")
+        if timed:
+            hip.event_record(ev[1], stream)
+        if grouped:
+            r.check(L.rns8_mi355x_gemm_rns_grouped_async(ctx.ptr, plan.ptr, tasks, T, stream), "grouped gemm")
+        else:
+            for Am, Bm, Cm, ws in quads:
+                r.check(L.rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, stream),
+                        "gemm")
+        if timed:
+            hip.event_record(ev[2], stream)
+        for (_, _, Cm, _), (_, _, dC) in zip(quads, dev):
+            r.check(L.rns8_mi355x_export_i64_device(ctx.ptr, plan.ptr, Cm.ptr, dC, N, dS, stream), "export")
+        if timed:
+            hip.event_record(ev[3], stream)
+
+    for _ in range(args.warmup):
+        step(False)
+    hip.stream_synchronize(stream)
+    stage = np.zeros(3)
+    ungrouped = 0.0
+    for _ in range(args.steps):
+        step(True)
+        stage += [hip.event_elapsed_ms(ev[i], ev[i + 1]) for i in range(3)]
+        step(True, grouped=False)
+        ungrouped += hip.event_elapsed_ms(ev[1], ev[2])
+    stage /= args.steps
+    ungrouped /= args.steps
+    log(f"[bench] stage ms: pack {stage[0]:.4f} grouped gemm {stage[1]:.4f} export {stage[2]:.4f}; "
+        f"{T} ungrouped gemms {ungrouped:.4f}")
+    hip.synchronize()
+    start, stop = hip.event_create(), hip.event_create()
+    hip.event_record(start, stream)
+    for _ in range(args.steps):
+        step(False)
+    hip.event_record(stop, stream)
+    hip.stream_synchronize(stream)
+    ms_per_step = hip.event_elapsed_ms(start, stop) / args.steps
+    status = np.zeros(16, dtype=np.uint32)
+    hip.from_device(status, dS)
+    out = np.empty((M, N), dtype=np.int64)
+    hip.from_device(out, dev[-1][2])
+    rows = np.arange(0, M, 64)
+    exact = bool(np.array_equal(out[rows], host[-1][0][rows] @ host[-1][1]))
+    log(f"[bench] {ms_per_step:.4f} ms per step; last task's sampled rows exact: {exact}")
+    ops = 2.0 * M * N * K * T
+    gemm_ops = ops * P
+    achieved = gemm_ops / (stage[1] * 1e-3) / 1e12
+    result = {
+        "metric": "exact int64 grouped GEMM effective TOPS (2MNK*tasks/s)",
+        "value": round(ops / (ms_per_step * 1e-3) / 1e12, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int64 (int8 residue MFMA)",
+        "data": f"synthetic: SplitMix64 uniform [-2^{bits}, 2^{bits}) int64 operands, resident in HBM",
+        "config": {"workload": f"{T} x RNS8_BOUNDED_I64 {M}x{N}x{K} prefix {P} (FORCE_FIXED_PREFIX), pack + "
+                               "rns8_gemm_rns_grouped + export device-resident",
+                   "tasks": T, "m": M, "n": N, "k": K, "prefix": P,
+                   "stage_ms": {"pack": round(stage[0], 4), "grouped_gemm": round(stage[1], 4),
+                                "export": round(stage[2], 4), "ungrouped_gemms": round(ungrouped, 4)},
+                   "range_status": int(status[0]), "rows_bit_exact": exact},
+        "roofline": {"bound": "mfma", "kernel": "plane_gemm_kernel<Cfg<4,4>,1,true,false,true> (grouped, persistent)",
+                     "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None, "per_launch_ops": gemm_ops},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result))
+    for e in ev + [start, stop]:
+        hip.event_destroy(e)
+    hip.stream_destroy(stream)
+    for d in dev:
+        for p in d:
+            hip.free(p)
+    hip.free(dS)
+    return 0
 
 
 def tiled_operands(A, bits, N, K):

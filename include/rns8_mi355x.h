@@ -95,6 +95,24 @@ RNS8_API rns8_status rns8_mi355x_gemm_finite_u8_async(
     rns8_workspace* workspace,
     void* stream);
 
+/* Stream-ordered rns8_gemm_rns_grouped / rns8_gemm_finite_u8_grouped
+ * (reference rns8.h:1061-1065, 1139-1144): the same validation, the group
+ * enqueued on `stream` as one persistent launch per 65536-K block and up to
+ * 32 tasks. */
+RNS8_API rns8_status rns8_mi355x_gemm_rns_grouped_async(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    const rns8_grouped_gemm_task* tasks,
+    uint32_t task_count,
+    void* stream);
+RNS8_API rns8_status rns8_mi355x_gemm_finite_u8_grouped_async(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    uint16_t modulus,
+    const rns8_grouped_gemm_task* tasks,
+    uint32_t task_count,
+    void* stream);
+
 /* Device-destination variants of the exports (reference rns8.h:1146-1242). */
 RNS8_API rns8_status rns8_mi355x_export_i64_device(
     rns8_context* ctx,

@@ -263,6 +263,31 @@ def gemm_finite_u8(ctx, plan, modulus, A, B, Cm, ws) -> int:
     return lib().rns8_gemm_finite_u8(ctx.ptr, plan.ptr, modulus, A.ptr, B.ptr, Cm.ptr, ws.ptr)
 
 
+def grouped_tasks(triplets):
+    """ctypes array of rns8_grouped_gemm_task from (A, B, C, workspace) handle tuples."""
+    arr = (abi.GroupedGemmTask * max(len(triplets), 1))()
+    for i, (a, b, c, w) in enumerate(triplets):
+        arr[i].struct_size = C.sizeof(abi.GroupedGemmTask)
+        arr[i].abi_version = abi.ABI_VERSION
+        arr[i].a, arr[i].b, arr[i].c, arr[i].workspace = a.ptr, b.ptr, c.ptr, w.ptr
+    return arr
+
+
+def gemm_rns_grouped(ctx, plan, triplets, tasks=None) -> int:
+    tasks = grouped_tasks(triplets) if tasks is None else tasks
+    return lib().rns8_gemm_rns_grouped(ctx.ptr, plan.ptr, tasks, len(triplets))
+
+
+def gemm_finite_u8_grouped(ctx, plan, modulus, triplets) -> int:
+    return lib().rns8_gemm_finite_u8_grouped(ctx.ptr, plan.ptr, modulus, grouped_tasks(triplets), len(triplets))
+
+
+def grouped_contract_info(plan, task_count) -> tuple[int, abi.GroupedDispatchContractInfo]:
+    info = abi.new_struct(abi.GroupedDispatchContractInfo)
+    st = lib().rns8_get_grouped_dispatch_contract_info(plan.ptr, task_count, C.byref(info))
+    return st, info
+
+
 def export_i64(ctx, plan, Cm, dst: np.ndarray) -> int:
     return lib().rns8_export_i64(ctx.ptr, plan.ptr, Cm.ptr, _ptr(dst), dst.shape[1])
 

@@ -216,6 +216,49 @@ class MatrixStorageInfo(C.Structure):
     ]
 
 
+class GroupedGemmTask(C.Structure):
+    _fields_ = [
+        ("struct_size", C.c_uint64),
+        ("abi_version", C.c_uint32),
+        ("a", C.c_void_p),
+        ("b", C.c_void_p),
+        ("c", C.c_void_p),
+        ("workspace", C.c_void_p),
+    ]
+
+
+class GroupedDispatchContractInfo(C.Structure):
+    _fields_ = [
+        ("struct_size", C.c_uint64),
+        ("abi_version", C.c_uint32),
+        ("backend", C.c_uint32),
+        ("semantics", C.c_uint32),
+        ("task_count", C.c_uint32),
+    ] + [(name, C.c_uint32) for name in (
+        "descriptor_contract_supported", "public_execution_available", "same_shape_required",
+        "same_semantics_required", "compact_row_major_required", "unique_matrix_handles_required",
+        "unique_workspace_handles_required", "same_plan_fingerprint_required", "same_device_required",
+        "device_resident_inputs_required", "per_task_source_versions_required", "produces_device_current_output",
+        "final_export_required_for_host_output", "per_task_status_required", "checksum_policy_required",
+        "descriptor_reuse_validated", "flags")] + [
+        ("descriptor_layout", C.c_char * 96),
+        ("bucket_policy", C.c_char * 96),
+        ("source_version_policy", C.c_char * 96),
+        ("workspace_policy", C.c_char * 96),
+        ("matrix_ownership_policy", C.c_char * 128),
+        ("descriptor_reuse_policy", C.c_char * 128),
+        ("stride_policy", C.c_char * 128),
+        ("output_currentness_policy", C.c_char * 128),
+        ("lifetime_policy", C.c_char * 128),
+        ("checksum_policy", C.c_char * 96),
+        ("status_policy", C.c_char * 96),
+        ("device_descriptor_policy", C.c_char * 96),
+        ("output_domain", C.c_char * 64),
+        ("unsupported_reason", C.c_char * 160),
+        ("detail", C.c_char * 256),
+    ]
+
+
 def new_struct(cls):
     s = cls()
     s.struct_size = C.sizeof(cls)
@@ -275,6 +318,11 @@ PROTOTYPES = {
     "rns8_mi355x_export_exact_wide_signed_limbs_device": (_U32, [_P, _P, _P, _P, _I64, _U32, _P, _P]),
     "rns8_mi355x_export_exact_wide_unsigned_limbs_device": (_U32, [_P, _P, _P, _P, _I64, _U32, _P, _P]),
     "rns8_mi355x_export_finite_u8_device": (_U32, [_P, _P, _U16, _P, _P, _I64, _P]),
+    "rns8_gemm_rns_grouped": (_U32, [_P, _P, C.POINTER(GroupedGemmTask), _U32]),
+    "rns8_gemm_finite_u8_grouped": (_U32, [_P, _P, _U16, C.POINTER(GroupedGemmTask), _U32]),
+    "rns8_mi355x_gemm_rns_grouped_async": (_U32, [_P, _P, C.POINTER(GroupedGemmTask), _U32, _P]),
+    "rns8_mi355x_gemm_finite_u8_grouped_async": (_U32, [_P, _P, _U16, C.POINTER(GroupedGemmTask), _U32, _P]),
+    "rns8_get_grouped_dispatch_contract_info": (_U32, [_P, _U32, C.POINTER(GroupedDispatchContractInfo)]),
     "rns8_mi355x_get_matrix_planes": (_U32, [_P, C.POINTER(_P), C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_U32)]),
 }
 

@@ -869,6 +869,87 @@ rns8_status rns8_get_plan_packing_info(const rns8_plan* plan, rns8_plan_packing_
   });
 }
 
+// reference api_plan_public_api.inc:255-368: the contract rns8_gemm_rns_grouped
+// and rns8_gemm_finite_u8_grouped enforce for this plan. The flags and the
+// policy names that describe the caller-visible contract are the reference's;
+// the layout and descriptor policies name this implementation's.
+rns8_status rns8_get_grouped_dispatch_contract_info(const rns8_plan* plan, uint32_t task_count,
+                                                    rns8_grouped_dispatch_contract_info* out) {
+  return guard([&]() -> rns8_status {
+    if (!plan || !out || !valid_abi(out->struct_size, out->abi_version, sizeof(*out))) return RNS8_INVALID_ARGUMENT;
+    reset_out(*out);
+    out->backend = plan->backend;
+    out->semantics = plan->desc.semantics;
+    out->task_count = task_count;
+    out->same_shape_required = 1;
+    out->same_semantics_required = 1;
+    out->compact_row_major_required = 1;
+    out->unique_matrix_handles_required = 1;
+    out->unique_workspace_handles_required = 1;
+    out->same_plan_fingerprint_required = 1;
+    out->same_device_required = 1;
+    out->device_resident_inputs_required = 1;
+    out->per_task_source_versions_required = 1;
+    out->produces_device_current_output = 1;
+    out->final_export_required_for_host_output = 1;
+    out->per_task_status_required = 1;
+    out->checksum_policy_required = 1;
+    out->descriptor_reuse_validated = 1;
+    out->flags = RNS8_GROUPED_DISPATCH_CONTRACT_SAME_SHAPE_REQUIRED |
+                 RNS8_GROUPED_DISPATCH_CONTRACT_COMPACT_ROW_MAJOR_REQUIRED |
+                 RNS8_GROUPED_DISPATCH_CONTRACT_UNIQUE_TASK_HANDLES_REQUIRED |
+                 RNS8_GROUPED_DISPATCH_CONTRACT_ONE_WORKSPACE_PER_TASK_REQUIRED |
+                 RNS8_GROUPED_DISPATCH_CONTRACT_SAME_DEVICE_REQUIRED |
+                 RNS8_GROUPED_DISPATCH_CONTRACT_PER_TASK_SOURCE_VERSION_REQUIRED |
+                 RNS8_GROUPED_DISPATCH_CONTRACT_DEVICE_CURRENT_OUTPUT_REQUIRED |
+                 RNS8_GROUPED_DISPATCH_CONTRACT_PUBLIC_PACK_EXPLICIT |
+                 RNS8_GROUPED_DISPATCH_CONTRACT_PUBLIC_EXPORT_EXPLICIT |
+                 RNS8_GROUPED_DISPATCH_CONTRACT_GENERIC_BUCKETING_UNAVAILABLE |
+                 RNS8_GROUPED_DISPATCH_CONTRACT_AUTO_ROUTING_DISABLED;
+    copy_text(out->descriptor_layout, sizeof(out->descriptor_layout), "same_shape_resident_task_triplets_v1");
+    copy_text(out->bucket_policy, sizeof(out->bucket_policy), "single_same_shape_bucket");
+    copy_text(out->source_version_policy, sizeof(out->source_version_policy),
+              "per_task_monotonic_source_version_repack");
+    copy_text(out->workspace_policy, sizeof(out->workspace_policy), "one_workspace_per_task_shared_plan");
+    copy_text(out->matrix_ownership_policy, sizeof(out->matrix_ownership_policy),
+              "caller_owns_unique_task_triplets_until_grouped_call_returns");
+    copy_text(out->descriptor_reuse_policy, sizeof(out->descriptor_reuse_policy),
+              "reuse_after_shape_workspace_source_validation");
+    copy_text(out->stride_policy, sizeof(out->stride_policy), "matrix_ld_matches_logical_shape_host_output_ld_explicit");
+    copy_text(out->output_currentness_policy, sizeof(out->output_currentness_policy),
+              "device_residue_current_after_grouped_gemm_host_output_after_export");
+    copy_text(out->lifetime_policy, sizeof(out->lifetime_policy),
+              "task_matrices_and_workspaces_valid_until_grouped_call_returns");
+    copy_text(out->checksum_policy, sizeof(out->checksum_policy), "combined_per_task_checksum_u64");
+    copy_text(out->status_policy, sizeof(out->status_policy), "fail_fast_per_task_operation_status");
+    copy_text(out->device_descriptor_policy, sizeof(out->device_descriptor_policy),
+              "task_pointer_table_in_kernel_arguments_32_per_launch");
+    const rns8_semantics s = plan->desc.semantics;
+    const char* domain = s == RNS8_BOUNDED_I64 || s == RNS8_BOUNDED_U64       ? "native_i64_u64_host"
+                         : s == RNS8_EXACT_WIDE_SIGNED || s == RNS8_EXACT_WIDE_UNSIGNED ? "exact_wide_limb_host"
+                         : s == RNS8_FINITE_FIELD_U8 || s == RNS8_FINITE_RING_U8       ? "finite_u8_host"
+                                                                                       : "wrap64_u64_host";
+    copy_text(out->output_domain, sizeof(out->output_domain), domain);
+    const char* reason = nullptr;
+    if (plan->backend != RNS8_BACKEND_HIP_DIRECT) reason = "backend_not_hip_direct";
+    else if (task_count <= 1) reason = "task_count_must_exceed_one";
+    else if (s == RNS8_WRAP_U64_MOD_2_64) reason = "unsupported_grouped_semantics";
+    else if (plan->desc.m <= 0 || plan->desc.n <= 0 || plan->desc.k <= 0) reason = "invalid_plan_shape";
+    if (reason) {
+      copy_text(out->unsupported_reason, sizeof(out->unsupported_reason), reason);
+      out->flags |= RNS8_GROUPED_DISPATCH_CONTRACT_BENCHMARK_ONLY_EXECUTION;
+      copy_text(out->detail, sizeof(out->detail), "grouped execution is not available for this plan and task count");
+    } else {
+      out->descriptor_contract_supported = 1;
+      out->public_execution_available = 1;
+      copy_text(out->detail, sizeof(out->detail),
+                "one persistent gfx950 launch per 65536-K block covers up to 32 tasks (task-major unit order); "
+                "inputs are packed before the call and outputs exported after it");
+    }
+    return RNS8_SUCCESS;
+  });
+}
+
 // ---- workspace ---------------------------------------------------------------------
 
 rns8_status rns8_create_workspace(rns8_context* ctx, const rns8_plan* plan, rns8_workspace** out) {

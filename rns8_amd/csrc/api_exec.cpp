@@ -490,6 +490,98 @@ rns8_status gemm_finite(rns8_context* ctx, const rns8_plan* plan, uint16_t modul
   return RNS8_SUCCESS;
 }
 
+// ---- grouped GEMM (reference api_gemm.cpp:200-336, hip_grouped_descriptor.cpp:474-512) ----
+
+// Same-shape resident GEMMs of one plan, each task with its own A, B, C and
+// workspace: every task passes the ungrouped checks, no handle appears twice
+// in the group, and no result is another task's operand (the tasks run
+// concurrently). Global and collapsed per-tile plans run as one persistent
+// launch per K block with the task folded into the unit order; per-tile plans
+// with a schedule run the listed GEMM per task.
+rns8_status gemm_grouped(rns8_context* ctx, const rns8_plan* plan, const rns8_grouped_gemm_task* tasks,
+                         uint32_t task_count, bool finite, uint16_t modulus, void* stream_arg, bool synchronous) {
+  if (!ctx || !plan) return RNS8_INVALID_ARGUMENT;
+  if (finite ? (!uses_finite_storage(plan->desc.semantics) || plan->desc.finite_modulus != modulus ||
+                !valid_finite_modulus(plan->desc.semantics, modulus))
+             : !uses_rns_storage(plan->desc.semantics))
+    return RNS8_INVALID_ARGUMENT;
+  if (!tasks || task_count <= 1) return RNS8_INVALID_ARGUMENT;
+  for (uint32_t i = 0; i < task_count; ++i) {
+    const rns8_grouped_gemm_task& t = tasks[i];
+    if (!valid_abi(t.struct_size, t.abi_version, sizeof(t)) || !t.a || !t.b || !t.c || !t.workspace)
+      return RNS8_INVALID_ARGUMENT;
+    const rns8_status st = check_plan_ctx_ws(*ctx, *plan, *t.workspace);
+    if (st != RNS8_SUCCESS) return st;
+  }
+  for (uint32_t i = 0; i < task_count; ++i) {
+    const rns8_grouped_gemm_task& t = tasks[i];
+    if (t.a == t.b) return RNS8_INVALID_ARGUMENT;
+    for (uint32_t j = 0; j < task_count; ++j) {
+      const rns8_grouped_gemm_task& u = tasks[j];
+      if (t.c == u.a || t.c == u.b) return RNS8_INVALID_ARGUMENT;
+      if (j < i && (t.a == u.a || t.b == u.b || t.c == u.c || t.workspace == u.workspace))
+        return RNS8_INVALID_ARGUMENT;
+    }
+    const rns8_status st = finite ? check_finite_operands(*ctx, *plan, modulus, *t.a, *t.b, *t.c)
+                                  : check_rns_operands(*ctx, *plan, *t.a, *t.b, *t.c);
+    if (st != RNS8_SUCCESS) return st;
+  }
+  std::vector<I256> bounds(task_count);
+  std::vector<std::vector<ExactAxis>> rows(task_count), cols(task_count);
+  if (!finite && exact_wide(plan->desc.semantics))
+    for (uint32_t i = 0; i < task_count; ++i) {
+      const rns8_status st = exact_gemm_range(*plan, *tasks[i].a, *tasks[i].b, bounds[i], &rows[i], &cols[i]);
+      if (st != RNS8_SUCCESS) return st;
+    }
+
+  const hipStream_t stream = pick_stream(*ctx, stream_arg);
+  if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  for (uint32_t i = 0; i < task_count; ++i) tasks[i].c->device_current = false;
+  rns8_status st = RNS8_SUCCESS;
+  if (!finite && per_tile_kind(plan->desc.bound_kind) && !plan->schedule.entries.empty()) {
+    for (uint32_t i = 0; i < task_count && st == RNS8_SUCCESS; ++i)
+      st = run_gemm_tiled(*ctx, *plan, *tasks[i].a, *tasks[i].b, *tasks[i].c, stream);
+  } else {
+    const rns8_matrix& a0 = *tasks[0].a;
+    const rns8_matrix& b0 = *tasks[0].b;
+    const rns8_matrix& c0 = *tasks[0].c;
+    GemmArgs g{};
+    g.m = plan->desc.m;
+    g.n = plan->desc.n;
+    g.k = plan->desc.k;
+    g.lda = a0.plane_ld;
+    g.ldb = b0.plane_ld;
+    g.ldc = c0.plane_ld;
+    g.pitch_a = a0.plane_pitch;
+    g.pitch_b = b0.plane_pitch;
+    g.pitch_c = c0.plane_pitch;
+    g.nplanes = finite ? 1u : plan->prefix;
+    g.slices = plan->splitk_slices;
+    std::vector<TaskPtrs> ptrs(task_count);
+    for (uint32_t i = 0; i < task_count; ++i)
+      ptrs[i] = TaskPtrs{tasks[i].a->planes, tasks[i].b->planes, tasks[i].c->planes,
+                         plan->splitk_slices > 1 ? tasks[i].workspace->splitk : nullptr};
+    const PlaneConsts consts = finite ? make_single_plane_consts(modulus) : make_ladder_plane_consts(plan->prefix);
+    const hipError_t e = launch_gemm_grouped(g, consts, ptrs.data(), task_count, stream);
+    st = e == hipSuccess ? RNS8_SUCCESS : e == hipErrorInvalidValue ? RNS8_UNSUPPORTED_BACKEND : RNS8_BACKEND_FAILURE;
+  }
+  if (st == RNS8_SUCCESS && synchronous) st = sync(stream);
+  if (st != RNS8_SUCCESS) return st;
+  for (uint32_t i = 0; i < task_count; ++i) {
+    rns8_matrix& C = *tasks[i].c;
+    C.device_current = true;
+    C.source_version = output_source_version(tasks[i].a->source_version, tasks[i].b->source_version);
+    if (finite) C.finite_modulus = modulus;
+    if (!finite && exact_wide(plan->desc.semantics)) {
+      C.exact_max = bounds[i];
+      C.exact_rows.swap(rows[i]);
+      C.exact_cols.swap(cols[i]);
+      C.exact_prefix = plan->prefix;
+    }
+  }
+  return RNS8_SUCCESS;
+}
+
 // ---- export ------------------------------------------------------------------------
 
 struct ExportRequest {
@@ -768,6 +860,16 @@ rns8_status rns8_export_finite_u8(rns8_context* ctx, const rns8_plan* plan, uint
   return guard([&] { return export_finite(ctx, plan, modulus, C, dst, ld, Source::Host, nullptr); });
 }
 
+rns8_status rns8_gemm_rns_grouped(rns8_context* ctx, const rns8_plan* plan, const rns8_grouped_gemm_task* tasks,
+                                  uint32_t task_count) {
+  return guard([&] { return gemm_grouped(ctx, plan, tasks, task_count, false, 0, nullptr, true); });
+}
+
+rns8_status rns8_gemm_finite_u8_grouped(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus,
+                                        const rns8_grouped_gemm_task* tasks, uint32_t task_count) {
+  return guard([&] { return gemm_grouped(ctx, plan, tasks, task_count, true, modulus, nullptr, true); });
+}
+
 rns8_status rns8_gemm_i64_oneshot(rns8_context* ctx, const rns8_gemm_desc* desc, const int64_t* A, int64_t lda,
                                   const int64_t* B, int64_t ldb, int64_t* C, int64_t ldc) {
   return guard([&] { return bounded_oneshot<int64_t>(ctx, desc, A, lda, B, ldb, C, ldc); });
@@ -820,6 +922,18 @@ rns8_status rns8_mi355x_gemm_finite_u8_async(rns8_context* ctx, const rns8_plan*
                                              const rns8_matrix* A, const rns8_matrix* B, rns8_matrix* C,
                                              rns8_workspace* workspace, void* stream) {
   return guard([&] { return gemm_finite(ctx, plan, modulus, A, B, C, workspace, stream, false); });
+}
+
+rns8_status rns8_mi355x_gemm_rns_grouped_async(rns8_context* ctx, const rns8_plan* plan,
+                                              const rns8_grouped_gemm_task* tasks, uint32_t task_count,
+                                              void* stream) {
+  return guard([&] { return gemm_grouped(ctx, plan, tasks, task_count, false, 0, stream, false); });
+}
+
+rns8_status rns8_mi355x_gemm_finite_u8_grouped_async(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus,
+                                                    const rns8_grouped_gemm_task* tasks, uint32_t task_count,
+                                                    void* stream) {
+  return guard([&] { return gemm_grouped(ctx, plan, tasks, task_count, true, modulus, stream, false); });
 }
 
 rns8_status rns8_mi355x_export_i64_device(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* C,

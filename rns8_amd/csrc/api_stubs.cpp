@@ -11,9 +11,6 @@
 
 #define RNS8X_UNSUPPORTED return RNS8_UNSUPPORTED_BACKEND
 
-rns8_status rns8_get_grouped_dispatch_contract_info(const rns8_plan*, uint32_t, rns8_grouped_dispatch_contract_info*) {
-  RNS8X_UNSUPPORTED;
-}
 rns8_status rns8_get_prepack_cache_key_info(const rns8_plan*, const rns8_matrix*, rns8_operand_role,
                                             rns8_prepack_cache_key_info*) {
   RNS8X_UNSUPPORTED;
@@ -80,9 +77,6 @@ rns8_status rns8_gemm_rns_incremental(rns8_context*, const rns8_plan*, const rns
                                       uint32_t) {
   RNS8X_UNSUPPORTED;
 }
-rns8_status rns8_gemm_rns_grouped(rns8_context*, const rns8_plan*, const rns8_grouped_gemm_task*, uint32_t) {
-  RNS8X_UNSUPPORTED;
-}
 rns8_status rns8_gemm_rns_prepacked_b(rns8_context*, const rns8_plan*, const rns8_matrix*, const rns8_prepack_cache*,
                                       rns8_matrix*, rns8_workspace*) {
   RNS8X_UNSUPPORTED;
@@ -98,10 +92,6 @@ rns8_status rns8_gemm_finite_u8_sparse_a(rns8_context*, const rns8_plan*, uint16
 rns8_status rns8_gemm_finite_u8_incremental(rns8_context*, const rns8_plan*, uint16_t, const rns8_matrix*,
                                             const rns8_matrix*, rns8_matrix*, rns8_workspace*, rns8_result_cache*,
                                             const rns8_dirty_region*, uint32_t) {
-  RNS8X_UNSUPPORTED;
-}
-rns8_status rns8_gemm_finite_u8_grouped(rns8_context*, const rns8_plan*, uint16_t, const rns8_grouped_gemm_task*,
-                                        uint32_t) {
   RNS8X_UNSUPPORTED;
 }
 rns8_status rns8_export_wrap_u64(rns8_context*, const rns8_plan*, const rns8_matrix*, uint64_t*, int64_t) {

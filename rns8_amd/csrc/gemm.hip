@@ -197,7 +197,19 @@ struct UnitMap {
   // listed launches: two words per unit, (plane << 24 | tile row) and
   // (quadrant mask << 24 | tile column), in place of the arithmetic order
   const uint32_t* list;
+  // grouped launches: units are numbered task-major, task_units per task
+  DivU31 task_units;
 };
+
+// Grouped launches carry their tasks' base pointers by value (kernel
+// arguments are read through the scalar cache); other launches an empty
+// struct.
+struct TaskTable {
+  TaskPtrs t[kMaxGroupTasks];
+};
+struct NoTaskTable {};
+template <bool kGrouped>
+using GroupArg = std::conditional_t<kGrouped, TaskTable, NoTaskTable>;
 
 // Reads accumulator elements 4g .. 4g+3 straight from their AGPRs. The asm
 // keeps the accumulators in AGPRs through the epilogue (the compiler
@@ -221,9 +233,10 @@ __device__ __forceinline__ Acc4 acc_read4(const v16i& acc, int g) {
 // floor(n / d) for n < 2^31 (make_div_u31).
 __device__ __forceinline__ uint32_t div_u31(uint32_t n, DivU31 v) { return __umulhi(n << 1, v.mul) >> v.shift; }
 
-template <typename C, int kMinBlocks, bool kUniform, bool kListed = false>
+template <typename C, int kMinBlocks, bool kUniform, bool kListed = false, bool kGrouped = false>
 __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmArgs args, PlaneConsts pc, UnitMap map,
-                                                                           uint32_t accumulate) {
+                                                                           uint32_t accumulate,
+                                                                           GroupArg<kGrouped> tasks) {
   constexpr int WM = C::kWM, WN = C::kWN, BM = C::BM, BN = C::BN, BK = C::BK;
   __shared__ __attribute__((aligned(16))) int8_t lds[C::kLds + C::kEpiLds];
 
@@ -262,7 +275,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
   // the host's reciprocals, branch-free, so the cursor below can advance
   // every K step without splitting the loop body.
   struct Unit {
-    uint32_t plane, slice, m0, n0, kbeg, kend, ktiles, quad;
+    uint32_t task, plane, slice, m0, n0, kbeg, kend, ktiles, quad;
   };
   // Listed units come from a per-tile schedule: a BM x BN tile of one plane
   // whose four quadrants (one per wave, 2 x 2) are stored only where the mask
@@ -271,6 +284,11 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
   static_assert(kThreads == 256, "quadrant masks assume four waves in a 2 x 2 grid");
   auto decode = [&](uint32_t u) {
     Unit U;
+    U.task = 0;
+    if constexpr (kGrouped) {
+      U.task = div_u31(u, map.task_units);
+      u -= U.task * map.task_units.d;
+    }
     if constexpr (kListed) {
       const uint32_t w0 = map.list[2u * u], w1 = map.list[2u * u + 1u];
       U.plane = w0 >> 24;
@@ -299,6 +317,24 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
     U.kend = min(map.k_stop, U.kbeg + map.k_slice);
     U.ktiles = U.kend > U.kbeg ? (U.kend - U.kbeg + BK - 1) / BK : 0u;
     return U;
+  };
+
+  // Base pointers of a unit's task (the launch's own in ungrouped launches).
+  auto base_a = [&](const Unit& U) -> const int8_t* {
+    if constexpr (kGrouped) return tasks.t[U.task].a;
+    else return args.a;
+  };
+  auto base_b = [&](const Unit& U) -> const int8_t* {
+    if constexpr (kGrouped) return tasks.t[U.task].b;
+    else return args.b;
+  };
+  auto base_c = [&](const Unit& U) -> int8_t* {
+    if constexpr (kGrouped) return tasks.t[U.task].c;
+    else return args.c;
+  };
+  auto base_ws = [&](const Unit& U) -> int32_t* {
+    if constexpr (kGrouped) return tasks.t[U.task].ws;
+    else return args.splitk_ws;
   };
 
   // ---- global -> LDS by DMA ------------------------------------------------
@@ -343,9 +379,9 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
     const uint32_t k0 = dU.kbeg + dkt * BK;
     const uint32_t a_rows = min(static_cast<uint32_t>(BM), m_rows - dU.m0);
     const uint32_t b_rows = min(static_cast<uint32_t>(BK), dU.kend - k0);
-    const int8_t* const a_panel = args.a + static_cast<uint64_t>(dU.plane) * args.pitch_a +
+    const int8_t* const a_panel = base_a(dU) + static_cast<uint64_t>(dU.plane) * args.pitch_a +
                                   static_cast<uint64_t>(dU.m0) * lda;
-    const int8_t* const b_slab = args.b + static_cast<uint64_t>(dU.plane) * args.pitch_b +
+    const int8_t* const b_slab = base_b(dU) + static_cast<uint64_t>(dU.plane) * args.pitch_b +
                                  static_cast<uint64_t>(k0) * ldb + dU.n0;
     nsrc = TileSrc{buffer_rsrc(a_panel + k0, live ? a_rows * lda - k0 : 0u),
                    buffer_rsrc(b_slab, live ? b_rows * ldb - dU.n0 : 0u)};
@@ -482,7 +518,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
     if (args.slices <= 1) {
       // a listed unit's wave stores its quadrant only if the mask selects it
       if (kListed && ((U.quad >> (wave_m * 2 + wave_n)) & 1u) == 0u) return;
-      int8_t* const Cp = args.c + static_cast<int64_t>(U.plane) * args.pitch_c + U.m0 * args.ldc + U.n0;
+      int8_t* const Cp = base_c(U) + static_cast<int64_t>(U.plane) * args.pitch_c + U.m0 * args.ldc + U.n0;
       const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(Cp, tile_rows * args.ldc - U.n0);
       const uint32_t m_comp = 256u - mc.m;
       const uint32_t half2 = mc.half * 0x00010001u;
@@ -568,7 +604,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
       // stores, to its own slot of the workspace [slice][plane][M][ldc]; the
       // finalize kernel adds the slices. No atomics, no zeroing, deterministic.
       int32_t* const W =
-          args.splitk_ws + ((static_cast<int64_t>(U.slice) * args.nplanes + U.plane) * args.m + U.m0) * args.ldc + U.n0;
+          base_ws(U) + ((static_cast<int64_t>(U.slice) * args.nplanes + U.plane) * args.m + U.m0) * args.ldc + U.n0;
       const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(W, 4 * (tile_rows * args.ldc - U.n0));
 #pragma unroll
       for (int i = 0; i < WM; ++i) {
@@ -808,8 +844,11 @@ int device_cu_count() {
   return cached[dev];
 }
 
-template <typename Cf, int kMinBlocks>
-hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream) {
+// Ungrouped launches pass a NoTaskTable and ntasks = 1; grouped ones the
+// task table and its task count (at most kMaxGroupTasks).
+template <typename Cf, int kMinBlocks, bool kGrouped>
+hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream,
+                           const GroupArg<kGrouped>& tab, uint32_t ntasks) {
   const uint32_t tiles_m = static_cast<uint32_t>((args.m + Cf::BM - 1) / Cf::BM);
   const uint32_t tiles_n = static_cast<uint32_t>((args.ldc + Cf::BN - 1) / Cf::BN);
   const uint64_t words = static_cast<uint64_t>(args.nplanes) * args.m * args.ldc / 4;
@@ -826,10 +865,12 @@ hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipS
       k_slice = (k_slice + Cf::BK - 1) / Cf::BK * Cf::BK;
       used_slices = static_cast<uint32_t>((kstop - kb + k_slice - 1) / k_slice);
     }
-    const uint64_t units = static_cast<uint64_t>(tiles_m) * tiles_n * args.nplanes * used_slices;
+    const uint64_t task_units = static_cast<uint64_t>(tiles_m) * tiles_n * args.nplanes * used_slices;
+    const uint64_t units = task_units * ntasks;
     if (units == 0 || units > 0x7FFFFFFFull) return hipErrorInvalidValue;
     UnitMap map{};
     map.units = static_cast<uint32_t>(units);
+    map.task_units = make_div_u31(static_cast<uint32_t>(task_units));
     map.tiles_m = tiles_m;
     map.tiles = make_div_u31(tiles_m * tiles_n);
     map.planes = make_div_u31(args.nplanes);
@@ -846,20 +887,29 @@ hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipS
     // every unit has the same K tiles when the slices divide the block evenly
     const bool uniform = (kstop - kb) % k_slice == 0;
     if (uniform)
-      hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks, true>), dim3(static_cast<unsigned>(grid)), dim3(kThreads),
-                         0, stream, args, consts, map, accumulate);
+      hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks, true, false, kGrouped>), dim3(static_cast<unsigned>(grid)),
+                         dim3(kThreads), 0, stream, args, consts, map, accumulate, tab);
     else
-      hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks, false>), dim3(static_cast<unsigned>(grid)), dim3(kThreads),
-                         0, stream, args, consts, map, accumulate);
+      hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks, false, false, kGrouped>),
+                         dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream, args, consts, map, accumulate,
+                         tab);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     if (args.slices > 1) {
       const uint64_t fblocks = (words + 255) / 256;
       const unsigned fgrid = static_cast<unsigned>(fblocks < 8192 ? fblocks : 8192);
-      hipLaunchKernelGGL(splitk_finalize_kernel, dim3(fgrid), dim3(256), 0, stream, args.splitk_ws, args.c, args.m,
-                         args.ldc, args.pitch_c, args.nplanes, used_slices, consts, accumulate);
-      err = hipGetLastError();
-      if (err != hipSuccess) return err;
+      for (uint32_t t = 0; t < ntasks; ++t) {
+        int32_t* ws = args.splitk_ws;
+        int8_t* c = args.c;
+        if constexpr (kGrouped) {
+          ws = tab.t[t].ws;
+          c = tab.t[t].c;
+        }
+        hipLaunchKernelGGL(splitk_finalize_kernel, dim3(fgrid), dim3(256), 0, stream, ws, c, args.m, args.ldc,
+                           args.pitch_c, args.nplanes, used_slices, consts, accumulate);
+        err = hipGetLastError();
+        if (err != hipSuccess) return err;
+      }
     }
   }
   return hipSuccess;
@@ -884,7 +934,7 @@ hipError_t launch_listed(const GemmArgs& args, const PlaneConsts& consts, const 
     map.k_slice = static_cast<uint32_t>(kstop - kb);
     map.list = d_units;
     hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks, true, true>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kThreads), 0, stream, args, consts, map, kb > 0 ? 1u : 0u);
+                       dim3(kThreads), 0, stream, args, consts, map, kb > 0 ? 1u : 0u, NoTaskTable{});
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
@@ -916,8 +966,41 @@ hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStrea
   const GemmShape shape = choose_gemm_shape(args.m, args.n, args.k, args.nplanes);
   // the workspace was sized for the plan's slice count: never use more
   if (args.slices > 1 && args.slices != shape.slices) return hipErrorInvalidValue;
-  if (shape.tile == 256) return launch_gemm_cfg<CfgLarge, 1>(args, consts, stream);
-  return launch_gemm_cfg<CfgSmall, 2>(args, consts, stream);
+  if (shape.tile == 256) return launch_gemm_cfg<CfgLarge, 1, false>(args, consts, stream, NoTaskTable{}, 1);
+  return launch_gemm_cfg<CfgSmall, 2, false>(args, consts, stream, NoTaskTable{}, 1);
+}
+
+hipError_t launch_gemm_grouped(const GemmArgs& shape, const PlaneConsts& consts, const TaskPtrs* tasks,
+                               uint32_t count, hipStream_t stream) {
+  if (!tasks || count == 0) return hipErrorInvalidValue;
+  // tile and K split for the whole group (the tasks count as extra planes);
+  // never more slices than the shape's own workspaces hold
+  const GemmShape g = choose_gemm_shape(shape.m, shape.n, shape.k, shape.nplanes * count);
+  if (g.slices > 1 && g.slices > shape.slices) return hipErrorInvalidValue;
+  for (uint32_t first = 0; first < count; first += kMaxGroupTasks) {
+    const uint32_t n = count - first < kMaxGroupTasks ? count - first : kMaxGroupTasks;
+    TaskTable tab{};
+    for (uint32_t t = 0; t < n; ++t) {
+      tab.t[t] = tasks[first + t];
+      // every task's operands pass the same checks as an ungrouped launch
+      GemmArgs a = shape;
+      a.a = tab.t[t].a;
+      a.b = tab.t[t].b;
+      a.c = tab.t[t].c;
+      a.splitk_ws = tab.t[t].ws;
+      a.slices = g.slices;
+      if (!gemm_shape_ok(a)) return hipErrorInvalidValue;
+    }
+    GemmArgs a = shape;
+    a.a = a.b = nullptr;
+    a.c = nullptr;
+    a.splitk_ws = nullptr;
+    a.slices = g.slices;
+    const hipError_t err = g.tile == 256 ? launch_gemm_cfg<CfgLarge, 1, true>(a, consts, stream, tab, n)
+                                         : launch_gemm_cfg<CfgSmall, 2, true>(a, consts, stream, tab, n);
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
 }
 
 }  // namespace rns8x

@@ -76,6 +76,19 @@ struct TileFill {
 };
 hipError_t launch_zero_tiles(int8_t* c, int64_t ldc, int64_t pitch_c, const TileFill* d_tiles, uint32_t count,
                              hipStream_t stream);
+// Grouped launches: tasks of one shape (the GemmArgs shape, pitches, planes
+// and slices), each with its own operands, result and split-K workspace; one
+// persistent launch per K block covers up to kMaxGroupTasks tasks, larger
+// groups run as consecutive launches (reference api_gemm.cpp:1199-1210).
+struct TaskPtrs {
+  const int8_t* a;
+  const int8_t* b;
+  int8_t* c;
+  int32_t* ws;  // split-K partials of this task (slices > 1 only)
+};
+constexpr uint32_t kMaxGroupTasks = 32;
+hipError_t launch_gemm_grouped(const GemmArgs& shape, const PlaneConsts& consts, const TaskPtrs* tasks,
+                               uint32_t count, hipStream_t stream);
 // Tile edge (256 or 128) and K slices the launcher uses for this shape
 // (k is the K of one launch block, at most 65536).
 struct GemmShape {
