@@ -63,6 +63,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--oneshot", action="store_true",
                     help="time the host-buffer oneshot entry point instead (PCIe transfers included)")
+    ap.add_argument("--rns8-bench-json", default="", metavar="PATH",
+                    help="also run the host-API lane on the same inputs and write an rns8-bench schema-v4 capture")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a device copy of BYTES (counter calibration) and exit")
     args = ap.parse_args()
@@ -242,7 +244,27 @@ def main() -> int:
     hip.stream_destroy(stream)
     for p in (dA, dB, dC, dS):
         hip.free(p)
+    if args.rns8_bench_json:
+        write_v4_capture(args, ctx, A, B, signed, bound, budget, forced, tile_bounds if tiled else None)
     return 0
+
+
+def write_v4_capture(args, ctx, A, B, signed, bound, budget, forced, tile_bounds) -> None:
+    """The same GEMM through the public host-buffer ABI (pack from host arrays,
+    rns8_gemm_rns, export to a host array; PCIe included), written as an
+    rns8-bench schema-v4 record (rns8_amd/bench_v4.py)."""
+    from rns8_amd import bench_v4
+
+    bits = CONFIGS[args.config][4]
+    dist = (f"splitmix64_{'signed' if signed else 'unsigned'}_uniform_2^{bits}"
+            + ("_tile_rows_scaled" if tile_bounds is not None else ""))
+    rec, _ = bench_v4.capture_bounded(
+        ctx, A, B, signed=signed, bound=bound, budget=budget, forced=forced,
+        tile_bounds_fn=(lambda: tile_bounds) if tile_bounds is not None else None, tile=TILED_EDGE,
+        warmups=1, repeats=3, seed=args.seed, input_distribution=dist, command_line=" ".join(sys.argv))
+    Path(args.rns8_bench_json).write_text(json.dumps(rec, indent=2) + "\n")
+    log(f"[bench] schema-v4 capture: {args.rns8_bench_json} (host-API end to end "
+        f"{rec['avg_end_to_end_us']:.0f} us, gemm {rec['avg_rns_gemm_us']:.0f} us)")
 
 
 def cpu_baseline(args, A, B, Cout, P, bound, signed) -> dict:

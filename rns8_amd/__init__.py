@@ -168,6 +168,11 @@ class Context(_Handle):
         st = lib().rns8_create_context(device_id, C.byref(opts) if opts is not None else None, C.byref(self.ptr))
         check(st, "rns8_create_context")
 
+    def device_info(self) -> abi.DeviceInfo:
+        info = abi.new_struct(abi.DeviceInfo)
+        check(lib().rns8_get_device_info(self.ptr, C.byref(info)), "rns8_get_device_info")
+        return info
+
 
 class Plan(_Handle):
     _destroy = "rns8_destroy_plan"

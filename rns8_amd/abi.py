@@ -216,6 +216,43 @@ class MatrixStorageInfo(C.Structure):
     ]
 
 
+class PlanBackendInfo(C.Structure):
+    _fields_ = [
+        ("struct_size", C.c_uint64),
+        ("abi_version", C.c_uint32),
+        ("backend", C.c_uint32),
+        ("is_accelerator", C.c_uint32),
+        ("is_correctness_backend", C.c_uint32),
+        ("is_matrix_engine_backend", C.c_uint32),
+        ("compiled_kernel_available", C.c_uint32),
+        ("exact_differential_validated", C.c_uint32),
+        ("performance_validated", C.c_uint32),
+        ("flags", C.c_uint32),
+        ("workspace_required_bytes", C.c_uint64),
+        ("selected_kernel", C.c_char * 128),
+        ("accelerator_library", C.c_char * 64),
+        ("accelerator_version", C.c_char * 64),
+        ("capability_status", C.c_char * 128),
+        ("epilogue_mode", C.c_char * 96),
+        ("workspace_mode", C.c_char * 96),
+        ("isa_evidence", C.c_char * 128),
+        ("autotune_key", C.c_char * 1024),
+        ("accumulator_k_block_size", C.c_uint64),
+        ("accumulator_k_block_cap", C.c_uint64),
+        ("accumulator_modulus", C.c_uint64),
+        ("accumulator_max_lhs_abs", C.c_uint64),
+        ("accumulator_max_rhs_abs", C.c_uint64),
+        ("accumulator_max_product", C.c_uint64),
+        ("accumulator_uses_int32_inner_product", C.c_uint32),
+        ("accumulator_safe_for_k_block", C.c_uint32),
+        ("accumulator_input_domain", C.c_char * 64),
+        ("accumulator_signedness", C.c_char * 64),
+        ("accumulator_type", C.c_char * 64),
+        ("accumulator_modulus_policy", C.c_char * 128),
+        ("accumulator_safety_status", C.c_char * 128),
+    ]
+
+
 class GroupedGemmTask(C.Structure):
     _fields_ = [
         ("struct_size", C.c_uint64),
@@ -318,6 +355,7 @@ PROTOTYPES = {
     "rns8_mi355x_export_exact_wide_signed_limbs_device": (_U32, [_P, _P, _P, _P, _I64, _U32, _P, _P]),
     "rns8_mi355x_export_exact_wide_unsigned_limbs_device": (_U32, [_P, _P, _P, _P, _I64, _U32, _P, _P]),
     "rns8_mi355x_export_finite_u8_device": (_U32, [_P, _P, _U16, _P, _P, _I64, _P]),
+    "rns8_get_plan_backend_info": (_U32, [_P, C.POINTER(PlanBackendInfo)]),
     "rns8_gemm_rns_grouped": (_U32, [_P, _P, C.POINTER(GroupedGemmTask), _U32]),
     "rns8_gemm_finite_u8_grouped": (_U32, [_P, _P, _U16, C.POINTER(GroupedGemmTask), _U32]),
     "rns8_mi355x_gemm_rns_grouped_async": (_U32, [_P, _P, C.POINTER(GroupedGemmTask), _U32, _P]),

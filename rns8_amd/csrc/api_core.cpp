@@ -812,8 +812,11 @@ rns8_status rns8_get_plan_backend_info(const rns8_plan* plan, rns8_plan_backend_
     out->compiled_kernel_available = 1;
     out->exact_differential_validated = 1;
     out->workspace_required_bytes = plan->splitk_bytes;
+    const bool listed = per_tile(plan->desc.bound_kind) && !plan->schedule.entries.empty();
     copy_text(out->selected_kernel, sizeof(out->selected_kernel),
-              plan->splitk_slices > 1 ? "plane_gemm_kernel 128x128 split-K + splitk_finalize_kernel"
+              listed ? (plan->unit_edge == 256 ? "plane_gemm_kernel listed 256x256 units (per-tile schedule)"
+                                               : "plane_gemm_kernel listed 128x128 units (per-tile schedule)")
+              : plan->splitk_slices > 1 ? "plane_gemm_kernel 128x128 split-K + splitk_finalize_kernel"
               : choose_gemm_shape(plan->desc.m, plan->desc.n, plan->desc.k, plan->prefix ? plan->prefix : 1u).tile == 256
                   ? "plane_gemm_kernel 256x256 tile, 4-stage LDS DMA ring"
                   : "plane_gemm_kernel 128x128 tile, 4-stage LDS DMA ring");
