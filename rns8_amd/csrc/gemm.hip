@@ -798,13 +798,17 @@ int64_t tile_count(int64_t m, int64_t n, uint32_t nplanes) {
 GemmShape choose_gemm_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes) {
   // 256 x 256 tiles when they already give every CU at least one; otherwise
   // 128 x 128 tiles (two per CU), and split K when even those leave the chip
-  // under-filled: slices of at least 1024 K until ~512 workgroups.
+  // under-filled: toward ~512 units, with slices of at least 4096 K. Each
+  // slice adds a partial tile per plane to write and sum, and short slices
+  // spend a larger share in the DMA prologue and the epilogue: at
+  // 128 x 128 x 65536 with 8 planes, 16 slices take 35 us, 32 take 38 us and
+  // 64 (1024 K each) 49 us.
   const int64_t kblock = k < kSafeKBlock ? k : kSafeKBlock;
   if (tile_count<CfgLarge>(m, n, nplanes) >= 256) return GemmShape{256, 1};
   const int64_t tiles = tile_count<CfgSmall>(m, n, nplanes);
-  if (tiles >= 256 || kblock < 2048 || padded_ld(n) >= kSplitMaxLd) return GemmShape{128, 1};
+  if (tiles >= 256 || kblock < 8192 || padded_ld(n) >= kSplitMaxLd) return GemmShape{128, 1};
   int64_t slices = (512 + tiles - 1) / tiles;
-  if (slices > kblock / 1024) slices = kblock / 1024;
+  if (slices > kblock / 4096) slices = kblock / 4096;
   if (slices > 64) slices = 64;
   if (slices < 1) slices = 1;
   return GemmShape{128, static_cast<uint32_t>(slices)};
