@@ -598,8 +598,9 @@ rns8_status rns8_destroy_context(rns8_context* ctx) {
     if (ctx->stream) {
       (void)hipSetDevice(ctx->device_id);
       (void)hipStreamSynchronize(ctx->stream);
-      (void)hipStreamDestroy(ctx->stream);
     }
+    release_oneshot_cache(*ctx);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return RNS8_SUCCESS;
   });

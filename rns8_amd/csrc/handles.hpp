@@ -27,12 +27,19 @@ struct ExactAxis {
   bool sum_known = false;
 };
 
+namespace rns8x {
+struct OneshotCache;
+}
+
 struct rns8_context {
   rns8_backend_kind backend = RNS8_BACKEND_HIP_DIRECT;
   int device_id = 0;
   hipStream_t stream = nullptr;
   rns8_device_info device_info{};
   rns8x::HostStaging host;  // pinned staging for host-memory operands and results
+  // device state (plan, matrices, workspace) of the last oneshot call, reused
+  // by the next oneshot call with an equal descriptor; freed with the context
+  rns8x::OneshotCache* oneshot = nullptr;
 };
 
 // Per-tile bounded schedule (reference src/core/internal.hpp:22-70, the
@@ -175,6 +182,9 @@ rns8_status validate_bound_contract(rns8_semantics s, rns8_bound_kind bk, uint64
 // validation + prefix selection shared by plan creation and select_prefix
 rns8_status plan_prefix(const rns8_gemm_desc& d, uint32_t& budget, uint32_t& selected, uint32_t& required,
                         uint32_t& range_bits, uint64_t& effective_bound);
+
+// Frees the context's cached oneshot state (api_exec.cpp).
+void release_oneshot_cache(rns8_context& ctx);
 
 // HIP helpers
 rns8_status hip_status(hipError_t e);

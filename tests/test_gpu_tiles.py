@@ -297,3 +297,51 @@ def test_k_above_int32_block(gpu_ctx):
     gst, est, out, planes, sp = _tile_run(gpu_ctx, True, A, B, 64, 64, bounds)
     assert gst == r.SUCCESS and est == r.SUCCESS
     np.testing.assert_array_equal(out, exact)
+
+
+def test_zero_row_col_proofs_and_unsigned_zero_tiles(gpu_ctx):
+    # proof masks flag the tiles they touch (the GEMM still computes them) and
+    # uint64 zero-output tiles export 0
+    rng = np.random.default_rng(17)
+    m, n, k = 200, 190, 7
+    A = rng.integers(0, 1 << 20, size=(m, k)).astype(np.uint64)
+    B = rng.integers(0, 1 << 20, size=(k, n)).astype(np.uint64)
+    A[5] = 0
+    B[:, 70] = 0
+    exact = A.astype(object) @ B.astype(object)
+    bounds = _tile_maxima(exact, 64, 64)
+    tc = -(-n // 64)
+    bounds[tc + 1] = 0  # zero-output tile (its product is not zero)
+    za = np.zeros(m, dtype=np.uint8)
+    zb = np.zeros(n, dtype=np.uint8)
+    za[5] = 1
+    zb[70] = 1
+    flags = r.abi.PLAN_ALLOW_PROVEN_ZERO_TILE_SKIPS | r.abi.PLAN_ALLOW_PROVEN_ZERO_ROW_COL_SKIPS
+    sem, bk, dt = _kinds(False)
+    desc = r.gemm_desc(sem, bk, m, n, k, max_prefix=9, flags=flags, tile_m=64, tile_n=64, tile_bounds=bounds,
+                       zero_a_rows=za, zero_b_cols=zb)
+    plan = r.Plan(gpu_ctx, desc)
+    entries = plan.tile_schedule()
+    assert any(e.flags & 2 for e in entries) and entries[tc + 1].flags & 1
+    st, oentries, summary = oracle.tile_schedule(False, m, n, 64, 64, bounds, 9, flags, za, zb)
+    assert st == 0 and [e.flags for e in entries] == [e.flags for e in oentries]
+    sp = plan.prefix
+    mk = lambda rows, cols: r.Matrix(gpu_ctx, r.matrix_desc(rows, cols, sem, bk, sp, tile_m=64, tile_n=64))
+    Am, Bm, Cm = mk(m, k), mk(k, n), mk(m, n)
+    ws = r.Workspace(gpu_ctx, plan)
+    r.check(r.pack_u64(gpu_ctx, Am, A, 1), "pack A")
+    r.check(r.pack_u64(gpu_ctx, Bm, B, 2), "pack B")
+    r.check(r.gemm_rns(gpu_ctx, plan, Am, Bm, Cm, ws), "gemm")
+    out = np.full((m, n), 3, dtype=np.uint64)
+    assert r.export_u64(gpu_ctx, plan, Cm, out) == r.SUCCESS
+    want = exact.copy()
+    r0, c0 = 64, 64
+    want[r0:r0 + 64, c0:c0 + 64] = 0
+    assert (out.astype(object) == want).all()
+    Cp = np.zeros((sp, m, n), dtype=np.int8)
+    Cp = oracle.gemm_rns_tiled(oracle.pack_u64(A, sp), oracle.pack_u64(B, sp), Cp, oentries)
+    got = Cm.read_residues(sp)
+    for e in oentries:  # planes each tile computes (the rest were never written: zero here)
+        sl = (slice(0, e.selected_prefix), slice(e.row_offset, e.row_offset + e.row_extent),
+              slice(e.col_offset, e.col_offset + e.col_extent))
+        np.testing.assert_array_equal(got[sl], Cp[sl])
