@@ -57,7 +57,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["grouped"])
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["grouped", "c2", "c4"])
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true")
@@ -78,6 +78,8 @@ def main() -> int:
         return 2
     if args.config == "grouped":
         return grouped_bench(args)
+    if args.config in ("c2", "c4"):
+        return finite_or_wide_bench(args)
 
     import rns8_amd as r
     from rns8_amd import hip, inputs
@@ -438,6 +440,143 @@ def grouped_bench(args) -> int:
         for p in d:
             hip.free(p)
     hip.free(dS)
+    return 0
+
+
+def finite_or_wide_bench(args) -> int:
+    """C2 (finite field 251, 4096^3 uint8, one plane) or C4 (exact-wide signed,
+    2048^3 full-range int64, prefix 20 forced, 3-limb export): pack A, pack B,
+    GEMM, export per step through the device entry points on one stream."""
+    import rns8_amd as r
+    from rns8_amd import hip, inputs
+
+    finite = args.config == "c2"
+    if finite:
+        M = N = K = 4096
+        P, modulus = 1, 251
+        sem, bk = r.FINITE_FIELD_U8, r.BOUND_NONE
+        desc = r.gemm_desc(sem, bk, M, N, K, finite_modulus=modulus)
+        A = inputs.bytes_below(inputs.operand_seed(args.seed, "A"), (M, K), modulus)
+        B = inputs.bytes_below(inputs.operand_seed(args.seed, "B"), (K, N), modulus)
+        elem = 1
+    else:
+        M = N = K = 2048
+        modulus, limbs = 0, 3
+        sem, bk = r.EXACT_WIDE_SIGNED, r.BOUND_NONE
+        desc = r.gemm_desc(sem, bk, M, N, K, max_prefix=20, flags=r.PLAN_FORCE_FIXED_PREFIX)
+        A = inputs.full_int64(inputs.operand_seed(args.seed, "A"), (M, K))
+        B = inputs.full_int64(inputs.operand_seed(args.seed, "B"), (K, N))
+        elem = 8 * limbs
+    log(f"[bench] config {args.config}: {M}x{N}x{K}")
+    ctx = r.Context()
+    plan = r.Plan(ctx, desc)
+    if not finite:
+        P = plan.prefix
+    mk = lambda rows, cols: r.Matrix(ctx, r.matrix_desc(rows, cols, sem, bk, 0 if finite else P))
+    Am, Bm, Cm = mk(M, K), mk(K, N), mk(M, N)
+    ws = r.Workspace(ctx, plan)
+    dA, dB, dC, dS = hip.malloc(A.nbytes), hip.malloc(B.nbytes), hip.malloc(M * N * elem), hip.malloc(64)
+    hip.to_device(dA, A)
+    hip.to_device(dB, B)
+    hip.memset(dS, 0, 64)
+    stream = hip.stream_create()
+    L = r.lib()
+    ev = [hip.event_create() for _ in range(5)]
+
+    def step(timed: bool, version: int):
+        if timed:
+            hip.event_record(ev[0], stream)
+        if finite:
+            r.check(L.rns8_mi355x_pack_finite_u8_device(ctx.ptr, Am.ptr, modulus, dA, K, 0, stream), "pack A")
+        else:
+            r.check(L.rns8_mi355x_pack_i64_device(ctx.ptr, Am.ptr, dA, K, 0, stream), "pack A")
+        if timed:
+            hip.event_record(ev[1], stream)
+        if finite:
+            r.check(L.rns8_mi355x_pack_finite_u8_device(ctx.ptr, Bm.ptr, modulus, dB, N, 0, stream), "pack B")
+        else:
+            r.check(L.rns8_mi355x_pack_i64_device(ctx.ptr, Bm.ptr, dB, N, 0, stream), "pack B")
+        if timed:
+            hip.event_record(ev[2], stream)
+        if finite:
+            r.check(L.rns8_mi355x_gemm_finite_u8_async(ctx.ptr, plan.ptr, modulus, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr,
+                                                        stream), "gemm")
+        else:
+            r.check(L.rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, stream), "gemm")
+        if timed:
+            hip.event_record(ev[3], stream)
+        if finite:
+            r.check(L.rns8_mi355x_export_finite_u8_device(ctx.ptr, plan.ptr, modulus, Cm.ptr, dC, N, stream), "export")
+        else:
+            r.check(L.rns8_mi355x_export_exact_wide_signed_limbs_device(ctx.ptr, plan.ptr, Cm.ptr, dC, N, limbs, dS,
+                                                                        stream), "export")
+        if timed:
+            hip.event_record(ev[4], stream)
+
+    for w in range(args.warmup):
+        step(False, w)
+    hip.stream_synchronize(stream)
+    stage = np.zeros(4)
+    for st_ in range(args.steps):
+        step(True, st_)
+        stage += [hip.event_elapsed_ms(ev[i], ev[i + 1]) for i in range(4)]
+    stage /= args.steps
+    log(f"[bench] stage ms: packA {stage[0]:.4f} packB {stage[1]:.4f} gemm {stage[2]:.4f} export {stage[3]:.4f}")
+    hip.synchronize()
+    start, stop = hip.event_create(), hip.event_create()
+    hip.event_record(start, stream)
+    for st_ in range(args.steps):
+        step(False, st_)
+    hip.event_record(stop, stream)
+    hip.stream_synchronize(stream)
+    ms_per_step = hip.event_elapsed_ms(start, stop) / args.steps
+    rows = np.arange(0, M, M // 16)
+    if finite:
+        out = np.empty((M, N), dtype=np.uint8)
+        hip.from_device(out, dC)
+        want = (A[rows].astype(np.int64) @ B.astype(np.int64)) % modulus
+        exact = bool(np.array_equal(out[rows], want))
+    else:
+        out = np.empty((M, N * limbs), dtype=np.uint64)
+        hip.from_device(out, dC)
+        rows = rows[:4]
+        Ao, Bo = A[rows].astype(object), B.astype(object)
+
+        def value(i, j):  # little-endian two's-complement limbs -> Python int
+            v = sum(int(w) << (64 * l) for l, w in enumerate(out[i, limbs * j:limbs * j + limbs]))
+            return v - (1 << (64 * limbs)) if v >> (64 * limbs - 1) else v
+
+        exact = all(value(i, j) == int((Ao[t] * Bo[:, j]).sum()) for t, i in enumerate(rows)
+                    for j in (0, 1, N // 2, N - 1))
+    status = np.zeros(16, dtype=np.uint32)
+    hip.from_device(status, dS)
+    log(f"[bench] {ms_per_step:.4f} ms per step; sampled outputs exact: {exact}")
+    ops = 2.0 * M * N * K
+    achieved = ops * P / (stage[2] * 1e-3) / 1e12
+    result = {
+        "metric": (f"exact finite-field u8 GEMM mod {modulus} effective TOPS at 4096\u00b3" if finite else
+                   f"exact-wide signed GEMM effective TOPS (2MNK/s) at 2048\u00b3 prefix {P}, 3-limb export"),
+        "value": round(ops / (ms_per_step * 1e-3) / 1e12, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u8" if finite else "int64 (int8 residue MFMA)",
+        "data": ("synthetic: SplitMix64 uniform [0, 251) uint8 operands" if finite else
+                 "synthetic: SplitMix64 full-range int64 operands") + ", resident in HBM",
+        "config": {"workload": f"{args.config} {M}x{N}x{K} prefix {P}, pack+GEMM+export device-resident",
+                   "m": M, "n": N, "k": K, "prefix": P,
+                   "stage_ms": {"pack_a": round(stage[0], 4), "pack_b": round(stage[1], 4),
+                                "gemm": round(stage[2], 4), "export": round(stage[3], 4)},
+                   "range_status": int(status[0]), "sampled_outputs_exact": exact},
+        "roofline": {"bound": "mfma", "kernel": "plane_gemm_kernel<Cfg<4,4>,1,true> (256x256 tiles, persistent)",
+                     "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None, "per_launch_ops": ops * P},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result))
+    for e in ev + [start, stop]:
+        hip.event_destroy(e)
+    hip.stream_destroy(stream)
+    for p_ in (dA, dB, dC, dS):
+        hip.free(p_)
     return 0
 
 

@@ -324,18 +324,37 @@ __global__ __launch_bounds__(256) void export_zero_tiles_kernel(ExportArgs a, co
   for (uint32_t e = 0; e < cells; ++e) out[e] = 0ull;
 }
 
-__global__ __launch_bounds__(256) void export_u8_kernel(ExportU8Args a, uint32_t groups_per_row) {
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Canonical bytes of 4 centered residues at once: a negative byte r (top bit
+// set) becomes r + m, i.e. its unsigned byte plus m modulo 256; bytes are
+// added without carries between them (m = 256 adds nothing).
+__device__ __forceinline__ uint32_t canonical4(uint32_t w, uint32_t m4) {
+  const uint32_t neg = ((w >> 7) & 0x01010101u) * 0xFFu;
+  const uint32_t add = neg & m4;
+  return ((w & 0x7F7F7F7Fu) + (add & 0x7F7F7F7Fu)) ^ ((w ^ add) & 0x80808080u);
+}
+
+// 16 cells per thread: one 16-byte plane load, one 16-byte store where the
+// destination row segment is aligned and whole, byte stores otherwise.
+__global__ __launch_bounds__(256) void export_u8_kernel(ExportU8Args a, uint32_t groups_per_row, uint32_t vec_store) {
   const uint32_t gc = blockIdx.x * blockDim.x + threadIdx.x;
   if (gc >= groups_per_row) return;
-  const int64_t c0 = static_cast<int64_t>(gc) * 4;
+  const int64_t c0 = static_cast<int64_t>(gc) * 16;
+  const uint32_t m4 = (a.modulus & 0xFFu) * 0x01010101u;
   for (int64_t row = blockIdx.y; row < a.m; row += gridDim.y) {
-    const uint32_t word = *reinterpret_cast<const uint32_t*>(a.c + row * a.ldc + c0);
+    const v4i w = *reinterpret_cast<const v4i*>(a.c + row * a.ldc + c0);
+    const v4i out = {static_cast<int>(canonical4(static_cast<uint32_t>(w[0]), m4)),
+                     static_cast<int>(canonical4(static_cast<uint32_t>(w[1]), m4)),
+                     static_cast<int>(canonical4(static_cast<uint32_t>(w[2]), m4)),
+                     static_cast<int>(canonical4(static_cast<uint32_t>(w[3]), m4))};
+    uint8_t* const d = a.dst + row * a.ld + c0;
+    if (vec_store && c0 + 16 <= a.n) {
+      *reinterpret_cast<v4i*>(d) = out;
+    } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (c0 + e < a.n) {
-        const int32_t r = static_cast<int32_t>(static_cast<int8_t>(word >> (8 * e)));
-        a.dst[row * a.ld + c0 + e] = static_cast<uint8_t>(r < 0 ? r + static_cast<int32_t>(a.modulus) : r);
-      }
+      for (int e = 0; e < 16; ++e)
+        if (c0 + e < a.n) d[e] = static_cast<uint8_t>(static_cast<uint32_t>(out[e >> 2]) >> (8 * (e & 3)));
     }
   }
 }
@@ -510,10 +529,12 @@ hipError_t launch_export(const ExportArgs& a, uint32_t prefix, hipStream_t strea
 
 hipError_t launch_export_u8(const ExportU8Args& a, hipStream_t stream) {
   if (!a.c || !a.dst || a.m <= 0 || a.n <= 0 || a.ld < a.n) return hipErrorInvalidValue;
-  if (a.ldc != padded_ld(a.n) || (reinterpret_cast<uintptr_t>(a.c) & 3u) != 0) return hipErrorInvalidValue;
+  if (a.ldc != padded_ld(a.n) || (reinterpret_cast<uintptr_t>(a.c) & 15u) != 0) return hipErrorInvalidValue;
   if (a.modulus < 2 || a.modulus > 256) return hipErrorInvalidValue;
-  const uint32_t groups_per_row = static_cast<uint32_t>(a.ldc / 4);
-  hipLaunchKernelGGL(export_u8_kernel, grid_2d(groups_per_row, a.m), dim3(256), 0, stream, a, groups_per_row);
+  if (a.ldc / 16 > 0xFFFFFFFFll) return hipErrorInvalidValue;
+  const uint32_t groups_per_row = static_cast<uint32_t>(a.ldc / 16);
+  const uint32_t vec = (reinterpret_cast<uintptr_t>(a.dst) % 16 == 0 && a.ld % 16 == 0) ? 1u : 0u;
+  hipLaunchKernelGGL(export_u8_kernel, grid_2d(groups_per_row, a.m), dim3(256), 0, stream, a, groups_per_row, vec);
   return hipGetLastError();
 }
 

@@ -90,19 +90,26 @@ __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConst
 // Finite u8: x < 256, s = x + H < 2^9 is inside the range of the int32
 // reduction constants (their s_max is at least 255 + H).
 __global__ __launch_bounds__(256) void pack_u8_kernel(PackU8Args a, ModulusConsts mc, uint32_t chunks_per_row,
-                                                      uint32_t total_chunks) {
+                                                      uint32_t total_chunks, uint32_t vec_load) {
   const uint32_t m_comp = 256u - mc.m;
   const uint32_t half2 = mc.half * 0x00010001u;
   for (uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x; ch < total_chunks; ch += gridDim.x * blockDim.x) {
     const uint32_t row = ch / chunks_per_row;
     const int64_t c0 = static_cast<int64_t>(ch - row * chunks_per_row) * 16;
     const uint8_t* const rp = a.src + static_cast<int64_t>(row) * a.ld;
+    uint32_t x[16];
+    if (vec_load && c0 + 16 <= a.cols) {
+      // whole aligned 16-byte segment: one load
+      const v4i w = *reinterpret_cast<const v4i*>(rp + c0);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[e] = (static_cast<uint32_t>(w[e >> 2]) >> (8 * (e & 3))) & 0xFFu;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[e] = (c0 + e < a.cols) ? rp[c0 + e] : 0u;
+    }
     uint32_t r[16];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint32_t x = (c0 + e < a.cols) ? rp[c0 + e] : 0u;
-      r[e] = mod_low_byte(x + mc.half, mc.q_shift, mc.q_recip, m_comp);
-    }
+    for (int e = 0; e < 16; ++e) r[e] = mod_low_byte(x[e] + mc.half, mc.q_shift, mc.q_recip, m_comp);
     const v4i w = {static_cast<int>(pack_centered(r[0], r[1], r[2], r[3], half2)),
                    static_cast<int>(pack_centered(r[4], r[5], r[6], r[7], half2)),
                    static_cast<int>(pack_centered(r[8], r[9], r[10], r[11], half2)),
@@ -111,26 +118,42 @@ __global__ __launch_bounds__(256) void pack_u8_kernel(PackU8Args a, ModulusConst
   }
 }
 
+// Maximum |x| of a rows x cols matrix: block (x, y) scans columns
+// [2048 x, 2048 x + 2048) of rows y, y + gridDim.y, ... (coalesced 8-byte
+// loads, no index division), reduces in the block and issues at most one
+// atomic, skipped when the running maximum already covers it.
 template <bool Signed>
 __global__ __launch_bounds__(256) void max_magnitude_kernel(const uint64_t* src, int64_t rows, int64_t cols,
                                                             int64_t ld, unsigned long long* out) {
-  const int64_t total = rows * cols;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 2048;
   unsigned long long best = 0;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t r = i / cols;
-    const uint64_t x = src[r * ld + (i - r * cols)];
-    // |INT64_MIN| = 2^63 is representable as an unsigned magnitude
-    const unsigned long long mag =
-        Signed ? (static_cast<int64_t>(x) < 0 ? 0ull - x : x) : static_cast<unsigned long long>(x);
-    best = mag > best ? mag : best;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const uint64_t* const rp = src + r * ld;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t c = c0 + e * 256 + threadIdx.x;
+      if (c < cols) {
+        const uint64_t x = rp[c];
+        // |INT64_MIN| = 2^63 is representable as an unsigned magnitude
+        const unsigned long long mag =
+            Signed ? (static_cast<int64_t>(x) < 0 ? 0ull - x : x) : static_cast<unsigned long long>(x);
+        best = mag > best ? mag : best;
+      }
+    }
   }
-  // wave reduction, then one atomic per wave
   for (int offset = 32; offset > 0; offset >>= 1) {
     const unsigned long long other = __shfl_down(best, offset, 64);
     best = other > best ? other : best;
   }
-  if ((threadIdx.x & 63) == 0 && best != 0) atomicMax(out, best);
+  __shared__ unsigned long long part[4];
+  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < 4; ++w) best = part[w] > best ? part[w] : best;
+    best = part[0] > best ? part[0] : best;
+    if (best != 0 && __hip_atomic_load(out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < best) atomicMax(out, best);
+  }
 }
 
 unsigned grid_for(int64_t items) {
@@ -169,7 +192,15 @@ hipError_t launch_pack_native(const PackArgs& a, const PlaneConsts& consts, hipS
 hipError_t launch_max_magnitude(const void* src, int64_t rows, int64_t cols, int64_t ld, NativeKind kind,
                                 unsigned long long* out, hipStream_t stream) {
   if (!src || !out || rows <= 0 || cols <= 0 || ld < cols) return hipErrorInvalidValue;
-  const dim3 grid(grid_for(rows * cols) < 2048 ? grid_for(rows * cols) : 2048);
+  // about 1024 blocks (four per CU, each scanning several rows): column
+  // chunks of 2048 across x, row strides across y
+  const int64_t gx = (cols + 2047) / 2048;
+  if (gx > 0x7FFFFFFFll) return hipErrorInvalidValue;
+  int64_t gy = 1024 / gx;
+  if (gy < 1) gy = 1;
+  if (gy > rows) gy = rows;
+  if (gy > 65535) gy = 65535;
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
   if (kind == NativeKind::I64)
     hipLaunchKernelGGL(max_magnitude_kernel<true>, grid, dim3(256), 0, stream, static_cast<const uint64_t*>(src), rows,
                        cols, ld, out);
@@ -186,8 +217,9 @@ hipError_t launch_pack_u8(const PackU8Args& a, hipStream_t stream) {
   const int64_t chunks_per_row = a.plane_ld / 16;
   const int64_t total = chunks_per_row * a.rows;
   if (total >= (int64_t{1} << 32)) return hipErrorInvalidValue;
+  const uint32_t vec = (reinterpret_cast<uintptr_t>(a.src) % 16 == 0 && a.ld % 16 == 0) ? 1u : 0u;
   hipLaunchKernelGGL(pack_u8_kernel, dim3(grid_for(total)), dim3(256), 0, stream, a, make_modulus_consts(a.modulus),
-                     static_cast<uint32_t>(chunks_per_row), static_cast<uint32_t>(total));
+                     static_cast<uint32_t>(chunks_per_row), static_cast<uint32_t>(total), vec);
   return hipGetLastError();
 }
 
