@@ -52,18 +52,15 @@ __device__ __forceinline__ bool limbs_le(const uint32_t (&a)[L], const uint32_t*
   return borrow == 0;
 }
 
-// One cell: centered residue bytes r_i (byte E of words[i]) -> the canonical
-// representative x in [0, prod m_i) as L 24-bit limbs.
-// words[i] holds the centered residue bytes of 4 cells for plane i; flipped[i]
-// is words[i] ^ 0x80808080 (each byte + 128, as unsigned bytes).
-template <uint32_t P, int L, int E>
-__device__ __forceinline__ void reconstruct_x(const uint32_t (&words)[P], const uint32_t (&flipped)[P],
-                                              uint32_t (&x)[L]) {
+// One cell's mixed-radix (Garner) digits v_0 .. v_{P-1}, packed 4 per dword,
+// from its centered residue bytes r_i (byte E of words[i]); flipped[i] is
+// words[i] ^ 0x80808080 (each byte + 128, as unsigned bytes).
+template <uint32_t P, int E>
+__device__ __forceinline__ void garner_digits(const uint32_t (&words)[P], const uint32_t (&flipped)[P],
+                                              uint32_t (&vp)[GarnerTable<P>::kWords]) {
   constexpr GarnerTable<P> T = make_garner_table<P>();
   static_assert(T.m[0] == 256, "digit 0 is the raw residue byte only for modulus 256");
   constexpr uint32_t W = GarnerTable<P>::kWords;
-  // ---- mixed-radix digits, packed 4 per dword ----
-  uint32_t vp[W];
 #pragma unroll
   for (uint32_t q = 0; q < W; ++q) vp[q] = 0u;
   // m_0 = 256: v_0 = r_0 mod 256 is the residue byte itself
@@ -83,15 +80,21 @@ __device__ __forceinline__ void reconstruct_x(const uint32_t (&words)[P], const 
       default: vp[i / 4] = insert_byte<3>(vp[i / 4], t); break;
     }
   }
-  // ---- Horner: x = (..(v_{P-1} m_{P-2} + v_{P-2}) ..) m_0 + v_0 ----
-  // Limbs are kept unmasked between steps: v_mad_u32_u24 reads only the low
-  // 24 bits of its multiplicand, and the bits above are the carry already
-  // passed on, so each limb is masked once, at the end.
+}
+
+// Horner over the low J digits: x = (..(v_{J-1} m_{J-2} + v_{J-2}) ..) m_0 +
+// v_0 = sum_{i<J} v_i M_i in L 24-bit limbs. Limbs are kept unmasked between
+// steps: v_mad_u32_u24 reads only the low 24 bits of its multiplicand, and
+// the bits above are the carry already passed on, so each limb is masked
+// once, at the end.
+template <uint32_t J, int L, uint32_t W>
+__device__ __forceinline__ void horner(const uint32_t (&vp)[W], uint32_t (&x)[L]) {
+  constexpr GarnerTable<J> T = make_garner_table<J>();
 #pragma unroll
   for (int l = 0; l < L; ++l) x[l] = 0u;
-  x[0] = (vp[(P - 1) / 4] >> (8 * ((P - 1) % 4))) & 0xFFu;
+  x[0] = (vp[(J - 1) / 4] >> (8 * ((J - 1) % 4))) & 0xFFu;
 #pragma unroll
-  for (int i = static_cast<int>(P) - 2; i >= 0; --i) {
+  for (int i = static_cast<int>(J) - 2; i >= 0; --i) {
     uint32_t carry = (vp[i / 4] >> (8 * (i % 4))) & 0xFFu;
 #pragma unroll
     for (int l = 0; l < L; ++l) {
@@ -103,6 +106,15 @@ __device__ __forceinline__ void reconstruct_x(const uint32_t (&words)[P], const 
   }
 #pragma unroll
   for (int l = 0; l < L; ++l) x[l] &= 0xFFFFFFu;
+}
+
+// One cell: the canonical representative x in [0, prod m_i) as L limbs.
+template <uint32_t P, int L, int E>
+__device__ __forceinline__ void reconstruct_x(const uint32_t (&words)[P], const uint32_t (&flipped)[P],
+                                              uint32_t (&x)[L]) {
+  uint32_t vp[GarnerTable<P>::kWords];
+  garner_digits<P, E>(words, flipped, vp);
+  horner<P, L>(vp, x);
 }
 
 // x >= ceil(P/2): the centered value is x - P (negative).
@@ -140,39 +152,77 @@ __device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], const ui
 }
 
 // One cell for the 64-bit kinds: the low 64 bits of the centered (Signed) or
-// canonical value v, and whether v is admissible. v is formed as a 24L-bit
-// two's complement value (x - P for a negative result); it has a 64-bit
-// representation iff its bits from 64 up repeat its sign, and then its
-// magnitude is -w or w modulo 2^64, except for v = -2^64, whose low 64 bits
-// are zero (caught by testing mag - 1 against the limit). Same decisions and
-// output bits as sign/magnitude with limbs_le.
+// canonical value v, and whether v is admissible.
+//
+// Prefixes above the digit split (int64: P > kSplitSigned, uint64:
+// P > kSplitUnsigned): Horner runs over the low J digits only, y = sum_{i<J}
+// v_i M_i < M_J, and the digits from J up decide: all 0 gives v = y, all
+// m_i - 1 (int64) gives v = y - M_J, anything else is out of every 64-bit
+// range (|v| >= M_J > 2^63, resp. v >= M_J >= 2^64).
+//
+// Other prefixes: v is formed as a 24L-bit two's complement value (x - P for
+// a negative result); it has a 64-bit representation iff its bits from 64 up
+// repeat its sign, and then its magnitude is -w or w modulo 2^64, except for
+// v = -2^64, whose low 64 bits are zero (caught by testing mag - 1 against the
+// limit).
+//
+// Both forms make the decisions of sign/magnitude with limbs_le; w is the low
+// 64 bits of v whenever v is admissible.
 template <uint32_t P, int L, int E, bool Signed>
 __device__ __forceinline__ uint64_t value64(const uint32_t (&words)[P], const uint32_t (&flipped)[P],
                                             const ExportLimits& lim, bool& ok) {
-  constexpr GarnerTable<P> T = make_garner_table<P>();
-  uint32_t x[L];
-  reconstruct_x<P, L, E>(words, flipped, x);
-  const bool neg = Signed && centered_negative<P, L>(x);
-  uint32_t v[L];
-  uint32_t borrow = 0;
+  constexpr uint32_t J = Signed ? kSplitSigned : kSplitUnsigned;
+  if constexpr (P > J) {
+    constexpr GarnerTable<P> T = make_garner_table<P>();
+    uint32_t vp[GarnerTable<P>::kWords];
+    garner_digits<P, E>(words, flipped, vp);
+    uint32_t y[3];  // M_J < 2^72
+    horner<J, 3>(vp, y);
+    bool zero_top = true, max_top = true;
 #pragma unroll
-  for (int l = 0; l < L; ++l) {
-    const uint32_t t = x[l] - (neg ? T.product[l] : 0u) - borrow;
-    borrow = t >> 31;
-    v[l] = t & 0xFFFFFFu;
+    for (uint32_t i = J; i < P; ++i) {
+      const uint32_t d = (vp[i / 4] >> (8 * (i % 4))) & 0xFFu;
+      zero_top &= d == 0u;
+      max_top &= d == T.m[i] - 1u;
+    }
+    const uint64_t y64 = static_cast<uint64_t>(y[0] | (y[1] << 24)) |
+                         (static_cast<uint64_t>((y[1] >> 8) | (y[2] << 16)) << 32);
+    if constexpr (Signed) {
+      // v < 0: |v| = M_J - y, and |v| - 1 < neg64 iff y > M_J - 1 - neg64
+      // (neg64 <= 2^63 < M_J)
+      constexpr uint64_t MJ = ladder_product64(J);
+      ok = zero_top ? y64 <= lim.pos64 : (max_top & (y64 > MJ - 1ull - lim.neg64));
+      return zero_top ? y64 : y64 - MJ;
+    } else {
+      ok = zero_top & ((y[2] >> 16) == 0u) & (y64 <= lim.pos64);
+      return y64;
+    }
+  } else {
+    constexpr GarnerTable<P> T = make_garner_table<P>();
+    uint32_t x[L];
+    reconstruct_x<P, L, E>(words, flipped, x);
+    const bool neg = Signed && centered_negative<P, L>(x);
+    uint32_t v[L];
+    uint32_t borrow = 0;
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+      const uint32_t t = x[l] - (neg ? T.product[l] : 0u) - borrow;
+      borrow = t >> 31;
+      v[l] = t & 0xFFFFFFu;
+    }
+    const uint64_t w = static_cast<uint64_t>(v[0] | (v[1] << 24)) |
+                       (static_cast<uint64_t>((v[1] >> 8) | (v[2] << 16)) << 32);
+    // branch-free: every term is evaluated (bitwise & / |, selects)
+    const uint32_t ext = neg ? 0xFFFFFFu : 0u;
+    uint32_t diff = (v[2] >> 16) ^ (ext & 0xFFu);
+#pragma unroll
+    for (int l = 3; l < L; ++l) diff |= v[l] ^ ext;
+    // ~w = -w - 1 = mag - 1 for v < 0
+    const bool in_neg = ~w < lim.neg64;
+    const bool in_pos = w <= lim.pos64;
+    ok = (diff == 0u) & (neg ? in_neg : in_pos);
+    return w;
   }
-  const uint64_t w = static_cast<uint64_t>(v[0] | (v[1] << 24)) |
-                     (static_cast<uint64_t>((v[1] >> 8) | (v[2] << 16)) << 32);
-  // branch-free: every term is evaluated (bitwise & / |, selects)
-  const uint32_t ext = neg ? 0xFFFFFFu : 0u;
-  uint32_t diff = (v[2] >> 16) ^ (ext & 0xFFu);
-#pragma unroll
-  for (int l = 3; l < L; ++l) diff |= v[l] ^ ext;
-  const uint64_t mag = neg ? 0ull - w : w;
-  const bool in_neg = mag - 1ull < lim.neg64;
-  const bool in_pos = mag <= lim.pos64;
-  ok = (diff == 0u) & (neg ? in_neg : in_pos);
-  return w;
 }
 
 template <uint32_t P, int L, ExportKind Kind>

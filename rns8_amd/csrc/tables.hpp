@@ -302,6 +302,28 @@ constexpr GarnerTable<P> make_garner_table() {
   return t;
 }
 
+// Product of the first j ladder moduli, for products below 2^64.
+constexpr uint64_t ladder_product64(uint32_t j) {
+  uint64_t p = 1;
+  for (uint32_t i = 0; i < j; ++i) p *= kLadder[i];
+  return p;
+}
+
+// Digit splits of the 64-bit exports. An admissible int64 result has
+// |v| <= 2^63 < M_J (M_j = product of the first j moduli, J = kSplitSigned),
+// so its mixed-radix digits from J up are all 0 (v >= 0) or all m_i - 1
+// (v < 0, x = P - |v|, no borrow past digit J - 1); an admissible uint64
+// result is below 2^64 <= M_J' (J' = kSplitUnsigned), so its digits from J'
+// up are all 0. Only the low J (J') digits need Horner's rule.
+constexpr uint32_t split_signed() {
+  uint32_t j = 0;
+  while (ladder_product64(j) <= (uint64_t{1} << 63)) ++j;
+  return j;
+}
+constexpr uint32_t kSplitSigned = split_signed();
+constexpr uint32_t kSplitUnsigned = kSplitSigned + 1;  // M_{J+1} >= 2 M_J > 2^64
+static_assert(kSplitSigned == 8 && ladder_product64(8) == 13057518384392951040ull, "ladder split");
+
 // 64-bit value as 24-bit limbs.
 inline void u64_to_limbs24(uint64_t v, uint32_t out[kWideLimbs]) {
   for (uint32_t i = 0; i < kWideLimbs; ++i) {
