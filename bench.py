@@ -63,6 +63,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--oneshot", action="store_true",
                     help="time the host-buffer oneshot entry point instead (PCIe transfers included)")
+    ap.add_argument("--graph", action="store_true",
+                    help="capture one step into a HIP graph and time graph replays in the back-to-back pass")
     ap.add_argument("--rns8-bench-json", default="", metavar="PATH",
                     help="also run the host-API lane on the same inputs and write an rns8-bench schema-v4 capture")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -166,12 +168,23 @@ def main() -> int:
     log(f"[bench] stage ms: packA {stage[0]:.4f} packB {stage[1]:.4f} gemm {stage[2]:.4f} export {stage[3]:.4f}")
 
     # end-to-end pass: K steps back to back, bracketed by synchronization
+    graph = None
+    if args.graph:
+        # the device entry points only enqueue kernels, so one step captures
+        hip.capture_begin(stream)
+        step(0, False)
+        graph = hip.capture_end(stream)
+        hip.graph_launch(graph[1], stream)
+        hip.stream_synchronize(stream)
     hip.synchronize()
     start, stop = hip.event_create(), hip.event_create()
     t0 = time.perf_counter()
     hip.event_record(start, stream)
     for s in range(args.steps):
-        step(s, False)
+        if graph:
+            hip.graph_launch(graph[1], stream)
+        else:
+            step(s, False)
     hip.event_record(stop, stream)
     hip.stream_synchronize(stream)
     t1 = time.perf_counter()
@@ -237,6 +250,7 @@ def main() -> int:
             "stage_ms": {"pack_a": round(stage[0], 4), "pack_b": round(stage[1], 4), "gemm": round(stage[2], 4),
                          "export": round(stage[3], 4)},
             "range_status": int(status[0]),
+            "graph_replay": bool(graph),
         },
         "roofline": roofline,
         "cpu_baseline": None,
@@ -252,6 +266,8 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(args, A, B, Cout, P, bound, signed)
 
     print(json.dumps(result))
+    if graph:
+        hip.graph_destroy(*graph)
     for e in ev + [start, stop]:
         hip.event_destroy(e)
     hip.stream_destroy(stream)

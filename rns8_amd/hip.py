@@ -115,3 +115,46 @@ def event_elapsed_ms(start: int, stop: int) -> float:
     _check(_bind_streams().hipEventElapsedTime(C.byref(ms), C.c_void_p(start), C.c_void_p(stop)),
            "hipEventElapsedTime")
     return float(ms.value)
+
+
+# ---- graphs (stream capture) ------------------------------------------------------
+
+CAPTURE_MODE_GLOBAL = 0  # hipStreamCaptureModeGlobal: unsafe calls from any thread fail the capture
+
+
+def _bind_graphs():
+    rt = _bind_streams()
+    if getattr(rt, "_graphs_bound", False):
+        return rt
+    rt.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+    rt.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    rt.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]
+    rt.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+    rt.hipGraphExecDestroy.argtypes = [C.c_void_p]
+    rt.hipGraphDestroy.argtypes = [C.c_void_p]
+    rt._graphs_bound = True
+    return rt
+
+
+def capture_begin(stream: int) -> None:
+    _check(_bind_graphs().hipStreamBeginCapture(C.c_void_p(stream), CAPTURE_MODE_GLOBAL), "hipStreamBeginCapture")
+
+
+def capture_end(stream: int) -> tuple[int, int]:
+    """Ends the capture; returns (graph, executable graph)."""
+    rt = _bind_graphs()
+    g = C.c_void_p()
+    _check(rt.hipStreamEndCapture(C.c_void_p(stream), C.byref(g)), "hipStreamEndCapture")
+    ex = C.c_void_p()
+    _check(rt.hipGraphInstantiate(C.byref(ex), g, None, None, 0), "hipGraphInstantiate")
+    return g.value, ex.value
+
+
+def graph_launch(exec_graph: int, stream: int) -> None:
+    _check(_bind_graphs().hipGraphLaunch(C.c_void_p(exec_graph), C.c_void_p(stream)), "hipGraphLaunch")
+
+
+def graph_destroy(graph: int, exec_graph: int) -> None:
+    rt = _bind_graphs()
+    _check(rt.hipGraphExecDestroy(C.c_void_p(exec_graph)), "hipGraphExecDestroy")
+    _check(rt.hipGraphDestroy(C.c_void_p(graph)), "hipGraphDestroy")
