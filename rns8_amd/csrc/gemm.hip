@@ -40,6 +40,7 @@
 //   * Split-K (tall-skinny K, 128x128 tiles): each slice stores its int32
 //     partial tile to its own workspace slot; a finalize kernel adds the
 //     slices, reduces to int8 and writes C (deterministic, no atomics).
+#include <atomic>
 #include <type_traits>
 
 #include "int_ops.hpp"
@@ -835,17 +836,18 @@ hipError_t launch_zero_words(uint32_t* dst, uint64_t words, hipStream_t stream) 
 
 namespace {
 
-// Compute units of the current device (cached per device id).
+// Compute units of the current device (cached per device id; contexts on
+// several threads may launch at once, so the cache is atomic).
 int device_cu_count() {
-  static int cached[64] = {};
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
+    cached[dev].store(cus, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return cus;
 }
 
 // Ungrouped launches pass a NoTaskTable and ntasks = 1; grouped ones the
