@@ -203,16 +203,16 @@ def main() -> int:
     if tiled:
         workload = (f"RNS8_BOUNDED_I64 {M}x{N}x{K}, per-tile bounds ({tile}x{tile} tiles, A tile rows at "
                     f"2^{TILED_ROW_BITS} cycling, B at 2^{bits}), storage prefix {P}, pack+GEMM+Garner device-resident")
-        kernel = "plane_gemm_kernel<Cfg<4,4>,1,true,true> (listed 256x256 units, persistent)"
+        kernel = "plane_gemm_kernel<Cfg<4,4>,1,true,true,false> (listed 256x256 units, persistent)"
     elif args.config == "c3":
         workload = f"RNS8_BOUNDED_I64 {M}x{N}x{K} prefix {P} (FORCE_FIXED_PREFIX), pack+GEMM+Garner device-resident"
-        kernel = "plane_gemm_kernel<Cfg<4,4>,1,true> (256x256 tiles, persistent)"
+        kernel = "plane_gemm_kernel<Cfg<4,4>,1,true,false,false> (256x256 tiles, persistent)"
     elif args.config == "c5":
         workload = f"c5 {sem} {M}x{N}x{K} prefix {P}, pack+GEMM+Garner device-resident"
-        kernel = "plane_gemm_kernel<Cfg<2,2>,2,true> split-K + splitk_finalize_kernel"
+        kernel = "plane_gemm_kernel<Cfg<2,2>,2,true,false,false> split-K + splitk_finalize_kernel"
     else:
         workload = f"{args.config} {sem} {M}x{N}x{K} prefix {P}, pack+GEMM+Garner device-resident"
-        kernel = "plane_gemm_kernel<Cfg<2,2>,2,true> (128x128 tiles, persistent)"
+        kernel = "plane_gemm_kernel<Cfg<2,2>,2,true,false,false> (128x128 tiles, persistent)"
 
     if args.config == "c3":
         metric = "exact int64 GEMM effective TOPS (2MNK/s) at 4096\u00b3 prefix 9; % int8 MFMA peak"
@@ -582,7 +582,7 @@ def finite_or_wide_bench(args) -> int:
                    "stage_ms": {"pack_a": round(stage[0], 4), "pack_b": round(stage[1], 4),
                                 "gemm": round(stage[2], 4), "export": round(stage[3], 4)},
                    "range_status": int(status[0]), "sampled_outputs_exact": exact},
-        "roofline": {"bound": "mfma", "kernel": "plane_gemm_kernel<Cfg<4,4>,1,true> (256x256 tiles, persistent)",
+        "roofline": {"bound": "mfma", "kernel": "plane_gemm_kernel<Cfg<4,4>,1,true,false,false> (256x256 tiles, persistent)",
                      "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None, "per_launch_ops": ops * P},
         "cpu_baseline": None,
