@@ -48,6 +48,37 @@ TILED_EDGE = 128
 TILED_ROW_BITS = [1, 5, 9, 13, 17, 21, 25]
 
 
+class StageTimer:
+    """HIP events at the stage boundaries of `steps` back-to-back steps on one
+    stream. Nothing synchronizes between the steps, so each stage runs as it
+    does in the timed pass; the elapsed times are read once, after the last
+    step, and averaged per stage."""
+
+    def __init__(self, steps: int, marks: int, stream):
+        from rns8_amd import hip
+
+        self.hip = hip
+        self.ev = [[hip.event_create() for _ in range(marks)] for _ in range(steps)]
+        self.stream = stream
+
+    def marker(self, step: int):
+        return lambda i: self.hip.event_record(self.ev[step][i], self.stream)
+
+    def stage_ms(self) -> np.ndarray:
+        self.hip.stream_synchronize(self.stream)
+        t = [[self.hip.event_elapsed_ms(e[i], e[i + 1]) for i in range(len(e) - 1)] for e in self.ev]
+        return np.array(t).mean(axis=0)
+
+    def destroy(self) -> None:
+        for row in self.ev:
+            for e in row:
+                self.hip.event_destroy(e)
+
+
+def _no_mark(_i: int) -> None:
+    pass
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -56,7 +87,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["grouped", "c2", "c4"])
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
@@ -135,44 +166,28 @@ def main() -> int:
     pack = L.rns8_mi355x_pack_i64_device if signed else L.rns8_mi355x_pack_u64_device
     export = L.rns8_mi355x_export_i64_device if signed else L.rns8_mi355x_export_u64_device
 
-    ev = [hip.event_create() for _ in range(5)]
-
-    def step(version: int, timed: bool):
-        if timed:
-            hip.event_record(ev[0], stream)
+    def step(mark=_no_mark):
+        mark(0)
         r.check(pack(ctx.ptr, Am.ptr, dA, K, 0, stream), "pack A")
-        if timed:
-            hip.event_record(ev[1], stream)
+        mark(1)
         r.check(pack(ctx.ptr, Bm.ptr, dB, N, 0, stream), "pack B")
-        if timed:
-            hip.event_record(ev[2], stream)
+        mark(2)
         r.check(L.rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, stream), "gemm")
-        if timed:
-            hip.event_record(ev[3], stream)
+        mark(3)
         r.check(export(ctx.ptr, plan.ptr, Cm.ptr, dC, N, dS, stream), "export")
-        if timed:
-            hip.event_record(ev[4], stream)
+        mark(4)
 
-    for w in range(args.warmup):
-        step(w, False)
+    for _ in range(args.warmup):
+        step()
     hip.stream_synchronize(stream)
     log("[bench] warmup done")
-
-    # stage timing pass (events between stages)
-    stage = np.zeros(4)
-    for s in range(args.steps):
-        step(s, True)
-        t = [hip.event_elapsed_ms(ev[i], ev[i + 1]) for i in range(4)]
-        stage += np.array(t)
-    stage /= args.steps
-    log(f"[bench] stage ms: packA {stage[0]:.4f} packB {stage[1]:.4f} gemm {stage[2]:.4f} export {stage[3]:.4f}")
 
     # end-to-end pass: K steps back to back, bracketed by synchronization
     graph = None
     if args.graph:
         # the device entry points only enqueue kernels, so one step captures
         hip.capture_begin(stream)
-        step(0, False)
+        step()
         graph = hip.capture_end(stream)
         hip.graph_launch(graph[1], stream)
         hip.stream_synchronize(stream)
@@ -184,7 +199,7 @@ def main() -> int:
         if graph:
             hip.graph_launch(graph[1], stream)
         else:
-            step(s, False)
+            step()
     hip.event_record(stop, stream)
     hip.stream_synchronize(stream)
     t1 = time.perf_counter()
@@ -192,6 +207,15 @@ def main() -> int:
     ms_total = hip.event_elapsed_ms(start, stop)
     ms_per_step = ms_total / args.steps
     log(f"[bench] {args.steps} steps: {ms_total:.3f} ms (host clock {1e3 * (t1 - t0):.3f} ms)")
+
+    # stage timing pass, after the timed one: K more steps back to back with
+    # events between the stages
+    timer = StageTimer(args.steps, 5, stream)
+    for s in range(args.steps):
+        step(timer.marker(s))
+    stage = timer.stage_ms()
+    timer.destroy()
+    log(f"[bench] stage ms: packA {stage[0]:.4f} packB {stage[1]:.4f} gemm {stage[2]:.4f} export {stage[3]:.4f}")
 
     status = np.zeros(16, dtype=np.uint32)
     hip.from_device(status, dS)
@@ -268,7 +292,7 @@ def main() -> int:
     print(json.dumps(result))
     if graph:
         hip.graph_destroy(*graph)
-    for e in ev + [start, stop]:
+    for e in (start, stop):
         hip.event_destroy(e)
     hip.stream_destroy(stream)
     for p in (dA, dB, dC, dS):
@@ -376,51 +400,45 @@ def grouped_bench(args) -> int:
     hip.memset(dS, 0, 64)
     stream = hip.stream_create()
     L = r.lib()
-    ev = [hip.event_create() for _ in range(4)]
-
-    def step(timed: bool, grouped: bool = True):
-        if timed:
-            hip.event_record(ev[0], stream)
+    def step(mark=_no_mark, grouped: bool = True):
+        mark(0)
         for (Am, Bm, _, _), (dA, dB, _) in zip(quads, dev):
             r.check(L.rns8_mi355x_pack_i64_device(ctx.ptr, Am.ptr, dA, K, 0, stream), "pack A")
             r.check(L.rns8_mi355x_pack_i64_device(ctx.ptr, Bm.ptr, dB, N, 0, stream), "pack B")
-        if timed:
-            hip.event_record(ev[1], stream)
+        mark(1)
         if grouped:
             r.check(L.rns8_mi355x_gemm_rns_grouped_async(ctx.ptr, plan.ptr, tasks, T, stream), "grouped gemm")
         else:
             for Am, Bm, Cm, ws in quads:
                 r.check(L.rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, stream),
                         "gemm")
-        if timed:
-            hip.event_record(ev[2], stream)
+        mark(2)
         for (_, _, Cm, _), (_, _, dC) in zip(quads, dev):
             r.check(L.rns8_mi355x_export_i64_device(ctx.ptr, plan.ptr, Cm.ptr, dC, N, dS, stream), "export")
-        if timed:
-            hip.event_record(ev[3], stream)
+        mark(3)
 
     for _ in range(args.warmup):
-        step(False)
-    hip.stream_synchronize(stream)
-    stage = np.zeros(3)
-    ungrouped = 0.0
-    for _ in range(args.steps):
-        step(True)
-        stage += [hip.event_elapsed_ms(ev[i], ev[i + 1]) for i in range(3)]
-        step(True, grouped=False)
-        ungrouped += hip.event_elapsed_ms(ev[1], ev[2])
-    stage /= args.steps
-    ungrouped /= args.steps
-    log(f"[bench] stage ms: pack {stage[0]:.4f} grouped gemm {stage[1]:.4f} export {stage[2]:.4f}; "
-        f"{T} ungrouped gemms {ungrouped:.4f}")
+        step()
     hip.synchronize()
     start, stop = hip.event_create(), hip.event_create()
     hip.event_record(start, stream)
     for _ in range(args.steps):
-        step(False)
+        step()
     hip.event_record(stop, stream)
     hip.stream_synchronize(stream)
     ms_per_step = hip.event_elapsed_ms(start, stop) / args.steps
+    # stage timing, after the timed pass: grouped and ungrouped steps back to
+    # back, alternating
+    timer, timer_ungrouped = StageTimer(args.steps, 4, stream), StageTimer(args.steps, 4, stream)
+    for s in range(args.steps):
+        step(timer.marker(s))
+        step(timer_ungrouped.marker(s), grouped=False)
+    stage = timer.stage_ms()
+    ungrouped = timer_ungrouped.stage_ms()[1]
+    timer.destroy()
+    timer_ungrouped.destroy()
+    log(f"[bench] stage ms: pack {stage[0]:.4f} grouped gemm {stage[1]:.4f} export {stage[2]:.4f}; "
+        f"{T} ungrouped gemms {ungrouped:.4f}")
     status = np.zeros(16, dtype=np.uint32)
     hip.from_device(status, dS)
     out = np.empty((M, N), dtype=np.int64)
@@ -449,7 +467,7 @@ def grouped_bench(args) -> int:
         "cpu_baseline": None,
     }
     print(json.dumps(result))
-    for e in ev + [start, stop]:
+    for e in (start, stop):
         hip.event_destroy(e)
     hip.stream_destroy(stream)
     for d in dev:
@@ -497,55 +515,48 @@ def finite_or_wide_bench(args) -> int:
     hip.memset(dS, 0, 64)
     stream = hip.stream_create()
     L = r.lib()
-    ev = [hip.event_create() for _ in range(5)]
-
-    def step(timed: bool, version: int):
-        if timed:
-            hip.event_record(ev[0], stream)
+    def step(mark=_no_mark):
+        mark(0)
         if finite:
             r.check(L.rns8_mi355x_pack_finite_u8_device(ctx.ptr, Am.ptr, modulus, dA, K, 0, stream), "pack A")
         else:
             r.check(L.rns8_mi355x_pack_i64_device(ctx.ptr, Am.ptr, dA, K, 0, stream), "pack A")
-        if timed:
-            hip.event_record(ev[1], stream)
+        mark(1)
         if finite:
             r.check(L.rns8_mi355x_pack_finite_u8_device(ctx.ptr, Bm.ptr, modulus, dB, N, 0, stream), "pack B")
         else:
             r.check(L.rns8_mi355x_pack_i64_device(ctx.ptr, Bm.ptr, dB, N, 0, stream), "pack B")
-        if timed:
-            hip.event_record(ev[2], stream)
+        mark(2)
         if finite:
             r.check(L.rns8_mi355x_gemm_finite_u8_async(ctx.ptr, plan.ptr, modulus, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr,
                                                         stream), "gemm")
         else:
             r.check(L.rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, stream), "gemm")
-        if timed:
-            hip.event_record(ev[3], stream)
+        mark(3)
         if finite:
             r.check(L.rns8_mi355x_export_finite_u8_device(ctx.ptr, plan.ptr, modulus, Cm.ptr, dC, N, stream), "export")
         else:
             r.check(L.rns8_mi355x_export_exact_wide_signed_limbs_device(ctx.ptr, plan.ptr, Cm.ptr, dC, N, limbs, dS,
                                                                         stream), "export")
-        if timed:
-            hip.event_record(ev[4], stream)
+        mark(4)
 
-    for w in range(args.warmup):
-        step(False, w)
-    hip.stream_synchronize(stream)
-    stage = np.zeros(4)
-    for st_ in range(args.steps):
-        step(True, st_)
-        stage += [hip.event_elapsed_ms(ev[i], ev[i + 1]) for i in range(4)]
-    stage /= args.steps
-    log(f"[bench] stage ms: packA {stage[0]:.4f} packB {stage[1]:.4f} gemm {stage[2]:.4f} export {stage[3]:.4f}")
+    for _ in range(args.warmup):
+        step()
     hip.synchronize()
     start, stop = hip.event_create(), hip.event_create()
     hip.event_record(start, stream)
-    for st_ in range(args.steps):
-        step(False, st_)
+    for _ in range(args.steps):
+        step()
     hip.event_record(stop, stream)
     hip.stream_synchronize(stream)
     ms_per_step = hip.event_elapsed_ms(start, stop) / args.steps
+    # stage timing, after the timed pass
+    timer = StageTimer(args.steps, 5, stream)
+    for s in range(args.steps):
+        step(timer.marker(s))
+    stage = timer.stage_ms()
+    timer.destroy()
+    log(f"[bench] stage ms: packA {stage[0]:.4f} packB {stage[1]:.4f} gemm {stage[2]:.4f} export {stage[3]:.4f}")
     rows = np.arange(0, M, M // 16)
     if finite:
         out = np.empty((M, N), dtype=np.uint8)
@@ -588,7 +599,7 @@ def finite_or_wide_bench(args) -> int:
         "cpu_baseline": None,
     }
     print(json.dumps(result))
-    for e in ev + [start, stop]:
+    for e in (start, stop):
         hip.event_destroy(e)
     hip.stream_destroy(stream)
     for p_ in (dA, dB, dC, dS):
