@@ -1,0 +1,126 @@
+"""Exact-wide admission decisions at the range threshold, through the C ABI.
+
+An exact-wide plan's prefix always covers K * 2^127 (signed) or K * 2^128
+(unsigned), so a product of two host operands is always admitted; the
+decision that can go either way is the one for a product whose operand is an
+earlier result. rns8_gemm_rns admits it iff its bound fits the prefix, 2 *
+bound < P (signed) or bound < P (unsigned), where the bound comes from the
+per-row and per-column summaries that C = A x B carries (reference
+exact_range.hpp:80-157), and those come from the candidates of
+exact_axis_product_bound over A's rows and B's columns.
+
+Each case is a chain D = (A x B) x E in which every bound is attained (checked
+by brute force against the oracle's restatement, oracle/exact_range.py), with E
+scaled so D's bound lands just inside and just outside the range: the library
+must admit the first (and export D exactly) and refuse the second with
+RNS8_RANGE_ERROR. The A x B pairs make a different candidate decide C's cell
+bounds each time, so a dropped candidate, a wrong centre or a wrong remainder
+in the library enlarges C's carried bound and changes a decision.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import rns8_amd as r
+from oracle import exact_range as xr
+
+pytestmark = pytest.mark.gpu
+
+# Row/column pairs where exactly one candidate of the bound equals |dot(a, b)|
+# (the same pairs pin the oracle on the CPU): absolute sum of a times max |b|;
+# max |a| times absolute sum of b; the centre term with a zero remainder; the
+# centre term with each of the remainder's deviation-sum terms strictly
+# smallest.
+UNIQUE = [([-3, 0], [6, 1], 18), ([-2, 1], [5, 0], 10), ([3, -5, -1], [-6, -6, -6], 18), ([5, -8], [4, 6], 28),
+          ([2, -1], [-5, -4], 6)]
+
+
+def _int_matmul(A, B):
+    return [[sum(int(x) * int(y) for x, y in zip(row, col)) for col in zip(*B)] for row in A]
+
+
+def _maxabs(M):
+    return max(abs(v) for row in M for v in row)
+
+
+def _limbs(P):
+    return P.bit_length() // 64 + 2
+
+
+def _oracle_bound(A, B, E):
+    _, C_op = xr.gemm_bound(xr.native_operand(A), xr.native_operand(B), len(A), len(B[0]), len(B))
+    bound, _ = xr.gemm_bound(C_op, xr.native_operand(E), len(A), len(E[0]), len(E))
+    return bound
+
+
+def _run_chain(ctx, A, B, E, prefix, signed):
+    """Packs host A, B, E at `prefix`, runs C = A x B (must be admitted) and
+    D = C x E; returns (status of D, exported D or None)."""
+    sem = r.EXACT_WIDE_SIGNED if signed else r.EXACT_WIDE_UNSIGNED
+    bk = r.BOUND_NONE
+    dt = np.int64 if signed else np.uint64
+    m, k1, k2, n = len(A), len(B), len(E), len(E[0])
+    flags = r.PLAN_FORCE_FIXED_PREFIX
+    p1 = r.Plan(ctx, r.gemm_desc(sem, bk, m, k2, k1, max_prefix=prefix, flags=flags))
+    p2 = r.Plan(ctx, r.gemm_desc(sem, bk, m, n, k2, max_prefix=prefix, flags=flags))
+    mats = {name: r.Matrix(ctx, r.matrix_desc(rows, cols, sem, bk, prefix))
+            for name, rows, cols in (("A", m, k1), ("B", k1, k2), ("C", m, k2), ("E", k2, n), ("D", m, n))}
+    pack = r.pack_i64 if signed else r.pack_u64
+    for version, (name, src) in enumerate((("A", A), ("B", B), ("E", E)), start=1):
+        r.check(pack(ctx, mats[name], np.array(src, dtype=dt), version), "pack " + name)
+    r.check(r.gemm_rns(ctx, p1, mats["A"], mats["B"], mats["C"], r.Workspace(ctx, p1)), "C = A x B")
+    st = r.gemm_rns(ctx, p2, mats["C"], mats["E"], mats["D"], r.Workspace(ctx, p2))
+    if st != r.SUCCESS:
+        return st, None
+    L = _limbs(oracle.modulus_product(prefix))
+    out = np.zeros((m, n * L), dtype=np.uint64)
+    export = r.export_exact_wide_signed_limbs if signed else r.export_exact_wide_unsigned_limbs
+    r.check(export(ctx, p2, mats["D"], out, L), "export D")
+    return st, [[oracle.limbs_to_int(out[i, L * j:L * j + L], signed) for j in range(n)] for i in range(m)]
+
+
+def _threshold_pair(ctx, A, B, e_row, prefix, signed):
+    """E = k2 copies of s * e_row with s the largest scale whose D bound still
+    fits (step 0, admitted) and s + 1 (step 1, refused)."""
+    P = oracle.modulus_product(prefix)
+    limit = (P - 1) // 2 if signed else P - 1  # largest admitted bound
+    k2 = len(B[0])
+    unit = _oracle_bound(A, B, [list(e_row)] * k2)  # bound at scale 1; bounds scale linearly in s
+    s = limit // unit
+    assert s >= 64, "the scale step must be small against every candidate's excess"
+    for step, want in ((0, r.SUCCESS), (1, r.RANGE_ERROR)):
+        E = [[(s + step) * v for v in e_row]] * k2
+        truth = _maxabs(_int_matmul(_int_matmul(A, B), E))
+        bound = _oracle_bound(A, B, E)
+        assert bound == truth
+        assert xr.fits(signed, bound, P) == (want == r.SUCCESS)
+        for M in (A, B, E):
+            assert xr.pack_admits(signed, M, P)
+        st, D = _run_chain(ctx, A, B, E, prefix, signed)
+        assert st == want, (prefix, step, bound, P)
+        if D is not None:
+            assert D == _int_matmul(_int_matmul(A, B), E)
+
+
+@pytest.mark.parametrize("prefix", [17, 19, 20])
+@pytest.mark.parametrize("case", range(len(UNIQUE)))
+def test_signed_chain_threshold_each_candidate(gpu_ctx, prefix, case):
+    a, b, _ = UNIQUE[case]
+    sa, sb = 1 << 59, -(1 << 59)  # |entries| <= 8 * 2^59 < 2^63
+    A = [[sa * x for x in a]] * 3
+    B = [[sb * y, sb * y] for y in b]  # equal columns: C's rows are one-signed, so D's bound is attained
+    _threshold_pair(gpu_ctx, A, B, [1, 1], prefix, True)
+
+
+@pytest.mark.parametrize("prefix", [18, 20])
+def test_signed_chain_threshold_constant(gpu_ctx, prefix):
+    A = [[-(1 << 62)] * 4] * 2
+    B = [[(1 << 62) - 1] * 3] * 4
+    _threshold_pair(gpu_ctx, A, B, [1, 1], prefix, True)
+
+
+@pytest.mark.parametrize("prefix", [17, 20])
+def test_unsigned_chain_threshold_one_signed_columns(gpu_ctx, prefix):
+    A = [[(1 << 63) + 5] * 4] * 2
+    B = [[3 << 40, 1 << 40], [1 << 40, 2 << 40], [4 << 40, 1], [1 << 40, 9 << 40]]
+    _threshold_pair(gpu_ctx, A, B, [1, 1], prefix, False)
