@@ -113,6 +113,36 @@ RNS8_API rns8_status rns8_mi355x_gemm_finite_u8_grouped_async(
     uint32_t task_count,
     void* stream);
 
+/* Fused native-input GEMM for bounded int64 / uint64 plans: C's residue
+ * planes straight from native device operands (m x k at row stride lda, k x n
+ * at row stride ldb, in elements), the pack folded into the GEMM's operand
+ * loads, enqueued on `stream` (reference hip_direct_gemm_native_kernels.cuh:
+ * 9-193, its native-operand GEMM behind the oneshot path,
+ * hip_backend_gemm_native_prefix.inc). Offered for outputs small enough that
+ * the product is split along K; returns RNS8_UNSUPPORTED_BACKEND for other
+ * plans, whose operands are packed once and multiplied by rns8_gemm_rns. The
+ * plan's declared bound covers the result exactly as for rns8_gemm_rns. */
+RNS8_API rns8_status rns8_mi355x_gemm_native_i64_async(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    const int64_t* d_A,
+    int64_t lda,
+    const int64_t* d_B,
+    int64_t ldb,
+    rns8_matrix* C,
+    rns8_workspace* workspace,
+    void* stream);
+RNS8_API rns8_status rns8_mi355x_gemm_native_u64_async(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    const uint64_t* d_A,
+    int64_t lda,
+    const uint64_t* d_B,
+    int64_t ldb,
+    rns8_matrix* C,
+    rns8_workspace* workspace,
+    void* stream);
+
 /* Device-destination variants of the exports (reference rns8.h:1146-1242). */
 RNS8_API rns8_status rns8_mi355x_export_i64_device(
     rns8_context* ctx,

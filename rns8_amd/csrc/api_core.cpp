@@ -700,6 +700,12 @@ rns8_status init_plan(const rns8_gemm_desc& d, rns8_backend_kind backend, rns8_p
   if (!per_tile(d.bound_kind)) {
     plan.splitk_slices = choose_splitk_slices(d.m, d.n, kblock, planes);
     plan.splitk_bytes = splitk_workspace_bytes(d.m, d.n, kblock, planes);
+    // the fused native-input GEMM shares the workspace
+    if ((d.semantics == RNS8_BOUNDED_I64 || d.semantics == RNS8_BOUNDED_U64) &&
+        choose_fused_shape(d.m, d.n, d.k, planes, padded_ld(d.n), plan.fused)) {
+      plan.fused_ok = true;
+      plan.splitk_bytes = std::max<uint64_t>(plan.splitk_bytes, plan.fused.ws_bytes);
+    }
   }
   return RNS8_SUCCESS;
 }
@@ -979,7 +985,7 @@ rns8_status rns8_create_workspace(rns8_context* ctx, const rns8_plan* plan, rns8
         return RNS8_BACKEND_FAILURE;
       }
       ws->splitk_bytes = plan->splitk_bytes;
-      // the GEMM leaves this buffer zeroed after every use
+      // zeroed once; every launch that uses it writes each cell it later reads
       if (launch_zero_words(reinterpret_cast<uint32_t*>(ws->splitk), plan->splitk_bytes / 4, ctx->stream) !=
               hipSuccess ||
           hipStreamSynchronize(ctx->stream) != hipSuccess) {

@@ -469,6 +469,52 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
   return RNS8_SUCCESS;
 }
 
+// Fused native-input GEMM (rns8_mi355x_gemm_native_*_async): bounded plans
+// whose output is small enough for the fused path (fused.hip). The plan's
+// declared bound covers the result as it does for rns8_gemm_rns, so no
+// operand proof is needed; C must be the plan's output matrix.
+template <typename T>
+rns8_status gemm_native(rns8_context* ctx, const rns8_plan* plan, const T* A, int64_t lda, const T* B, int64_t ldb,
+                        rns8_matrix* C, rns8_workspace* ws, void* stream_arg) {
+  constexpr bool is_signed = std::is_same<T, int64_t>::value;
+  const rns8_semantics sem = is_signed ? RNS8_BOUNDED_I64 : RNS8_BOUNDED_U64;
+  if (!ctx || !plan || !A || !B || !C || !ws) return RNS8_INVALID_ARGUMENT;
+  if (plan->desc.semantics != sem) return RNS8_INVALID_ARGUMENT;
+  rns8_status st = check_plan_ctx_ws(*ctx, *plan, *ws);
+  if (st != RNS8_SUCCESS) return st;
+  const int64_t m = plan->desc.m, n = plan->desc.n, k = plan->desc.k;
+  if (!valid_access(m, k, lda) || !valid_access(k, n, ldb)) return RNS8_INVALID_ARGUMENT;
+  if (C->backend != plan->backend || C->device_id != ctx->device_id) return RNS8_INVALID_ARGUMENT;
+  if (!matrix_matches(*C, sem, storage_bound_kind(*plan), m, n, storage_prefix(*plan), plan->desc.tile_m,
+                      plan->desc.tile_n))
+    return RNS8_INVALID_ARGUMENT;
+  if (!plan->fused_ok || plan->fused.ws_bytes > ws->splitk_bytes) return RNS8_UNSUPPORTED_BACKEND;
+  const hipStream_t stream = pick_stream(*ctx, stream_arg);
+  if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  C->device_current = false;
+  FusedArgs f{};
+  f.a = A;
+  f.b = B;
+  f.lda = lda;
+  f.ldb = ldb;
+  f.m = m;
+  f.n = n;
+  f.k = k;
+  f.c = C->planes;
+  f.ldc = C->plane_ld;
+  f.pitch_c = C->plane_pitch;
+  f.nplanes = plan->prefix;
+  f.kind = is_signed ? NativeKind::I64 : NativeKind::U64;
+  f.ws = reinterpret_cast<int8_t*>(ws->splitk);
+  f.shape = plan->fused;
+  const hipError_t e = launch_fused_native(f, make_ladder_plane_consts(plan->prefix), stream);
+  if (e == hipErrorInvalidValue) return RNS8_UNSUPPORTED_BACKEND;
+  if (e != hipSuccess) return RNS8_BACKEND_FAILURE;
+  C->device_current = true;
+  C->source_version = 0;  // native device operands carry no source version
+  return RNS8_SUCCESS;
+}
+
 rns8_status gemm_finite(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus, const rns8_matrix* A,
                         const rns8_matrix* B, rns8_matrix* C, rns8_workspace* ws, void* stream_arg, bool synchronous) {
   if (!ctx || !plan || !A || !B || !C || !ws) return RNS8_INVALID_ARGUMENT;
@@ -990,6 +1036,18 @@ rns8_status rns8_mi355x_gemm_finite_u8_async(rns8_context* ctx, const rns8_plan*
                                              const rns8_matrix* A, const rns8_matrix* B, rns8_matrix* C,
                                              rns8_workspace* workspace, void* stream) {
   return guard([&] { return gemm_finite(ctx, plan, modulus, A, B, C, workspace, stream, false); });
+}
+
+rns8_status rns8_mi355x_gemm_native_i64_async(rns8_context* ctx, const rns8_plan* plan, const int64_t* d_A,
+                                              int64_t lda, const int64_t* d_B, int64_t ldb, rns8_matrix* C,
+                                              rns8_workspace* workspace, void* stream) {
+  return guard([&] { return gemm_native<int64_t>(ctx, plan, d_A, lda, d_B, ldb, C, workspace, stream); });
+}
+
+rns8_status rns8_mi355x_gemm_native_u64_async(rns8_context* ctx, const rns8_plan* plan, const uint64_t* d_A,
+                                              int64_t lda, const uint64_t* d_B, int64_t ldb, rns8_matrix* C,
+                                              rns8_workspace* workspace, void* stream) {
+  return guard([&] { return gemm_native<uint64_t>(ctx, plan, d_A, lda, d_B, ldb, C, workspace, stream); });
 }
 
 rns8_status rns8_mi355x_gemm_rns_grouped_async(rns8_context* ctx, const rns8_plan* plan,

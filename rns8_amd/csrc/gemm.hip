@@ -126,15 +126,6 @@ __device__ __forceinline__ int swizzle_b(int k, int chunk) {
     return chunk ^ x;
 }
 
-// For u = x + 2^31 (x an int32 sum), returns a value whose low byte is
-// (x + H) mod m, H = floor(m/2): s = dot(bytes(u), 2^(8b) mod m) + off_i32 is
-// congruent to x + H and at most s_max, q = floor(s / m) by the 24-bit
-// quotient of tables.hpp, and s + q*(256 - m) is congruent to s - q*m modulo
-// 256. m_comp = 256 - m.
-__device__ __forceinline__ uint32_t residue_plus_half(uint32_t u, const ModulusConsts& mc, uint32_t m_comp) {
-  return mod_low_byte(__builtin_amdgcn_udot4(u, mc.pow_lo, mc.off_i32, false), mc.q_shift, mc.q_recip, m_comp);
-}
-
 // Raw buffer resource over [p, p + bytes). The inputs are wave-uniform; they
 // are passed through readfirstlane so the descriptor is built in SGPRs.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
@@ -211,25 +202,6 @@ struct TaskTable {
 struct NoTaskTable {};
 template <bool kGrouped>
 using GroupArg = std::conditional_t<kGrouped, TaskTable, NoTaskTable>;
-
-// Reads accumulator elements 4g .. 4g+3 straight from their AGPRs. The asm
-// keeps the accumulators in AGPRs through the epilogue (the compiler
-// otherwise copies all of them to VGPRs at once) and, being volatile, keeps
-// the reads in program order with the epilogue's LDS stores, so only a few
-// values are live at a time; four per statement leave the scheduler four
-// independent chains to interleave.
-struct Acc4 {
-  uint32_t v[4];
-};
-__device__ __forceinline__ Acc4 acc_read4(const v16i& acc, int g) {
-  Acc4 r;
-  asm volatile(
-      "v_accvgpr_read_b32 %0, %4\n\tv_accvgpr_read_b32 %1, %5\n\t"
-      "v_accvgpr_read_b32 %2, %6\n\tv_accvgpr_read_b32 %3, %7"
-      : "=v"(r.v[0]), "=v"(r.v[1]), "=v"(r.v[2]), "=v"(r.v[3])
-      : "a"(acc[4 * g]), "a"(acc[4 * g + 1]), "a"(acc[4 * g + 2]), "a"(acc[4 * g + 3]));
-  return r;
-}
 
 // floor(n / d) for n < 2^31 (make_div_u31).
 __device__ __forceinline__ uint32_t div_u31(uint32_t n, DivU31 v) { return __umulhi(n << 1, v.mul) >> v.shift; }

@@ -67,7 +67,11 @@ struct rns8_plan {
   rns8x::I256 product;           // modulus product of the selected prefix
   uint64_t tile_rows = 0, tile_cols = 0, tile_count = 0;
   uint32_t splitk_slices = 1;
-  uint64_t splitk_bytes = 0;
+  uint64_t splitk_bytes = 0;  // workspace bytes: the larger of the split-K and the fused path's needs
+  // Bounded int64/uint64 plans whose output is small enough for the fused
+  // native-input GEMM (fused.hip): its K split and partial-residue bytes.
+  bool fused_ok = false;
+  rns8x::FusedShape fused{};
   TileSchedule schedule;  // per-tile bound kinds only
   // Per-tile plans: device lists the GEMM and export run from, built when the
   // plan is created and never changed. `units` (two words per unit, see

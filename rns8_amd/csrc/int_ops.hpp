@@ -34,6 +34,35 @@ __device__ __forceinline__ uint32_t mod_low_byte(uint32_t s, uint32_t shift, uin
   return mad_u24(mulhi_u24(s << shift, recip), m_comp, s);
 }
 
+// For u = x + 2^31 (x an int32 sum), returns a value whose low byte is
+// (x + H) mod m, H = floor(m/2): s = dot(bytes(u), 2^(8b) mod m) + off_i32 is
+// congruent to x + H and at most s_max, q = floor(s / m) by the 24-bit
+// quotient of tables.hpp, and s + q*(256 - m) is congruent to s - q*m modulo
+// 256. m_comp = 256 - m.
+__device__ __forceinline__ uint32_t residue_plus_half(uint32_t u, const ModulusConsts& mc, uint32_t m_comp) {
+  return mod_low_byte(__builtin_amdgcn_udot4(u, mc.pow_lo, mc.off_i32, false), mc.q_shift, mc.q_recip, m_comp);
+}
+
+// Reads accumulator elements 4g .. 4g+3 of a 32x32 MFMA tile straight from
+// their AGPRs. The asm keeps the accumulators in AGPRs through an epilogue
+// (the compiler otherwise copies all of them to VGPRs at once) and, being
+// volatile, keeps the reads in program order with the epilogue's stores, so
+// only a few values are live at a time; four per statement leave the
+// scheduler four independent chains to interleave.
+typedef int v16i __attribute__((ext_vector_type(16)));
+struct Acc4 {
+  uint32_t v[4];
+};
+__device__ __forceinline__ Acc4 acc_read4(const v16i& acc, int g) {
+  Acc4 r;
+  asm volatile(
+      "v_accvgpr_read_b32 %0, %4\n\tv_accvgpr_read_b32 %1, %5\n\t"
+      "v_accvgpr_read_b32 %2, %6\n\tv_accvgpr_read_b32 %3, %7"
+      : "=v"(r.v[0]), "=v"(r.v[1]), "=v"(r.v[2]), "=v"(r.v[3])
+      : "a"(acc[4 * g]), "a"(acc[4 * g + 1]), "a"(acc[4 * g + 2]), "a"(acc[4 * g + 3]));
+  return r;
+}
+
 // Packs (r_e - H) mod 256 for e = 0..3 into one little-endian dword, where
 // r_e holds (x_e + H) mod m in its low byte (other bytes ignored): the
 // centered residues as int8. half2 = H * 0x10001. v_perm_b32(s0, s1, sel)

@@ -62,6 +62,31 @@ struct GemmArgs {
   uint32_t slices;
 };
 hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream);
+
+// Fused native-input GEMM (fused.hip): C's residue planes straight from
+// int64/uint64 device operands, for outputs small enough that the product is
+// split along K. `shape` comes from choose_fused_shape, which returns false
+// where the fused path is not offered (its int8 workspace of partial residues,
+// [slices][planes][m][ldc], would exceed its limit).
+struct FusedShape {
+  uint32_t slices;    // K slices, each a multiple of 32 and at most 65536 deep
+  int64_t k_slice;
+  uint64_t ws_bytes;
+};
+bool choose_fused_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, int64_t ldc, FusedShape& out);
+struct FusedArgs {
+  const void* a;  // device, m x k native elements at row stride lda
+  const void* b;  // device, k x n native elements at row stride ldb
+  int64_t lda, ldb;
+  int64_t m, n, k;
+  int8_t* c;  // [nplanes][m][ldc] centered residues
+  int64_t ldc, pitch_c;
+  uint32_t nplanes;
+  NativeKind kind;
+  int8_t* ws;  // shape.ws_bytes of workspace
+  FusedShape shape;
+};
+hipError_t launch_fused_native(const FusedArgs& args, const PlaneConsts& consts, hipStream_t stream);
 // Per-tile schedules: `units` edge x edge tile-planes (edge 256 or 128) from a
 // device list of two words each, (plane << 24 | tile row) and (quadrant mask
 // << 24 | tile column); bit q = 2 * (row half) + (column half) of the mask
