@@ -92,6 +92,9 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--fused", action="store_true",
+                    help="c5/c1: one fused native-input GEMM (rns8_mi355x_gemm_native_*_async) in place of the two "
+                         "packs and the plane GEMM")
     ap.add_argument("--oneshot", action="store_true",
                     help="time the host-buffer oneshot entry point instead (PCIe transfers included)")
     ap.add_argument("--graph", action="store_true",
@@ -165,14 +168,24 @@ def main() -> int:
     L = r.lib()
     pack = L.rns8_mi355x_pack_i64_device if signed else L.rns8_mi355x_pack_u64_device
     export = L.rns8_mi355x_export_i64_device if signed else L.rns8_mi355x_export_u64_device
+    native = L.rns8_mi355x_gemm_native_i64_async if signed else L.rns8_mi355x_gemm_native_u64_async
+    if args.fused and tiled:
+        log("[bench] --fused applies to plans with a global bound only")
+        return 2
 
     def step(mark=_no_mark):
         mark(0)
-        r.check(pack(ctx.ptr, Am.ptr, dA, K, 0, stream), "pack A")
-        mark(1)
-        r.check(pack(ctx.ptr, Bm.ptr, dB, N, 0, stream), "pack B")
-        mark(2)
-        r.check(L.rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, stream), "gemm")
+        if args.fused:
+            # the packs are inside the fused launch: their stages are empty
+            mark(1)
+            mark(2)
+            r.check(native(ctx.ptr, plan.ptr, dA, K, dB, N, Cm.ptr, ws.ptr, stream), "fused gemm")
+        else:
+            r.check(pack(ctx.ptr, Am.ptr, dA, K, 0, stream), "pack A")
+            mark(1)
+            r.check(pack(ctx.ptr, Bm.ptr, dB, N, 0, stream), "pack B")
+            mark(2)
+            r.check(L.rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, stream), "gemm")
         mark(3)
         r.check(export(ctx.ptr, plan.ptr, Cm.ptr, dC, N, dS, stream), "export")
         mark(4)
@@ -247,7 +260,16 @@ def main() -> int:
         "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles("plane_gemm_kernel", args.config),
         "per_launch_ops": gemm_ops,
     }
-    if args.config == "c5":
+    if args.fused:
+        # pack and GEMM in one pass: the native operands are read (8 bytes per
+        # element) and the C planes written; HBM bounds it for tall-skinny shapes
+        kernel = "fused_native_kernel<Signed,Vec,NP> + residue_finalize_kernel"
+        workload = workload.replace("pack+GEMM", "fused pack+GEMM")
+        gemm_bytes = 8 * K * (M + N) + P * M * N
+        gbs = gemm_bytes / ((stage[0] + stage[1] + stage[2]) * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "kernel": kernel, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "per_launch_bytes": gemm_bytes}
+    elif args.config == "c5":
         # tall and skinny: the GEMM streams P planes of A and B once (K x (M + N) bytes
         # each) and does little MFMA work per byte, so HBM bounds it
         gemm_bytes = P * K * (M + N) + P * M * N

@@ -3,14 +3,16 @@
 // (reference hip_direct_gemm_native_kernels.cuh:9-193 converts native
 // operands inside its tile loads the same way, one plane per launch slice).
 //
-// Where it pays: outputs too small to fill the chip, so the work is split
-// along K (tall-skinny products such as 128 x 128 x 65536). There the planes
-// of A and B are read once by the GEMM anyway, so writing them out in a pack
-// pass and reading them back costs more than the conversion: the fused launch
-// reads each native element once per plane group and never stores its
-// residues to HBM. For large outputs every operand panel is read by many
-// output tiles, and packing once is cheaper (the host offers the fused path
-// only below a workspace limit).
+// Scope: outputs too small to fill the chip, so the work is split along K
+// (tall-skinny products such as 128 x 128 x 65536), where the packed planes
+// would be read only once by the GEMM; the fused launch reads each native
+// element once per plane group and never stores its residues to HBM. For
+// large outputs every operand panel is read by many output tiles and packing
+// once is cheaper, so the host offers the fused path only below a workspace
+// limit. Measured at 128 x 128 x 65536 it is still slower than two packs and
+// the split-K GEMM (100 against 83 us of kernels): with four planes of
+// accumulators in the AGPRs only one workgroup runs per CU, and one step of
+// native loads in flight per thread does not hide their latency.
 //
 // Work split: a workgroup owns a 128 x 128 output tile, a group of up to four
 // planes and one K slice. Its four waves each hold a 64 x 64 quadrant of all
@@ -50,18 +52,19 @@ constexpr int64_t kMaxSliceK = 65536;                 // |int32 sum| <= 65536 * 
 constexpr int64_t kMinSliceK = 512;                   // 16 steps: amortizes the epilogue
 constexpr uint64_t kMaxWorkspace = uint64_t{64} << 20;
 
-// Centered residues of four native values (split in 32-bit halves, the sign
-// bit of signed inputs already flipped) for one modulus, packed little-endian
+// Centered residues of native values 4q .. 4q+3 (split in 32-bit halves, the
+// sign bit of signed inputs already flipped) for one modulus, packed
+// little-endian
 // (reference cpu_reference.cpp:53-130; the same arithmetic as the pack kernel).
-__device__ __forceinline__ uint32_t residues4(const uint32_t* lo, const uint32_t* hi, const ModulusConsts& mc,
-                                              uint32_t off) {
-  if (mc.m == 256u) return pack_low_bytes(lo[0], lo[1], lo[2], lo[3]);
+__device__ __forceinline__ uint32_t residues4(const uint32_t (&lo)[16], const uint32_t (&hi)[16], int q,
+                                              const ModulusConsts& mc, uint32_t off) {
+  if (mc.m == 256u) return pack_low_bytes(lo[4 * q], lo[4 * q + 1], lo[4 * q + 2], lo[4 * q + 3]);
   const uint32_t m_comp = 256u - mc.m;
   uint32_t r[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const uint32_t t = __builtin_amdgcn_udot4(lo[e], mc.pow_lo, off, false);
-    r[e] = mod_low_byte(__builtin_amdgcn_udot4(hi[e], mc.pow_hi, t, false), mc.pq_shift, mc.pq_recip, m_comp);
+    const uint32_t t = __builtin_amdgcn_udot4(lo[4 * q + e], mc.pow_lo, off, false);
+    r[e] = mod_low_byte(__builtin_amdgcn_udot4(hi[4 * q + e], mc.pow_hi, t, false), mc.pq_shift, mc.pq_recip, m_comp);
   }
   return pack_centered(r[0], r[1], r[2], r[3], mc.half * 0x00010001u);
 }
@@ -95,59 +98,77 @@ __global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, Plane
   const int b_col = t & 127, b_half = t >> 7;
   const bool a_ok = m0 + a_row < a.m;
   const bool b_ok = n0 + b_col < a.n;
+  // Rows past m and columns past n read row / column 0, k past the slice
+  // reads its last element, and the values are replaced by 0 afterwards: every
+  // load is in bounds and unconditional, so a thread's loads are all in flight
+  // together (a load under a condition followed by a select waits for each
+  // one in turn).
   const uint64_t* const a_src = static_cast<const uint64_t*>(a.a) + (a_ok ? (m0 + a_row) * a.lda : 0);
   const uint64_t* const b_src = static_cast<const uint64_t*>(a.b) + (b_ok ? n0 + b_col : 0);
 
-  uint32_t alo[16], ahi[16], blo[16], bhi[16];
-  auto load = [&](int64_t k0) {
+  // raw operand words of one step
+  struct Raw {
+    uint32_t alo[16], ahi[16], blo[16], bhi[16];
+  };
+  auto load = [&](Raw& raw, int64_t k0) {
     const int64_t ka = k0 + 16 * a_half;
-    if (Vec && a_ok && ka + 16 <= ke) {
+    if (Vec && ka + 16 <= ke) {
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
         const v2u64 v = *reinterpret_cast<const v2u64*>(a_src + ka + e);
-        alo[e] = static_cast<uint32_t>(v[0]);
-        ahi[e] = static_cast<uint32_t>(v[0] >> 32);
-        alo[e + 1] = static_cast<uint32_t>(v[1]);
-        ahi[e + 1] = static_cast<uint32_t>(v[1] >> 32);
+        raw.alo[e] = static_cast<uint32_t>(v[0]);
+        raw.ahi[e] = static_cast<uint32_t>(v[0] >> 32);
+        raw.alo[e + 1] = static_cast<uint32_t>(v[1]);
+        raw.ahi[e + 1] = static_cast<uint32_t>(v[1] >> 32);
       }
     } else {
+      uint64_t x[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[e] = a_src[min(ka + e, ke - 1)];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const uint64_t x = (a_ok && ka + e < ke) ? a_src[ka + e] : 0ull;  // out of range packs as 0
-        alo[e] = static_cast<uint32_t>(x);
-        ahi[e] = static_cast<uint32_t>(x >> 32);
+        const uint64_t v = ka + e < ke ? x[e] : 0ull;  // out of range packs as 0
+        raw.alo[e] = static_cast<uint32_t>(v);
+        raw.ahi[e] = static_cast<uint32_t>(v >> 32);
       }
     }
+    if (!a_ok) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) raw.alo[e] = raw.ahi[e] = 0u;
+    }
     const int64_t kk = k0 + 16 * b_half;
+    uint64_t y[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) y[e] = b_src[min(kk + e, ke - 1) * a.ldb];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const uint64_t x = (b_ok && kk + e < ke) ? b_src[(kk + e) * a.ldb] : 0ull;
-      blo[e] = static_cast<uint32_t>(x);
-      bhi[e] = static_cast<uint32_t>(x >> 32);
+      const uint64_t v = b_ok && kk + e < ke ? y[e] : 0ull;
+      raw.blo[e] = static_cast<uint32_t>(v);
+      raw.bhi[e] = static_cast<uint32_t>(v >> 32);
     }
     if (Signed) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        ahi[e] ^= 0x80000000u;
-        bhi[e] ^= 0x80000000u;
+        raw.ahi[e] ^= 0x80000000u;
+        raw.bhi[e] ^= 0x80000000u;
       }
     }
   };
   // residues of the loaded elements for every plane of the group, into stage
   // `stage`: A row r at r*32 + 16*half, B column c at 4096 + c*32 + 16*half
-  auto convert_store = [&](int stage) {
+  auto convert_store = [&](const Raw& raw, int stage) {
     int8_t* const st = lds + stage * kStageLds;
 #pragma unroll
     for (int pl = 0; pl < NP; ++pl) {
       {
         const ModulusConsts mc = pc.mod[p0 + pl];
         const uint32_t off = Signed ? mc.off_i64 : mc.off_u64;
-        const v4i wa = {static_cast<int>(residues4(alo, ahi, mc, off)), static_cast<int>(residues4(alo + 4, ahi + 4, mc, off)),
-                        static_cast<int>(residues4(alo + 8, ahi + 8, mc, off)),
-                        static_cast<int>(residues4(alo + 12, ahi + 12, mc, off))};
-        const v4i wb = {static_cast<int>(residues4(blo, bhi, mc, off)), static_cast<int>(residues4(blo + 4, bhi + 4, mc, off)),
-                        static_cast<int>(residues4(blo + 8, bhi + 8, mc, off)),
-                        static_cast<int>(residues4(blo + 12, bhi + 12, mc, off))};
+        const v4i wa = {static_cast<int>(residues4(raw.alo, raw.ahi, 0, mc, off)), static_cast<int>(residues4(raw.alo, raw.ahi, 1, mc, off)),
+                        static_cast<int>(residues4(raw.alo, raw.ahi, 2, mc, off)),
+                        static_cast<int>(residues4(raw.alo, raw.ahi, 3, mc, off))};
+        const v4i wb = {static_cast<int>(residues4(raw.blo, raw.bhi, 0, mc, off)), static_cast<int>(residues4(raw.blo, raw.bhi, 1, mc, off)),
+                        static_cast<int>(residues4(raw.blo, raw.bhi, 2, mc, off)),
+                        static_cast<int>(residues4(raw.blo, raw.bhi, 3, mc, off))};
         *reinterpret_cast<v4i*>(st + pl * kPlaneLds + a_row * kStepK + 16 * a_half) = wa;
         *reinterpret_cast<v4i*>(st + pl * kPlaneLds + kOperandLds + b_col * kStepK + 16 * b_half) = wb;
       }
@@ -188,16 +209,18 @@ __global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, Plane
     }
   };
 
-  load(kb);
-  convert_store(0);
+  // Step s computes from stage s & 1 while the next step's loads are in
+  // flight and its residues go into the other stage, which the barrier ending
+  // step s-1 retired.
+  Raw raw;
+  load(raw, kb);
+  convert_store(raw, 0);
   __syncthreads();
   for (int s = 0; s < steps; ++s) {
     const bool more = s + 1 < steps;
-    if (more) load(kb + static_cast<int64_t>(kStepK) * (s + 1));
+    if (more) load(raw, kb + static_cast<int64_t>(kStepK) * (s + 1));
     mma(s & 1);
-    // stage (s+1)&1 was last read by step s-1, which the barrier ending it
-    // retired
-    if (more) convert_store((s + 1) & 1);
+    if (more) convert_store(raw, (s + 1) & 1);
     __syncthreads();
   }
 
@@ -240,30 +263,51 @@ __global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, Plane
 
 // Adds the slices' centered residues of four consecutive cells (one dword per
 // slice) and writes their centered residue into C (reference
-// cpu_reference.cpp:156-311: the plane result is the sum's residue).
+// cpu_reference.cpp:156-311: the plane result is the sum's residue). A block
+// covers 32 dwords; its eight 32-thread groups each add every eighth slice,
+// so the loads of many slices are in flight at once, and group 0 combines
+// the eight partial sums.
+constexpr int kFinalWords = 32;
+constexpr int kFinalGroups = 8;
 __global__ __launch_bounds__(256) void residue_finalize_kernel(const int8_t* ws, int8_t* c, int64_t m, int64_t ldc,
                                                                int64_t pitch_c, uint32_t nplanes, uint32_t slices,
                                                                PlaneConsts pc) {
+  __shared__ int32_t part[kFinalGroups][kFinalWords][4];
   const int64_t words_per_plane = m * ldc / 4;
   const int64_t total = words_per_plane * nplanes;
   const int64_t slice_words = static_cast<int64_t>(nplanes) * words_per_plane;
   const uint32_t* const src = reinterpret_cast<const uint32_t*>(ws);
-  for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < total;
-       w += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+  const int lw = threadIdx.x % kFinalWords;
+  const int grp = threadIdx.x / kFinalWords;
+  for (int64_t w0 = static_cast<int64_t>(blockIdx.x) * kFinalWords; w0 < total;
+       w0 += static_cast<int64_t>(gridDim.x) * kFinalWords) {
+    const int64_t w = w0 + lw;
     int32_t sum[4] = {0, 0, 0, 0};
-    for (uint32_t s = 0; s < slices; ++s) {
-      const uint32_t v = src[static_cast<int64_t>(s) * slice_words + w];
+    if (w < total) {
+      for (uint32_t s = grp; s < slices; s += kFinalGroups) {
+        const uint32_t v = src[static_cast<int64_t>(s) * slice_words + w];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sum[e] += static_cast<int32_t>(static_cast<int8_t>(v >> (8 * e)));
+        for (int e = 0; e < 4; ++e) sum[e] += static_cast<int32_t>(static_cast<int8_t>(v >> (8 * e)));
+      }
     }
-    const uint32_t plane = static_cast<uint32_t>(w / words_per_plane);
-    const int64_t in_plane = w - static_cast<int64_t>(plane) * words_per_plane;
-    const ModulusConsts mc = pc.mod[plane];
-    uint32_t r[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = residue_plus_half(static_cast<uint32_t>(sum[e]) ^ 0x80000000u, mc, 256u - mc.m);
-    *reinterpret_cast<uint32_t*>(c + static_cast<int64_t>(plane) * pitch_c + in_plane * 4) =
-        pack_centered(r[0], r[1], r[2], r[3], mc.half * 0x00010001u);
+    for (int e = 0; e < 4; ++e) part[grp][lw][e] = sum[e];
+    __syncthreads();
+    if (grp == 0 && w < total) {
+#pragma unroll
+      for (int g = 1; g < kFinalGroups; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[e] += part[g][lw][e];
+      const uint32_t plane = static_cast<uint32_t>(w / words_per_plane);
+      const int64_t in_plane = w - static_cast<int64_t>(plane) * words_per_plane;
+      const ModulusConsts mc = pc.mod[plane];
+      uint32_t r[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = residue_plus_half(static_cast<uint32_t>(sum[e]) ^ 0x80000000u, mc, 256u - mc.m);
+      *reinterpret_cast<uint32_t*>(c + static_cast<int64_t>(plane) * pitch_c + in_plane * 4) =
+          pack_centered(r[0], r[1], r[2], r[3], mc.half * 0x00010001u);
+    }
+    __syncthreads();
   }
 }
 
@@ -329,7 +373,7 @@ hipError_t launch_fused_native(const FusedArgs& a, const PlaneConsts& consts, hi
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t words = static_cast<int64_t>(a.nplanes) * a.m * a.ldc / 4;
-  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((words + 255) / 256, 2048));
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((words + kFinalWords - 1) / kFinalWords, 4096));
   hipLaunchKernelGGL(residue_finalize_kernel, dim3(blocks), dim3(256), 0, stream, a.ws, a.c, a.m, a.ldc, a.pitch_c,
                      a.nplanes, a.shape.slices, consts);
   return hipGetLastError();
