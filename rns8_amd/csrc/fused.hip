@@ -5,25 +5,25 @@
 //
 // Scope: outputs too small to fill the chip, so the work is split along K
 // (tall-skinny products such as 128 x 128 x 65536), where the packed planes
-// would be read only once by the GEMM; the fused launch reads each native
-// element once per plane group and never stores its residues to HBM. For
-// large outputs every operand panel is read by many output tiles and packing
-// once is cheaper, so the host offers the fused path only below a workspace
-// limit. Measured at 128 x 128 x 65536 it is still slower than two packs and
-// the split-K GEMM (100 against 83 us of kernels): with four planes of
-// accumulators in the AGPRs only one workgroup runs per CU, and one step of
-// native loads in flight per thread does not hide their latency.
+// would be read only once by the GEMM; the fused launch never stores
+// residues to HBM. For large outputs every operand panel is read by many
+// output tiles and packing once is cheaper, so the host offers the fused path
+// only below a workspace limit. Measured at 128 x 128 x 65536 it is still
+// slower than two packs and the split-K GEMM (96 against 83 us of kernels):
+// the residue arithmetic is VALU-bound, and here A's elements are reduced
+// once per 64-column tile and per plane group, 1.5 times the packs' work.
 //
-// Work split: a workgroup owns a 128 x 128 output tile, a group of up to four
-// planes and one K slice. Its four waves each hold a 64 x 64 quadrant of all
-// four planes (4 planes x 2 x 2 blocks of v_mfma_i32_32x32x32_i8, 256
-// accumulator registers). Per 32-deep K step every thread loads 16 native
-// elements of A (one row, 16 consecutive k) and 16 of B (one column, 16
+// Work split: a workgroup owns a 128 x 64 output tile, a group of up to four
+// planes and one K slice; two workgroups run per CU. Its four waves each hold
+// a 64 x 32 part of all four planes (4 planes x 2 blocks of
+// v_mfma_i32_32x32x32_i8, 128 accumulator registers). Per 32-deep K step
+// every thread loads 16 native elements of A (two consecutive k of eight rows,
+// so a wave's load covers whole row segments) and 8 of B (one column, 8
 // consecutive k), reduces them to centered residues for each plane of the
 // group with the pack's arithmetic (two v_dot4_u32_u8 and a 24-bit quotient,
-// tables.hpp), and stores 16 bytes per plane into a k-contiguous LDS layout,
-// so every MFMA fragment is one ds_read_b128. LDS is double-buffered: the
-// next step's loads and residues overlap this step's MFMAs.
+// tables.hpp), and stores them into a k-contiguous LDS layout, so every MFMA
+// fragment is one ds_read_b128. LDS is double-buffered: the next step's loads
+// and residues overlap this step's MFMAs.
 //
 // Each slice reduces its int32 sums to centered int8 residues in the
 // epilogue and stores them into its own slot of the workspace; a finalize
@@ -40,14 +40,17 @@ namespace rns8x {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
 
-constexpr int kTile = 128;                            // output rows and columns per workgroup
+constexpr int kTileM = 128;                           // output rows per workgroup
+constexpr int kTileN = 64;                            // output columns per workgroup
 constexpr int kStepK = 32;                            // K per step (one MFMA depth)
 constexpr int kGroupPlanes = 4;                       // planes per workgroup
-constexpr int kOperandLds = kTile * kStepK;           // 4 KB: 128 rows (or columns) x 32 k
-constexpr int kPlaneLds = 2 * kOperandLds;            // A block, then B block
-constexpr int kStageLds = kGroupPlanes * kPlaneLds;   // 32 KB
+constexpr int kALds = kTileM * kStepK;                // 4 KB: 128 rows x 32 k
+constexpr int kBLds = kTileN * kStepK;                // 2 KB: 64 columns x 32 k
+constexpr int kPlaneLds = kALds + kBLds;              // A block, then B block
+constexpr int kStageLds = kGroupPlanes * kPlaneLds;   // 24 KB
 constexpr int64_t kMaxSliceK = 65536;                 // |int32 sum| <= 65536 * 128 * 128 = 2^30
 constexpr int64_t kMinSliceK = 512;                   // 16 steps: amortizes the epilogue
 constexpr uint64_t kMaxWorkspace = uint64_t{64} << 20;
@@ -56,7 +59,8 @@ constexpr uint64_t kMaxWorkspace = uint64_t{64} << 20;
 // sign bit of signed inputs already flipped) for one modulus, packed
 // little-endian
 // (reference cpu_reference.cpp:53-130; the same arithmetic as the pack kernel).
-__device__ __forceinline__ uint32_t residues4(const uint32_t (&lo)[16], const uint32_t (&hi)[16], int q,
+template <int N>
+__device__ __forceinline__ uint32_t residues4(const uint32_t (&lo)[N], const uint32_t (&hi)[N], int q,
                                               const ModulusConsts& mc, uint32_t off) {
   if (mc.m == 256u) return pack_low_bytes(lo[4 * q], lo[4 * q + 1], lo[4 * q + 2], lo[4 * q + 3]);
   const uint32_t m_comp = 256u - mc.m;
@@ -75,7 +79,7 @@ __device__ __forceinline__ uint32_t residues4(const uint32_t (&lo)[16], const ui
 // rows. NP is a template parameter so that every accumulator is updated
 // unconditionally and stays in its AGPRs.
 template <bool Signed, bool Vec, int NP>
-__global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, PlaneConsts pc, uint32_t tiles_n,
+__global__ __launch_bounds__(256, 2) void fused_native_kernel(FusedArgs a, PlaneConsts pc, uint32_t tiles_n,
                                                               uint32_t plane_base) {
   __shared__ __attribute__((aligned(16))) int8_t lds[2 * kStageLds];
   const int t = threadIdx.x;
@@ -84,78 +88,77 @@ __global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, Plane
   const int wm = wave >> 1, wn = wave & 1;
   const uint32_t tr = blockIdx.x / tiles_n;
   const uint32_t tc = blockIdx.x - tr * tiles_n;
-  const int64_t m0 = static_cast<int64_t>(tr) * kTile;
-  const int64_t n0 = static_cast<int64_t>(tc) * kTile;
+  const int64_t m0 = static_cast<int64_t>(tr) * kTileM;
+  const int64_t n0 = static_cast<int64_t>(tc) * kTileN;
   const uint32_t slice = blockIdx.y;
   const uint32_t p0 = plane_base + blockIdx.z * kGroupPlanes;
   const int64_t kb = static_cast<int64_t>(slice) * a.shape.k_slice;
   const int64_t ke = min(kb + a.shape.k_slice, a.k);
   const int steps = static_cast<int>((ke - kb + kStepK - 1) / kStepK);
 
-  // loader roles: A row a_row, k 16*a_half .. +15 of the step; B column
-  // b_col, k 16*b_half .. +15
-  const int a_row = t >> 1, a_half = t & 1;
-  const int b_col = t & 127, b_half = t >> 7;
-  const bool a_ok = m0 + a_row < a.m;
+  // Loader roles. A: sixteen threads per row, two consecutive k each, so a
+  // wave's load covers four whole 256-byte row segments; thread t holds rows
+  // (t >> 4) + 16j, j = 0..7, at k = 2*(t & 15), +1 (element 2j, 2j+1 of its
+  // arrays). B: column b_col, k 8*b_q .. +7.
+  const int a_r0 = t >> 4, a_k2 = 2 * (t & 15);
+  const int b_col = t & 63, b_q = t >> 6;
   const bool b_ok = n0 + b_col < a.n;
   // Rows past m and columns past n read row / column 0, k past the slice
   // reads its last element, and the values are replaced by 0 afterwards: every
   // load is in bounds and unconditional, so a thread's loads are all in flight
   // together (a load under a condition followed by a select waits for each
   // one in turn).
-  const uint64_t* const a_src = static_cast<const uint64_t*>(a.a) + (a_ok ? (m0 + a_row) * a.lda : 0);
+  const uint64_t* const a_base = static_cast<const uint64_t*>(a.a);
   const uint64_t* const b_src = static_cast<const uint64_t*>(a.b) + (b_ok ? n0 + b_col : 0);
 
   // raw operand words of one step
   struct Raw {
-    uint32_t alo[16], ahi[16], blo[16], bhi[16];
+    uint32_t alo[16], ahi[16], blo[8], bhi[8];
   };
   auto load = [&](Raw& raw, int64_t k0) {
-    const int64_t ka = k0 + 16 * a_half;
-    if (Vec && ka + 16 <= ke) {
+    const int64_t ka = k0 + a_k2;
 #pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        const v2u64 v = *reinterpret_cast<const v2u64*>(a_src + ka + e);
-        raw.alo[e] = static_cast<uint32_t>(v[0]);
-        raw.ahi[e] = static_cast<uint32_t>(v[0] >> 32);
-        raw.alo[e + 1] = static_cast<uint32_t>(v[1]);
-        raw.ahi[e + 1] = static_cast<uint32_t>(v[1] >> 32);
+    for (int j = 0; j < 8; ++j) {
+      const int64_t row = m0 + a_r0 + 16 * j;
+      const bool ok = row < a.m;
+      const uint64_t* const rp = a_base + (ok ? row * a.lda : 0);
+      uint64_t x0, x1;
+      if (Vec && ka + 2 <= ke) {
+        const v2u64 v = *reinterpret_cast<const v2u64*>(rp + ka);
+        x0 = v[0];
+        x1 = v[1];
+      } else {
+        const uint64_t y0 = rp[min(ka, ke - 1)];
+        const uint64_t y1 = rp[min(ka + 1, ke - 1)];
+        x0 = ka < ke ? y0 : 0ull;  // out of range packs as 0
+        x1 = ka + 1 < ke ? y1 : 0ull;
       }
-    } else {
-      uint64_t x[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) x[e] = a_src[min(ka + e, ke - 1)];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const uint64_t v = ka + e < ke ? x[e] : 0ull;  // out of range packs as 0
-        raw.alo[e] = static_cast<uint32_t>(v);
-        raw.ahi[e] = static_cast<uint32_t>(v >> 32);
-      }
+      x0 = ok ? x0 : 0ull;
+      x1 = ok ? x1 : 0ull;
+      raw.alo[2 * j] = static_cast<uint32_t>(x0);
+      raw.ahi[2 * j] = static_cast<uint32_t>(x0 >> 32);
+      raw.alo[2 * j + 1] = static_cast<uint32_t>(x1);
+      raw.ahi[2 * j + 1] = static_cast<uint32_t>(x1 >> 32);
     }
-    if (!a_ok) {
+    const int64_t kk = k0 + 8 * b_q;
+    uint64_t y[8];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) raw.alo[e] = raw.ahi[e] = 0u;
-    }
-    const int64_t kk = k0 + 16 * b_half;
-    uint64_t y[16];
+    for (int e = 0; e < 8; ++e) y[e] = b_src[min(kk + e, ke - 1) * a.ldb];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) y[e] = b_src[min(kk + e, ke - 1) * a.ldb];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
+    for (int e = 0; e < 8; ++e) {
       const uint64_t v = b_ok && kk + e < ke ? y[e] : 0ull;
       raw.blo[e] = static_cast<uint32_t>(v);
       raw.bhi[e] = static_cast<uint32_t>(v >> 32);
     }
     if (Signed) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        raw.ahi[e] ^= 0x80000000u;
-        raw.bhi[e] ^= 0x80000000u;
-      }
+      for (int e = 0; e < 16; ++e) raw.ahi[e] ^= 0x80000000u;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) raw.bhi[e] ^= 0x80000000u;
     }
   };
   // residues of the loaded elements for every plane of the group, into stage
-  // `stage`: A row r at r*32 + 16*half, B column c at 4096 + c*32 + 16*half
+  // `stage`: A row r, k at r*32 + k; B column c, k at 4096 + c*32 + k
   auto convert_store = [&](const Raw& raw, int stage) {
     int8_t* const st = lds + stage * kStageLds;
 #pragma unroll
@@ -163,14 +166,18 @@ __global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, Plane
       {
         const ModulusConsts mc = pc.mod[p0 + pl];
         const uint32_t off = Signed ? mc.off_i64 : mc.off_u64;
-        const v4i wa = {static_cast<int>(residues4(raw.alo, raw.ahi, 0, mc, off)), static_cast<int>(residues4(raw.alo, raw.ahi, 1, mc, off)),
-                        static_cast<int>(residues4(raw.alo, raw.ahi, 2, mc, off)),
-                        static_cast<int>(residues4(raw.alo, raw.ahi, 3, mc, off))};
-        const v4i wb = {static_cast<int>(residues4(raw.blo, raw.bhi, 0, mc, off)), static_cast<int>(residues4(raw.blo, raw.bhi, 1, mc, off)),
-                        static_cast<int>(residues4(raw.blo, raw.bhi, 2, mc, off)),
-                        static_cast<int>(residues4(raw.blo, raw.bhi, 3, mc, off))};
-        *reinterpret_cast<v4i*>(st + pl * kPlaneLds + a_row * kStepK + 16 * a_half) = wa;
-        *reinterpret_cast<v4i*>(st + pl * kPlaneLds + kOperandLds + b_col * kStepK + 16 * b_half) = wb;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          // residues of rows a_r0 + 16*(2q) and + 16*(2q + 1): bytes 0-1 and 2-3
+          const uint32_t w = residues4(raw.alo, raw.ahi, q, mc, off);
+          *reinterpret_cast<uint16_t*>(st + pl * kPlaneLds + (a_r0 + 32 * q) * kStepK + a_k2) =
+              static_cast<uint16_t>(w);
+          *reinterpret_cast<uint16_t*>(st + pl * kPlaneLds + (a_r0 + 32 * q + 16) * kStepK + a_k2) =
+              static_cast<uint16_t>(w >> 16);
+        }
+        const v2i wb = {static_cast<int>(residues4(raw.blo, raw.bhi, 0, mc, off)),
+                        static_cast<int>(residues4(raw.blo, raw.bhi, 1, mc, off))};
+        *reinterpret_cast<v2i*>(st + pl * kPlaneLds + kALds + b_col * kStepK + 8 * b_q) = wb;
       }
     }
   };
@@ -180,30 +187,30 @@ __global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, Plane
   // A as src1, register 4g+e of acc[pl][i][j] holds C[row][col] of plane
   // p0 + pl with row = m0 + 64*wm + 32*i + (l & 31) and col = n0 + 64*wn +
   // 32*j + 8*g + 4*(l >> 5) + e.
-  v16i acc[NP][2][2];
+  v16i acc[NP][2][1];
 #pragma unroll
   for (int pl = 0; pl < NP; ++pl)
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[pl][i][j] = v16i{};
+      for (int j = 0; j < 1; ++j) acc[pl][i][j] = v16i{};
   const int frag = (lane & 31) * kStepK + 16 * (lane >> 5);
   auto mma = [&](int stage) {
     const int8_t* const st = lds + stage * kStageLds;
 #pragma unroll
     for (int pl = 0; pl < NP; ++pl) {
       {
-        v4i af[2], bf[2];
+        v4i af[2], bf[1];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
           af[i] = *reinterpret_cast<const v4i*>(st + pl * kPlaneLds + (64 * wm + 32 * i) * kStepK + frag);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          bf[j] = *reinterpret_cast<const v4i*>(st + pl * kPlaneLds + kOperandLds + (64 * wn + 32 * j) * kStepK + frag);
+        for (int j = 0; j < 1; ++j)
+          bf[j] = *reinterpret_cast<const v4i*>(st + pl * kPlaneLds + kALds + (32 * wn + 32 * j) * kStepK + frag);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
+          for (int j = 0; j < 1; ++j)
             acc[pl][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[pl][i][j], 0, 0, 0);
       }
     }
@@ -240,10 +247,10 @@ __global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, Plane
       for (int i = 0; i < 2; ++i) {
         const int64_t row = m0 + 64 * wm + 32 * i + (lane & 31);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < 1; ++j) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const int64_t col = n0 + 64 * wn + 32 * j + 8 * g + 4 * (lane >> 5);
+            const int64_t col = n0 + 32 * wn + 32 * j + 8 * g + 4 * (lane >> 5);
             const Acc4 a4 = acc_read4(acc[pl][i][j], g);
             uint32_t r[4];
 #pragma unroll
@@ -317,12 +324,12 @@ bool choose_fused_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, int64
   out = FusedShape{};
   if (m <= 0 || n <= 0 || k <= 0 || nplanes == 0 || nplanes > kMaxPrefix || ldc < n || ldc % 16 != 0) return false;
   if (m >= (int64_t{1} << 31) || n >= (int64_t{1} << 31)) return false;
-  const int64_t tiles = ((m + kTile - 1) / kTile) * ((n + kTile - 1) / kTile);
+  const int64_t tiles = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN);
   const int64_t groups = (nplanes + kGroupPlanes - 1) / kGroupPlanes;
   if (tiles >= (int64_t{1} << 31)) return false;
   // about one workgroup per CU, slices of at least kMinSliceK and at most
   // kMaxSliceK, every slice non-empty
-  const int64_t target = (256 + tiles * groups - 1) / (tiles * groups);
+  const int64_t target = (512 + tiles * groups - 1) / (tiles * groups);
   int64_t slices = std::max((k + kMaxSliceK - 1) / kMaxSliceK, std::min(target, (k + kMinSliceK - 1) / kMinSliceK));
   slices = std::max<int64_t>(slices, 1);
   int64_t k_slice = (k + slices - 1) / slices;
@@ -346,8 +353,8 @@ hipError_t launch_fused_native(const FusedArgs& a, const PlaneConsts& consts, hi
   if (a.pitch_c < a.m * a.ldc || (reinterpret_cast<uintptr_t>(a.c) & 3u) != 0 ||
       (reinterpret_cast<uintptr_t>(a.ws) & 3u) != 0)
     return hipErrorInvalidValue;
-  const uint32_t tiles_n = static_cast<uint32_t>((a.n + kTile - 1) / kTile);
-  const uint32_t tiles = static_cast<uint32_t>((a.m + kTile - 1) / kTile) * tiles_n;
+  const uint32_t tiles_n = static_cast<uint32_t>((a.n + kTileN - 1) / kTileN);
+  const uint32_t tiles = static_cast<uint32_t>((a.m + kTileM - 1) / kTileM) * tiles_n;
   const bool vec = (reinterpret_cast<uintptr_t>(a.a) & 15u) == 0 && (a.lda % 2) == 0;
   const bool sgn = a.kind == NativeKind::I64;
   // full groups of four planes in one grid, the remaining 1-3 planes in another
