@@ -10,8 +10,9 @@
 // output tiles and packing once is cheaper, so the host offers the fused path
 // only below a workspace limit. Measured at 128 x 128 x 65536 it is still
 // slower than two packs and the split-K GEMM (96 against 83 us of kernels):
-// the residue arithmetic is VALU-bound, and here A's elements are reduced
-// once per 64-column tile and per plane group, 1.5 times the packs' work.
+// it does 1.5 times the packs' residue arithmetic (A's elements are reduced
+// once per 64-column tile and per plane group), which keeps its VALU about
+// half busy, and its waves wait on their loads for most of the rest.
 //
 // Work split: a workgroup owns a 128 x 64 output tile, a group of up to four
 // planes and one K slice; two workgroups run per CU. Its four waves each hold
