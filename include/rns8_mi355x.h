@@ -119,8 +119,9 @@ RNS8_API rns8_status rns8_mi355x_gemm_finite_u8_grouped_async(
  * loads, enqueued on `stream` (reference hip_direct_gemm_native_kernels.cuh:
  * 9-193, its native-operand GEMM behind the oneshot path,
  * hip_backend_gemm_native_prefix.inc). Offered for outputs small enough that
- * the product is split along K; returns RNS8_UNSUPPORTED_BACKEND for other
- * plans, whose operands are packed once and multiplied by rns8_gemm_rns. The
+ * the product is split along K, with 16-byte aligned operands and even row
+ * strides below 2^21 elements; returns RNS8_UNSUPPORTED_BACKEND otherwise
+ * (such plans pack their operands once and multiply with rns8_gemm_rns). The
  * plan's declared bound covers the result exactly as for rns8_gemm_rns. */
 RNS8_API rns8_status rns8_mi355x_gemm_native_i64_async(
     rns8_context* ctx,

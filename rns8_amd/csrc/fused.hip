@@ -9,22 +9,21 @@
 // residues to HBM. For large outputs every operand panel is read by many
 // output tiles and packing once is cheaper, so the host offers the fused path
 // only below a workspace limit. Measured at 128 x 128 x 65536 it is still
-// slower than two packs and the split-K GEMM (96 against 83 us of kernels):
-// it does 1.5 times the packs' residue arithmetic (A's elements are reduced
-// once per 64-column tile and per plane group), which keeps its VALU about
-// half busy, and its waves wait on their loads for most of the rest.
+// slower than two packs and the split-K GEMM (92 against 83 us of kernels).
 //
-// Work split: a workgroup owns a 128 x 64 output tile, a group of up to four
-// planes and one K slice; two workgroups run per CU. Its four waves each hold
-// a 64 x 32 part of all four planes (4 planes x 2 blocks of
-// v_mfma_i32_32x32x32_i8, 128 accumulator registers). Per 32-deep K step
-// every thread loads 16 native elements of A (two consecutive k of eight rows,
-// so a wave's load covers whole row segments) and 8 of B (one column, 8
-// consecutive k), reduces them to centered residues for each plane of the
-// group with the pack's arithmetic (two v_dot4_u32_u8 and a 24-bit quotient,
-// tables.hpp), and stores them into a k-contiguous LDS layout, so every MFMA
-// fragment is one ds_read_b128. LDS is double-buffered: the next step's loads
-// and residues overlap this step's MFMAs.
+// Work split: a workgroup owns a 128 x 128 output tile, a group of up to four
+// planes and one K slice; its four waves each hold a 64 x 64 quadrant of all
+// four planes (4 planes x 2 x 2 blocks of v_mfma_i32_32x32x32_i8, 256
+// accumulator registers), so one workgroup runs per CU. The raw int64 tiles
+// of each 32-deep K step (32 KB of A, 32 KB of B) are loaded straight into
+// LDS two steps ahead, holding no registers while in flight. Per step every
+// thread reads 16 native elements of A (one row, 16 consecutive k) and 16 of B
+// (one column, 16 consecutive k) from LDS, reduces them to centered residues
+// for each plane of the group with the pack's arithmetic (two v_dot4_u32_u8
+// and a 24-bit quotient, tables.hpp), and stores them into a k-contiguous
+// residue stage, so every MFMA fragment is one ds_read_b128. Each element is
+// reduced once per plane, as in the packs. LDS: a 32 KB residue stage and two
+// 64 KB raw stages, 160 KB.
 //
 // Each slice reduces its int32 sums to centered int8 residues in the
 // epilogue and stores them into its own slot of the workspace; a finalize
@@ -34,24 +33,29 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "dma.hpp"
 #include "int_ops.hpp"
 #include "kernels.hpp"
 
 namespace rns8x {
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
 
 constexpr int kTileM = 128;                           // output rows per workgroup
-constexpr int kTileN = 64;                            // output columns per workgroup
+constexpr int kTileN = 128;                           // output columns per workgroup
 constexpr int kStepK = 32;                            // K per step (one MFMA depth)
 constexpr int kGroupPlanes = 4;                       // planes per workgroup
-constexpr int kALds = kTileM * kStepK;                // 4 KB: 128 rows x 32 k
-constexpr int kBLds = kTileN * kStepK;                // 2 KB: 64 columns x 32 k
-constexpr int kPlaneLds = kALds + kBLds;              // A block, then B block
-constexpr int kStageLds = kGroupPlanes * kPlaneLds;   // 24 KB
+constexpr int kALds = kTileM * kStepK;                // 4 KB of residues: 128 rows x 32 k
+constexpr int kBLds = kTileN * kStepK;                // 4 KB of residues: 128 columns x 32 k
+constexpr int kPlaneLds = kALds + kBLds;
+constexpr int kResLds = kGroupPlanes * kPlaneLds;     // 32 KB: the residue stage
+constexpr int kRawA = kTileM * kStepK * 8;            // 32 KB: 128 rows x 256 bytes of native A
+constexpr int kRawB = kStepK * kTileN * 8;            // 32 KB: 32 k rows x 1 KB of native B
+constexpr int kRawLds = kRawA + kRawB;
+constexpr int kLdsBytes = kResLds + 2 * kRawLds;      // 160 KB: residues + two raw stages
+constexpr int kDmaPerWave = (kRawLds / 1024) / 4;     // 16 one-KB loads per wave per step
 constexpr int64_t kMaxSliceK = 65536;                 // |int32 sum| <= 65536 * 128 * 128 = 2^30
 constexpr int64_t kMinSliceK = 512;                   // 16 steps: amortizes the epilogue
 constexpr uint64_t kMaxWorkspace = uint64_t{64} << 20;
@@ -76,13 +80,16 @@ __device__ __forceinline__ uint32_t residues4(const uint32_t (&lo)[N], const uin
 
 // Grid: x = output tile (tiles_n per tile row), y = K slice, z = plane group
 // (planes p0 .. p0 + NP - 1, p0 = plane_base + 4 * z). The host guarantees
-// every slice holds at least one K element and (for Vec) 16-byte aligned A
-// rows. NP is a template parameter so that every accumulator is updated
-// unconditionally and stays in its AGPRs.
-template <bool Signed, bool Vec, int NP>
-__global__ __launch_bounds__(256, 2) void fused_native_kernel(FusedArgs a, PlaneConsts pc, uint32_t tiles_n,
+// every slice holds at least one K element, 16-byte aligned operands with
+// even row strides, and row strides below 2^21 elements. NP is a template
+// parameter so that every accumulator is updated unconditionally and stays
+// in its AGPRs.
+template <bool Signed, int NP>
+__global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, PlaneConsts pc, uint32_t tiles_n,
                                                               uint32_t plane_base) {
-  __shared__ __attribute__((aligned(16))) int8_t lds[2 * kStageLds];
+  __shared__ __attribute__((aligned(16))) int8_t lds[kLdsBytes];
+  int8_t* const res = lds;                 // residue stage
+  int8_t* const raw0 = lds + kResLds;      // raw stages: A rows then B k rows
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
@@ -96,90 +103,82 @@ __global__ __launch_bounds__(256, 2) void fused_native_kernel(FusedArgs a, Plane
   const int64_t kb = static_cast<int64_t>(slice) * a.shape.k_slice;
   const int64_t ke = min(kb + a.shape.k_slice, a.k);
   const int steps = static_cast<int>((ke - kb + kStepK - 1) / kStepK);
+  const int64_t rows_valid = min(static_cast<int64_t>(kTileM), a.m - m0);
 
-  // Loader roles. A: sixteen threads per row, two consecutive k each, so a
-  // wave's load covers four whole 256-byte row segments; thread t holds rows
-  // (t >> 4) + 16j, j = 0..7, at k = 2*(t & 15), +1 (element 2j, 2j+1 of its
-  // arrays). B: column b_col, k 8*b_q .. +7.
-  const int a_r0 = t >> 4, a_k2 = 2 * (t & 15);
-  const int b_col = t & 63, b_q = t >> 6;
-  const bool b_ok = n0 + b_col < a.n;
-  // Rows past m and columns past n read row / column 0, k past the slice
-  // reads its last element, and the values are replaced by 0 afterwards: every
-  // load is in bounds and unconditional, so a thread's loads are all in flight
-  // together (a load under a condition followed by a select waits for each
-  // one in turn).
-  const uint64_t* const a_base = static_cast<const uint64_t*>(a.a);
-  const uint64_t* const b_src = static_cast<const uint64_t*>(a.b) + (b_ok ? n0 + b_col : 0);
-
-  // raw operand words of one step
-  struct Raw {
-    uint32_t alo[16], ahi[16], blo[8], bhi[8];
+  // Raw loads, straight into LDS (16 bytes per lane, no registers held while
+  // in flight). Wave w loads A rows 32w .. 32w+31 as 8 blocks of 4 rows x 256
+  // bytes, and B k rows 8w .. 8w+7 as 8 blocks of 1 KB. In A, the 16-byte
+  // chunk c of row r is stored at chunk position c ^ (r & 7) of its LDS row,
+  // so the conversion's reads (two rows per 8-lane group, same chunk index)
+  // fall on distinct banks. Out-of-range rows read 0 through the buffer
+  // resources' ranges; k past the slice and columns past n are zeroed when
+  // converted.
+  const uint32_t lds_raw0 = lds_address(raw0);
+  uint32_t a_voff[8], b_voff[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = 32 * wave + 4 * j + (lane >> 4);
+    const int chunk = (lane & 15) ^ (row & 7);
+    a_voff[j] = static_cast<uint32_t>(row) * static_cast<uint32_t>(a.lda) * 8u + 16u * static_cast<uint32_t>(chunk);
+    const int kr = 8 * wave + j;
+    b_voff[j] = static_cast<uint32_t>(kr) * static_cast<uint32_t>(a.ldb) * 8u + 16u * static_cast<uint32_t>(lane);
+  }
+  const uint64_t* const abase = static_cast<const uint64_t*>(a.a) + m0 * a.lda;
+  const uint64_t* const bbase = static_cast<const uint64_t*>(a.b) + n0;
+  auto issue = [&](int s, int stage) {
+    const int64_t k0 = kb + static_cast<int64_t>(kStepK) * s;
+    const v4i ra = buffer_rsrc(abase + k0, (rows_valid * a.lda - k0) * 8);
+    const int64_t krows = min(static_cast<int64_t>(kStepK), a.k - k0);
+    const v4i rb = buffer_rsrc(bbase + k0 * a.ldb, (krows * a.ldb - n0) * 8);
+    const uint32_t dst = lds_raw0 + static_cast<uint32_t>(stage * kRawLds);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dma16(dst + static_cast<uint32_t>((8 * wave + j) * 1024), a_voff[j], ra);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dma16(dst + static_cast<uint32_t>(kRawA + (8 * wave + j) * 1024), b_voff[j], rb);
   };
-  auto load = [&](Raw& raw, int64_t k0) {
-    const int64_t ka = k0 + a_k2;
+
+  // Conversion roles: A row a_r, k 16*a_h .. +15; B column b_c, k 16*b_h .. +15.
+  const int a_r = t >> 1, a_h = t & 1;
+  const int b_c = t & 127, b_h = t >> 7;
+  const bool b_ok = n0 + b_c < a.n;
+  auto convert = [&](int s, int stage) {
+    const int64_t k0 = kb + static_cast<int64_t>(kStepK) * s;
+    const int8_t* const raw = raw0 + stage * kRawLds;
+    uint32_t alo[16], ahi[16], blo[16], bhi[16];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int64_t row = m0 + a_r0 + 16 * j;
-      const bool ok = row < a.m;
-      const uint64_t* const rp = a_base + (ok ? row * a.lda : 0);
-      uint64_t x0, x1;
-      if (Vec && ka + 2 <= ke) {
-        const v2u64 v = *reinterpret_cast<const v2u64*>(rp + ka);
-        x0 = v[0];
-        x1 = v[1];
-      } else {
-        const uint64_t y0 = rp[min(ka, ke - 1)];
-        const uint64_t y1 = rp[min(ka + 1, ke - 1)];
-        x0 = ka < ke ? y0 : 0ull;  // out of range packs as 0
-        x1 = ka + 1 < ke ? y1 : 0ull;
-      }
-      x0 = ok ? x0 : 0ull;
-      x1 = ok ? x1 : 0ull;
-      raw.alo[2 * j] = static_cast<uint32_t>(x0);
-      raw.ahi[2 * j] = static_cast<uint32_t>(x0 >> 32);
-      raw.alo[2 * j + 1] = static_cast<uint32_t>(x1);
-      raw.ahi[2 * j + 1] = static_cast<uint32_t>(x1 >> 32);
+      const int chunk = (8 * a_h + j) ^ (a_r & 7);
+      const v4i v = *reinterpret_cast<const v4i*>(raw + a_r * 256 + 16 * chunk);
+      const bool ok0 = k0 + 16 * a_h + 2 * j < ke, ok1 = k0 + 16 * a_h + 2 * j + 1 < ke;
+      alo[2 * j] = ok0 ? static_cast<uint32_t>(v[0]) : 0u;
+      ahi[2 * j] = ok0 ? static_cast<uint32_t>(v[1]) : 0u;
+      alo[2 * j + 1] = ok1 ? static_cast<uint32_t>(v[2]) : 0u;
+      ahi[2 * j + 1] = ok1 ? static_cast<uint32_t>(v[3]) : 0u;
     }
-    const int64_t kk = k0 + 8 * b_q;
-    uint64_t y[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = b_src[min(kk + e, ke - 1) * a.ldb];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint64_t v = b_ok && kk + e < ke ? y[e] : 0ull;
-      raw.blo[e] = static_cast<uint32_t>(v);
-      raw.bhi[e] = static_cast<uint32_t>(v >> 32);
+    for (int e = 0; e < 16; ++e) {
+      const v2i v = *reinterpret_cast<const v2i*>(raw + kRawA + (16 * b_h + e) * 1024 + 8 * b_c);
+      const bool ok = b_ok && k0 + 16 * b_h + e < ke;
+      blo[e] = ok ? static_cast<uint32_t>(v[0]) : 0u;
+      bhi[e] = ok ? static_cast<uint32_t>(v[1]) : 0u;
     }
     if (Signed) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) raw.ahi[e] ^= 0x80000000u;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) raw.bhi[e] ^= 0x80000000u;
+      for (int e = 0; e < 16; ++e) {
+        ahi[e] ^= 0x80000000u;
+        bhi[e] ^= 0x80000000u;
+      }
     }
-  };
-  // residues of the loaded elements for every plane of the group, into stage
-  // `stage`: A row r, k at r*32 + k; B column c, k at 4096 + c*32 + k
-  auto convert_store = [&](const Raw& raw, int stage) {
-    int8_t* const st = lds + stage * kStageLds;
 #pragma unroll
     for (int pl = 0; pl < NP; ++pl) {
-      {
-        const ModulusConsts mc = pc.mod[p0 + pl];
-        const uint32_t off = Signed ? mc.off_i64 : mc.off_u64;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          // residues of rows a_r0 + 16*(2q) and + 16*(2q + 1): bytes 0-1 and 2-3
-          const uint32_t w = residues4(raw.alo, raw.ahi, q, mc, off);
-          *reinterpret_cast<uint16_t*>(st + pl * kPlaneLds + (a_r0 + 32 * q) * kStepK + a_k2) =
-              static_cast<uint16_t>(w);
-          *reinterpret_cast<uint16_t*>(st + pl * kPlaneLds + (a_r0 + 32 * q + 16) * kStepK + a_k2) =
-              static_cast<uint16_t>(w >> 16);
-        }
-        const v2i wb = {static_cast<int>(residues4(raw.blo, raw.bhi, 0, mc, off)),
-                        static_cast<int>(residues4(raw.blo, raw.bhi, 1, mc, off))};
-        *reinterpret_cast<v2i*>(st + pl * kPlaneLds + kALds + b_col * kStepK + 8 * b_q) = wb;
-      }
+      const ModulusConsts mc = pc.mod[p0 + pl];
+      const uint32_t off = Signed ? mc.off_i64 : mc.off_u64;
+      const v4i wa = {static_cast<int>(residues4(alo, ahi, 0, mc, off)), static_cast<int>(residues4(alo, ahi, 1, mc, off)),
+                      static_cast<int>(residues4(alo, ahi, 2, mc, off)), static_cast<int>(residues4(alo, ahi, 3, mc, off))};
+      const v4i wb = {static_cast<int>(residues4(blo, bhi, 0, mc, off)), static_cast<int>(residues4(blo, bhi, 1, mc, off)),
+                      static_cast<int>(residues4(blo, bhi, 2, mc, off)), static_cast<int>(residues4(blo, bhi, 3, mc, off))};
+      *reinterpret_cast<v4i*>(res + pl * kPlaneLds + a_r * kStepK + 16 * a_h) = wa;
+      *reinterpret_cast<v4i*>(res + pl * kPlaneLds + kALds + b_c * kStepK + 16 * b_h) = wb;
     }
   };
 
@@ -188,49 +187,53 @@ __global__ __launch_bounds__(256, 2) void fused_native_kernel(FusedArgs a, Plane
   // A as src1, register 4g+e of acc[pl][i][j] holds C[row][col] of plane
   // p0 + pl with row = m0 + 64*wm + 32*i + (l & 31) and col = n0 + 64*wn +
   // 32*j + 8*g + 4*(l >> 5) + e.
-  v16i acc[NP][2][1];
+  v16i acc[NP][2][2];
 #pragma unroll
   for (int pl = 0; pl < NP; ++pl)
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 1; ++j) acc[pl][i][j] = v16i{};
+      for (int j = 0; j < 2; ++j) acc[pl][i][j] = v16i{};
   const int frag = (lane & 31) * kStepK + 16 * (lane >> 5);
-  auto mma = [&](int stage) {
-    const int8_t* const st = lds + stage * kStageLds;
+  auto mma = [&]() {
 #pragma unroll
     for (int pl = 0; pl < NP; ++pl) {
-      {
-        v4i af[2], bf[1];
+      v4i af[2], bf[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-          af[i] = *reinterpret_cast<const v4i*>(st + pl * kPlaneLds + (64 * wm + 32 * i) * kStepK + frag);
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const v4i*>(res + pl * kPlaneLds + (64 * wm + 32 * i) * kStepK + frag);
 #pragma unroll
-        for (int j = 0; j < 1; ++j)
-          bf[j] = *reinterpret_cast<const v4i*>(st + pl * kPlaneLds + kALds + (32 * wn + 32 * j) * kStepK + frag);
+      for (int j = 0; j < 2; ++j)
+        bf[j] = *reinterpret_cast<const v4i*>(res + pl * kPlaneLds + kALds + (64 * wn + 32 * j) * kStepK + frag);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 1; ++j)
-            acc[pl][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[pl][i][j], 0, 0, 0);
-      }
+        for (int j = 0; j < 2; ++j)
+          acc[pl][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[pl][i][j], 0, 0, 0);
     }
   };
 
-  // Step s computes from stage s & 1 while the next step's loads are in
-  // flight and its residues go into the other stage, which the barrier ending
-  // step s-1 retired.
-  Raw raw;
-  load(raw, kb);
-  convert_store(raw, 0);
-  __syncthreads();
+  // Pipeline: the raw data of steps s+1 and s+2 are in flight (or landed)
+  // while step s is converted and multiplied. Every step issues exactly
+  // kDmaPerWave loads per wave (past the last step the last step's data is
+  // loaded again into the free stage and never converted, so the vmcnt
+  // bookkeeping stays uniform); loads complete in order, so before
+  // converting step s each wave waits until only the newest step's loads are
+  // outstanding, and the barrier after that wait publishes every wave's loads
+  // of step s.
+  issue(0, 0);
+  issue(min(1, steps - 1), 1);
   for (int s = 0; s < steps; ++s) {
-    const bool more = s + 1 < steps;
-    if (more) load(raw, kb + static_cast<int64_t>(kStepK) * (s + 1));
-    mma(s & 1);
-    if (more) convert_store(raw, (s + 1) & 1);
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(wait_vm(kDmaPerWave));  // step s landed (this wave's part)
+    __syncthreads();                                  // every wave's part; step s-1's MFMAs retired
+    convert(s, s & 1);
+    __syncthreads();                                  // residues of step s stored; raw stage s&1 free
+    // the raw stage just converted takes step s+2 (a repeat of the last step
+    // past the end, never converted)
+    issue(min(s + 2, steps - 1), s & 1);
+    mma();
   }
+  __builtin_amdgcn_s_waitcnt(wait_vm(0));  // no load outlives the workgroup's LDS
 
   // Epilogue: each int32 sum x (|x| <= 2^30) reduced to its centered residue,
   // four columns per dword, into slot [slice][plane][row][col] of the
@@ -248,10 +251,10 @@ __global__ __launch_bounds__(256, 2) void fused_native_kernel(FusedArgs a, Plane
       for (int i = 0; i < 2; ++i) {
         const int64_t row = m0 + 64 * wm + 32 * i + (lane & 31);
 #pragma unroll
-        for (int j = 0; j < 1; ++j) {
+        for (int j = 0; j < 2; ++j) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const int64_t col = n0 + 32 * wn + 32 * j + 8 * g + 4 * (lane >> 5);
+            const int64_t col = n0 + 64 * wn + 32 * j + 8 * g + 4 * (lane >> 5);
             const Acc4 a4 = acc_read4(acc[pl][i][j], g);
             uint32_t r[4];
 #pragma unroll
@@ -321,6 +324,11 @@ __global__ __launch_bounds__(256) void residue_finalize_kernel(const int8_t* ws,
 
 }  // namespace
 
+bool fused_operands_ok(const void* a, int64_t lda, const void* b, int64_t ldb) {
+  return (reinterpret_cast<uintptr_t>(a) & 15u) == 0 && (reinterpret_cast<uintptr_t>(b) & 15u) == 0 && lda % 2 == 0 &&
+         ldb % 2 == 0 && lda < (int64_t{1} << 21) && ldb < (int64_t{1} << 21);
+}
+
 bool choose_fused_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, int64_t ldc, FusedShape& out) {
   out = FusedShape{};
   if (m <= 0 || n <= 0 || k <= 0 || nplanes == 0 || nplanes > kMaxPrefix || ldc < n || ldc % 16 != 0) return false;
@@ -330,7 +338,7 @@ bool choose_fused_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, int64
   if (tiles >= (int64_t{1} << 31)) return false;
   // about one workgroup per CU, slices of at least kMinSliceK and at most
   // kMaxSliceK, every slice non-empty
-  const int64_t target = (512 + tiles * groups - 1) / (tiles * groups);
+  const int64_t target = (256 + tiles * groups - 1) / (tiles * groups);
   int64_t slices = std::max((k + kMaxSliceK - 1) / kMaxSliceK, std::min(target, (k + kMinSliceK - 1) / kMinSliceK));
   slices = std::max<int64_t>(slices, 1);
   int64_t k_slice = (k + slices - 1) / slices;
@@ -354,9 +362,10 @@ hipError_t launch_fused_native(const FusedArgs& a, const PlaneConsts& consts, hi
   if (a.pitch_c < a.m * a.ldc || (reinterpret_cast<uintptr_t>(a.c) & 3u) != 0 ||
       (reinterpret_cast<uintptr_t>(a.ws) & 3u) != 0)
     return hipErrorInvalidValue;
+  // the direct-to-LDS loads read 16-byte chunks at 32-bit byte offsets
+  if (!fused_operands_ok(a.a, a.lda, a.b, a.ldb)) return hipErrorInvalidValue;
   const uint32_t tiles_n = static_cast<uint32_t>((a.n + kTileN - 1) / kTileN);
   const uint32_t tiles = static_cast<uint32_t>((a.m + kTileM - 1) / kTileM) * tiles_n;
-  const bool vec = (reinterpret_cast<uintptr_t>(a.a) & 15u) == 0 && (a.lda % 2) == 0;
   const bool sgn = a.kind == NativeKind::I64;
   // full groups of four planes in one grid, the remaining 1-3 planes in another
   const uint32_t full = a.nplanes / kGroupPlanes;
@@ -364,14 +373,10 @@ hipError_t launch_fused_native(const FusedArgs& a, const PlaneConsts& consts, hi
   auto launch = [&](auto np, uint32_t groups, uint32_t base) {
     constexpr int NP = decltype(np)::value;
     const dim3 grid(tiles, a.shape.slices, groups);
-    if (sgn && vec)
-      hipLaunchKernelGGL((fused_native_kernel<true, true, NP>), grid, dim3(256), 0, stream, a, consts, tiles_n, base);
-    else if (sgn)
-      hipLaunchKernelGGL((fused_native_kernel<true, false, NP>), grid, dim3(256), 0, stream, a, consts, tiles_n, base);
-    else if (vec)
-      hipLaunchKernelGGL((fused_native_kernel<false, true, NP>), grid, dim3(256), 0, stream, a, consts, tiles_n, base);
+    if (sgn)
+      hipLaunchKernelGGL((fused_native_kernel<true, NP>), grid, dim3(256), 0, stream, a, consts, tiles_n, base);
     else
-      hipLaunchKernelGGL((fused_native_kernel<false, false, NP>), grid, dim3(256), 0, stream, a, consts, tiles_n, base);
+      hipLaunchKernelGGL((fused_native_kernel<false, NP>), grid, dim3(256), 0, stream, a, consts, tiles_n, base);
   };
   if (full) launch(std::integral_constant<int, kGroupPlanes>{}, full, 0);
   const uint32_t base = full * kGroupPlanes;

@@ -43,6 +43,7 @@
 #include <atomic>
 #include <type_traits>
 
+#include "dma.hpp"
 #include "int_ops.hpp"
 #include "kernels.hpp"
 
@@ -57,21 +58,11 @@ typedef __attribute__((address_space(3))) v2i lds_v2i;
 __device__ __forceinline__ lds_v2i* as_lds_v2i(const int8_t* p) {
   return (lds_v2i*)(const_cast<int8_t*>(p));  // generic -> LDS address space
 }
-__device__ __forceinline__ uint32_t lds_address(const int8_t* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t*)(const_cast<int8_t*>(p))));
-}
-
-// s_waitcnt immediates "vmcnt <= n" leaving expcnt and lgkmcnt unconstrained
-// (gfx9 encoding: vmcnt[3:0] bits 3:0, expcnt bits 6:4, lgkmcnt bits 11:8,
-// vmcnt[5:4] bits 15:14).
-constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int kWaitVm[9] = {wait_vm(0), wait_vm(1), wait_vm(2), wait_vm(3), wait_vm(4),
                             wait_vm(5), wait_vm(6), wait_vm(7), wait_vm(8)};
 
 constexpr int kThreads = 256;
 constexpr int kGroupM = 4;  // tile rows per L2 reuse group
-// Buffer resource word 3 for gfx9-family raw buffers (32-bit data format).
-constexpr int kBufferFlags = 0x00020000;
 // Accumulator start value: the MFMAs then produce u = 2^31 + sum (mod 2^32),
 // the biased form the reduction reads (|sum| < 2^31).
 constexpr int kAccBias = static_cast<int>(0x80000000u);
@@ -137,29 +128,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64
   return __builtin_amdgcn_make_buffer_rsrc(base, static_cast<short>(0), n, kBufferFlags);
 }
 
-// The same resource as four wave-uniform dwords, for the DMA asm below.
-__device__ __forceinline__ v4i buffer_rsrc(const void* p, int64_t bytes) {
-  const uint64_t addr = reinterpret_cast<uint64_t>(p);
-  return v4i{__builtin_amdgcn_readfirstlane(static_cast<int>(addr)),
-             __builtin_amdgcn_readfirstlane(static_cast<int>(addr >> 32)),
-             __builtin_amdgcn_readfirstlane(static_cast<int>(bytes)), kBufferFlags};
-}
-
-// 16 bytes per lane from a raw buffer straight into LDS: lane l's bytes land
-// at lds_addr + 16*l (M0 = lds_addr, wave-uniform). Written as asm so the
-// compiler does not track the LDS write (it would otherwise wait for every
-// outstanding DMA before each LDS read); callers order the DMA against LDS
-// reads with explicit vmcnt waits and barriers. M0 is a reserved register the
-// compiler re-initialises before any use of its own.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(uint32_t lds_addr, uint32_t voffset, v4i rsrc) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc)
-               : "m0");
-}
-#pragma clang diagnostic pop
 
 // Scheduling slots of a K sub-step region: slot Q is one MFMA followed by up
 // to kPerSlot of the region's kReads LDS fragment reads.

@@ -74,6 +74,9 @@ struct FusedShape {
   uint64_t ws_bytes;
 };
 bool choose_fused_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, int64_t ldc, FusedShape& out);
+// The fused path's operand requirements: 16-byte aligned operands, even row
+// strides below 2^21 elements.
+bool fused_operands_ok(const void* a, int64_t lda, const void* b, int64_t ldb);
 struct FusedArgs {
   const void* a;  // device, m x k native elements at row stride lda
   const void* b;  // device, k x n native elements at row stride ldb

@@ -6,9 +6,10 @@ for small cases), and export to the exact product.
 Cases cover: one and several 128 x 128 output tiles with ragged edges; plane
 counts 1, 3, 4, 5, 8, 9 and 20 (full groups of four planes and tails of one to
 three); K below one step, K not a multiple of 32, K above 65536 (several
-slices); row strides above the width, and odd strides (the element-wise load
-path); full-range int64/uint64 operands (every byte of the inputs matters for
-the residues) and the 4096 x 4096 plan the fused path is not offered for.
+slices); row strides above the width; full-range int64/uint64 operands (every
+byte of the inputs matters for the residues); and the refusals: the 4096 x
+4096 plan the fused path is not offered for, odd row strides and operands not
+16-byte aligned (its loads move 16-byte chunks straight into LDS).
 """
 import ctypes
 
@@ -79,13 +80,13 @@ def _operands(seed, m, n, k, lda, ldb, signed):
 PLANE_CASES = [
     (128, 128, 65536, 8, 0, 0, False),   # the C5 shape
     (100, 70, 3000, 9, 0, 0, True),      # ragged single tile, 4 + 4 + 1 planes
-    (1, 1, 1, 1, 0, 0, True),            # one element, one plane
-    (1, 1, 31, 3, 0, 0, False),          # K below one step
-    (130, 257, 5000, 5, 6, 2, True),     # 2 x 3 tiles, 4 + 1 planes, strided
+    (1, 1, 1, 1, 1, 1, True),            # one element, one plane (strides padded to even)
+    (1, 1, 31, 3, 1, 1, False),          # K below one step
+    (130, 257, 5000, 5, 6, 3, True),     # 2 x 3 tiles, 4 + 1 planes, strided
     (64, 64, 70000, 7, 0, 0, False),     # K above 65536: several slices, 4 + 3 planes
     (256, 128, 1000, 20, 0, 0, True),    # five full plane groups
-    (77, 45, 999, 4, 1, 3, True),        # odd strides: element-wise A loads
-    (33, 129, 4097, 2, 0, 0, False),     # two planes, a second tile column of one
+    (77, 45, 999, 4, 1, 3, True),        # ragged everything, strides above the width
+    (33, 129, 4097, 2, 1, 1, False),     # two planes, a second tile column of one
 ]
 
 
@@ -155,3 +156,22 @@ def test_fused_rejects_mismatched_arguments(gpu_ctx):
     # the unsigned entry on a signed plan
     assert L.rns8_mi355x_gemm_native_u64_async(gpu_ctx.ptr, plan.ptr, _vp(16), k, _vp(16), n, C.ptr, ws.ptr,
                                                None) == r.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("lda_extra,ldb_extra,offset", [(1, 0, 0), (0, 1, 0), (0, 0, 8)])
+def test_fused_refuses_unaligned_operands(gpu_ctx, lda_extra, ldb_extra, offset):
+    m, n, k = 64, 64, 1024  # even widths: each extra element makes a stride odd
+    lda, ldb = k + lda_extra, n + ldb_extra
+    plan, sem, bk = _plans(gpu_ctx, True, m, n, k, 9, 1 << 62)
+    C = r.Matrix(gpu_ctx, r.matrix_desc(m, n, sem, bk, 9))
+    ws = r.Workspace(gpu_ctx, plan)
+    dA, dB = hip.malloc(m * lda * 8 + 64), hip.malloc(k * ldb * 8 + 64)
+    try:
+        # refused before any kernel runs
+        st = r.lib().rns8_mi355x_gemm_native_i64_async(gpu_ctx.ptr, plan.ptr, _vp(dA + offset), lda, _vp(dB), ldb,
+                                                       C.ptr, ws.ptr, None)
+        hip.synchronize()
+    finally:
+        hip.free(dA)
+        hip.free(dB)
+    assert st == r.UNSUPPORTED_BACKEND
