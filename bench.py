@@ -260,6 +260,9 @@ def main() -> int:
         "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles("plane_gemm_kernel", args.config),
         "per_launch_ops": gemm_ops,
     }
+    if roofline["traffic"] is not None:
+        roofline["traffic_source"] = ("profiles/traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE per dispatch of "
+                                      "this kernel at this workload, copy-calibrated; not measured in this run")
     if args.fused:
         # pack and GEMM in one pass: the native operands are read (8 bytes per
         # element) and the C planes written; HBM bounds it for tall-skinny shapes
@@ -351,7 +354,7 @@ def cpu_baseline(args, A, B, Cout, P, bound, signed) -> dict:
     the GPU result."""
     import oracle
 
-    threads = min(16, os.cpu_count() or 1)
+    threads, share = cpu_share()
     oracle.set_threads(threads)
     run = oracle.gemm_i64 if signed else oracle.gemm_u64
     M, K = A.shape
@@ -384,11 +387,29 @@ def cpu_baseline(args, A, B, Cout, P, bound, signed) -> dict:
         "value": round(cpu_tops, 6),
         "unit": "TOPS",
         "cores": threads,
+        "cpu_share": share,
         "kind": "port",
         "sample": f"rows 0..{rows - 1} of C ({rows}x{N}x{K}, prefix {P}; pack of all of B included), "
                   f"{t_cpu:.2f} s per run, {reps} run(s), on {threads} threads of {_cpu_model()}",
         "rows_bit_exact_vs_gpu": match,
     }
+
+
+def cpu_share() -> tuple[int, dict]:
+    """Threads for the CPU baseline: the CPUs this process may run on
+    (sched_getaffinity), capped by the cgroup CPU quota where one is set (a
+    quota of Q CPUs gives at most Q threads' worth of time). Returns the
+    thread count and what it was derived from."""
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    quota = None
+    try:
+        q, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = int(q) / int(period)
+    except (OSError, ValueError):
+        pass
+    threads = affinity if quota is None else max(1, min(affinity, int(quota)))
+    return threads, {"nproc": os.cpu_count(), "affinity": affinity, "cgroup_quota_cpus": quota}
 
 
 def grouped_bench(args) -> int:

@@ -44,141 +44,15 @@ uint64_t output_source_version(uint64_t a, uint64_t b) {
   return h == 0 ? 1 : h;
 }
 
-// ---- exact-wide magnitude proofs (reference exact_range.hpp) ----------------
-
-bool exact_range_fits(rns8_semantics s, const I256& bound, const I256& product) {
-  if (bound.negative()) return false;
-  return s == RNS8_EXACT_WIDE_SIGNED ? (bound + bound) < product : bound < product;
-}
-
-void add_exact_value(ExactAxis& a, const I256& v, bool first) {
-  const I256 mag = v.abs();
-  a.max_magnitude = imax(a.max_magnitude, mag);
-  a.absolute_sum = a.absolute_sum + mag;
-  a.sum = a.sum + v;
-  if (first) {
-    a.minimum = v;
-    a.maximum = v;
-  } else {
-    a.minimum = imin(a.minimum, v);
-    a.maximum = imax(a.maximum, v);
-  }
-  a.sum_known = true;
-}
-
-I256 axis_center(const ExactAxis& a) { return (a.minimum + a.maximum).half_trunc(); }
-
-I256 axis_deviation_max(const ExactAxis& a, const I256& c) { return imax((a.minimum - c).abs(), (a.maximum - c).abs()); }
-
-// exact_range.hpp:52-78 (two linear scans of the host input)
-template <typename T>
-void native_exact_ranges(const T* src, int64_t rows, int64_t cols, int64_t ld, I256& maximum,
-                         std::vector<ExactAxis>& row_axes, std::vector<ExactAxis>& col_axes) {
-  row_axes.assign(static_cast<std::size_t>(rows), ExactAxis{});
-  col_axes.assign(static_cast<std::size_t>(cols), ExactAxis{});
-  auto value = [](T x) { return std::is_signed<T>::value ? I256::from_i64(static_cast<int64_t>(x))
-                                                         : I256::from_u64(static_cast<uint64_t>(x)); };
-  maximum = I256();
-  for (int64_t r = 0; r < rows; ++r) {
-    for (int64_t c = 0; c < cols; ++c) {
-      const I256 v = value(src[r * ld + c]);
-      add_exact_value(row_axes[r], v, c == 0);
-      add_exact_value(col_axes[c], v, r == 0);
-    }
-    maximum = imax(maximum, row_axes[r].max_magnitude);
-  }
-  std::vector<I256> col_center(static_cast<std::size_t>(cols));
-  for (int64_t c = 0; c < cols; ++c) col_center[c] = axis_center(col_axes[c]);
-  for (int64_t r = 0; r < rows; ++r) {
-    const I256 rc = axis_center(row_axes[r]);
-    for (int64_t c = 0; c < cols; ++c) {
-      const I256 v = value(src[r * ld + c]);
-      row_axes[r].deviation_sum = row_axes[r].deviation_sum + (v - rc).abs();
-      col_axes[c].deviation_sum = col_axes[c].deviation_sum + (v - col_center[c]).abs();
-    }
-  }
-}
-
-// exact_range.hpp:80-99
-I256 axis_product_bound(const ExactAxis& a, const ExactAxis& b, int64_t k) {
-  const I256 kk = I256::from_u64(static_cast<uint64_t>(k));
-  I256 bound = kk * a.max_magnitude * b.max_magnitude;
-  bound = imin(bound, a.absolute_sum * b.max_magnitude);
-  bound = imin(bound, a.max_magnitude * b.absolute_sum);
-  if (a.sum_known && b.sum_known) {
-    const I256 ca = axis_center(a), cb = axis_center(b);
-    const I256 da = axis_deviation_max(a, ca), db = axis_deviation_max(b, cb);
-    I256 rem = kk * da * db;
-    rem = imin(rem, a.deviation_sum * db);
-    rem = imin(rem, da * b.deviation_sum);
-    const I256 center_term = ca * b.sum + cb * a.sum - kk * ca * cb;
-    bound = imin(bound, center_term.abs() + rem);
-  }
-  return bound;
-}
-
-ExactAxis uniform_axis(const I256& maximum, int64_t length) {
-  ExactAxis a;
-  a.max_magnitude = maximum;
-  a.absolute_sum = I256::from_u64(static_cast<uint64_t>(length)) * maximum;
-  return a;
-}
-
-// exact_range.hpp:104-141 + 143-157: output bound of C = A x B and the
-// per-row / per-column summaries C carries into a later GEMM.
-rns8_status exact_gemm_range(const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B, I256& bound,
+// exact_range.hpp:104-157 on the operands' carried proofs.
+rns8_status exact_gemm_range(const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B, I512& bound,
                              std::vector<ExactAxis>* out_rows, std::vector<ExactAxis>* out_cols) {
   if (!exact_wide(plan.desc.semantics)) return RNS8_SUCCESS;
   if (A.exact_prefix < plan.prefix || B.exact_prefix < plan.prefix) return RNS8_RANGE_ERROR;
-  const int64_t m = plan.desc.m, n = plan.desc.n, k = plan.desc.k;
-  const bool a_rows = A.exact_rows.size() == static_cast<std::size_t>(m);
-  const bool b_cols = B.exact_cols.size() == static_cast<std::size_t>(n);
-  bound = I256::from_u64(static_cast<uint64_t>(k)) * A.exact_max * B.exact_max;
-  if (out_rows) out_rows->clear();
-  if (out_cols) out_cols->clear();
-  if (a_rows || b_cols) {
-    const ExactAxis fa = uniform_axis(A.exact_max, k);
-    const ExactAxis fb = uniform_axis(B.exact_max, k);
-    std::vector<ExactAxis> rows(static_cast<std::size_t>(m)), cols(static_cast<std::size_t>(n));
-    // rows are independent: split them over host threads; column summaries
-    // are merged per thread then reduced
-    unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
-    if (static_cast<int64_t>(nt) > m) nt = static_cast<unsigned>(m);
-    std::vector<std::vector<ExactAxis>> col_parts(nt, std::vector<ExactAxis>(static_cast<std::size_t>(n)));
-    std::vector<I256> maxima(nt);
-    std::vector<std::thread> pool;
-    for (unsigned t = 0; t < nt; ++t) {
-      pool.emplace_back([&, t]() {
-        const int64_t r0 = m * t / nt, r1 = m * (t + 1) / nt;
-        for (int64_t r = r0; r < r1; ++r) {
-          const ExactAxis& a = a_rows ? A.exact_rows[r] : fa;
-          for (int64_t c = 0; c < n; ++c) {
-            const ExactAxis& b = b_cols ? B.exact_cols[c] : fb;
-            const I256 cell = axis_product_bound(a, b, k);
-            maxima[t] = imax(maxima[t], cell);
-            rows[r].max_magnitude = imax(rows[r].max_magnitude, cell);
-            rows[r].absolute_sum = rows[r].absolute_sum + cell;
-            ExactAxis& cc = col_parts[t][c];
-            cc.max_magnitude = imax(cc.max_magnitude, cell);
-            cc.absolute_sum = cc.absolute_sum + cell;
-          }
-        }
-      });
-    }
-    for (auto& th : pool) th.join();
-    I256 maximum;
-    for (unsigned t = 0; t < nt; ++t) {
-      maximum = imax(maximum, maxima[t]);
-      for (int64_t c = 0; c < n; ++c) {
-        cols[c].max_magnitude = imax(cols[c].max_magnitude, col_parts[t][c].max_magnitude);
-        cols[c].absolute_sum = cols[c].absolute_sum + col_parts[t][c].absolute_sum;
-      }
-    }
-    bound = imin(bound, maximum);
-    if (out_rows) out_rows->swap(rows);
-    if (out_cols) out_cols->swap(cols);
-  }
-  return exact_range_fits(plan.desc.semantics, bound, plan.product) ? RNS8_SUCCESS : RNS8_RANGE_ERROR;
+  const ExactOperand a{&A.exact_max, &A.exact_rows, &A.exact_cols};
+  const ExactOperand b{&B.exact_max, &B.exact_rows, &B.exact_cols};
+  return exact_product_range(plan.desc.semantics, plan.desc.m, plan.desc.n, plan.desc.k, a, b, plan.product, bound,
+                             out_rows, out_cols);
 }
 
 // ---- shared validation --------------------------------------------------------
@@ -285,7 +159,7 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
   if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
 
   // exact-wide proof (api_pack.cpp:47-65); kept when the source is unchanged
-  I256 proof_max;
+  I512 proof_max;
   std::vector<ExactAxis> proof_rows, proof_cols;
   const bool is_wide = matrix->desc.semantics == wide;
   if (is_wide) {
@@ -304,7 +178,7 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
               hipSuccess ||
           hipStreamSynchronize(stream) != hipSuccess)
         return RNS8_BACKEND_FAILURE;
-      proof_max = I256::from_u64(host_max);
+      proof_max = I512::from_u64(host_max);
     }
     if (!exact_range_fits(matrix->desc.semantics, proof_max, modulus_product(matrix->prefix))) return RNS8_RANGE_ERROR;
   }
@@ -443,7 +317,7 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
   if (st != RNS8_SUCCESS) return st;
   st = check_rns_operands(*ctx, *plan, *A, *B, *C);
   if (st != RNS8_SUCCESS) return st;
-  I256 bound;
+  I512 bound;
   std::vector<ExactAxis> out_rows, out_cols;
   st = exact_gemm_range(*plan, *A, *B, bound, &out_rows, &out_cols);
   if (st != RNS8_SUCCESS) return st;
@@ -490,8 +364,6 @@ rns8_status gemm_native(rns8_context* ctx, const rns8_plan* plan, const T* A, in
     return RNS8_INVALID_ARGUMENT;
   if (!plan->fused_ok || plan->fused.ws_bytes > ws->splitk_bytes) return RNS8_UNSUPPORTED_BACKEND;
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
-  if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
-  C->device_current = false;
   FusedArgs f{};
   f.a = A;
   f.b = B;
@@ -507,6 +379,10 @@ rns8_status gemm_native(rns8_context* ctx, const rns8_plan* plan, const T* A, in
   f.kind = is_signed ? NativeKind::I64 : NativeKind::U64;
   f.ws = reinterpret_cast<int8_t*>(ws->splitk);
   f.shape = plan->fused;
+  // a refused call leaves C as it was
+  if (!fused_args_ok(f)) return RNS8_UNSUPPORTED_BACKEND;
+  if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  C->device_current = false;
   const hipError_t e = launch_fused_native(f, make_ladder_plane_consts(plan->prefix), stream);
   if (e == hipErrorInvalidValue) return RNS8_UNSUPPORTED_BACKEND;
   if (e != hipSuccess) return RNS8_BACKEND_FAILURE;
@@ -572,7 +448,7 @@ rns8_status gemm_grouped(rns8_context* ctx, const rns8_plan* plan, const rns8_gr
                                   : check_rns_operands(*ctx, *plan, *t.a, *t.b, *t.c);
     if (st != RNS8_SUCCESS) return st;
   }
-  std::vector<I256> bounds(task_count);
+  std::vector<I512> bounds(task_count);
   std::vector<std::vector<ExactAxis>> rows(task_count), cols(task_count);
   if (!finite && exact_wide(plan->desc.semantics))
     for (uint32_t i = 0; i < task_count; ++i) {

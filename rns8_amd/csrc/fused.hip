@@ -110,9 +110,10 @@ __global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, Plane
   // bytes, and B k rows 8w .. 8w+7 as 8 blocks of 1 KB. In A, the 16-byte
   // chunk c of row r is stored at chunk position c ^ (r & 7) of its LDS row,
   // so the conversion's reads (two rows per 8-lane group, same chunk index)
-  // fall on distinct banks. Out-of-range rows read 0 through the buffer
+  // fall on distinct banks. Rows past the operand read 0 through the buffer
   // resources' ranges; k past the slice and columns past n are zeroed when
-  // converted.
+  // converted (within a row they may hold the row padding of a strided
+  // operand).
   const uint32_t lds_raw0 = lds_address(raw0);
   uint32_t a_voff[8], b_voff[8];
 #pragma unroll
@@ -127,9 +128,13 @@ __global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, Plane
   const uint64_t* const bbase = static_cast<const uint64_t*>(a.b) + n0;
   auto issue = [&](int s, int stage) {
     const int64_t k0 = kb + static_cast<int64_t>(kStepK) * s;
-    const v4i ra = buffer_rsrc(abase + k0, (rows_valid * a.lda - k0) * 8);
+    // The ranges end at the operands' last logical elements (row rows_valid - 1,
+    // column k - 1 of A; k row k0 + krows - 1, column n - 1 of B), so no lane
+    // reads past an allocation of exactly (m - 1) * lda + k resp.
+    // (k - 1) * ldb + n elements; lanes past them read 0.
+    const v4i ra = buffer_rsrc(abase + k0, ((rows_valid - 1) * a.lda + a.k - k0) * 8);
     const int64_t krows = min(static_cast<int64_t>(kStepK), a.k - k0);
-    const v4i rb = buffer_rsrc(bbase + k0 * a.ldb, (krows * a.ldb - n0) * 8);
+    const v4i rb = buffer_rsrc(bbase + k0 * a.ldb, ((krows - 1) * a.ldb + a.n - n0) * 8);
     const uint32_t dst = lds_raw0 + static_cast<uint32_t>(stage * kRawLds);
 #pragma unroll
     for (int j = 0; j < 8; ++j) dma16(dst + static_cast<uint32_t>((8 * wave + j) * 1024), a_voff[j], ra);
@@ -353,17 +358,21 @@ bool choose_fused_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, int64
   return true;
 }
 
-hipError_t launch_fused_native(const FusedArgs& a, const PlaneConsts& consts, hipStream_t stream) {
+bool fused_args_ok(const FusedArgs& a) {
   FusedShape expect;
-  if (!a.a || !a.b || !a.c || !a.ws || a.lda < a.k || a.ldb < a.n) return hipErrorInvalidValue;
+  if (!a.a || !a.b || !a.c || !a.ws || a.lda < a.k || a.ldb < a.n) return false;
   if (!choose_fused_shape(a.m, a.n, a.k, a.nplanes, a.ldc, expect) || expect.slices != a.shape.slices ||
       expect.k_slice != a.shape.k_slice)
-    return hipErrorInvalidValue;
+    return false;
   if (a.pitch_c < a.m * a.ldc || (reinterpret_cast<uintptr_t>(a.c) & 3u) != 0 ||
       (reinterpret_cast<uintptr_t>(a.ws) & 3u) != 0)
-    return hipErrorInvalidValue;
+    return false;
   // the direct-to-LDS loads read 16-byte chunks at 32-bit byte offsets
-  if (!fused_operands_ok(a.a, a.lda, a.b, a.ldb)) return hipErrorInvalidValue;
+  return fused_operands_ok(a.a, a.lda, a.b, a.ldb);
+}
+
+hipError_t launch_fused_native(const FusedArgs& a, const PlaneConsts& consts, hipStream_t stream) {
+  if (!fused_args_ok(a)) return hipErrorInvalidValue;
   const uint32_t tiles_n = static_cast<uint32_t>((a.n + kTileN - 1) / kTileN);
   const uint32_t tiles = static_cast<uint32_t>((a.m + kTileM - 1) / kTileM) * tiles_n;
   const bool sgn = a.kind == NativeKind::I64;

@@ -13,19 +13,9 @@
 #include "host_copy.hpp"
 #include "kernels.hpp"
 #include "tables.hpp"
+#include "exact_range.hpp"
 #include "wide_int.hpp"
 
-// Exact-wide per-axis magnitude summary (reference src/core/internal.hpp:72-86
-// rns8_exact_axis_range): used to tighten the output bound of a GEMM.
-struct ExactAxis {
-  rns8x::I256 max_magnitude;
-  rns8x::I256 absolute_sum;
-  rns8x::I256 sum;
-  rns8x::I256 minimum;
-  rns8x::I256 maximum;
-  rns8x::I256 deviation_sum;
-  bool sum_known = false;
-};
 
 namespace rns8x {
 struct OneshotCache;
@@ -105,7 +95,7 @@ struct rns8_matrix {
   int64_t plane_pitch = 0;
   uint64_t plane_bytes = 0;
   // exact-wide proofs: exact_prefix == 0 means no proof
-  rns8x::I256 exact_max;
+  rns8x::I512 exact_max;
   uint32_t exact_prefix = 0;
   std::vector<ExactAxis> exact_rows;
   std::vector<ExactAxis> exact_cols;

@@ -89,6 +89,9 @@ struct FusedArgs {
   int8_t* ws;  // shape.ws_bytes of workspace
   FusedShape shape;
 };
+// Whether launch_fused_native accepts `args` (it returns hipErrorInvalidValue
+// otherwise, before enqueuing anything).
+bool fused_args_ok(const FusedArgs& args);
 hipError_t launch_fused_native(const FusedArgs& args, const PlaneConsts& consts, hipStream_t stream);
 // Per-tile schedules: `units` edge x edge tile-planes (edge 256 or 128) from a
 // device list of two words each, (plane << 24 | tile row) and (quadrant mask

@@ -1,0 +1,173 @@
+"""The library's exact-wide admission math against unbounded integers (CPU).
+
+tests/exact_range_check.cpp is built from rns8_amd/csrc/exact_range.hpp, the
+header librns8.so's rns8_gemm_rns uses to admit exact-wide products (reference
+src/core/exact_range.hpp:80-157). Each case here goes through it and through
+oracle/exact_range.py (Python integers, as unbounded as the reference's
+cpp_int); the bound, the status and every carried row/column summary must be
+equal. The cases include carried summaries far above 2^128, where a 256-bit
+product would wrap: two results of bound 2^128 multiplied with k = 1 have a
+bound of 2^256, which must be refused at every prefix, never wrapped to 0 and
+admitted.
+"""
+from __future__ import annotations
+
+import random
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import oracle
+from oracle import exact_range as xr
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+@pytest.fixture(scope="module")
+def checker(tmp_path_factory) -> Path:
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    exe = tmp_path_factory.mktemp("exact") / "exact_range_check"
+    subprocess.run([gxx, "-O2", "-std=c++17", "-pthread", "-I", str(ROOT / "rns8_amd" / "csrc"), "-I",
+                    str(ROOT / "include"), str(ROOT / "tests" / "exact_range_check.cpp"), "-o", str(exe)],
+                   check=True)
+    return exe
+
+
+def _h(v: int) -> str:
+    return ("-" if v < 0 else "") + format(abs(v), "x")
+
+
+def _axis(a: xr.Axis) -> str:
+    return " ".join([_h(a.max_magnitude), _h(a.absolute_sum), _h(a.sum), _h(a.minimum), _h(a.maximum),
+                     _h(a.deviation_sum), "1" if a.sum_known else "0"])
+
+
+def _encode(signed, m, n, k, product, A: xr.Operand, B: xr.Operand) -> str:
+    lines = [f"case {'S' if signed else 'U'} {m} {n} {k} {_h(product)}",
+             f"{_h(A.max_magnitude)} {len(A.rows)}", *(_axis(a) for a in A.rows),
+             f"{_h(B.max_magnitude)} {len(B.cols)}", *(_axis(b) for b in B.cols)]
+    return "\n".join(lines) + "\n"
+
+
+def _run(exe, cases):
+    """cases: (signed, m, n, k, product, A, B); returns the checker's
+    (status, bound, rows, cols) per case."""
+    text = "".join(_encode(*c) for c in cases)
+    res = subprocess.run([str(exe)], input=text, capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    lines = res.stdout.split("\n")
+    out, i = [], 0
+    for signed, m, n, k, product, A, B in cases:
+        st, bound = lines[i].split()
+        i += 1
+        carried = len(A.rows) == m or len(B.cols) == n
+        rows, cols = [], []
+        if carried:
+            rows = [tuple(int(x, 16) for x in lines[i + j].split()) for j in range(m)]
+            i += m
+            cols = [tuple(int(x, 16) for x in lines[i + j].split()) for j in range(n)]
+            i += n
+        out.append((int(st), int(bound, 16), rows, cols))
+    return out
+
+
+def _expect(signed, m, n, k, product, A, B):
+    bound, C = xr.gemm_bound(A, B, m, n, k)
+    st = 0 if xr.fits(signed, bound, product) else 5  # RNS8_SUCCESS / RNS8_RANGE_ERROR
+    rows = [(a.max_magnitude, a.absolute_sum) for a in C.rows]
+    cols = [(b.max_magnitude, b.absolute_sum) for b in C.cols]
+    return st, bound, rows, cols
+
+
+def _check(exe, cases):
+    got = _run(exe, cases)
+    for case, g in zip(cases, got):
+        assert g == _expect(*case), case[:5]
+
+
+def _native(rng, rows, cols, lo, hi):
+    return [[rng.randint(lo, hi) for _ in range(cols)] for _ in range(rows)]
+
+
+def test_native_operands_match_unbounded(checker):
+    """Host operands over the whole int64 / uint64 ranges, both semantics,
+    every prefix from 17 to 20."""
+    rng = random.Random(11)
+    cases = []
+    for t in range(24):
+        signed = t % 2 == 0
+        m, k, n = rng.randint(1, 5), rng.randint(1, 6), rng.randint(1, 5)
+        lo, hi = (-(1 << 63), (1 << 63) - 1) if signed else (0, (1 << 64) - 1)
+        if t % 3 == 1:  # small magnitudes: the centre and remainder candidates decide
+            lo, hi = (-40, 40) if signed else (0, 80)
+        A = xr.native_operand(_native(rng, m, k, lo, hi))
+        B = xr.native_operand(_native(rng, k, n, lo, hi))
+        cases.append((signed, m, n, k, oracle.modulus_product(17 + t % 4), A, B))
+    _check(checker, cases)
+
+
+def test_chained_results_above_2_128(checker):
+    """C = A x B with bound 2^128 (attained: k = 4 products of 2^63 * 2^63 in
+    the signed case, 2^64 - 1 unsigned), then C x C' with k = 1: the bound is
+    2^256 (about 2^256 unsigned) and must be refused at prefix 20, as the
+    reference's unbounded arithmetic refuses it."""
+    P20 = oracle.modulus_product(20)
+    for signed in (True, False):
+        v = -(1 << 63) if signed else (1 << 64) - 1
+        A = xr.native_operand([[v] * 4])
+        B = xr.native_operand([[v]] * 4)
+        bound, C = xr.gemm_bound(A, B, 1, 1, 4)
+        assert xr.fits(signed, bound, P20)
+        st, b2, rows, cols = _expect(signed, 1, 1, 1, P20, C, C)
+        assert st == 5 and b2 >= 1 << 254
+        _check(checker, [(signed, 1, 1, 4, P20, A, B), (signed, 1, 1, 1, P20, C, C)])
+
+
+def test_large_carried_summaries(checker):
+    """Synthetic carried summaries near the largest an admitted product can
+    leave (max below P/2 < 2^155, absolute sums up to 2^218, k up to 2^62),
+    against native operands and each other: every candidate product is far
+    above 2^256 and the decisions must still equal the unbounded ones."""
+    rng = random.Random(12)
+    P = oracle.modulus_product(20)
+    cases = []
+    for t in range(16):
+        signed = t % 2 == 0
+        m, n = rng.randint(1, 4), rng.randint(1, 4)
+        k = rng.choice([1, 2, 3, 1 << 31, (1 << 62) + 7])
+
+        def carried(count, length):
+            axes = []
+            for _ in range(count):
+                mx = rng.randint(1, P // 2 - 1) >> rng.randint(0, 150)
+                axes.append(xr.Axis(max_magnitude=mx, absolute_sum=mx * rng.randint(1, length)))
+            return xr.Operand(max(a.max_magnitude for a in axes), axes, axes)
+
+        A = carried(m, k) if t % 4 != 3 else xr.native_operand(_native(rng, m, 3, -(1 << 63), (1 << 63) - 1))
+        B = carried(n, k) if t % 4 != 2 else xr.native_operand(_native(rng, 3, n, -(1 << 63), (1 << 63) - 1))
+        if t % 4 == 3:
+            k = 3
+            A.cols = []
+            B = xr.Operand(B.max_magnitude, [], B.cols)
+        if t % 4 == 2:
+            k = 3
+        cases.append((signed, m, n, k, P, A, B))
+    _check(checker, cases)
+
+
+def test_planted_wrap_is_detected(checker):
+    """The comparison can see a wrap: with the multiplication reduced mod 2^256
+    (what the 256-bit version did) the chained 2^128 case would be admitted;
+    the oracle with the same planted reduction disagrees with the unbounded
+    one, so equality with the unbounded oracle above is a real check."""
+    P20 = oracle.modulus_product(20)
+    A = xr.native_operand([[-(1 << 63)] * 4])
+    B = xr.native_operand([[-(1 << 63)]] * 4)
+    _, C = xr.gemm_bound(A, B, 1, 1, 4)
+    wrapped = (1 * C.max_magnitude * C.max_magnitude) % (1 << 256)
+    assert xr.fits(True, wrapped, P20)  # the planted mistake admits it
+    assert not xr.fits(True, 1 * C.max_magnitude * C.max_magnitude, P20)

@@ -124,3 +124,42 @@ def test_unsigned_chain_threshold_one_signed_columns(gpu_ctx, prefix):
     A = [[(1 << 63) + 5] * 4] * 2
     B = [[3 << 40, 1 << 40], [1 << 40, 2 << 40], [4 << 40, 1], [1 << 40, 9 << 40]]
     _threshold_pair(gpu_ctx, A, B, [1, 1], prefix, False)
+
+
+@pytest.mark.parametrize("signed", [True, False])
+def test_product_of_two_large_results_is_refused(gpu_ctx, signed):
+    """C1 = A x B and C2 = A x B each carry the attained bound 2^128 (signed:
+    four products of (-2^63)^2; unsigned: (2^64 - 1)^2 * 4 < 2^130) and are
+    admitted at prefix 20. D = C1 x C2 with k = 1 has the bound C1 * C2, about
+    2^256, far outside P20 (about 2^155): it must be refused with
+    RNS8_RANGE_ERROR, as the reference's unbounded arithmetic refuses it (a
+    256-bit product of the two bounds wraps to a small value)."""
+    prefix = 20
+    sem = r.EXACT_WIDE_SIGNED if signed else r.EXACT_WIDE_UNSIGNED
+    bk = r.BOUND_NONE
+    flags = r.PLAN_FORCE_FIXED_PREFIX
+    v = -(1 << 63) if signed else (1 << 64) - 1
+    dt = np.int64 if signed else np.uint64
+    ctx = gpu_ctx
+    p1 = r.Plan(ctx, r.gemm_desc(sem, bk, 1, 1, 4, max_prefix=prefix, flags=flags))
+    p2 = r.Plan(ctx, r.gemm_desc(sem, bk, 1, 1, 1, max_prefix=prefix, flags=flags))
+    A = r.Matrix(ctx, r.matrix_desc(1, 4, sem, bk, prefix))
+    B = r.Matrix(ctx, r.matrix_desc(4, 1, sem, bk, prefix))
+    C1 = r.Matrix(ctx, r.matrix_desc(1, 1, sem, bk, prefix))
+    C2 = r.Matrix(ctx, r.matrix_desc(1, 1, sem, bk, prefix))
+    D = r.Matrix(ctx, r.matrix_desc(1, 1, sem, bk, prefix))
+    pack = r.pack_i64 if signed else r.pack_u64
+    r.check(pack(ctx, A, np.full((1, 4), v, dtype=dt), 1), "pack A")
+    r.check(pack(ctx, B, np.full((4, 1), v, dtype=dt), 2), "pack B")
+    ws1 = r.Workspace(ctx, p1)
+    r.check(r.gemm_rns(ctx, p1, A, B, C1, ws1), "C1 = A x B")
+    r.check(r.gemm_rns(ctx, p1, A, B, C2, ws1), "C2 = A x B")
+    L = _limbs(oracle.modulus_product(prefix))
+    out = np.zeros((1, L), dtype=np.uint64)
+    export = r.export_exact_wide_signed_limbs if signed else r.export_exact_wide_unsigned_limbs
+    r.check(export(ctx, p1, C1, out, L), "export C1")
+    c1 = oracle.limbs_to_int(out[0], signed)
+    assert c1 == 4 * v * v
+    bound = xr.gemm_bound(xr.uniform_operand(abs(c1)), xr.uniform_operand(abs(c1)), 1, 1, 1)[0]
+    assert not xr.fits(signed, bound, oracle.modulus_product(prefix))
+    assert r.gemm_rns(ctx, p2, C1, C2, D, r.Workspace(ctx, p2)) == r.RANGE_ERROR

@@ -175,3 +175,62 @@ def test_fused_refuses_unaligned_operands(gpu_ctx, lda_extra, ldb_extra, offset)
         hip.free(dA)
         hip.free(dB)
     assert st == r.UNSUPPORTED_BACKEND
+
+
+@pytest.mark.parametrize("signed", [True, False])
+def test_fused_reads_stay_in_logical_extent(gpu_ctx, signed):
+    """Strided operands in buffers of exactly (m - 1) * lda + k and
+    (k - 1) * ldb + n elements, each placed at the very end of a 64 KiB-aligned
+    allocation: the loads' ranges end at the last logical element, so the
+    padding of the last row, which such a buffer does not hold, is never
+    read, and the planes equal the packed GEMM's."""
+    m, n, k, prefix = 130, 200, 3000, 9
+    lda, ldb = k + 30, n + 126  # the padding the loads of the last row would cover
+    A, B = _operands(970 + signed, m, n, k, lda, ldb, signed)
+    plan, sem, bk = _plans(gpu_ctx, signed, m, n, k, prefix, 2)
+    a_elems, b_elems = (m - 1) * lda + k, (k - 1) * ldb + n
+    a_bytes, b_bytes = a_elems * 8, b_elems * 8
+    a_alloc = (a_bytes + 65535) // 65536 * 65536
+    b_alloc = (b_bytes + 65535) // 65536 * 65536
+    C = r.Matrix(gpu_ctx, r.matrix_desc(m, n, sem, bk, prefix))
+    ws = r.Workspace(gpu_ctx, plan)
+    baseA, baseB = hip.malloc(a_alloc), hip.malloc(b_alloc)
+    try:
+        dA, dB = baseA + a_alloc - a_bytes, baseB + b_alloc - b_bytes
+        assert dA % 16 == 0 and dB % 16 == 0
+        hip.to_device(dA, np.ascontiguousarray(A.reshape(-1)[:a_elems]))
+        hip.to_device(dB, np.ascontiguousarray(B.reshape(-1)[:b_elems]))
+        fn = r.lib().rns8_mi355x_gemm_native_i64_async if signed else r.lib().rns8_mi355x_gemm_native_u64_async
+        st = fn(gpu_ctx.ptr, plan.ptr, _vp(dA), lda, _vp(dB), ldb, C.ptr, ws.ptr, None)
+        hip.synchronize()
+    finally:
+        hip.free(baseA)
+        hip.free(baseB)
+    assert st == r.SUCCESS
+    Cp = _packed(gpu_ctx, plan, sem, bk, A, B, m, n, k, prefix, lda, ldb, signed)
+    np.testing.assert_array_equal(C.read_residues(), Cp.read_residues())
+
+
+def test_fused_refusal_leaves_result_current(gpu_ctx):
+    """A refused call (odd stride) enqueues nothing and leaves C as it was: a
+    result computed before it still exports."""
+    m, n, k, prefix = 64, 64, 1024, 9
+    A = inputs.int_range(inputs.operand_seed(980, "A"), (m, k), 20)
+    B = inputs.int_range(inputs.operand_seed(980, "B"), (k, n), 20)
+    plan, sem, bk = _plans(gpu_ctx, True, m, n, k, prefix, 1 << 60)
+    C = r.Matrix(gpu_ctx, r.matrix_desc(m, n, sem, bk, prefix))
+    ws = r.Workspace(gpu_ctx, plan)
+    dA, dB = _device(A), _device(B)
+    try:
+        fn = r.lib().rns8_mi355x_gemm_native_i64_async
+        assert fn(gpu_ctx.ptr, plan.ptr, _vp(dA), k, _vp(dB), n, C.ptr, ws.ptr, None) == r.SUCCESS
+        hip.synchronize()
+        assert fn(gpu_ctx.ptr, plan.ptr, _vp(dA), k - 1, _vp(dB), n, C.ptr, ws.ptr, None) == r.INVALID_ARGUMENT
+        assert fn(gpu_ctx.ptr, plan.ptr, _vp(dA + 8), k, _vp(dB), n, C.ptr, ws.ptr, None) == r.UNSUPPORTED_BACKEND
+        hip.synchronize()
+    finally:
+        hip.free(dA)
+        hip.free(dB)
+    out = np.zeros((m, n), dtype=np.int64)
+    r.check(r.export_i64(gpu_ctx, plan, C, out), "export after refused calls")
+    np.testing.assert_array_equal(out, oracle.exact_gemm_i64(A, B, limbs=1).view(np.int64))
