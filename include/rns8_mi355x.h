@@ -95,6 +95,27 @@ RNS8_API rns8_status rns8_mi355x_gemm_finite_u8_async(
     rns8_workspace* workspace,
     void* stream);
 
+/* rns8_mi355x_gemm_rns_async for bounded int64 / uint64 plans (global or
+ * per-tile bounds) without a workspace, for callers that cannot allocate:
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation. No counterpart in the reference. The call allocates nothing,
+ * on the device or the host: split-K partials (tall-skinny shapes) go to a
+ * static per-device scratch array of 16 MiB that the library holds until the
+ * process ends (its address is looked up when a context is created). Plans
+ * whose split-K partials exceed 16 MiB return RNS8_WORKSPACE_TOO_SMALL;
+ * exact-wide plans return RNS8_UNSUPPORTED_BACKEND (their admission proofs
+ * live in host memory). Every call on one device shares that device's
+ * scratch: calls that overlap on one device (on different streams, or from
+ * several threads) race and must be ordered by the caller; calls ordered on
+ * one stream do not. Results equal rns8_mi355x_gemm_rns_async's. */
+RNS8_API rns8_status rns8_mi355x_gemm_rns_noalloc(
+    rns8_context* ctx,
+    const rns8_plan* plan,
+    const rns8_matrix* A,
+    const rns8_matrix* B,
+    rns8_matrix* C,
+    void* stream);
+
 /* Stream-ordered rns8_gemm_rns_grouped / rns8_gemm_finite_u8_grouped
  * (reference rns8.h:1061-1065, 1139-1144): the same validation, the group
  * enqueued on `stream` as one persistent launch per 65536-K block and up to

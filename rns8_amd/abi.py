@@ -349,6 +349,7 @@ PROTOTYPES = {
     "rns8_mi355x_pack_u64_device": (_U32, [_P, _P, _P, _I64, _U64, _P]),
     "rns8_mi355x_pack_finite_u8_device": (_U32, [_P, _P, _U16, _P, _I64, _U64, _P]),
     "rns8_mi355x_gemm_rns_async": (_U32, [_P, _P, _P, _P, _P, _P, _P]),
+    "rns8_mi355x_gemm_rns_noalloc": (_U32, [_P, _P, _P, _P, _P, _P]),
     "rns8_mi355x_gemm_native_i64_async": (_U32, [_P, _P, _P, _I64, _P, _I64, _P, _P, _P]),
     "rns8_mi355x_gemm_native_u64_async": (_U32, [_P, _P, _P, _I64, _P, _I64, _P, _P, _P]),
     "rns8_mi355x_gemm_finite_u8_async": (_U32, [_P, _P, _U16, _P, _P, _P, _P, _P]),

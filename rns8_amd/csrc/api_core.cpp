@@ -579,6 +579,9 @@ rns8_status rns8_create_context(int device_id, const rns8_context_options* optio
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return RNS8_BACKEND_FAILURE;
     // The kernels are built for gfx950 only.
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return RNS8_UNSUPPORTED_ARCH;
+    // the device's address of the static scratch used by calls that allocate
+    // nothing (rns8_mi355x_gemm_rns_noalloc); a failure here surfaces there
+    (void)resolve_noalloc_scratch(dev);
     auto* ctx = new (std::nothrow) rns8_context();
     if (!ctx) return RNS8_INTERNAL_ERROR;
     ctx->device_id = dev;

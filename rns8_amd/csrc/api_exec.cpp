@@ -257,7 +257,7 @@ rns8_status pack_u8(rns8_context* ctx, rns8_matrix* matrix, uint16_t modulus, co
 // ---- GEMM --------------------------------------------------------------------------
 
 rns8_status run_gemm(rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B,
-                     rns8_matrix& C, rns8_workspace& ws, uint32_t nplanes, const PlaneConsts& consts,
+                     rns8_matrix& C, int32_t* splitk_ws, uint32_t nplanes, const PlaneConsts& consts,
                      hipStream_t stream) {
   GemmArgs g{};
   g.a = A.planes;
@@ -274,7 +274,7 @@ rns8_status run_gemm(rns8_context& ctx, const rns8_plan& plan, const rns8_matrix
   g.pitch_c = C.plane_pitch;
   g.nplanes = nplanes;
   g.slices = plan.splitk_slices;
-  g.splitk_ws = plan.splitk_slices > 1 ? ws.splitk : nullptr;
+  g.splitk_ws = plan.splitk_slices > 1 ? splitk_ws : nullptr;
   if (hipSetDevice(ctx.device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
   const hipError_t e = launch_gemm(g, consts, stream);
   if (e == hipErrorInvalidValue) return RNS8_UNSUPPORTED_BACKEND;  // shape outside the kernel's limits
@@ -326,7 +326,7 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
   if (per_tile_kind(plan->desc.bound_kind) && !plan->schedule.entries.empty())
     st = run_gemm_tiled(*ctx, *plan, *A, *B, *C, stream);
   else
-    st = run_gemm(*ctx, *plan, *A, *B, *C, *ws, plan->prefix, make_ladder_plane_consts(plan->prefix), stream);
+    st = run_gemm(*ctx, *plan, *A, *B, *C, ws->splitk, plan->prefix, make_ladder_plane_consts(plan->prefix), stream);
   if (st != RNS8_SUCCESS) return st;
   if (synchronous) {
     st = sync(stream);
@@ -340,6 +340,39 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
     C->exact_cols.swap(out_cols);
     C->exact_prefix = plan->prefix;
   }
+  return RNS8_SUCCESS;
+}
+
+// rns8_mi355x_gemm_rns_noalloc: the bounded int64/uint64 GEMM of
+// rns8_mi355x_gemm_rns_async without a workspace argument. Split-K partials
+// go to the library's per-device static scratch (kNoAllocScratchBytes); the
+// call allocates nothing, host or device. Exact-wide plans are refused: their
+// admission builds per-row and per-column proofs in host memory.
+rns8_status gemm_rns_noalloc(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* A, const rns8_matrix* B,
+                             rns8_matrix* C, void* stream_arg) {
+  if (!ctx || !plan || !A || !B || !C) return RNS8_INVALID_ARGUMENT;
+  if (plan->backend != ctx->backend || plan->device_id != ctx->device_id) return RNS8_INVALID_ARGUMENT;
+  rns8_status st = check_rns_operands(*ctx, *plan, *A, *B, *C);
+  if (st != RNS8_SUCCESS) return st;
+  if (plan->desc.semantics != RNS8_BOUNDED_I64 && plan->desc.semantics != RNS8_BOUNDED_U64)
+    return RNS8_UNSUPPORTED_BACKEND;
+  const bool tiled = per_tile_kind(plan->desc.bound_kind) && !plan->schedule.entries.empty();
+  int32_t* scratch = nullptr;
+  if (!tiled && plan->splitk_slices > 1) {
+    const int64_t kblock = plan->desc.k > kSafeKBlock ? kSafeKBlock : plan->desc.k;
+    if (splitk_workspace_bytes(plan->desc.m, plan->desc.n, kblock, plan->prefix) > kNoAllocScratchBytes)
+      return RNS8_WORKSPACE_TOO_SMALL;
+    scratch = noalloc_scratch(ctx->device_id);
+    if (!scratch) return RNS8_BACKEND_FAILURE;
+  }
+  const hipStream_t stream = pick_stream(*ctx, stream_arg);
+  C->device_current = false;
+  st = tiled ? run_gemm_tiled(*ctx, *plan, *A, *B, *C, stream)
+             : run_gemm(*ctx, *plan, *A, *B, *C, scratch, plan->prefix, make_ladder_plane_consts(plan->prefix),
+                        stream);
+  if (st != RNS8_SUCCESS) return st;
+  C->device_current = true;
+  C->source_version = output_source_version(A->source_version, B->source_version);
   return RNS8_SUCCESS;
 }
 
@@ -400,7 +433,7 @@ rns8_status gemm_finite(rns8_context* ctx, const rns8_plan* plan, uint16_t modul
   if (st != RNS8_SUCCESS) return st;
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
   C->device_current = false;
-  st = run_gemm(*ctx, *plan, *A, *B, *C, *ws, 1, make_single_plane_consts(modulus), stream);
+  st = run_gemm(*ctx, *plan, *A, *B, *C, ws->splitk, 1, make_single_plane_consts(modulus), stream);
   if (st != RNS8_SUCCESS) return st;
   if (synchronous) {
     st = sync(stream);
@@ -906,6 +939,11 @@ rns8_status rns8_mi355x_gemm_rns_async(rns8_context* ctx, const rns8_plan* plan,
                                        const rns8_matrix* B, rns8_matrix* C, rns8_workspace* workspace,
                                        void* stream) {
   return guard([&] { return gemm_rns(ctx, plan, A, B, C, workspace, stream, false); });
+}
+
+rns8_status rns8_mi355x_gemm_rns_noalloc(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* A,
+                                         const rns8_matrix* B, rns8_matrix* C, void* stream) {
+  return guard([&] { return gemm_rns_noalloc(ctx, plan, A, B, C, stream); });
 }
 
 rns8_status rns8_mi355x_gemm_finite_u8_async(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus,

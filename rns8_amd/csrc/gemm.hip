@@ -41,6 +41,7 @@
 //     partial tile to its own workspace slot; a finalize kernel adds the
 //     slices, reduces to int8 and writes C (deterministic, no atomics).
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "dma.hpp"
@@ -905,6 +906,40 @@ hipError_t launch_zero_tiles(int8_t* c, int64_t ldc, int64_t pitch_c, const Tile
   if (!c || !d_tiles || ldc <= 0 || ldc % 16 || pitch_c < ldc || count > 0x7FFFFFFFu) return hipErrorInvalidValue;
   hipLaunchKernelGGL(zero_tiles_kernel, dim3(count), dim3(256), 0, stream, c, ldc, pitch_c, d_tiles);
   return hipGetLastError();
+}
+
+// ---- static scratch for calls that allocate nothing ---------------------------
+// The split-K partials of rns8_mi355x_gemm_rns_noalloc live here instead of
+// in a caller's workspace. Each device holds its own copy of the array for
+// the life of the process. On the host the array's name is not a device
+// address: host code uses the per-device address resolve_noalloc_scratch
+// records (hipGetSymbolAddress with that device current).
+static __device__ __align__(256) int32_t scratch[kNoAllocScratchBytes / 4];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<int32_t*> g_scratch[kMaxDevices] = {};
+std::mutex g_scratch_mutex;
+}  // namespace
+
+hipError_t resolve_noalloc_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  if (g_scratch[device].load(std::memory_order_acquire)) return hipSuccess;
+  int current = -1;
+  if (hipGetDevice(&current) != hipSuccess || current != device) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[device].load(std::memory_order_acquire)) return hipSuccess;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if (!ptr || (reinterpret_cast<uintptr_t>(ptr) & 255u) != 0) return hipErrorInvalidSymbol;
+  g_scratch[device].store(static_cast<int32_t*>(ptr), std::memory_order_release);
+  return hipSuccess;
+}
+
+int32_t* noalloc_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  return g_scratch[device].load(std::memory_order_acquire);
 }
 
 hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream) {

@@ -133,6 +133,16 @@ uint32_t choose_splitk_slices(int64_t m, int64_t n, int64_t k, uint32_t nplanes)
 // one [plane][M][ldc] int32 slot per slice.
 uint64_t splitk_workspace_bytes(int64_t m, int64_t n, int64_t k, uint32_t nplanes);
 
+// Per-device static split-K scratch (gemm.hip) for GEMM calls that bring no
+// workspace and may allocate nothing: kNoAllocScratchBytes of int32 partials.
+constexpr uint64_t kNoAllocScratchBytes = uint64_t{16} << 20;
+// Records `device`'s address of the scratch (hipGetSymbolAddress), once per
+// device; `device` must be the current device. Returns the HIP error of the
+// lookup, or hipSuccess when the address is (already) recorded.
+hipError_t resolve_noalloc_scratch(int device);
+// The recorded address for `device`, or nullptr when it was never resolved.
+int32_t* noalloc_scratch(int device);
+
 // ---- export ------------------------------------------------------------------
 enum class ExportKind : uint32_t { I64 = 0, U64 = 1, WIDE_SIGNED = 2, WIDE_UNSIGNED = 3 };
 
