@@ -1049,10 +1049,21 @@ rns8_status rns8_create_matrix(rns8_context* ctx, const rns8_matrix_desc* desc, 
       delete m;
       return RNS8_BACKEND_FAILURE;
     }
+    // exact-wide matrices: two words and an event for proofs left on the device
+    if (exact_wide(desc->semantics) &&
+        (hipMalloc(reinterpret_cast<void**>(&m->proof_device), 16) != hipSuccess ||
+         hipEventCreateWithFlags(&m->proof_event, hipEventDisableTiming) != hipSuccess)) {
+      free_device(m->planes);
+      free_device(m->proof_device);
+      delete m;
+      return RNS8_BACKEND_FAILURE;
+    }
     // zero planes: a fresh matrix holds the integer 0 and keeps padding zero
     if (launch_zero_words(reinterpret_cast<uint32_t*>(m->planes), m->plane_bytes / 4, ctx->stream) != hipSuccess ||
         hipStreamSynchronize(ctx->stream) != hipSuccess) {
       free_device(m->planes);
+      free_device(m->proof_device);
+      if (m->proof_event) (void)hipEventDestroy(m->proof_event);
       delete m;
       return RNS8_BACKEND_FAILURE;
     }
@@ -1070,7 +1081,8 @@ rns8_status rns8_destroy_matrix(rns8_matrix* matrix) {
     free_device(matrix->upload);
     free_device(matrix->staging);
     free_device(matrix->status);
-    free_device(matrix->scratch64);
+    free_device(matrix->proof_device);
+    if (matrix->proof_event) (void)hipEventDestroy(matrix->proof_event);
     delete matrix;
     return RNS8_SUCCESS;
   });

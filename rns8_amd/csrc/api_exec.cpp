@@ -44,15 +44,81 @@ uint64_t output_source_version(uint64_t a, uint64_t b) {
   return h == 0 ? 1 : h;
 }
 
-// exact_range.hpp:104-157 on the operands' carried proofs.
+// The largest magnitude a 64-bit operand can have: what a device-pointer
+// pack's proof holds until it is read back.
+I512 native_worst_case(rns8_semantics s) {
+  return s == RNS8_EXACT_WIDE_SIGNED ? I512::pow2(63) : I512::from_u64(~uint64_t{0});
+}
+
+// Reads a proof left on the device back into exact_max (waits for the work
+// that writes it). No-op for a proof that is already exact.
+rns8_status resolve_exact_proof(const rns8_matrix& m) {
+  if (!m.exact_pending) return RNS8_SUCCESS;
+  unsigned long long w[2] = {0, 0};
+  if (hipSetDevice(m.device_id) != hipSuccess || hipEventSynchronize(m.proof_event) != hipSuccess ||
+      hipMemcpy(w, m.proof_device, sizeof(w), hipMemcpyDeviceToHost) != hipSuccess)
+    return RNS8_BACKEND_FAILURE;
+  m.exact_max = m.pending_product
+                    ? I512::from_u64(m.proof_k) * I512::from_u64(w[0]) * I512::from_u64(w[1])
+                    : I512::from_u64(w[0]);
+  m.exact_pending = false;
+  return RNS8_SUCCESS;
+}
+
+// exact_range.hpp:104-157 on the operands' carried proofs. Operands whose
+// proofs are still on the device (device-pointer packs) carry no per-axis
+// summaries, so the bound is k * maxA * maxB; when the worst case of that
+// product is admitted the exact one is too, and the result is left pending
+// as well (*pending: the caller copies the operands' device maxima into the
+// result's proof words). Otherwise the proofs are read back and the decision
+// is made on exact values.
 rns8_status exact_gemm_range(const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B, I512& bound,
-                             std::vector<ExactAxis>* out_rows, std::vector<ExactAxis>* out_cols) {
+                             std::vector<ExactAxis>* out_rows, std::vector<ExactAxis>* out_cols,
+                             bool* pending = nullptr) {
+  if (pending) *pending = false;
   if (!exact_wide(plan.desc.semantics)) return RNS8_SUCCESS;
   if (A.exact_prefix < plan.prefix || B.exact_prefix < plan.prefix) return RNS8_RANGE_ERROR;
+  if (A.exact_pending || B.exact_pending) {
+    const bool natives = A.exact_pending && !A.pending_product && B.exact_pending && !B.pending_product;
+    if (natives && pending) {
+      const I512 worst = I512::from_u64(static_cast<uint64_t>(plan.desc.k)) * A.exact_max * B.exact_max;
+      if (exact_range_fits(plan.desc.semantics, worst, plan.product)) {
+        bound = worst;
+        if (out_rows) out_rows->clear();
+        if (out_cols) out_cols->clear();
+        *pending = true;
+        return RNS8_SUCCESS;
+      }
+    }
+    rns8_status st = resolve_exact_proof(A);
+    if (st == RNS8_SUCCESS) st = resolve_exact_proof(B);
+    if (st != RNS8_SUCCESS) return st;
+  }
   const ExactOperand a{&A.exact_max, &A.exact_rows, &A.exact_cols};
   const ExactOperand b{&B.exact_max, &B.exact_rows, &B.exact_cols};
   return exact_product_range(plan.desc.semantics, plan.desc.m, plan.desc.n, plan.desc.k, a, b, plan.product, bound,
                              out_rows, out_cols);
+}
+
+// Records C's proof after C = A x B: exact values from the host proofs, or,
+// for a pending result, the operands' device maxima copied into C's proof
+// words on the GEMM's stream (ordered after their packs as the planes are).
+rns8_status commit_exact_proof(rns8_matrix& C, const rns8_matrix& A, const rns8_matrix& B, const rns8_plan& plan,
+                               const I512& bound, std::vector<ExactAxis>& rows, std::vector<ExactAxis>& cols,
+                               bool pending, hipStream_t stream) {
+  if (pending) {
+    if (launch_proof_factors(A.proof_device, B.proof_device, C.proof_device, stream) != hipSuccess ||
+        hipEventRecord(C.proof_event, stream) != hipSuccess)
+      return RNS8_BACKEND_FAILURE;
+    C.proof_k = static_cast<uint64_t>(plan.desc.k);
+  }
+  C.exact_max = bound;
+  C.exact_pending = pending;
+  C.pending_product = pending;
+  C.exact_rows.swap(rows);
+  C.exact_cols.swap(cols);
+  C.exact_prefix = plan.prefix;
+  return RNS8_SUCCESS;
 }
 
 // ---- shared validation --------------------------------------------------------
@@ -118,9 +184,16 @@ rns8_status check_export(const rns8_context& ctx, const rns8_plan& plan, const r
                       plan.desc.tile_m, plan.desc.tile_n))
     return RNS8_INVALID_ARGUMENT;
   if (!C.device_current) return RNS8_INVALID_ARGUMENT;
-  if (exact_wide(semantics) && C.exact_prefix != 0 &&
-      (C.exact_prefix < plan.prefix || !exact_range_fits(semantics, C.exact_max, plan.product)))
-    return RNS8_RANGE_ERROR;
+  if (exact_wide(semantics) && C.exact_prefix != 0) {
+    if (C.exact_prefix < plan.prefix) return RNS8_RANGE_ERROR;
+    // a pending proof whose worst case fits needs no read back
+    if (!exact_range_fits(semantics, C.exact_max, plan.product)) {
+      if (!C.exact_pending) return RNS8_RANGE_ERROR;
+      const rns8_status st = resolve_exact_proof(C);
+      if (st != RNS8_SUCCESS) return st;
+      if (!exact_range_fits(semantics, C.exact_max, plan.product)) return RNS8_RANGE_ERROR;
+    }
+  }
   return RNS8_SUCCESS;
 }
 
@@ -158,29 +231,38 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
   if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
 
-  // exact-wide proof (api_pack.cpp:47-65); kept when the source is unchanged
+  // exact-wide proof (api_pack.cpp:47-65); kept when the source is unchanged.
+  // A device-pointer pack into a matrix whose prefix admits every 64-bit
+  // value (P > 2^64: prefix 9 and up) proves its maximum |x| in the pack
+  // launch itself and leaves it on the device (`deferred`): no decision at
+  // pack time depends on it. Smaller prefixes need the maximum before
+  // anything is written (a refused pack leaves the matrix as it was), so it
+  // is computed and read back first.
   I512 proof_max;
   std::vector<ExactAxis> proof_rows, proof_cols;
   const bool is_wide = matrix->desc.semantics == wide;
+  const I256 matrix_product = modulus_product(matrix->prefix);
+  bool deferred = false;
   if (is_wide) {
     if (same_source) {
-      proof_max = matrix->exact_max;
+      proof_max = matrix->exact_max;  // a pending proof keeps its worst case
     } else if (where == Source::Host) {
       native_exact_ranges(src, rows, cols, ld, proof_max, proof_rows, proof_cols);
+    } else if (exact_range_fits(matrix->desc.semantics, native_worst_case(matrix->desc.semantics), matrix_product)) {
+      deferred = true;
+      proof_max = native_worst_case(matrix->desc.semantics);
     } else {
-      if (!matrix->scratch64 && hipMalloc(reinterpret_cast<void**>(&matrix->scratch64), 16) != hipSuccess)
-        return RNS8_BACKEND_FAILURE;
       unsigned long long host_max = 0;
-      if (launch_zero_words(reinterpret_cast<uint32_t*>(matrix->scratch64), 2, stream) != hipSuccess ||
+      if (launch_zero_words(reinterpret_cast<uint32_t*>(matrix->proof_device), 2, stream) != hipSuccess ||
           launch_max_magnitude(src, rows, cols, ld, is_signed ? NativeKind::I64 : NativeKind::U64,
-                               reinterpret_cast<unsigned long long*>(matrix->scratch64), stream) != hipSuccess ||
-          hipMemcpyAsync(&host_max, matrix->scratch64, sizeof(host_max), hipMemcpyDeviceToHost, stream) !=
+                               matrix->proof_device, stream) != hipSuccess ||
+          hipMemcpyAsync(&host_max, matrix->proof_device, sizeof(host_max), hipMemcpyDeviceToHost, stream) !=
               hipSuccess ||
           hipStreamSynchronize(stream) != hipSuccess)
         return RNS8_BACKEND_FAILURE;
       proof_max = I512::from_u64(host_max);
     }
-    if (!exact_range_fits(matrix->desc.semantics, proof_max, modulus_product(matrix->prefix))) return RNS8_RANGE_ERROR;
+    if (!exact_range_fits(matrix->desc.semantics, proof_max, matrix_product)) return RNS8_RANGE_ERROR;
   }
   if (same_source) return RNS8_SUCCESS;
 
@@ -203,9 +285,13 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
                 matrix->plane_ld,
                 matrix->plane_pitch,
                 matrix->prefix,
-                is_signed ? NativeKind::I64 : NativeKind::U64};
+                is_signed ? NativeKind::I64 : NativeKind::U64,
+                deferred ? matrix->proof_device : nullptr};
+  if (deferred && launch_zero_words(reinterpret_cast<uint32_t*>(matrix->proof_device), 2, stream) != hipSuccess)
+    return RNS8_BACKEND_FAILURE;
   if (launch_pack_native(args, make_ladder_plane_consts(matrix->prefix), stream) != hipSuccess)
     return RNS8_BACKEND_FAILURE;
+  if (deferred && hipEventRecord(matrix->proof_event, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
   if (where == Source::Host) {
     const rns8_status st = sync(stream);
     if (st != RNS8_SUCCESS) return st;
@@ -214,6 +300,8 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
   matrix->source_version = sv;
   if (is_wide) {
     matrix->exact_max = proof_max;
+    matrix->exact_pending = deferred;
+    matrix->pending_product = false;
     matrix->exact_rows.swap(proof_rows);
     matrix->exact_cols.swap(proof_cols);
     matrix->exact_prefix = matrix->prefix;
@@ -319,7 +407,8 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
   if (st != RNS8_SUCCESS) return st;
   I512 bound;
   std::vector<ExactAxis> out_rows, out_cols;
-  st = exact_gemm_range(*plan, *A, *B, bound, &out_rows, &out_cols);
+  bool pending = false;
+  st = exact_gemm_range(*plan, *A, *B, bound, &out_rows, &out_cols, &pending);
   if (st != RNS8_SUCCESS) return st;
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
   C->device_current = false;
@@ -328,18 +417,16 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
   else
     st = run_gemm(*ctx, *plan, *A, *B, *C, ws->splitk, plan->prefix, make_ladder_plane_consts(plan->prefix), stream);
   if (st != RNS8_SUCCESS) return st;
+  if (exact_wide(plan->desc.semantics)) {
+    st = commit_exact_proof(*C, *A, *B, *plan, bound, out_rows, out_cols, pending, stream);
+    if (st != RNS8_SUCCESS) return st;
+  }
   if (synchronous) {
     st = sync(stream);
     if (st != RNS8_SUCCESS) return st;
   }
   C->device_current = true;
   C->source_version = output_source_version(A->source_version, B->source_version);
-  if (exact_wide(plan->desc.semantics)) {
-    C->exact_max = bound;
-    C->exact_rows.swap(out_rows);
-    C->exact_cols.swap(out_cols);
-    C->exact_prefix = plan->prefix;
-  }
   return RNS8_SUCCESS;
 }
 
@@ -483,10 +570,14 @@ rns8_status gemm_grouped(rns8_context* ctx, const rns8_plan* plan, const rns8_gr
   }
   std::vector<I512> bounds(task_count);
   std::vector<std::vector<ExactAxis>> rows(task_count), cols(task_count);
+  std::vector<uint8_t> pendings(task_count, 0);
   if (!finite && exact_wide(plan->desc.semantics))
     for (uint32_t i = 0; i < task_count; ++i) {
-      const rns8_status st = exact_gemm_range(*plan, *tasks[i].a, *tasks[i].b, bounds[i], &rows[i], &cols[i]);
+      bool pending = false;
+      const rns8_status st =
+          exact_gemm_range(*plan, *tasks[i].a, *tasks[i].b, bounds[i], &rows[i], &cols[i], &pending);
       if (st != RNS8_SUCCESS) return st;
+      pendings[i] = pending ? 1 : 0;
     }
 
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
@@ -520,6 +611,10 @@ rns8_status gemm_grouped(rns8_context* ctx, const rns8_plan* plan, const rns8_gr
     const hipError_t e = launch_gemm_grouped(g, consts, ptrs.data(), task_count, stream);
     st = e == hipSuccess ? RNS8_SUCCESS : e == hipErrorInvalidValue ? RNS8_UNSUPPORTED_BACKEND : RNS8_BACKEND_FAILURE;
   }
+  if (st == RNS8_SUCCESS && !finite && exact_wide(plan->desc.semantics))
+    for (uint32_t i = 0; i < task_count && st == RNS8_SUCCESS; ++i)
+      st = commit_exact_proof(*tasks[i].c, *tasks[i].a, *tasks[i].b, *plan, bounds[i], rows[i], cols[i],
+                              pendings[i] != 0, stream);
   if (st == RNS8_SUCCESS && synchronous) st = sync(stream);
   if (st != RNS8_SUCCESS) return st;
   for (uint32_t i = 0; i < task_count; ++i) {
@@ -527,12 +622,6 @@ rns8_status gemm_grouped(rns8_context* ctx, const rns8_plan* plan, const rns8_gr
     C.device_current = true;
     C.source_version = output_source_version(tasks[i].a->source_version, tasks[i].b->source_version);
     if (finite) C.finite_modulus = modulus;
-    if (!finite && exact_wide(plan->desc.semantics)) {
-      C.exact_max = bounds[i];
-      C.exact_rows.swap(rows[i]);
-      C.exact_cols.swap(cols[i]);
-      C.exact_prefix = plan->prefix;
-    }
   }
   return RNS8_SUCCESS;
 }

@@ -95,10 +95,23 @@ struct rns8_matrix {
   int64_t plane_pitch = 0;
   uint64_t plane_bytes = 0;
   // exact-wide proofs: exact_prefix == 0 means no proof
-  rns8x::I512 exact_max;
+  mutable rns8x::I512 exact_max;
   uint32_t exact_prefix = 0;
   std::vector<ExactAxis> exact_rows;
   std::vector<ExactAxis> exact_cols;
+  // A proof left on the device: by a device-pointer pack (max |x| in
+  // proof_device[0]) or by a GEMM of two such operands (their maxima in
+  // proof_device[0..1]; the exact bound is proof_k * [0] * [1]). While
+  // exact_pending is set, exact_max holds a worst case the exact value never
+  // exceeds, so a decision that the worst case passes is the exact decision;
+  // resolve_exact_proof reads the words back (after proof_event) when a
+  // decision needs the exact value. Exact-wide matrices own the two words and
+  // the event from creation.
+  mutable bool exact_pending = false;
+  bool pending_product = false;
+  uint64_t proof_k = 0;
+  unsigned long long* proof_device = nullptr;
+  hipEvent_t proof_event = nullptr;
   // cached staging buffers (export is logically const, reference
   // api_export.cpp:276-287 keeps the same kind of cache on the matrix)
   void* upload = nullptr;
@@ -106,7 +119,6 @@ struct rns8_matrix {
   void* staging = nullptr;
   std::size_t staging_bytes = 0;
   uint32_t* status = nullptr;
-  uint64_t* scratch64 = nullptr;
 };
 
 struct rns8_workspace {

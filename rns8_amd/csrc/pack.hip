@@ -17,6 +17,8 @@
 // with two v_dot4_u32_u8 (s < 2^19), then the full-rate 24-bit quotient.
 // Signed inputs are biased by 2^63 (flip the top bit) and the bias is folded
 // into `off`, so int64 and uint64 share the same arithmetic.
+#include <type_traits>
+
 #include "int_ops.hpp"
 #include "kernels.hpp"
 
@@ -27,13 +29,35 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
 
+// Largest of a block's values, combined into *out by at most one atomic max,
+// skipped when the running maximum already covers it. Every thread of the
+// block must call it.
+__device__ __forceinline__ void block_max_to(unsigned long long best, unsigned long long* out) {
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    const unsigned long long other = __shfl_down(best, offset, 64);
+    best = other > best ? other : best;
+  }
+  __shared__ unsigned long long part[4];
+  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < 4; ++w) best = part[w] > best ? part[w] : best;
+    best = part[0] > best ? part[0] : best;
+    if (best != 0 && __hip_atomic_load(out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < best) atomicMax(out, best);
+  }
+}
+
 // Grid-stride over 8-column chunks with 32-bit indices (the launchers reject
-// matrices with 2^32 chunks or more).
-template <bool Signed, bool Vec>
+// matrices with 2^32 chunks or more). With kMax the kernel also proves the
+// operand's magnitude for exact-wide matrices: max |x| over the valid
+// elements goes to *a.max_out (zero on entry), from the same loads.
+template <bool Signed, bool Vec, bool kMax>
 __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConsts pc, uint32_t chunks_per_row,
                                                           uint32_t total_chunks) {
   constexpr int kCols = 8;
   const uint64_t* const src = static_cast<const uint64_t*>(a.src);
+  unsigned long long best = 0;  // kMax: largest |x| this thread has seen
   for (uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x; ch < total_chunks; ch += gridDim.x * blockDim.x) {
     const uint32_t row = ch / chunks_per_row;
     const int64_t c0 = static_cast<int64_t>(ch - row * chunks_per_row) * kCols;
@@ -55,6 +79,16 @@ __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConst
         const uint64_t x = (c0 + e < a.cols) ? rp[c0 + e] : 0ull;  // padding packs as 0
         lo[e] = static_cast<uint32_t>(x);
         hi[e] = static_cast<uint32_t>(x >> 32);
+      }
+    }
+    if constexpr (kMax) {
+      // padding columns read as 0 and do not change the maximum
+#pragma unroll
+      for (int e = 0; e < kCols; ++e) {
+        const unsigned long long x = (static_cast<unsigned long long>(hi[e]) << 32) | lo[e];
+        // |INT64_MIN| = 2^63 is representable as an unsigned magnitude
+        const unsigned long long mag = (Signed && static_cast<int64_t>(x) < 0) ? 0ull - x : x;
+        best = mag > best ? mag : best;
       }
     }
     if (Signed) {
@@ -85,6 +119,7 @@ __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConst
       *reinterpret_cast<v2i*>(out + static_cast<int64_t>(p) * a.plane_pitch) = w;
     }
   }
+  if constexpr (kMax) block_max_to(best, a.max_out);
 }
 
 // Finite u8: x < 256, s = x + H < 2^9 is inside the range of the int32
@@ -141,19 +176,15 @@ __global__ __launch_bounds__(256) void max_magnitude_kernel(const uint64_t* src,
       }
     }
   }
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    const unsigned long long other = __shfl_down(best, offset, 64);
-    best = other > best ? other : best;
-  }
-  __shared__ unsigned long long part[4];
-  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = best;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int w = 1; w < 4; ++w) best = part[w] > best ? part[w] : best;
-    best = part[0] > best ? part[0] : best;
-    if (best != 0 && __hip_atomic_load(out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < best) atomicMax(out, best);
-  }
+  block_max_to(best, out);
+}
+
+// Proof factors of a GEMM result whose operands both carry device-resident
+// maxima: out[0] = a[0], out[1] = b[0] (one thread).
+__global__ void copy_proof_factors_kernel(const unsigned long long* a, const unsigned long long* b,
+                                          unsigned long long* out) {
+  out[0] = a[0];
+  out[1] = b[0];
 }
 
 unsigned grid_for(int64_t items) {
@@ -174,18 +205,29 @@ hipError_t launch_pack_native(const PackArgs& a, const PlaneConsts& consts, hipS
   if (total >= (int64_t{1} << 32)) return hipErrorInvalidValue;
   const bool vec = (reinterpret_cast<uintptr_t>(a.src) & 15u) == 0 && (a.ld % 2) == 0;
   const dim3 grid(grid_for(total));
-  if (a.kind == NativeKind::I64) {
-    if (vec)
-      hipLaunchKernelGGL((pack_native_kernel<true, true>), grid, dim3(256), 0, stream, a, consts, static_cast<uint32_t>(chunks_per_row), static_cast<uint32_t>(total));
-    else
-      hipLaunchKernelGGL((pack_native_kernel<true, false>), grid, dim3(256), 0, stream, a, consts, static_cast<uint32_t>(chunks_per_row), static_cast<uint32_t>(total));
-  } else {
-    if (vec)
-      hipLaunchKernelGGL((pack_native_kernel<false, true>), grid, dim3(256), 0, stream, a, consts, static_cast<uint32_t>(chunks_per_row), static_cast<uint32_t>(total));
-    else
-      hipLaunchKernelGGL((pack_native_kernel<false, false>), grid, dim3(256), 0, stream, a, consts, static_cast<uint32_t>(chunks_per_row),
-                         static_cast<uint32_t>(total));
-  }
+  const uint32_t cpr = static_cast<uint32_t>(chunks_per_row), tot = static_cast<uint32_t>(total);
+  auto launch = [&](auto sgn, auto vc, auto mx) {
+    hipLaunchKernelGGL((pack_native_kernel<decltype(sgn)::value, decltype(vc)::value, decltype(mx)::value>), grid,
+                       dim3(256), 0, stream, a, consts, cpr, tot);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  const bool sgn = a.kind == NativeKind::I64, mx = a.max_out != nullptr;
+  if (sgn && vec && mx) launch(T{}, T{}, T{});
+  else if (sgn && vec) launch(T{}, T{}, F{});
+  else if (sgn && mx) launch(T{}, F{}, T{});
+  else if (sgn) launch(T{}, F{}, F{});
+  else if (vec && mx) launch(F{}, T{}, T{});
+  else if (vec) launch(F{}, T{}, F{});
+  else if (mx) launch(F{}, F{}, T{});
+  else launch(F{}, F{}, F{});
+  return hipGetLastError();
+}
+
+hipError_t launch_proof_factors(const unsigned long long* a, const unsigned long long* b, unsigned long long* out,
+                                hipStream_t stream) {
+  if (!a || !b || !out) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(copy_proof_factors_kernel, dim3(1), dim3(1), 0, stream, a, b, out);
   return hipGetLastError();
 }
 
