@@ -240,6 +240,14 @@ rns8_status plan_prefix(const rns8_gemm_desc& d, uint32_t& budget, uint32_t& sel
   budget = d.max_prefix == 0 ? default_prefix(d.semantics) : d.max_prefix;
   const rns8_status v = validate_gemm_desc(d, budget);
   if (v != RNS8_SUCCESS) return v;
+  // the schedule's tile grid must have a representable tile count, for every
+  // plan (reference api_plan_schedule.inc:113-118)
+  {
+    const uint64_t tm = d.tile_m == 0 ? 128u : d.tile_m, tn = d.tile_n == 0 ? 128u : d.tile_n;
+    const uint64_t rows = (static_cast<uint64_t>(d.m) + tm - 1) / tm;
+    const uint64_t cols = (static_cast<uint64_t>(d.n) + tn - 1) / tn;
+    if (cols != 0 && rows > std::numeric_limits<uint64_t>::max() / cols) return RNS8_RANGE_ERROR;
+  }
   effective_bound = d.bound;
   if (d.bound_kind == RNS8_BOUND_INPUT_RANGE_AND_K && !input_range_output_bound(d, effective_bound))
     return RNS8_RANGE_ERROR;
@@ -351,13 +359,21 @@ rns8_status build_tile_schedule(const rns8_gemm_desc& d, uint32_t budget, TileSc
   const uint64_t cols = (static_cast<uint64_t>(d.n) + tn - 1) / tn;
   const uint64_t count = rows * cols;
   const bool proofs = (d.flags & RNS8_PLAN_ALLOW_PROVEN_ZERO_ROW_COL_SKIPS) != 0;
+  if (cols != 0 && rows > std::numeric_limits<uint64_t>::max() / cols) return RNS8_RANGE_ERROR;
   if (proofs) {
     s.zero_a_rows.assign(d.zero_a_rows, d.zero_a_rows + d.zero_a_rows_count);
     s.zero_b_cols.assign(d.zero_b_cols, d.zero_b_cols + d.zero_b_cols_count);
     for (uint8_t v : s.zero_a_rows) s.zero_a_row_count += v != 0;
     for (uint8_t v : s.zero_b_cols) s.zero_b_col_count += v != 0;
-    s.zero_row_col_product_count = s.zero_a_row_count * static_cast<uint64_t>(d.n) +
-                                   (static_cast<uint64_t>(d.m) - s.zero_a_row_count) * s.zero_b_col_count;
+    // the count of proven-zero products must be representable
+    // (api_plan_schedule.inc:144-156)
+    const uint64_t nonzero_a_rows = static_cast<uint64_t>(d.m) - s.zero_a_row_count;
+    if (s.zero_a_row_count != 0 && static_cast<uint64_t>(d.n) > std::numeric_limits<uint64_t>::max() / s.zero_a_row_count)
+      return RNS8_RANGE_ERROR;
+    if (s.zero_b_col_count != 0 && nonzero_a_rows > std::numeric_limits<uint64_t>::max() / s.zero_b_col_count)
+      return RNS8_RANGE_ERROR;
+    s.zero_row_col_product_count =
+        s.zero_a_row_count * static_cast<uint64_t>(d.n) + nonzero_a_rows * s.zero_b_col_count;
   }
   if (!d.tile_bounds || d.tile_bounds_count != count) return RNS8_INVALID_ARGUMENT;
   s.bounds.assign(d.tile_bounds, d.tile_bounds + count);
