@@ -15,6 +15,8 @@
 // dword load; a 2-D grid (column groups x rows) needs no index division.
 #include <utility>
 
+#include "crt_export.hpp"
+#include "dma.hpp"
 #include "int_ops.hpp"
 #include "kernels.hpp"
 
@@ -409,6 +411,198 @@ __global__ __launch_bounds__(256) void export_u8_kernel(ExportU8Args a, uint32_t
   }
 }
 
+// ---- CRT-basis export on the matrix cores ----------------------------------------
+//
+// The reconstruction of crt_export.hpp for the exact-wide kinds: the int8
+// MFMA multiplies each cell's residues (K dimension: planes, zero past P) by
+// the signed base-256 digits of the CRT basis and the quotient estimate (N
+// dimension: digit columns), and an integer tail turns the column sums into
+// the centered value, ~115 full-rate operations per cell at any P. The
+// Garner digits and Horner steps of export_kernel cost more for the wide
+// kinds (every limb of the result is a multi-limb Horner chain), and less for
+// the 64-bit kinds, which keep export_kernel: on MI355X at 4096 x 4096 the
+// 3-limb signed export takes 180 us here against 341 us there at P = 20, and
+// the 64-bit export 59 us there against 70 us here at P = 9.
+//
+// Per wave and iteration: 64 consecutive cells of one row. Two 16-byte DMAs
+// stage planes 0..31 of those cells (zero past P, through the buffer range)
+// into the wave's 2 KB of LDS as rows of 64 bytes; the 16-byte chunk c of
+// plane row k sits at chunk position c ^ crt_swz(k), so the transpose reads
+// below (8 rows x 16 bytes per 16-lane group) hit distinct banks. Transpose
+// reads give lane l the 16 planes 16 (l >> 5) .. +15 of cell 32 jb + (l & 31)
+// (the GEMM's B-fragment gather); two MFMAs (cells 0-31 and 32-63) leave
+// column 8g + 4h + e of cell (l & 31) in register 4g + e of lane 32 h + (l &
+// 31); one permlane32 swap per register then gives every lane all columns of
+// cell l.
+template <uint32_t P>
+__device__ constexpr CrtTable<P> kCrt = make_crt_table<P>();
+
+__device__ __forceinline__ uint32_t crt_swz(uint32_t k) { return (k >> 2) & 1u; }
+
+typedef int v16i_crt __attribute__((ext_vector_type(16)));
+typedef int v2i_crt __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i_crt lds_v2i_crt;
+typedef unsigned v2u32_crt __attribute__((ext_vector_type(2)));
+
+// Pipelined: each wave cycles through kDepth tiles of kDma KB (16 planes per
+// KB), and the DMAs of its next kDepth - 1 units are in flight while the
+// current one computes (the kernel is bound by its integer tail, and deeper
+// pipelines measured no faster). Every iteration issues kDma DMAs (a DMA past the
+// last unit has an empty range and lands zeros), then the cell's stores: 8 L
+// bytes per lane, which the compiler may merge into as few as kStores =
+// ceil(L / 2) buffer stores of at most 16 bytes. Vector memory operations
+// retire in order, and after iteration i has issued its DMA the operations
+// newer than unit i's DMAs are the kDepth - 1 later DMA groups and the stores
+// of min(i, kDepth - 1) earlier iterations; waiting until no more than those
+// are outstanding retires unit i's DMAs whether the stores were merged or not
+// (unmerged ones only make the wait stricter). kL is the limb count (0: any
+// count, which waits for every outstanding access).
+template <uint32_t P, ExportKind Kind, uint32_t kL>
+__global__ __launch_bounds__(256) void crt_export_kernel(ExportArgs a, uint32_t chunks_per_row, uint32_t units,
+                                                         uint64_t plane_span) {
+  using T = CrtTable<P>;
+  static_assert(Kind == ExportKind::WIDE_SIGNED || Kind == ExportKind::WIDE_UNSIGNED, "exact-wide kinds only");
+  constexpr uint32_t kNeeded = (T::kCols + 7) / 8 * 4;  // registers holding columns < kCols
+  constexpr uint32_t kDma = P > 16 ? 2 : 1;              // 16 planes per DMA
+  constexpr uint32_t kTile = 1024 * kDma;
+  constexpr uint32_t kDepth = 2;
+  constexpr uint32_t kStores = (kL + 1) / 2;  // fewest store instructions of 8 L bytes
+  __shared__ __attribute__((aligned(16))) int8_t lds[4 * kDepth * kTile];
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int8_t* const tiles = lds + wave * kDepth * kTile;
+  const uint32_t tiles_lds = lds_address(tiles);
+  const v4i wfrag = *reinterpret_cast<const v4i*>(kCrt<P>.frag[lane]);
+  uint32_t dma_off[kDma];
+#pragma unroll
+  for (uint32_t b = 0; b < kDma; ++b) {
+    const uint32_t k = 16u * b + (lane >> 2);
+    dma_off[b] = k < P ? k * static_cast<uint32_t>(a.pitch_c) + 16u * ((lane & 3u) ^ crt_swz(k)) : 0x80000000u;
+  }
+  // transpose-read addresses within a tile; with one DMA per tile the rows of
+  // planes 16..31 are not held, and those lanes re-read planes 0..15 (their
+  // weights are zero)
+  constexpr uint32_t kRowMask = kDma == 1 ? 15u : 31u;
+  const uint32_t tr_j = lane & 15u, tr_g = lane >> 4;
+  uint32_t rd_lo[2], rd_hi[2];
+#pragma unroll
+  for (uint32_t jb = 0; jb < 2; ++jb) {
+    const uint32_t ncol = 32u * jb + 16u * (tr_g & 1u) + 8u * (tr_j & 1u);
+    const uint32_t k = (16u * (tr_g >> 1) + (tr_j >> 1)) & kRowMask;
+    rd_lo[jb] = k * 64u + ((ncol >> 4) ^ crt_swz(k)) * 16u + (ncol & 8u);
+    rd_hi[jb] = (k + 8u) * 64u + ((ncol >> 4) ^ crt_swz(k + 8u)) * 16u + (ncol & 8u);
+  }
+  auto issue = [&](uint32_t u, uint32_t slot) {
+    const bool live = u < units;
+    const uint32_t uu = live ? u : 0u;
+    const uint32_t row = uu / chunks_per_row;
+    const int64_t start = static_cast<int64_t>(row) * a.ldc + static_cast<int64_t>(uu - row * chunks_per_row) * 64;
+    const v4i rsrc = buffer_rsrc(a.c + start, live ? static_cast<int64_t>(plane_span) - start : 0);
+#pragma unroll
+    for (uint32_t b = 0; b < kDma; ++b) dma16(tiles_lds + slot * kTile + 1024u * b, dma_off[b], rsrc);
+  };
+  const uint32_t first = blockIdx.x * 4u + wave, step = gridDim.x * 4u;
+  if (first >= units) return;
+  bool violation = false;
+#pragma unroll
+  for (uint32_t d = 0; d + 1 < kDepth; ++d) issue(first + d * step, d);
+  uint32_t it = 0;
+  for (uint32_t u = first; u < units; u += step, ++it) {
+    const uint32_t slot = it % kDepth;
+    issue(u + (kDepth - 1) * step, (it + kDepth - 1) % kDepth);
+    if constexpr (kStores == 0u) {
+      __builtin_amdgcn_s_waitcnt(wait_vm(0));
+    } else {
+      constexpr uint32_t kDmas = (kDepth - 1) * kDma;
+      static_assert(kDepth == 2, "the waits below cover one earlier iteration's stores");
+      if (it == 0)
+        __builtin_amdgcn_s_waitcnt(wait_vm(kDmas));
+      else
+        __builtin_amdgcn_s_waitcnt(wait_vm(kDmas + kStores));
+    }
+    const int8_t* const tile = tiles + slot * kTile;
+    const uint32_t row = u / chunks_per_row;
+    const int64_t c0 = static_cast<int64_t>(u - row * chunks_per_row) * 64;
+    v16i_crt acc[2];
+#pragma unroll
+    for (uint32_t jb = 0; jb < 2; ++jb) {
+      const v2i_crt lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_crt*)(tile + rd_lo[jb]));
+      const v2i_crt hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_crt*)(tile + rd_hi[jb]));
+      acc[jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wfrag, v4i{lo[0], lo[1], hi[0], hi[1]}, v16i_crt{}, 0, 0, 0);
+    }
+    // lanes 0-31 keep cell l's columns 8g+e and take its 8g+4+e from lanes
+    // 32-63; lanes 32-63 the reverse for cell l
+    int32_t s[32] = {};
+#pragma unroll
+    for (uint32_t r = 0; r < kNeeded; ++r) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(acc[0][r]),
+                                                       static_cast<uint32_t>(acc[1][r]), false, false);
+      s[8 * (r / 4) + r % 4] = static_cast<int32_t>(sw[0]);
+      s[8 * (r / 4) + 4 + r % 4] = static_cast<int32_t>(sw[1]);
+    }
+    uint32_t limb[T::kLimbs];
+    int32_t sign = 0;
+    crt_centered<P>(kCrt<P>, s, limb, sign);
+    const int64_t col = c0 + lane;
+    const bool valid = col < a.n;
+    const uint32_t sg16 = static_cast<uint32_t>(sign) & 0xFFFFu;
+    auto lm = [&](uint32_t j) { return j < T::kLimbs ? limb[j] : sg16; };
+    // stores through a buffer over the row's n cells: lanes past n are dropped
+    const uint32_t L = kL ? kL : a.limbs;
+    const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<uint64_t*>(a.dst) + static_cast<int64_t>(row) * a.ld * L, static_cast<short>(0),
+        static_cast<int>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a.n * 8 * L))), kBufferFlags);
+    const int out_off = static_cast<int>(static_cast<uint32_t>(col) * 8u * L);
+    constexpr uint32_t kND = (T::kLimbs + 1) / 2;
+    uint32_t d[kND];
+    uint32_t fill;
+    if constexpr (Kind == ExportKind::WIDE_SIGNED) {
+#pragma unroll
+      for (uint32_t q = 0; q < kND; ++q) d[q] = lm(2 * q) | (lm(2 * q + 1) << 16);
+      fill = static_cast<uint32_t>(sign);
+    } else {
+      uint32_t x[T::kLimbs];
+      int32_t cx = 0;
+#pragma unroll
+      for (uint32_t j = 0; j < T::kLimbs; ++j) {
+        const int32_t t =
+            static_cast<int32_t>(limb[j]) + (sign < 0 ? static_cast<int32_t>(kCrt<P>.m16[j]) : 0) + cx;
+        x[j] = static_cast<uint32_t>(t) & 0xFFFFu;
+        cx = t >> 16;
+      }
+#pragma unroll
+      for (uint32_t q = 0; q < kND; ++q)
+        d[q] = (2 * q < T::kLimbs ? x[2 * q] : 0u) | ((2 * q + 1 < T::kLimbs ? x[2 * q + 1] : 0u) << 16);
+      fill = 0u;
+    }
+    // fits in L limbs: signed, every bit from 64 L - 1 up repeats the sign;
+    // unsigned, every bit from 64 L up is zero
+    bool fits = true;
+#pragma unroll
+    for (uint32_t q = 0; q < kND; ++q) {
+      if (q >= 2 * L) fits &= d[q] == fill;
+      if (Kind == ExportKind::WIDE_SIGNED && q + 1 == 2 * L) fits &= (d[q] >> 31) == (fill & 1u);
+    }
+    violation |= valid && !fits;
+    auto store = [&](uint32_t l) {
+      const uint32_t lo = 2 * l < kND ? d[2 * l] : fill;
+      const uint32_t hi = 2 * l + 1 < kND ? d[2 * l + 1] : fill;
+      __builtin_amdgcn_raw_buffer_store_b64(v2u32_crt{lo, hi}, out, out_off + static_cast<int>(8 * l), 0, 0);
+    };
+    if constexpr (kL != 0) {
+#pragma unroll
+      for (uint32_t l = 0; l < kL; ++l) store(l);
+    } else {
+      for (uint32_t l = 0; l < L; ++l) store(l);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(wait_vm(0));  // no DMA outlives the wave's LDS
+  const uint64_t voters = __ballot(violation);
+  if (voters != 0 && lane == static_cast<uint32_t>(__ffsll(static_cast<long long>(voters)) - 1) &&
+      __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u)
+    atomicOr(a.status, 1u);
+}
+
 // Column groups of 4 cells x rows; rows beyond the grid's y extent are
 // covered by the row loop.
 dim3 grid_2d(uint32_t groups_per_row, int64_t rows) {
@@ -455,6 +649,46 @@ hipError_t launch_export_p(const ExportArgs& a, const ExportLimits& lim, hipStre
       break;
   }
   return hipGetLastError();
+}
+
+// The CRT-basis export of the exact-wide kinds, used when every plane byte it
+// reads lies within 2^31 of the first plane (31-bit buffer offsets, so
+// 0x80000000 marks the planes past P as out of range); export_kernel
+// otherwise.
+template <uint32_t P>
+hipError_t launch_crt_export_p(const ExportArgs& a, uint64_t plane_span, hipStream_t stream) {
+  const uint32_t chunks_per_row = static_cast<uint32_t>((a.n + 63) / 64);
+  const uint32_t units = static_cast<uint32_t>(a.m) * chunks_per_row;
+  const uint32_t blocks = (units + 3u) / 4u < 4096u ? (units + 3u) / 4u : 4096u;
+  auto go = [&](auto kind, auto limbs) {
+    hipLaunchKernelGGL((crt_export_kernel<P, decltype(kind)::value, decltype(limbs)::value>), dim3(blocks),
+                       dim3(256), 0, stream, a, chunks_per_row, units, plane_span);
+  };
+  using K = ExportKind;
+  auto wide = [&](auto kind) {
+    switch (a.limbs) {
+      case 1: go(kind, std::integral_constant<uint32_t, 1>{}); break;
+      case 2: go(kind, std::integral_constant<uint32_t, 2>{}); break;
+      case 3: go(kind, std::integral_constant<uint32_t, 3>{}); break;
+      case 4: go(kind, std::integral_constant<uint32_t, 4>{}); break;
+      default: go(kind, std::integral_constant<uint32_t, 0>{}); break;
+    }
+  };
+  if (a.kind == K::WIDE_SIGNED)
+    wide(std::integral_constant<K, K::WIDE_SIGNED>{});
+  else if (a.kind == K::WIDE_UNSIGNED)
+    wide(std::integral_constant<K, K::WIDE_UNSIGNED>{});
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+template <uint32_t... Ps>
+hipError_t dispatch_crt(uint32_t prefix, const ExportArgs& a, uint64_t plane_span, hipStream_t stream,
+                        std::integer_sequence<uint32_t, Ps...>) {
+  hipError_t err = hipErrorInvalidValue;
+  ((prefix == Ps + 1 ? (err = launch_crt_export_p<Ps + 1>(a, plane_span, stream), 0) : 0), ...);
+  return err;
 }
 
 template <uint32_t... Ps>
@@ -574,6 +808,13 @@ hipError_t launch_export(const ExportArgs& a, uint32_t prefix, hipStream_t strea
       }
       break;
   }
+  // bytes from the first plane's start to the end of the last plane's rows
+  const uint64_t plane_span = static_cast<uint64_t>(prefix - 1) * static_cast<uint64_t>(a.pitch_c) +
+                              static_cast<uint64_t>(a.m) * static_cast<uint64_t>(a.ldc);
+  const bool wide = a.kind == ExportKind::WIDE_SIGNED || a.kind == ExportKind::WIDE_UNSIGNED;
+  const bool crt = wide && plane_span < (uint64_t{1} << 31) && (reinterpret_cast<uintptr_t>(a.c) & 15u) == 0 &&
+                   (a.pitch_c % 16) == 0 && static_cast<uint64_t>(a.m) * ((a.n + 63) / 64) < (uint64_t{1} << 32);
+  if (crt) return dispatch_crt(prefix, a, plane_span, stream, std::make_integer_sequence<uint32_t, kMaxPrefix>{});
   return dispatch_prefix(prefix, a, lim, stream, std::make_integer_sequence<uint32_t, kMaxPrefix>{});
 }
 

@@ -15,6 +15,11 @@
 //   div       unit-index division: make_div_u31 over n < 2^31
 //   export64  the int64 / uint64 export tail at every prefix around the
 //             64-bit edges, against __int128 arithmetic
+//   crt       prints the CRT-basis export tables (crt_export.hpp) of every
+//             prefix, then reads residue vectors ("P r_0 .. r_{P-1}" lines)
+//             from stdin and prints the centered value the export tail
+//             computes from their column sums; tests/test_tables.py checks
+//             both against Python big integers
 // Exit status 0 and a final "ok" line when every check passes.
 #include <cinttypes>
 #include <cstdint>
@@ -24,6 +29,7 @@
 #include <utility>
 #include <vector>
 
+#include "crt_export.hpp"
 #include "tables.hpp"
 
 using namespace rns8x;
@@ -501,6 +507,58 @@ void check_div() {
 
 }  // namespace
 
+// ---- CRT-basis export (crt_export.hpp) ------------------------------------------
+
+template <uint32_t P>
+void crt_dump_table() {
+  constexpr CrtTable<P> t = make_crt_table<P>();
+  using T = CrtTable<P>;
+  std::printf("table %u %u %u %u\n", P, T::kBits, T::kDigits, T::kLimbs);
+  for (uint32_t i = 0; i < P; ++i) {
+    std::printf("w %u", i);
+    for (uint32_t c = 0; c < T::kCols; ++c) std::printf(" %d", static_cast<int>(t.w[i][c]));
+    std::printf("\n");
+  }
+  std::printf("m16");
+  for (uint32_t j = 0; j < T::kLimbs; ++j) std::printf(" %u", t.m16[j]);
+  std::printf("\n");
+  // the MFMA operand layout holds the same weights
+  for (uint32_t l = 0; l < 64; ++l)
+    for (uint32_t b = 0; b < 16; ++b) {
+      const uint32_t plane = 16 * (l >> 5) + b;
+      const int8_t want = plane < P ? t.w[plane][l & 31] : int8_t{0};
+      const int8_t got = static_cast<int8_t>((t.frag[l][b / 4] >> (8 * (b % 4))) & 0xFFu);
+      if (got != want) fail("crt fragment layout", P, l, b, got);
+    }
+}
+
+template <uint32_t P>
+void crt_value(const int* r) {
+  constexpr CrtTable<P> t = make_crt_table<P>();
+  using T = CrtTable<P>;
+  int32_t s[T::kCols] = {};
+  for (uint32_t c = 0; c < T::kCols; ++c)
+    for (uint32_t i = 0; i < P; ++i) s[c] += r[i] * static_cast<int32_t>(t.w[i][c]);
+  uint32_t limb[T::kLimbs] = {};
+  int32_t sign = 0;
+  crt_centered<P>(t, s, limb, sign);
+  std::printf("v %u %d", P, sign);
+  for (uint32_t j = 0; j < T::kLimbs; ++j) std::printf(" %u", limb[j]);
+  std::printf("\n");
+}
+
+template <uint32_t... Ps>
+void crt_all(std::integer_sequence<uint32_t, Ps...>) {
+  (crt_dump_table<Ps + 1>(), ...);
+  uint32_t p = 0;
+  while (std::scanf("%u", &p) == 1) {
+    int r[kMaxPrefix] = {};
+    for (uint32_t i = 0; i < p && i < kMaxPrefix; ++i)
+      if (std::scanf("%d", &r[i]) != 1) return;
+    ((p == Ps + 1 ? (crt_value<Ps + 1>(r), 0) : 0), ...);
+  }
+}
+
 int main(int argc, char** argv) {
   if (argc < 2) return 2;
   if (!std::strcmp(argv[1], "quot")) check_quot();
@@ -509,6 +567,7 @@ int main(int argc, char** argv) {
   else if (!std::strcmp(argv[1], "garner")) garner_dump();
   else if (!std::strcmp(argv[1], "div")) check_div();
   else if (!std::strcmp(argv[1], "export64")) export64_all(std::make_integer_sequence<uint32_t, kMaxPrefix>{});
+  else if (!std::strcmp(argv[1], "crt")) crt_all(std::make_integer_sequence<uint32_t, kMaxPrefix>{});
   else return 2;
   if (failures) {
     std::printf("failures %d\n", failures);

@@ -193,7 +193,7 @@ def test_finite_oneshot_matches_oracle(gpu_ctx, modulus, field):
     np.testing.assert_array_equal(C, want)
 
 
-@pytest.mark.parametrize("prefix,limbs", [(18, 3), (20, 3), (20, 4), (20, 1)])
+@pytest.mark.parametrize("prefix,limbs", [(18, 3), (20, 3), (20, 4), (20, 1), (20, 6), (18, 5)])
 def test_exact_wide_signed_limbs_match_oracle(gpu_ctx, prefix, limbs):
     m_, n_, k_ = 40, 24, 64
     A = rand_i64(21, (m_, k_))

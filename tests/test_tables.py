@@ -137,3 +137,95 @@ def test_garner_tables_and_digits(checker):
         elif key == "ok":
             pass
     assert cases == 64 * 20
+
+
+# ---- CRT-basis export (rns8_amd/csrc/crt_export.hpp) ---------------------------
+
+
+def _centered(x: int, m: int) -> int:
+    r = x % m
+    return r - m if r >= (m + 1) // 2 else r
+
+
+def _crt_vectors(P: int, M: int, rng) -> list:
+    """(residue vector, expected centered value) pairs: random centered
+    residues, arbitrary int8 residues, and integers at the edges of the
+    centered range [-M/2, M/2) and in the band 0.42 M .. 0.5 M where the
+    quotient estimate can be off by one."""
+    mods = LADDER[:P]
+    out = []
+
+    def add_x(x):
+        out.append(([_centered(x, m) for m in mods], (x + M // 2) % M - M // 2))
+
+    for x in (0, 1, -1, 2, -2, M // 2 - 1, -(M // 2), M // 2, -(M // 2) + 1, M // 2 - 2, (1 << 63) - 1, -(1 << 63),
+              (1 << 64) - 1, 1 << 63):
+        add_x(x)
+    for k in range(6):
+        add_x(M // 2 - 1 - k)
+        add_x(-(M // 2) + k)
+    for _ in range(120):
+        add_x(rng.randrange(-(M // 2), M // 2))
+    for _ in range(60):
+        mag = rng.randrange(M * 42 // 100, M // 2)
+        add_x(mag if rng.random() < 0.5 else -mag)
+    for _ in range(40):
+        r = [rng.randrange(-128, 128) for _ in mods]
+        # the class of an arbitrary residue vector, centered
+        x = 0
+        for i, (ri, mi) in enumerate(zip(r, mods)):
+            mi_rest = M // mi
+            x += ri * mi_rest * pow(mi_rest, -1, mi)
+        out.append((r, (x + M // 2) % M - M // 2))
+    return out
+
+
+def test_crt_export_tables_and_tail(checker):
+    """The MFMA export's tables and per-cell tail (crt_export.hpp), run on the
+    CPU by tables_check: the signed base-256 digits of every CRT basis
+    element K_i reconstruct K_i, the quotient digits F_i are within 1/2 of
+    2^14 K_i / M, M's 16-bit limbs are M, and for every prefix 1..20 the tail
+    turns the column sums of a residue vector into the centered value of its
+    class, checked against Python big integers on ~250 vectors per prefix
+    (range edges, the off-by-one band of the quotient estimate, arbitrary
+    int8 residues)."""
+    import random
+
+    rng = random.Random(77)
+    vectors = []
+    for P in range(1, 21):
+        M = math.prod(LADDER[:P])
+        vectors += [(P, r, v) for r, v in _crt_vectors(P, M, rng)]
+    text = "".join(f"{P} {' '.join(map(str, r))}\n" for P, r, _ in vectors)
+    res = subprocess.run([str(checker), "crt"], input=text, capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-2000:]
+    lines = res.stdout.split("\n")
+    assert lines[-2] == "ok"
+    tables, i = {}, 0
+    while lines[i].startswith("table"):
+        _, P, bits, digits, limbs = lines[i].split()
+        P, bits, digits, limbs = int(P), int(bits), int(digits), int(limbs)
+        w = [list(map(int, lines[i + 1 + t].split()[2:])) for t in range(P)]
+        m16 = list(map(int, lines[i + 1 + P].split()[1:]))
+        tables[P] = (bits, digits, limbs, w, m16)
+        i += P + 2
+    assert sorted(tables) == list(range(1, 21))
+    for P, (bits, digits, limbs, w, m16) in tables.items():
+        mods = LADDER[:P]
+        M = math.prod(mods)
+        assert bits == M.bit_length()
+        assert sum(v << (16 * j) for j, v in enumerate(m16)) == M
+        for t, m in enumerate(mods):
+            K = (M // m) * pow(M // m, -1, m) if P > 1 else 1
+            assert all(-128 <= d <= 127 for d in w[t])
+            assert sum(d * 256 ** b for b, d in enumerate(w[t][:digits])) == K
+            F = w[t][digits] + 256 * w[t][digits + 1]
+            assert abs(F * M - (K << 14)) * 2 <= M  # |F - 2^14 K / M| <= 1/2
+    outs = [ln for ln in lines[i:] if ln.startswith("v ")]
+    assert len(outs) == len(vectors)
+    for (P, r, want), ln in zip(vectors, outs):
+        parts = ln.split()
+        assert int(parts[1]) == P
+        sign, limbs_out = int(parts[2]), list(map(int, parts[3:]))
+        got = sum(v << (16 * j) for j, v in enumerate(limbs_out)) + sign * (1 << (16 * len(limbs_out)))
+        assert got == want, (P, r)
