@@ -19,10 +19,11 @@
 
 namespace rns8x {
 
-void copy_text(char* dst, std::size_t size, const std::string& src) {
+// no allocation: the getters that call it leave their outputs whole
+void copy_text(char* dst, std::size_t size, const char* src) {
   if (size == 0) return;
-  const std::size_t n = src.size() < size - 1 ? src.size() : size - 1;
-  std::memcpy(dst, src.data(), n);
+  const std::size_t n = src ? strnlen(src, size - 1) : 0;
+  if (n) std::memcpy(dst, src, n);
   dst[n] = '\0';
 }
 
@@ -525,12 +526,12 @@ rns8_status rns8_validate_default_moduli(void) {
 rns8_status rns8_mi355x_select_prefix(const rns8_gemm_desc* desc, uint32_t* out_prefix) {
   return guard([&]() -> rns8_status {
     if (!desc || !out_prefix) return RNS8_INVALID_ARGUMENT;
-    uint32_t budget = 0, selected = 0, required = 0, bits = 0;
-    uint64_t eff = 0;
-    const rns8_status st = plan_prefix(*desc, budget, selected, required, bits, eff);
+    // the whole of rns8_create_plan's validation, routing and schedule, so
+    // the status is the one rns8_create_plan returns for this descriptor
+    rns8_plan plan;
+    const rns8_status st = init_plan(*desc, RNS8_BACKEND_HIP_DIRECT, plan);
     if (st != RNS8_SUCCESS) return st;
-    if (desc->semantics == RNS8_WRAP_U64_MOD_2_64) return RNS8_UNSUPPORTED_BACKEND;
-    *out_prefix = selected;
+    *out_prefix = plan.prefix;
     return RNS8_SUCCESS;
   });
 }
@@ -737,10 +738,17 @@ rns8_status rns8_create_plan(rns8_context* ctx, const rns8_gemm_desc* desc, rns8
     *out = nullptr;
     auto* plan = new (std::nothrow) rns8_plan();
     if (!plan) return RNS8_INTERNAL_ERROR;
-    rns8_status st = init_plan(*desc, ctx->backend, *plan);
-    plan->device_id = ctx->device_id;
-    if (st == RNS8_SUCCESS && per_tile(plan->desc.bound_kind))
-      st = hipSetDevice(ctx->device_id) == hipSuccess ? upload_tile_lists(*plan, ctx->stream) : RNS8_BACKEND_FAILURE;
+    rns8_status st;
+    try {
+      st = init_plan(*desc, ctx->backend, *plan);
+      plan->device_id = ctx->device_id;
+      if (st == RNS8_SUCCESS && per_tile(plan->desc.bound_kind))
+        st = hipSetDevice(ctx->device_id) == hipSuccess ? upload_tile_lists(*plan, ctx->stream) : RNS8_BACKEND_FAILURE;
+    } catch (...) {
+      free_tile_lists(*plan);
+      delete plan;
+      throw;
+    }
     if (st != RNS8_SUCCESS) {
       free_tile_lists(*plan);
       delete plan;

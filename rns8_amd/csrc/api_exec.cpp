@@ -12,6 +12,7 @@
 // host entry points synchronize before returning, like the reference.
 #include <algorithm>
 #include <cstring>
+#include <exception>
 #include <limits>
 #include <thread>
 #include <vector>
@@ -580,6 +581,11 @@ rns8_status gemm_grouped(rns8_context* ctx, const rns8_plan* plan, const rns8_gr
       pendings[i] = pending ? 1 : 0;
     }
 
+  // every host allocation comes before the first change to a result
+  std::vector<TaskPtrs> ptrs(task_count);
+  for (uint32_t i = 0; i < task_count; ++i)
+    ptrs[i] = TaskPtrs{tasks[i].a->planes, tasks[i].b->planes, tasks[i].c->planes,
+                       plan->splitk_slices > 1 ? tasks[i].workspace->splitk : nullptr};
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
   if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
   for (uint32_t i = 0; i < task_count; ++i) tasks[i].c->device_current = false;
@@ -603,10 +609,6 @@ rns8_status gemm_grouped(rns8_context* ctx, const rns8_plan* plan, const rns8_gr
     g.pitch_c = c0.plane_pitch;
     g.nplanes = finite ? 1u : plan->prefix;
     g.slices = plan->splitk_slices;
-    std::vector<TaskPtrs> ptrs(task_count);
-    for (uint32_t i = 0; i < task_count; ++i)
-      ptrs[i] = TaskPtrs{tasks[i].a->planes, tasks[i].b->planes, tasks[i].c->planes,
-                         plan->splitk_slices > 1 ? tasks[i].workspace->splitk : nullptr};
     const PlaneConsts consts = finite ? make_single_plane_consts(modulus) : make_ladder_plane_consts(plan->prefix);
     const hipError_t e = launch_gemm_grouped(g, consts, ptrs.data(), task_count, stream);
     st = e == hipSuccess ? RNS8_SUCCESS : e == hipErrorInvalidValue ? RNS8_UNSUPPORTED_BACKEND : RNS8_BACKEND_FAILURE;
@@ -822,6 +824,15 @@ rns8_status oneshot_state(rns8_context* ctx, const rns8_gemm_desc& desc, Oneshot
   return RNS8_SUCCESS;
 }
 
+// A oneshot call that ends in an exception (an allocation failure, caught at
+// the API boundary) keeps no cached state either.
+struct KeepOneshotOnSuccess {
+  rns8_context* ctx;
+  ~KeepOneshotOnSuccess() {
+    if (std::uncaught_exceptions() > 0) release_oneshot_cache(*ctx);
+  }
+};
+
 // reference api_oneshot.cpp:440-466
 rns8_status typed_oneshot_contract(const rns8_context& ctx, const rns8_gemm_desc& desc, rns8_semantics expected,
                                    int64_t lda, int64_t ldb, int64_t ldc) {
@@ -867,6 +878,7 @@ rns8_status bounded_oneshot(rns8_context* ctx, const rns8_gemm_desc* desc, const
   OneshotState* sp = nullptr;
   rns8_status st = oneshot_state(ctx, *desc, sp);
   if (st != RNS8_SUCCESS) return st;
+  const KeepOneshotOnSuccess keep{ctx};
   OneshotState& s = *sp;
   st = pack_native<T>(ctx, s.A, A, lda, 0, Source::Host, nullptr);
   if (st == RNS8_SUCCESS) st = pack_native<T>(ctx, s.B, B, ldb, 0, Source::Host, nullptr);
@@ -891,6 +903,7 @@ rns8_status finite_oneshot(rns8_context* ctx, const rns8_gemm_desc* desc, rns8_s
   OneshotState* sp = nullptr;
   rns8_status st = oneshot_state(ctx, *desc, sp);
   if (st != RNS8_SUCCESS) return st;
+  const KeepOneshotOnSuccess keep{ctx};
   OneshotState& s = *sp;
   st = pack_u8(ctx, s.A, modulus, A, lda, 0, Source::Host, nullptr);
   if (st == RNS8_SUCCESS) st = pack_u8(ctx, s.B, modulus, B, ldb, 0, Source::Host, nullptr);

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "rns8/rns8.h"
+#include "shards.hpp"
 #include "wide_int.hpp"
 
 // Exact-wide per-axis magnitude summary (reference src/core/internal.hpp:72-86
@@ -165,13 +166,7 @@ inline rns8_status exact_product_range(rns8_semantics semantics, int64_t m, int6
         }
       }
     };
-    if (nt == 1) {
-      work(0);
-    } else {
-      std::vector<std::thread> pool;
-      for (unsigned t = 0; t < nt; ++t) pool.emplace_back(work, t);
-      for (auto& th : pool) th.join();
-    }
+    run_shards(nt, work);
     I512 maximum;
     for (unsigned t = 0; t < nt; ++t) {
       maximum = imax(maximum, maxima[t]);

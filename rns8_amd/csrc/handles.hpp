@@ -159,7 +159,7 @@ inline bool valid_abi(uint64_t struct_size, uint32_t abi_version, std::size_t ex
   return abi_version == RNS8_ABI_VERSION && struct_size >= expected;
 }
 
-void copy_text(char* dst, std::size_t size, const std::string& src);
+void copy_text(char* dst, std::size_t size, const char* src);
 
 // out-struct helper: keep caller's size/version, zero the rest
 template <typename T>

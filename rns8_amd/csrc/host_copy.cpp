@@ -6,6 +6,8 @@
 #include <thread>
 #include <vector>
 
+#include "shards.hpp"
+
 namespace rns8x {
 namespace {
 
@@ -54,14 +56,11 @@ void copy_piece(const Piece& p, char* packed, char* strided, std::size_t pitch, 
     run(p.row0, p.row0 + p.nrows);
     return;
   }
-  std::vector<std::thread> pool;
   const int64_t per = (p.nrows + threads - 1) / threads;
-  for (int64_t t = 1; t < threads; ++t) {
+  run_shards(static_cast<unsigned>(threads), [&](unsigned t) {
     const int64_t r0 = p.row0 + t * per, r1 = std::min(p.row0 + p.nrows, r0 + per);
-    if (r0 < r1) pool.emplace_back(run, r0, r1);
-  }
-  run(p.row0, std::min(p.row0 + p.nrows, p.row0 + per));
-  for (auto& th : pool) th.join();
+    if (r0 < r1) run(r0, r1);
+  });
 }
 
 }  // namespace

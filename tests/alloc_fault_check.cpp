@@ -1,0 +1,793 @@
+// Allocation-failure injection over the library's host layer (librns8.so),
+// after the reference's tests/support/allocation_fault.cpp:18-118 and
+// tests/unit/test_exact_cpu_allocation_faults.cpp:247-300: every allocation
+// the library makes during one API call is failed in turn, and each failure
+// must come back through the C API with nothing committed.
+//
+// Allocation points are the calls the library itself makes (the caller's
+// return address lies in librns8.so) to
+//   * operator new / new[] (all forms): an injected failure throws
+//     std::bad_alloc, or returns null for the nothrow forms, and must come
+//     back as RNS8_INTERNAL_ERROR;
+//   * hipMalloc, hipHostMalloc and hipEventCreateWithFlags, interposed here
+//     (the executable's definitions bind first, and the real ones are reached
+//     through dlsym(RTLD_NEXT)): an injected failure returns
+//     hipErrorOutOfMemory and must come back as RNS8_BACKEND_FAILURE.
+// Allocations of the HIP runtime and of this program are never failed, so
+// the runtime is never left half-way through an operation.
+//
+// For every scenario: a profile run counts the points (twice: the count must
+// repeat), then for each point the state is restored, the call is made with
+// that point failing, and the checks are: the expected status, no allocation
+// of either kind outlives the call, outputs and handles are as before (out
+// handles null, destination sentinels intact, matrices export their old
+// values with unchanged storage info), and a retry succeeds with the right
+// result. The one failure the library absorbs instead is a helper thread
+// that cannot start (its shard runs on the calling thread): such a call must
+// succeed with the right result. Buffers a matrix or context keeps between
+// calls (upload and staging buffers, pinned host chunks) are created by the
+// scenario's set-up, so the points are the allocations each call makes.
+//
+//   alloc_fault_check host     device-free entries (no GPU needed)
+//   alloc_fault_check device   entries that need a context (GPU)
+#include <dlfcn.h>
+#include <link.h>
+
+#include <atomic>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "rns8/rns8.h"
+#include "rns8_mi355x.h"
+
+extern "C" {
+typedef int hipError_t;
+typedef struct ihipEvent_t* hipEvent_t;
+hipError_t hipMalloc(void** ptr, size_t size);
+hipError_t hipFree(void* ptr);
+hipError_t hipHostMalloc(void** ptr, size_t size, unsigned int flags);
+hipError_t hipHostFree(void* ptr);
+hipError_t hipEventCreateWithFlags(hipEvent_t* event, unsigned flags);
+hipError_t hipEventDestroy(hipEvent_t event);
+}
+
+namespace {
+
+constexpr hipError_t kHipOutOfMemory = 2;
+
+// ---- the library's code range ------------------------------------------------------
+
+uintptr_t g_lib_lo = 0, g_lib_hi = 0;
+
+int find_library(struct dl_phdr_info* info, size_t, void*);
+
+bool from_library(const void* ret) {
+  const auto a = reinterpret_cast<uintptr_t>(ret);
+  return a >= g_lib_lo && a < g_lib_hi;
+}
+
+// ---- injection state ---------------------------------------------------------------
+
+enum Kind : int { HOST = 1, DEVICE = 2 };
+
+std::atomic<bool> g_active{false};
+std::atomic<long> g_calls{0};
+std::atomic<long> g_fail_at{-1};
+std::atomic<int> g_triggered{0};      // Kind of the failed point, 0 if none
+std::atomic<long> g_live_host{0};     // library operator-new blocks alive
+std::atomic<long> g_live_device{0};   // library hipMalloc/hipHostMalloc/event objects alive
+
+// true: fail this allocation
+bool inject(const void* caller, Kind kind) {
+  if (!g_active.load(std::memory_order_relaxed) || !from_library(caller)) return false;
+  const long idx = g_calls.fetch_add(1);
+  if (idx == g_fail_at.load()) {
+    g_triggered.store(kind);
+    return true;
+  }
+  return false;
+}
+
+// ---- operator new / delete with a header recording library ownership -------------
+
+struct alignas(std::max_align_t) Header {
+  void* base;
+  uint64_t counted;
+};
+
+void* allocate(std::size_t bytes, std::size_t alignment, const void* caller, bool nothrow) {
+  const bool lib = from_library(caller);
+  if (inject(caller, HOST)) {
+    if (nothrow) return nullptr;
+    throw std::bad_alloc();
+  }
+  const std::size_t size = bytes == 0 ? 1 : bytes;
+  if (alignment < alignof(Header)) alignment = alignof(Header);
+  void* base = std::malloc(size + sizeof(Header) + alignment);
+  if (!base) {
+    if (nothrow) return nullptr;
+    throw std::bad_alloc();
+  }
+  const auto start = reinterpret_cast<uintptr_t>(base) + sizeof(Header);
+  const auto address = (start + alignment - 1) & ~(static_cast<uintptr_t>(alignment) - 1);
+  auto* h = reinterpret_cast<Header*>(address - sizeof(Header));
+  h->base = base;
+  h->counted = lib && g_active.load() ? 1u : 0u;
+  if (h->counted) g_live_host.fetch_add(1);
+  return reinterpret_cast<void*>(address);
+}
+
+void release(void* p) noexcept {
+  if (!p) return;
+  auto* h = reinterpret_cast<Header*>(static_cast<char*>(p) - sizeof(Header));
+  if (h->counted) g_live_host.fetch_sub(1);
+  std::free(h->base);
+}
+
+// ---- device allocations ------------------------------------------------------------
+
+std::mutex g_dev_mu;
+std::map<void*, int>* g_dev_live = nullptr;  // pointers the library allocated while active
+
+template <typename F>
+F real(const char* name) {
+  static std::mutex mu;
+  std::lock_guard<std::mutex> lock(mu);
+  void* sym = dlsym(RTLD_NEXT, name);
+  if (!sym) {
+    std::fprintf(stderr, "FAILED: no %s to forward to\n", name);
+    std::_Exit(3);
+  }
+  return reinterpret_cast<F>(sym);
+}
+
+void track(void* p) {
+  std::lock_guard<std::mutex> lock(g_dev_mu);
+  if (!g_dev_live) g_dev_live = new std::map<void*, int>();
+  (*g_dev_live)[p] = 1;
+  g_live_device.fetch_add(1);
+}
+
+void untrack(void* p) {
+  std::lock_guard<std::mutex> lock(g_dev_mu);
+  if (g_dev_live && g_dev_live->erase(p)) g_live_device.fetch_sub(1);
+}
+
+}  // namespace
+
+// ---- interposed entry points -------------------------------------------------------
+
+void* operator new(std::size_t n) { return allocate(n, alignof(std::max_align_t), __builtin_return_address(0), false); }
+void* operator new[](std::size_t n) {
+  return allocate(n, alignof(std::max_align_t), __builtin_return_address(0), false);
+}
+void* operator new(std::size_t n, const std::nothrow_t&) noexcept {
+  return allocate(n, alignof(std::max_align_t), __builtin_return_address(0), true);
+}
+void* operator new[](std::size_t n, const std::nothrow_t&) noexcept {
+  return allocate(n, alignof(std::max_align_t), __builtin_return_address(0), true);
+}
+void* operator new(std::size_t n, std::align_val_t a) {
+  return allocate(n, static_cast<std::size_t>(a), __builtin_return_address(0), false);
+}
+void* operator new[](std::size_t n, std::align_val_t a) {
+  return allocate(n, static_cast<std::size_t>(a), __builtin_return_address(0), false);
+}
+void* operator new(std::size_t n, std::align_val_t a, const std::nothrow_t&) noexcept {
+  return allocate(n, static_cast<std::size_t>(a), __builtin_return_address(0), true);
+}
+void* operator new[](std::size_t n, std::align_val_t a, const std::nothrow_t&) noexcept {
+  return allocate(n, static_cast<std::size_t>(a), __builtin_return_address(0), true);
+}
+void operator delete(void* p) noexcept { release(p); }
+void operator delete[](void* p) noexcept { release(p); }
+void operator delete(void* p, std::size_t) noexcept { release(p); }
+void operator delete[](void* p, std::size_t) noexcept { release(p); }
+void operator delete(void* p, std::align_val_t) noexcept { release(p); }
+void operator delete[](void* p, std::align_val_t) noexcept { release(p); }
+void operator delete(void* p, std::size_t, std::align_val_t) noexcept { release(p); }
+void operator delete[](void* p, std::size_t, std::align_val_t) noexcept { release(p); }
+void operator delete(void* p, const std::nothrow_t&) noexcept { release(p); }
+void operator delete[](void* p, const std::nothrow_t&) noexcept { release(p); }
+
+extern "C" hipError_t hipMalloc(void** ptr, size_t size) {
+  static auto fn = real<hipError_t (*)(void**, size_t)>("hipMalloc");
+  const void* caller = __builtin_return_address(0);
+  if (inject(caller, DEVICE)) return kHipOutOfMemory;
+  const hipError_t e = fn(ptr, size);
+  if (e == 0 && from_library(caller) && g_active.load()) track(*ptr);
+  return e;
+}
+
+extern "C" hipError_t hipFree(void* ptr) {
+  static auto fn = real<hipError_t (*)(void*)>("hipFree");
+  if (ptr) untrack(ptr);
+  return fn(ptr);
+}
+
+extern "C" hipError_t hipHostMalloc(void** ptr, size_t size, unsigned int flags) {
+  static auto fn = real<hipError_t (*)(void**, size_t, unsigned int)>("hipHostMalloc");
+  const void* caller = __builtin_return_address(0);
+  if (inject(caller, DEVICE)) return kHipOutOfMemory;
+  const hipError_t e = fn(ptr, size, flags);
+  if (e == 0 && from_library(caller) && g_active.load()) track(*ptr);
+  return e;
+}
+
+extern "C" hipError_t hipHostFree(void* ptr) {
+  static auto fn = real<hipError_t (*)(void*)>("hipHostFree");
+  if (ptr) untrack(ptr);
+  return fn(ptr);
+}
+
+extern "C" hipError_t hipEventCreateWithFlags(hipEvent_t* event, unsigned flags) {
+  static auto fn = real<hipError_t (*)(hipEvent_t*, unsigned)>("hipEventCreateWithFlags");
+  const void* caller = __builtin_return_address(0);
+  if (inject(caller, DEVICE)) return kHipOutOfMemory;
+  const hipError_t e = fn(event, flags);
+  if (e == 0 && from_library(caller) && g_active.load()) track(*event);
+  return e;
+}
+
+extern "C" hipError_t hipEventDestroy(hipEvent_t event) {
+  static auto fn = real<hipError_t (*)(hipEvent_t)>("hipEventDestroy");
+  if (event) untrack(event);
+  return fn(event);
+}
+
+namespace {
+
+int find_library(struct dl_phdr_info* info, size_t, void*) {
+  if (!info->dlpi_name || !std::strstr(info->dlpi_name, "librns8.so")) return 0;
+  for (int i = 0; i < info->dlpi_phnum; ++i) {
+    const auto& ph = info->dlpi_phdr[i];
+    if (ph.p_type == PT_LOAD && (ph.p_flags & PF_X)) {
+      g_lib_lo = info->dlpi_addr + ph.p_vaddr;
+      g_lib_hi = g_lib_lo + ph.p_memsz;
+    }
+  }
+  return 1;
+}
+
+// ---- harness -----------------------------------------------------------------------
+
+const char* g_case = "setup";
+
+[[noreturn]] void fail(const char* what, long point = -1) {
+  std::fprintf(stderr, "FAILED: case=%s point=%ld: %s\n", g_case, point, what);
+  std::exit(2);
+}
+
+void require(bool ok, const char* what, long point = -1) {
+  if (!ok) fail(what, point);
+}
+
+struct Scenario {
+  const char* name;
+  std::function<void()> restore;            // bring inputs/outputs to the pre-call state
+  std::function<rns8_status()> call;        // the API call under test
+  std::function<void(long)> verify_same;    // after a failure: nothing committed
+  std::function<void(long)> verify_result;  // after a success: the right result
+};
+
+long exercise(Scenario& s) {
+  g_case = s.name;
+  long counts[2] = {0, 0};
+  for (int rep = 0; rep < 2; ++rep) {
+    s.restore();
+    g_calls = 0;
+    g_fail_at = -1;
+    g_triggered = 0;
+    g_active = true;
+    const rns8_status st = s.call();
+    g_active = false;
+    if (st != RNS8_SUCCESS) {
+      std::fprintf(stderr, "status %d\n", static_cast<int>(st));
+      fail("profile run succeeds");
+    }
+    require(g_triggered.load() == 0, "profile run injects nothing");
+    s.verify_result(-1);
+    counts[rep] = g_calls.load();
+  }
+  require(counts[0] == counts[1], "repeatable allocation profile");
+  long absorbed = 0;
+  require(counts[0] <= 4096, "bounded allocation points");
+  for (long point = 0; point < counts[0]; ++point) {
+    s.restore();
+    const long host0 = g_live_host.load(), dev0 = g_live_device.load();
+    g_calls = 0;
+    g_fail_at = point;
+    g_triggered = 0;
+    g_active = true;
+    const rns8_status st = s.call();
+    g_active = false;
+    const int kind = g_triggered.load();
+    require(kind != 0, "the point is reached again", point);
+    if (st == RNS8_SUCCESS) {
+      // absorbed: a helper thread that could not start, whose shard ran on
+      // the calling thread; the call must still be complete and right
+      s.verify_result(point);
+      ++absorbed;
+      continue;
+    }
+    const rns8_status want = kind == HOST ? RNS8_INTERNAL_ERROR : RNS8_BACKEND_FAILURE;
+    if (st != want) {
+      std::fprintf(stderr, "case=%s point=%ld kind=%d status=%d\n", s.name, point, kind, static_cast<int>(st));
+      fail("an injected failure comes back through the C API", point);
+    }
+    require(g_live_host.load() == host0, "no library operator-new block outlives a failed call", point);
+    require(g_live_device.load() == dev0, "no device/pinned allocation or event outlives a failed call", point);
+    s.verify_same(point);
+    // recoverable: the same call succeeds afterwards
+    s.restore();
+    require(s.call() == RNS8_SUCCESS, "retry after the failure succeeds", point);
+    s.verify_result(point);
+  }
+  std::printf("case=%s allocation_points=%ld absorbed=%ld\n", s.name, counts[0], absorbed);
+  return counts[0];
+}
+
+template <typename T>
+T abi_struct() {
+  T v;
+  std::memset(&v, 0, sizeof(v));
+  v.struct_size = sizeof(T);
+  v.abi_version = RNS8_ABI_VERSION;
+  return v;
+}
+
+rns8_gemm_desc gemm_desc(rns8_semantics sem, rns8_bound_kind bk, int64_t m, int64_t n, int64_t k, uint32_t prefix) {
+  auto d = abi_struct<rns8_gemm_desc>();
+  d.semantics = sem;
+  d.bound_kind = bk;
+  d.requested_backend = RNS8_BACKEND_AUTO;
+  d.m = m;
+  d.n = n;
+  d.k = k;
+  d.max_prefix = prefix;
+  d.flags = prefix ? RNS8_PLAN_FORCE_FIXED_PREFIX : 0;
+  return d;
+}
+
+rns8_matrix_desc matrix_desc(rns8_semantics sem, rns8_bound_kind bk, int64_t rows, int64_t cols, uint32_t prefix) {
+  auto d = abi_struct<rns8_matrix_desc>();
+  d.semantics = sem;
+  d.bound_kind = bk;
+  d.rows = rows;
+  d.cols = cols;
+  d.logical_ld = cols;
+  d.logical_layout = RNS8_LAYOUT_ROW_MAJOR;
+  d.max_prefix = prefix;
+  return d;
+}
+
+void check_ok(rns8_status st, const char* what) {
+  if (st != RNS8_SUCCESS) {
+    std::fprintf(stderr, "%s: status %d\n", what, static_cast<int>(st));
+    fail(what);
+  }
+}
+
+// splitmix64 test values
+uint64_t mix(uint64_t& s) {
+  uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// ---- device-free entries -----------------------------------------------------------
+
+long run_host() {
+  long total = 0;
+  // per-tile schedule: 4 x 4 tiles of 64, bounds and zero masks
+  {
+    const int64_t m = 256, n = 256, k = 96;
+    std::vector<uint64_t> bounds(16);
+    for (std::size_t t = 0; t < bounds.size(); ++t) bounds[t] = (uint64_t{1} << (8 + 3 * t)) - 1;
+    std::vector<uint8_t> zero_rows(m, 0), zero_cols(n, 0);
+    for (int64_t r = 0; r < 64; ++r) zero_rows[r] = 1;
+    auto desc = gemm_desc(RNS8_BOUNDED_I64, RNS8_BOUND_PER_TILE_MAX_ABS, m, n, k, 0);
+    desc.flags = RNS8_PLAN_ALLOW_PROVEN_ZERO_ROW_COL_SKIPS | RNS8_PLAN_ALLOW_PROVEN_ZERO_TILE_SKIPS;
+    desc.tile_m = 64;
+    desc.tile_n = 64;
+    desc.tile_bounds = bounds.data();
+    desc.tile_bounds_count = bounds.size();
+    desc.zero_a_rows = zero_rows.data();
+    desc.zero_a_rows_count = zero_rows.size();
+    desc.zero_b_cols = zero_cols.data();
+    desc.zero_b_cols_count = zero_cols.size();
+    auto info = abi_struct<rns8_plan_schedule_info>();
+    std::vector<rns8_plan_tile_schedule_entry> entries(16), want(16);
+    uint64_t written = 0;
+    rns8_plan_schedule_info want_info = abi_struct<rns8_plan_schedule_info>(), sentinel_info{};
+    uint64_t want_written = 0;
+    check_ok(rns8_mi355x_plan_schedule(&desc, &want_info, want.data(), want.size(), &want_written), "reference schedule");
+    Scenario s{"plan_schedule/per-tile",
+               [&] {
+                 info = abi_struct<rns8_plan_schedule_info>();
+                 info.tile_count = 0xA5A5;
+                 sentinel_info = info;
+                 std::memset(entries.data(), 0x5A, entries.size() * sizeof(entries[0]));
+                 written = 0xA5A5;
+               },
+               [&] { return rns8_mi355x_plan_schedule(&desc, &info, entries.data(), entries.size(), &written); },
+               [&](long point) {
+                 require(written == 0xA5A5, "written untouched", point);
+                 require(std::memcmp(&info, &sentinel_info, sizeof(info)) == 0, "info untouched", point);
+                 for (const auto& e : entries) {
+                   const auto* b = reinterpret_cast<const uint8_t*>(&e);
+                   for (std::size_t i = 0; i < sizeof(e); ++i) require(b[i] == 0x5A, "entries untouched", point);
+                 }
+               },
+               [&](long point) {
+                 require(written == want_written, "written", point);
+                 require(std::memcmp(&info, &want_info, sizeof(info)) == 0, "schedule info", point);
+                 require(std::memcmp(entries.data(), want.data(), entries.size() * sizeof(entries[0])) == 0,
+                         "schedule entries", point);
+               }};
+    total += exercise(s);
+  }
+  {
+    auto desc = gemm_desc(RNS8_EXACT_WIDE_SIGNED, RNS8_BOUND_NONE, 64, 64, 4096, 0);
+    uint32_t prefix = 0;
+    Scenario s{"select_prefix/exact-wide", [&] { prefix = 777; }, [&] { return rns8_mi355x_select_prefix(&desc, &prefix); },
+               [&](long point) { require(prefix == 777, "prefix untouched", point); },
+               [&](long point) { require(prefix >= 17 && prefix <= 20, "prefix", point); }};
+    total += exercise(s);
+  }
+  return total;
+}
+
+// ---- entries that need a context ---------------------------------------------------
+
+struct Ctx {
+  rns8_context* ctx = nullptr;
+  Ctx() {
+    auto opts = abi_struct<rns8_context_options>();
+    opts.requested_backend = RNS8_BACKEND_AUTO;
+    check_ok(rns8_create_context(0, &opts, &ctx), "create context");
+  }
+  ~Ctx() { rns8_destroy_context(ctx); }
+};
+
+rns8_plan* make_plan(rns8_context* ctx, const rns8_gemm_desc& d) {
+  rns8_plan* p = nullptr;
+  check_ok(rns8_create_plan(ctx, &d, &p), "create plan");
+  return p;
+}
+
+rns8_matrix* make_matrix(rns8_context* ctx, const rns8_matrix_desc& d) {
+  rns8_matrix* m = nullptr;
+  check_ok(rns8_create_matrix(ctx, &d, &m), "create matrix");
+  return m;
+}
+
+rns8_matrix_storage_info storage(const rns8_matrix* m) {
+  auto info = abi_struct<rns8_matrix_storage_info>();
+  check_ok(rns8_get_matrix_storage_info(m, &info), "storage info");
+  return info;
+}
+
+bool same_storage(const rns8_matrix_storage_info& a, const rns8_matrix_storage_info& b) {
+  return std::memcmp(&a, &b, sizeof(a)) == 0;
+}
+
+// exact signed product of int64 matrices, as 3 limbs (two's complement, 192 bits)
+std::vector<uint64_t> exact3(const std::vector<int64_t>& A, const std::vector<int64_t>& B, int64_t m, int64_t n,
+                             int64_t k) {
+  std::vector<uint64_t> out(static_cast<std::size_t>(m * n * 3));
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) {
+      uint64_t w[3] = {0, 0, 0};  // 192-bit two's complement sum of the k products
+      for (int64_t t = 0; t < k; ++t) {
+        const __int128 p = static_cast<__int128>(A[i * k + t]) * B[t * n + j];
+        const uint64_t plo = static_cast<uint64_t>(p), phi = static_cast<uint64_t>(p >> 64);
+        const uint64_t ext = p < 0 ? ~0ull : 0ull;
+        unsigned __int128 s0 = static_cast<unsigned __int128>(w[0]) + plo;
+        unsigned __int128 s1 = static_cast<unsigned __int128>(w[1]) + phi + static_cast<uint64_t>(s0 >> 64);
+        w[0] = static_cast<uint64_t>(s0);
+        w[1] = static_cast<uint64_t>(s1);
+        w[2] = w[2] + ext + static_cast<uint64_t>(s1 >> 64);
+      }
+      for (int l = 0; l < 3; ++l) out[static_cast<std::size_t>((i * n + j) * 3 + l)] = w[l];
+    }
+  return out;
+}
+
+long run_device() {
+  long total = 0;
+  {
+    rns8_context* out = nullptr;
+    auto opts = abi_struct<rns8_context_options>();
+    opts.requested_backend = RNS8_BACKEND_AUTO;
+    Scenario s{"create_context",
+               [&] {
+                 if (out) rns8_destroy_context(out);
+                 out = reinterpret_cast<rns8_context*>(0x1);
+               },
+               [&] { return rns8_create_context(0, &opts, &out); },
+               [&](long point) { require(out == nullptr, "out handle null", point); },
+               [&](long point) { require(out != nullptr, "context created", point); }};
+    total += exercise(s);
+    if (out) rns8_destroy_context(out);
+  }
+  Ctx c;
+  rns8_context* ctx = c.ctx;
+  const int64_t m = 48, n = 40, k = 70;
+  const uint32_t P = 20;
+  uint64_t seed = 12345;
+  std::vector<int64_t> A(m * k), B(k * n), A2(m * k);
+  for (auto& v : A) v = static_cast<int64_t>(mix(seed));
+  for (auto& v : B) v = static_cast<int64_t>(mix(seed));
+  for (auto& v : A2) v = static_cast<int64_t>(mix(seed)) >> 3;
+  const auto want = exact3(A, B, m, n, k);
+  const auto want2 = exact3(A2, B, m, n, k);
+  const auto sem = RNS8_EXACT_WIDE_SIGNED;
+  const auto gdesc = gemm_desc(sem, RNS8_BOUND_NONE, m, n, k, P);
+  rns8_plan* plan = make_plan(ctx, gdesc);
+  rns8_matrix* Am = make_matrix(ctx, matrix_desc(sem, RNS8_BOUND_NONE, m, k, P));
+  rns8_matrix* Bm = make_matrix(ctx, matrix_desc(sem, RNS8_BOUND_NONE, k, n, P));
+  rns8_matrix* Cm = make_matrix(ctx, matrix_desc(sem, RNS8_BOUND_NONE, m, n, P));
+  rns8_workspace* ws = nullptr;
+  check_ok(rns8_create_workspace(ctx, plan, &ws), "create workspace");
+  auto export3 = [&](const rns8_matrix* M, int64_t rows, int64_t cols) {
+    std::vector<uint64_t> out(static_cast<std::size_t>(rows * cols * 3), 0);
+    check_ok(rns8_export_exact_wide_signed_limbs(ctx, plan, M, out.data(), cols, 3), "export");
+    return out;
+  };
+  auto to_limbs = [](const std::vector<int64_t>& v) {
+    std::vector<uint64_t> out(v.size() * 3);
+    for (std::size_t i = 0; i < v.size(); ++i) {
+      out[3 * i] = static_cast<uint64_t>(v[i]);
+      out[3 * i + 1] = out[3 * i + 2] = v[i] < 0 ? ~0ull : 0ull;
+    }
+    return out;
+  };
+  // A as an m x k result of the plan's shape is not exportable through `plan`
+  // (m x n); check A through a product instead where needed
+
+  // create_plan with per-tile bounds (device tile lists)
+  {
+    std::vector<uint64_t> bounds(16, (uint64_t{1} << 20) - 1);
+    auto d = gemm_desc(RNS8_BOUNDED_I64, RNS8_BOUND_PER_TILE_MAX_ABS, 256, 256, 64, 0);
+    d.tile_m = d.tile_n = 64;
+    d.tile_bounds = bounds.data();
+    d.tile_bounds_count = bounds.size();
+    rns8_plan* out = nullptr;
+    Scenario s{"create_plan/per-tile",
+               [&] {
+                 if (out) rns8_destroy_plan(out);
+                 out = reinterpret_cast<rns8_plan*>(0x1);
+               },
+               [&] { return rns8_create_plan(ctx, &d, &out); },
+               [&](long point) {
+                 require(out == nullptr, "out handle null", point);
+               },
+               [&](long point) { require(out != nullptr, "plan created", point); }};
+    total += exercise(s);
+    if (out) rns8_destroy_plan(out);
+  }
+  // create_matrix (exact-wide: planes, proof words, event)
+  {
+    rns8_matrix* out = nullptr;
+    const auto d = matrix_desc(sem, RNS8_BOUND_NONE, m, n, P);
+    Scenario s{"create_matrix/exact-wide",
+               [&] {
+                 if (out) rns8_destroy_matrix(out);
+                 out = reinterpret_cast<rns8_matrix*>(0x1);
+               },
+               [&] { return rns8_create_matrix(ctx, &d, &out); },
+               [&](long point) { require(out == nullptr, "out handle null", point); },
+               [&](long point) { require(out != nullptr, "matrix created", point); }};
+    total += exercise(s);
+    if (out) rns8_destroy_matrix(out);
+  }
+  // create_workspace with split-K scratch
+  {
+    const auto d = gemm_desc(RNS8_BOUNDED_I64, RNS8_BOUND_GLOBAL_MAX_ABS, 64, 64, 1 << 20, 9);
+    auto dd = d;
+    dd.bound = 1000;
+    rns8_plan* p = make_plan(ctx, dd);
+    rns8_workspace* out = nullptr;
+    Scenario s{"create_workspace/split-k",
+               [&] {
+                 if (out) rns8_destroy_workspace(out);
+                 out = reinterpret_cast<rns8_workspace*>(0x1);
+               },
+               [&] { return rns8_create_workspace(ctx, p, &out); },
+               [&](long point) { require(out == nullptr, "out handle null", point); },
+               [&](long point) { require(out != nullptr, "workspace created", point); }};
+    total += exercise(s);
+    if (out) rns8_destroy_workspace(out);
+    // the allocation-free entry point on the same split-K plan: no allocation point at all
+    rns8_matrix* a = make_matrix(ctx, matrix_desc(RNS8_BOUNDED_I64, RNS8_BOUND_GLOBAL_MAX_ABS, 64, 1 << 20, 9));
+    rns8_matrix* b = make_matrix(ctx, matrix_desc(RNS8_BOUNDED_I64, RNS8_BOUND_GLOBAL_MAX_ABS, 1 << 20, 64, 9));
+    rns8_matrix* cm = make_matrix(ctx, matrix_desc(RNS8_BOUNDED_I64, RNS8_BOUND_GLOBAL_MAX_ABS, 64, 64, 9));
+    g_case = "gemm_rns_noalloc";
+    g_calls = 0;
+    g_fail_at = -1;
+    g_active = true;
+    const rns8_status st = rns8_mi355x_gemm_rns_noalloc(ctx, p, a, b, cm, nullptr);
+    g_active = false;
+    check_ok(st, "noalloc gemm");
+    require(g_calls.load() == 0, "the allocation-free entry point allocates nothing");
+    std::printf("case=gemm_rns_noalloc allocation_points=0\n");
+    rns8_destroy_matrix(cm);
+    rns8_destroy_matrix(b);
+    rns8_destroy_matrix(a);
+    rns8_destroy_plan(p);
+  }
+  // host pack into an exact-wide matrix holding A2 (staging, exact axes)
+  {
+    rns8_matrix* M = make_matrix(ctx, matrix_desc(sem, RNS8_BOUND_NONE, m, n, P));
+    std::vector<int64_t> old(m * n), fresh(m * n);
+    for (auto& v : old) v = static_cast<int64_t>(mix(seed)) >> 5;
+    for (auto& v : fresh) v = static_cast<int64_t>(mix(seed));
+    rns8_matrix_storage_info before{};
+    Scenario s{"pack_i64/exact-wide",
+               [&] {
+                 check_ok(rns8_pack_i64(ctx, M, old.data(), n, 5), "pack old");
+                 before = storage(M);
+               },
+               [&] { return rns8_pack_i64(ctx, M, fresh.data(), n, 6); },
+               [&](long point) {
+                 require(same_storage(storage(M), before), "matrix storage info unchanged", point);
+                 require(export3(M, m, n) == to_limbs(old), "matrix holds the old values", point);
+               },
+               [&](long point) {
+                 require(storage(M).source_version == 6, "source version", point);
+                 require(export3(M, m, n) == to_limbs(fresh), "matrix holds the new values", point);
+               }};
+    total += exercise(s);
+    rns8_destroy_matrix(M);
+  }
+  // gemm_rns with exact-wide admission; C holds an older product
+  {
+    check_ok(rns8_pack_i64(ctx, Bm, B.data(), n, 2), "pack B");
+    rns8_matrix_storage_info before{};
+    Scenario s{"gemm_rns/exact-wide",
+               [&] {
+                 check_ok(rns8_pack_i64(ctx, Am, A2.data(), k, 3), "pack A2");
+                 check_ok(rns8_gemm_rns(ctx, plan, Am, Bm, Cm, ws), "old product");
+                 check_ok(rns8_pack_i64(ctx, Am, A.data(), k, 4), "pack A");
+                 before = storage(Cm);
+               },
+               [&] { return rns8_gemm_rns(ctx, plan, Am, Bm, Cm, ws); },
+               [&](long point) {
+                 require(same_storage(storage(Cm), before), "C storage info unchanged", point);
+                 require(export3(Cm, m, n) == want2, "C holds the old product", point);
+               },
+               [&](long point) { require(export3(Cm, m, n) == want, "C holds the product", point); }};
+    total += exercise(s);
+  }
+  // host export (staging); dst keeps its sentinel on failure
+  {
+    check_ok(rns8_pack_i64(ctx, Am, A.data(), k, 7), "pack A");
+    check_ok(rns8_gemm_rns(ctx, plan, Am, Bm, Cm, ws), "product");
+    std::vector<uint64_t> dst(m * n * 3);
+    Scenario s{"export_exact_wide_signed_limbs",
+               [&] { std::fill(dst.begin(), dst.end(), 0xA5A5A5A5A5A5A5A5ull); },
+               [&] { return rns8_export_exact_wide_signed_limbs(ctx, plan, Cm, dst.data(), n, 3); },
+               [&](long point) {
+                 for (uint64_t v : dst) require(v == 0xA5A5A5A5A5A5A5A5ull, "dst untouched", point);
+               },
+               [&](long point) { require(dst == want, "exported product", point); }};
+    total += exercise(s);
+  }
+  // grouped GEMM (two tasks) with exact-wide admission
+  {
+    rns8_matrix* C2 = make_matrix(ctx, matrix_desc(sem, RNS8_BOUND_NONE, m, n, P));
+    rns8_workspace* ws2 = nullptr;
+    check_ok(rns8_create_workspace(ctx, plan, &ws2), "workspace 2");
+    rns8_matrix* A2m = make_matrix(ctx, matrix_desc(sem, RNS8_BOUND_NONE, m, k, P));
+    check_ok(rns8_pack_i64(ctx, A2m, A2.data(), k, 1), "pack A2");
+    // grouped tasks share no operand matrix
+    rns8_matrix* B2m = make_matrix(ctx, matrix_desc(sem, RNS8_BOUND_NONE, k, n, P));
+    check_ok(rns8_pack_i64(ctx, B2m, B.data(), n, 2), "pack B copy");
+    rns8_grouped_gemm_task tasks[2];
+    for (auto& t : tasks) {
+      std::memset(&t, 0, sizeof(t));
+      t.struct_size = sizeof(t);
+      t.abi_version = RNS8_ABI_VERSION;
+    }
+    tasks[0].a = Am;
+    tasks[0].b = Bm;
+    tasks[0].c = Cm;
+    tasks[0].workspace = ws;
+    tasks[1].a = A2m;
+    tasks[1].b = B2m;
+    tasks[1].c = C2;
+    tasks[1].workspace = ws2;
+    rns8_matrix_storage_info b0{}, b1{};
+    Scenario s{"gemm_rns_grouped/exact-wide",
+               [&] {
+                 // both results start from zero matrices of a known product
+                 check_ok(rns8_gemm_rns(ctx, plan, A2m, Bm, Cm, ws), "old C");
+                 check_ok(rns8_gemm_rns(ctx, plan, Am, B2m, C2, ws2), "old C2");
+                 b0 = storage(Cm);
+                 b1 = storage(C2);
+               },
+               [&] { return rns8_gemm_rns_grouped(ctx, plan, tasks, 2); },
+               [&](long point) {
+                 require(same_storage(storage(Cm), b0) && same_storage(storage(C2), b1), "storage unchanged", point);
+                 require(export3(Cm, m, n) == want2 && export3(C2, m, n) == want, "old products", point);
+               },
+               [&](long point) {
+                 require(export3(Cm, m, n) == want && export3(C2, m, n) == want2, "grouped products", point);
+               }};
+    total += exercise(s);
+    rns8_destroy_matrix(B2m);
+    rns8_destroy_matrix(A2m);
+    rns8_destroy_workspace(ws2);
+    rns8_destroy_matrix(C2);
+  }
+  // bounded int64 oneshot (cached state on first use)
+  {
+    const int64_t om = 33, on = 17, ok = 29;
+    std::vector<int64_t> oa(om * ok), ob(ok * on), oc(om * on), want_c(om * on);
+    for (auto& v : oa) v = static_cast<int64_t>(mix(seed) % 2001) - 1000;
+    for (auto& v : ob) v = static_cast<int64_t>(mix(seed) % 2001) - 1000;
+    for (int64_t i = 0; i < om; ++i)
+      for (int64_t j = 0; j < on; ++j) {
+        int64_t acc = 0;
+        for (int64_t t = 0; t < ok; ++t) acc += oa[i * ok + t] * ob[t * on + j];
+        want_c[i * on + j] = acc;
+      }
+    auto d = gemm_desc(RNS8_BOUNDED_I64, RNS8_BOUND_GLOBAL_MAX_ABS, om, on, ok, 0);
+    d.bound = 1 << 30;
+    auto other = d;  // a different descriptor: the call under test builds its cached state anew
+    other.bound = uint64_t{1} << 31;
+    std::vector<int64_t> scratch(om * on);
+    Scenario s{"gemm_i64_oneshot",
+               [&] {
+                 check_ok(rns8_gemm_i64_oneshot(ctx, &other, oa.data(), ok, ob.data(), on, scratch.data(), on),
+                          "oneshot with another descriptor");
+                 std::fill(oc.begin(), oc.end(), static_cast<int64_t>(0x5A5A5A5A5A5A5A5Aull));
+               },
+               [&] { return rns8_gemm_i64_oneshot(ctx, &d, oa.data(), ok, ob.data(), on, oc.data(), on); },
+               [&](long point) {
+                 for (int64_t v : oc) require(v == static_cast<int64_t>(0x5A5A5A5A5A5A5A5Aull), "C untouched", point);
+               },
+               [&](long point) { require(oc == want_c, "oneshot product", point); }};
+    total += exercise(s);
+  }
+  rns8_destroy_workspace(ws);
+  rns8_destroy_matrix(Cm);
+  rns8_destroy_matrix(Bm);
+  rns8_destroy_matrix(Am);
+  rns8_destroy_plan(plan);
+  return total;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc != 2 || (std::strcmp(argv[1], "host") != 0 && std::strcmp(argv[1], "device") != 0)) {
+    std::fprintf(stderr, "usage: alloc_fault_check host|device\n");
+    return 1;
+  }
+  dl_iterate_phdr(find_library, nullptr);
+  require(g_lib_hi > g_lib_lo, "librns8.so is mapped");
+  std::setvbuf(stdout, nullptr, _IOLBF, 0);
+  // self-check of the hooks: a library-free caller is never failed
+  g_calls = 0;
+  g_fail_at = 0;
+  g_active = true;
+  int* probe = new int(1);
+  g_active = false;
+  require(g_calls.load() == 0 && probe, "allocations outside the library are not counted");
+  delete probe;
+  const long points = std::strcmp(argv[1], "host") == 0 ? run_host() : run_device();
+  std::printf("PASS mode=%s allocation_failures=%ld\n", argv[1], points);
+  return 0;
+}

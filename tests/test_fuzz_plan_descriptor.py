@@ -1,0 +1,37 @@
+"""libFuzzer + AddressSanitizer + UndefinedBehaviorSanitizer over the
+device-free planning entries rns8_mi355x_select_prefix and
+rns8_mi355x_plan_schedule (tests/fuzz/fuzz_plan_descriptor.cpp, built by
+tests/fuzz/Makefile; reference tests/fuzz/rns8_fuzz_plan_descriptor.cpp).
+CPU only: the library's host sources are compiled instrumented, and no
+device is touched. A fixed seed and run count make the run repeatable."""
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+CLANG = Path("/opt/rocm/llvm/bin/clang++")
+DEVICE_OBJS = [ROOT / "rns8_amd" / "_build" / f"{n}.o" for n in ("export", "fused", "gemm", "pack")]
+
+
+@pytest.fixture(scope="module")
+def fuzzer(tmp_path_factory):
+    if not CLANG.is_file() or shutil.which("make") is None:
+        pytest.skip("clang++ with libFuzzer or make not available")
+    if not all(p.is_file() for p in DEVICE_OBJS):
+        pytest.skip("library objects missing: run __graft_entry__.build()")
+    out = tmp_path_factory.mktemp("fuzz")
+    subprocess.run(["make", "-s", "-j8", "-C", str(ROOT / "tests" / "fuzz"), f"OUT={out}"], check=True,
+                   timeout=600)
+    return out
+
+
+def test_plan_descriptor_fuzz(fuzzer):
+    corpus = fuzzer / "corpus"
+    corpus.mkdir()
+    res = subprocess.run([str(fuzzer / "fuzz_plan_descriptor"), "-seed=1", "-runs=1500000", "-max_len=512",
+                          "-print_final_stats=1", str(corpus)], capture_output=True, text=True, timeout=600,
+                         cwd=fuzzer)
+    assert res.returncode == 0, res.stderr[-4000:]
+    assert "Done 1500000 runs" in res.stderr
