@@ -30,6 +30,18 @@ __device__ __forceinline__ v4i buffer_rsrc(const void* p, int64_t bytes) {
              __builtin_amdgcn_readfirstlane(static_cast<int>(bytes)), kBufferFlags};
 }
 
+// The same resource as the compiler's buffer-resource type, for the raw
+// buffer load/store builtins (out-of-range dwords read as zero and are not
+// written).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32));
+  const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  void* const base = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(base, static_cast<short>(0), n, kBufferFlags);
+}
+
 // 16 bytes per lane from a raw buffer straight into LDS: lane l's bytes land
 // at lds_addr + 16*l (M0 = lds_addr, wave-uniform). Written as asm so the
 // compiler does not track the LDS write (it would otherwise wait for every

@@ -4,26 +4,33 @@
 // operands inside its tile loads the same way, one plane per launch slice).
 //
 // Scope: outputs too small to fill the chip, so the work is split along K
-// (tall-skinny products such as 128 x 128 x 65536), where the packed planes
-// would be read only once by the GEMM; the fused launch never stores
-// residues to HBM. For large outputs every operand panel is read by many
+// (tall-skinny products such as 128 x 128 x 65536). Each native element is
+// read from HBM once and reduced once per plane; no residue plane of A or B is
+// ever stored. For large outputs every operand panel would be read by many
 // output tiles and packing once is cheaper, so the host offers the fused path
-// only below a workspace limit. Measured at 128 x 128 x 65536 it is still
-// slower than two packs and the split-K GEMM (92 against 83 us of kernels).
+// only below a workspace limit.
 //
-// Work split: a workgroup owns a 128 x 128 output tile, a group of up to four
-// planes and one K slice; its four waves each hold a 64 x 64 quadrant of all
-// four planes (4 planes x 2 x 2 blocks of v_mfma_i32_32x32x32_i8, 256
-// accumulator registers), so one workgroup runs per CU. The raw int64 tiles
-// of each 32-deep K step (32 KB of A, 32 KB of B) are loaded straight into
-// LDS two steps ahead, holding no registers while in flight. Per step every
-// thread reads 16 native elements of A (one row, 16 consecutive k) and 16 of B
-// (one column, 16 consecutive k) from LDS, reduces them to centered residues
-// for each plane of the group with the pack's arithmetic (two v_dot4_u32_u8
-// and a 24-bit quotient, tables.hpp), and stores them into a k-contiguous
-// residue stage, so every MFMA fragment is one ds_read_b128. Each element is
-// reduced once per plane, as in the packs. LDS: a 32 KB residue stage and two
-// 64 KB raw stages, 160 KB.
+// Work split: a workgroup owns a 128 x 128 output tile, a pair of planes and
+// one K slice. Its eight waves run two per SIMD, so one wave's conversion
+// arithmetic issues next to the other's MFMAs and LDS traffic. Roles:
+//   * conversion: waves 0-3 take A, waves 4-7 take B, and every load is
+//     coalesced: an A load covers four rows x 32 k (16 lanes per 256-byte row
+//     segment, two k per lane), a B load one k row x 128 columns (two columns
+//     per lane). A lane thus holds two k of eight rows (A) or eight k of two
+//     columns (B). Both roles issue eight 16-byte loads per step; the raw
+//     values of step s+2 are requested while step s is converted. Each lane
+//     reduces its 16 elements for both planes (the pack's arithmetic: two
+//     v_dot4_u32_u8 and a 24-bit quotient, or one dot product when every
+//     element of the wave's step fits in 32 bits) and stores its residues
+//     into the k-contiguous stage (2 bytes per A row, 8 per B column);
+//   * MFMA: wave w multiplies plane w / 4 of the pair over a 64 x 64 quadrant
+//     (2 x 2 blocks of v_mfma_i32_32x32x32_i8, 64 accumulator registers),
+//     one step behind the conversion: the residue stages are double-buffered
+//     and one barrier per step separates a stage's writers from its readers.
+// Residue stage layout per plane and operand: [2 k-chunks][128 rows or
+// columns][16 bytes], so both the conversion's stores and the fragment reads
+// (lane l: row or column l & 31 of a block, k-chunk l >> 5) are contiguous
+// 512-byte runs, free of bank conflicts. LDS: 2 stages x 2 planes x 8 KB.
 //
 // Each slice reduces its int32 sums to centered int8 residues in the
 // epilogue and stores them into its own slot of the workspace; a finalize
@@ -41,59 +48,41 @@ namespace rns8x {
 namespace {
 
 typedef int v2i __attribute__((ext_vector_type(2)));
-typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
 
-constexpr int kTileM = 128;                           // output rows per workgroup
-constexpr int kTileN = 128;                           // output columns per workgroup
-constexpr int kStepK = 32;                            // K per step (one MFMA depth)
-constexpr int kGroupPlanes = 4;                       // planes per workgroup
-constexpr int kALds = kTileM * kStepK;                // 4 KB of residues: 128 rows x 32 k
-constexpr int kBLds = kTileN * kStepK;                // 4 KB of residues: 128 columns x 32 k
-constexpr int kPlaneLds = kALds + kBLds;
-constexpr int kResLds = kGroupPlanes * kPlaneLds;     // 32 KB: the residue stage
-constexpr int kRawA = kTileM * kStepK * 8;            // 32 KB: 128 rows x 256 bytes of native A
-constexpr int kRawB = kStepK * kTileN * 8;            // 32 KB: 32 k rows x 1 KB of native B
-constexpr int kRawLds = kRawA + kRawB;
-constexpr int kLdsBytes = kResLds + 2 * kRawLds;      // 160 KB: residues + two raw stages
-constexpr int kDmaPerWave = (kRawLds / 1024) / 4;     // 16 one-KB loads per wave per step
-constexpr int64_t kMaxSliceK = 65536;                 // |int32 sum| <= 65536 * 128 * 128 = 2^30
-constexpr int64_t kMinSliceK = 512;                   // 16 steps: amortizes the epilogue
+constexpr int kThreads = 512;                        // eight waves, two per SIMD
+constexpr int kTileM = 128;                          // output rows per workgroup
+constexpr int kTileN = 128;                          // output columns per workgroup
+constexpr int kStepK = 32;                           // K per step (one MFMA depth)
+constexpr int kGroupPlanes = 2;                      // planes per workgroup
+constexpr int kChunkLds = 128 * 16;                  // one k-chunk of 128 rows or columns
+constexpr int kOperandLds = 2 * kChunkLds;           // 4 KB: 128 x 32 residues
+constexpr int kPlaneLds = 2 * kOperandLds;           // A then B
+constexpr int kStageLds = kGroupPlanes * kPlaneLds;  // 16 KB
+constexpr int kLdsBytes = 2 * kStageLds;             // two stages
+constexpr int64_t kMaxSliceK = 65536;                // |int32 sum| <= 65536 * 128 * 128 = 2^30
+constexpr int64_t kMinSliceK = 512;                  // 16 steps: amortizes the epilogue
 constexpr uint64_t kMaxWorkspace = uint64_t{64} << 20;
+constexpr uint32_t kOutOfRange = 0x80000000u;        // a buffer offset past every resource
 
-// Centered residues of native values 4q .. 4q+3 (split in 32-bit halves, the
-// sign bit of signed inputs already flipped) for one modulus, packed
-// little-endian
-// (reference cpu_reference.cpp:53-130; the same arithmetic as the pack kernel).
-template <int N>
-__device__ __forceinline__ uint32_t residues4(const uint32_t (&lo)[N], const uint32_t (&hi)[N], int q,
-                                              const ModulusConsts& mc, uint32_t off) {
-  if (mc.m == 256u) return pack_low_bytes(lo[4 * q], lo[4 * q + 1], lo[4 * q + 2], lo[4 * q + 3]);
-  const uint32_t m_comp = 256u - mc.m;
-  uint32_t r[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t t = __builtin_amdgcn_udot4(lo[4 * q + e], mc.pow_lo, off, false);
-    r[e] = mod_low_byte(__builtin_amdgcn_udot4(hi[4 * q + e], mc.pow_hi, t, false), mc.pq_shift, mc.pq_recip, m_comp);
-  }
-  return pack_centered(r[0], r[1], r[2], r[3], mc.half * 0x00010001u);
-}
+// A lane's eight 16-byte loads of one step, as issued. Element (j, h) is
+// v[j][2h] (low half) and v[j][2h + 1] (high half): for an A lane row
+// 4j + (lane >> 4) of its wave's 32 rows at k = 2 (lane & 15) + h, for a B
+// lane k = j of its column h.
+struct Raw {
+  v4i v[8];
+};
 
-// Grid: x = output tile (tiles_n per tile row), y = K slice, z = plane group
-// (planes p0 .. p0 + NP - 1, p0 = plane_base + 4 * z). The host guarantees
+// Grid: x = output tile (tiles_n per tile row), y = K slice, z = plane pair
+// (planes p0 .. p0 + NP - 1, p0 = plane_base + 2 * z). The host guarantees
 // every slice holds at least one K element, 16-byte aligned operands with
-// even row strides, and row strides below 2^21 elements. NP is a template
-// parameter so that every accumulator is updated unconditionally and stays
-// in its AGPRs.
+// even row strides, and row strides below 2^21 elements.
 template <bool Signed, int NP>
-__global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, PlaneConsts pc, uint32_t tiles_n,
-                                                              uint32_t plane_base) {
+__global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, PlaneConsts pc, uint32_t tiles_n,
+                                                                   uint32_t plane_base) {
   __shared__ __attribute__((aligned(16))) int8_t lds[kLdsBytes];
-  int8_t* const res = lds;                 // residue stage
-  int8_t* const raw0 = lds + kResLds;      // raw stages: A rows then B k rows
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const uint32_t tr = blockIdx.x / tiles_n;
   const uint32_t tc = blockIdx.x - tr * tiles_n;
   const int64_t m0 = static_cast<int64_t>(tr) * kTileM;
@@ -103,175 +92,249 @@ __global__ __launch_bounds__(256, 1) void fused_native_kernel(FusedArgs a, Plane
   const int64_t kb = static_cast<int64_t>(slice) * a.shape.k_slice;
   const int64_t ke = min(kb + a.shape.k_slice, a.k);
   const int steps = static_cast<int>((ke - kb + kStepK - 1) / kStepK);
+  const bool ragged = (ke - kb) % kStepK != 0;  // the last step ends inside its 32 k
   const int64_t rows_valid = min(static_cast<int64_t>(kTileM), a.m - m0);
+  const ModulusConsts mc0 = pc.mod[p0];
+  const ModulusConsts mc1 = pc.mod[NP > 1 ? p0 + 1 : p0];
 
-  // Raw loads, straight into LDS (16 bytes per lane, no registers held while
-  // in flight). Wave w loads A rows 32w .. 32w+31 as 8 blocks of 4 rows x 256
-  // bytes, and B k rows 8w .. 8w+7 as 8 blocks of 1 KB. In A, the 16-byte
-  // chunk c of row r is stored at chunk position c ^ (r & 7) of its LDS row,
-  // so the conversion's reads (two rows per 8-lane group, same chunk index)
-  // fall on distinct banks. Rows past the operand read 0 through the buffer
-  // resources' ranges; k past the slice and columns past n are zeroed when
-  // converted (within a row they may hold the row padding of a strided
-  // operand).
-  const uint32_t lds_raw0 = lds_address(raw0);
-  uint32_t a_voff[8], b_voff[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int row = 32 * wave + 4 * j + (lane >> 4);
-    const int chunk = (lane & 15) ^ (row & 7);
-    a_voff[j] = static_cast<uint32_t>(row) * static_cast<uint32_t>(a.lda) * 8u + 16u * static_cast<uint32_t>(chunk);
-    const int kr = 8 * wave + j;
-    b_voff[j] = static_cast<uint32_t>(kr) * static_cast<uint32_t>(a.ldb) * 8u + 16u * static_cast<uint32_t>(lane);
-  }
+  // ---- conversion role -------------------------------------------------------
+  // A lanes (waves 0-3): rows 32 * wave + 4j + (lane >> 4), j = 0..7, k
+  // 2 (lane & 15) and 2 (lane & 15) + 1 of the step. B lanes (waves 4-7):
+  // columns 2 * lane and 2 * lane + 1, k 8 * (wave - 4) .. +7. Rows past m and
+  // k past the operand read 0 through the resources' ranges, which end at the
+  // operands' last logical elements (a row's offset past the last valid row
+  // exceeds the range since lda >= k). Column pairs past n get an offset
+  // outside every resource. A pair that straddles n reads its second column
+  // from the row padding (strides are even); the epilogue stores zero for
+  // that column.
+  const bool is_a = wave < 4;
+  const int ra = 32 * wave + (lane >> 4);  // an A lane's first row (then +4 per load)
+  const int kfirst = is_a ? 2 * (lane & 15) : 8 * (wave - 4);  // the lane's first k within a step
+  const uint32_t lda8 = static_cast<uint32_t>(a.lda) * 8u, ldb8 = static_cast<uint32_t>(a.ldb) * 8u;
+  const uint32_t voff = is_a ? static_cast<uint32_t>(ra) * lda8 + 8u * kfirst
+                             : (n0 + 2 * lane < a.n ? static_cast<uint32_t>(kfirst) * ldb8 + 16u * lane : kOutOfRange);
   const uint64_t* const abase = static_cast<const uint64_t*>(a.a) + m0 * a.lda;
   const uint64_t* const bbase = static_cast<const uint64_t*>(a.b) + n0;
-  auto issue = [&](int s, int stage) {
+  const uint32_t vstride = is_a ? 4u * lda8 : ldb8;  // bytes between a lane's loads
+  auto load = [&](Raw& x, int s) {
     const int64_t k0 = kb + static_cast<int64_t>(kStepK) * s;
-    // The ranges end at the operands' last logical elements (row rows_valid - 1,
-    // column k - 1 of A; k row k0 + krows - 1, column n - 1 of B), so no lane
-    // reads past an allocation of exactly (m - 1) * lda + k resp.
-    // (k - 1) * ldb + n elements; lanes past them read 0.
-    const v4i ra = buffer_rsrc(abase + k0, ((rows_valid - 1) * a.lda + a.k - k0) * 8);
     const int64_t krows = min(static_cast<int64_t>(kStepK), a.k - k0);
-    const v4i rb = buffer_rsrc(bbase + k0 * a.ldb, ((krows - 1) * a.ldb + a.n - n0) * 8);
-    const uint32_t dst = lds_raw0 + static_cast<uint32_t>(stage * kRawLds);
+    const __amdgpu_buffer_rsrc_t rs =
+        is_a ? make_rsrc(abase + k0, ((rows_valid - 1) * a.lda + a.k - k0) * 8)
+             : make_rsrc(bbase + k0 * a.ldb, ((krows - 1) * a.ldb + a.n - n0) * 8);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dma16(dst + static_cast<uint32_t>((8 * wave + j) * 1024), a_voff[j], ra);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) dma16(dst + static_cast<uint32_t>(kRawA + (8 * wave + j) * 1024), b_voff[j], rb);
+    for (int j = 0; j < 8; ++j)
+      x.v[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + vstride * j, 0, 0));
   };
-
-  // Conversion roles: A row a_r, k 16*a_h .. +15; B column b_c, k 16*b_h .. +15.
-  const int a_r = t >> 1, a_h = t & 1;
-  const int b_c = t & 127, b_h = t >> 7;
-  const bool b_ok = n0 + b_c < a.n;
-  auto convert = [&](int s, int stage) {
-    const int64_t k0 = kb + static_cast<int64_t>(kStepK) * s;
-    const int8_t* const raw = raw0 + stage * kRawLds;
-    uint32_t alo[16], ahi[16], blo[16], bhi[16];
+  // Elements at k >= ke of the slice's last, ragged step belong to the next
+  // slice (or to a row's padding) and count as zero.
+  auto mask_tail = [&](Raw& x, int s) {
+    const int64_t first = kb + static_cast<int64_t>(kStepK) * s + kfirst;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int chunk = (8 * a_h + j) ^ (a_r & 7);
-      const v4i v = *reinterpret_cast<const v4i*>(raw + a_r * 256 + 16 * chunk);
-      const bool ok0 = k0 + 16 * a_h + 2 * j < ke, ok1 = k0 + 16 * a_h + 2 * j + 1 < ke;
-      alo[2 * j] = ok0 ? static_cast<uint32_t>(v[0]) : 0u;
-      ahi[2 * j] = ok0 ? static_cast<uint32_t>(v[1]) : 0u;
-      alo[2 * j + 1] = ok1 ? static_cast<uint32_t>(v[2]) : 0u;
-      ahi[2 * j + 1] = ok1 ? static_cast<uint32_t>(v[3]) : 0u;
-    }
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const v2i v = *reinterpret_cast<const v2i*>(raw + kRawA + (16 * b_h + e) * 1024 + 8 * b_c);
-      const bool ok = b_ok && k0 + 16 * b_h + e < ke;
-      blo[e] = ok ? static_cast<uint32_t>(v[0]) : 0u;
-      bhi[e] = ok ? static_cast<uint32_t>(v[1]) : 0u;
-    }
-    if (Signed) {
+      for (int h = 0; h < 2; ++h)
+        if (first + (is_a ? h : j) >= ke) x.v[j][2 * h] = x.v[j][2 * h + 1] = 0;
+  };
+  // A: rows ra + 4j, k-chunk kfirst / 16, bytes kfirst % 16 .. +1 of each
+  // row's chunk: one 2-byte store per row. B: columns 2 lane and 2 lane + 1,
+  // k-chunk kfirst / 16, bytes 8 .. 15 of each column's chunk when kfirst % 16
+  // = 8: one 8-byte store per column.
+  int8_t* const dst_off = is_a ? lds + (kfirst >> 4) * kChunkLds + ra * 16 + (kfirst & 15)
+                               : lds + kOperandLds + (kfirst >> 4) * kChunkLds + 2 * lane * 16 + (kfirst & 8);
+  auto convert = [&](const Raw& x, int stage) {
+    uint32_t wide = 0;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        ahi[e] ^= 0x80000000u;
-        bhi[e] ^= 0x80000000u;
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t lo = static_cast<uint32_t>(x.v[j][2 * h]), hi = static_cast<uint32_t>(x.v[j][2 * h + 1]);
+        wide |= Signed ? hi ^ static_cast<uint32_t>(static_cast<int32_t>(lo) >> 31) : hi;
       }
-    }
+    // One plane's residues, stored into its stage. The modulus-256 plane
+    // (the low byte of each element) is a separate instantiation so that
+    // neither form carries the other's selects.
+    auto plane_as = [&](auto fast, auto m256c, const ModulusConsts& mc, int8_t* dst) {
+      constexpr bool kFast = decltype(fast)::value;
+      constexpr bool kM256 = decltype(m256c)::value;
+      // r[j][h]: the element's residue (plus H when m < 256) in its low byte.
+      // The reduction runs in phases over all 16 elements (dot products, then
+      // shifts, quotients and remainders), so independent chains interleave
+      // and each dependent pair is 16 instructions apart.
+      uint32_t r[8][2];
+      const uint32_t m_comp = 256u - mc.m;
+      if constexpr (kM256) {
 #pragma unroll
-    for (int pl = 0; pl < NP; ++pl) {
-      const ModulusConsts mc = pc.mod[p0 + pl];
-      const uint32_t off = Signed ? mc.off_i64 : mc.off_u64;
-      const v4i wa = {static_cast<int>(residues4(alo, ahi, 0, mc, off)), static_cast<int>(residues4(alo, ahi, 1, mc, off)),
-                      static_cast<int>(residues4(alo, ahi, 2, mc, off)), static_cast<int>(residues4(alo, ahi, 3, mc, off))};
-      const v4i wb = {static_cast<int>(residues4(blo, bhi, 0, mc, off)), static_cast<int>(residues4(blo, bhi, 1, mc, off)),
-                      static_cast<int>(residues4(blo, bhi, 2, mc, off)), static_cast<int>(residues4(blo, bhi, 3, mc, off))};
-      *reinterpret_cast<v4i*>(res + pl * kPlaneLds + a_r * kStepK + 16 * a_h) = wa;
-      *reinterpret_cast<v4i*>(res + pl * kPlaneLds + kALds + b_c * kStepK + 16 * b_h) = wb;
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) r[j][h] = static_cast<uint32_t>(x.v[j][2 * h]);
+      } else {
+        // the fast signed form is the accumulator reduction of lo ^ 2^31
+        constexpr bool kI32 = kFast && Signed;
+        const uint32_t shift = kI32 ? mc.q_shift : mc.pq_shift;
+        const uint32_t recip = kI32 ? mc.q_recip : mc.pq_recip;
+        const uint32_t off = kI32 ? mc.off_i32 : Signed ? mc.off_i64 : mc.off_u64;
+        uint32_t s[8][2], q[8][2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t lo = static_cast<uint32_t>(x.v[j][2 * h]);
+            s[j][h] = __builtin_amdgcn_udot4(kI32 ? lo ^ 0x80000000u : lo, mc.pow_lo, off, false);
+          }
+        if constexpr (!kFast) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const uint32_t hi = static_cast<uint32_t>(x.v[j][2 * h + 1]);
+              s[j][h] = __builtin_amdgcn_udot4(Signed ? hi ^ 0x80000000u : hi, mc.pow_hi, s[j][h], false);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) q[j][h] = s[j][h] << shift;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) q[j][h] = mulhi_u24(q[j][h], recip);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) r[j][h] = mad_u24(q[j][h], m_comp, s[j][h]);
+      }
+      const uint32_t half2 = mc.half * 0x00010001u;
+      auto pack4 = [&](uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3) {
+        if constexpr (kM256)
+          return pack_low_bytes(r0, r1, r2, r3);
+        else
+          return pack_centered(r0, r1, r2, r3, half2);
+      };
+      if (is_a) {
+        // rows 4j and 4(j + 1) share a packed dword: its low half goes to one
+        // row, its high half to the other
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t w = pack4(r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]);
+          *reinterpret_cast<uint16_t*>(dst + 8 * q * 16) = static_cast<uint16_t>(w);
+          *reinterpret_cast<uint16_t*>(dst + (8 * q + 4) * 16) = static_cast<uint16_t>(w >> 16);
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          *reinterpret_cast<v2i*>(dst + 16 * h) = v2i{static_cast<int>(pack4(r[0][h], r[1][h], r[2][h], r[3][h])),
+                                                      static_cast<int>(pack4(r[4][h], r[5][h], r[6][h], r[7][h]))};
+      }
+    };
+    auto plane = [&](auto fast, const ModulusConsts& mc, int8_t* dst) {
+      if (mc.m == 256u)
+        plane_as(fast, std::true_type{}, mc, dst);
+      else
+        plane_as(fast, std::false_type{}, mc, dst);
+    };
+    int8_t* const dst = dst_off + stage * kStageLds;
+    // one branch per wave: the 32-bit form when no lane has a wide element
+    if (__builtin_amdgcn_ballot_w64(wide != 0u) == 0u) {
+      plane(std::true_type{}, mc0, dst);
+      if constexpr (NP > 1) plane(std::true_type{}, mc1, dst + kPlaneLds);
+    } else {
+      plane(std::false_type{}, mc0, dst);
+      if constexpr (NP > 1) plane(std::false_type{}, mc1, dst + kPlaneLds);
     }
   };
 
-  // Fragments: lane l takes row (A) or column (B) l & 31 of a 32-block and the
-  // 16 k values 16*(l >> 5) .. +15, one ds_read_b128 each. With B as src0 and
-  // A as src1, register 4g+e of acc[pl][i][j] holds C[row][col] of plane
-  // p0 + pl with row = m0 + 64*wm + 32*i + (l & 31) and col = n0 + 64*wn +
-  // 32*j + 8*g + 4*(l >> 5) + e.
-  v16i acc[NP][2][2];
+  // ---- MFMA role -------------------------------------------------------------
+  // Wave w: plane w / 4 of the pair, quadrant rows 64 * ((w >> 1) & 1), columns
+  // 64 * (w & 1). With B as src0 and A as src1, register 4g+e of acc[i][j]
+  // holds C[row][col] with row = m0 + 64 wm + 32 i + (l & 31) and col = n0 +
+  // 64 wn + 32 j + 8 g + 4 (l >> 5) + e.
+  const int pl = wave >> 2, wm = (wave >> 1) & 1, wn = wave & 1;
+  const bool mfma_wave = pl < NP;
+  const int frag = (lane >> 5) * kChunkLds + (lane & 31) * 16;
+  v16i acc[2][2];
 #pragma unroll
-  for (int pl = 0; pl < NP; ++pl)
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
+  auto mma = [&](const int8_t* stage) {
+    if (!mfma_wave) return;
+    const int8_t* const sa = stage + pl * kPlaneLds + frag;
+    const int8_t* const sb = sa + kOperandLds;
+    v4i af[2], bf[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const v4i*>(sa + (64 * wm + 32 * i) * 16);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const v4i*>(sb + (64 * wn + 32 * j) * 16);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[pl][i][j] = v16i{};
-  const int frag = (lane & 31) * kStepK + 16 * (lane >> 5);
-  auto mma = [&]() {
-#pragma unroll
-    for (int pl = 0; pl < NP; ++pl) {
-      v4i af[2], bf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const v4i*>(res + pl * kPlaneLds + (64 * wm + 32 * i) * kStepK + frag);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *reinterpret_cast<const v4i*>(res + pl * kPlaneLds + kALds + (64 * wn + 32 * j) * kStepK + frag);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[pl][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[pl][i][j], 0, 0, 0);
-    }
+      for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
   };
 
-  // Pipeline: the raw data of steps s+1 and s+2 are in flight (or landed)
-  // while step s is converted and multiplied. Every step issues exactly
-  // kDmaPerWave loads per wave (past the last step the last step's data is
-  // loaded again into the free stage and never converted, so the vmcnt
-  // bookkeeping stays uniform); loads complete in order, so before
-  // converting step s each wave waits until only the newest step's loads are
-  // outstanding, and the barrier after that wait publishes every wave's loads
-  // of step s.
-  issue(0, 0);
-  issue(min(1, steps - 1), 1);
-  for (int s = 0; s < steps; ++s) {
-    __builtin_amdgcn_s_waitcnt(wait_vm(kDmaPerWave));  // step s landed (this wave's part)
-    __syncthreads();                                  // every wave's part; step s-1's MFMAs retired
-    convert(s, s & 1);
-    __syncthreads();                                  // residues of step s stored; raw stage s&1 free
-    // the raw stage just converted takes step s+2 (a repeat of the last step
-    // past the end, never converted)
-    issue(min(s + 2, steps - 1), s & 1);
-    mma();
+  // ---- pipeline ----------------------------------------------------------------
+  // Step s: step s-1 (stage (s-1) & 1, converted in the last step) is
+  // multiplied, step s is converted into stage s & 1 and the raw values of
+  // step s+2 are requested (those of step s+1 are in flight); the barrier that
+  // ends the step publishes stage s & 1 and retires every read of stage
+  // (s-1) & 1, which step s+1 overwrites. Three register sets hold the raw
+  // values (the loop is unrolled by three so each set keeps its registers).
+  auto step = [&](Raw& cur, Raw& ahead, int s) {
+    // the MFMAs of step s-1 first: they run in the matrix pipe while the
+    // conversion below occupies the VALU
+    if (s > 0) mma(lds + ((s - 1) & 1) * kStageLds);
+    if (ragged && s == steps - 1) mask_tail(cur, s);
+    convert(cur, s & 1);
+    // The loads of step s+2 go out after the conversion: issued at the top of
+    // the step, the workgroup's 64 loads queue in the texture path ahead of
+    // the later waves' MFMAs and conversion (measured 10% slower). They are
+    // unconditional, so every step has the same loads in flight (past the
+    // end the last step is loaded again and never converted).
+    load(ahead, min(s + 2, steps - 1));
+    __syncthreads();
+  };
+  Raw r0, r1, r2;
+  load(r0, 0);
+  load(r1, min(1, steps - 1));
+  for (int s = 0;;) {
+    step(r0, r2, s);
+    if (++s >= steps) break;
+    step(r1, r0, s);
+    if (++s >= steps) break;
+    step(r2, r1, s);
+    if (++s >= steps) break;
   }
-  __builtin_amdgcn_s_waitcnt(wait_vm(0));  // no load outlives the workgroup's LDS
+  mma(lds + ((steps - 1) & 1) * kStageLds);
 
-  // Epilogue: each int32 sum x (|x| <= 2^30) reduced to its centered residue,
-  // four columns per dword, into slot [slice][plane][row][col] of the
-  // workspace (row stride ldc). Columns in [n, ldc) hold residues of zero
-  // sums; rows past m are not stored.
+  // ---- epilogue --------------------------------------------------------------
+  // Each int32 sum x (|x| <= 2^30) reduced to its centered residue, four
+  // columns per dword, into slot [slice][plane][row][col] of the workspace
+  // (row stride ldc). Columns in [n, ldc) are stored as zero; rows past m are
+  // not stored.
+  if (!mfma_wave) return;
+  const uint32_t plane = p0 + pl;
+  const ModulusConsts mc = pl == 0 ? mc0 : mc1;
+  const uint32_t m_comp = 256u - mc.m;
+  const uint32_t half2 = mc.half * 0x00010001u;
+  int8_t* const w = a.ws + (static_cast<int64_t>(slice) * a.nplanes + plane) * a.m * a.ldc;
 #pragma unroll
-  for (int pl = 0; pl < NP; ++pl) {
-    {
-      const uint32_t plane = p0 + pl;
-      const ModulusConsts mc = pc.mod[plane];
-      const uint32_t m_comp = 256u - mc.m;
-      const uint32_t half2 = mc.half * 0x00010001u;
-      int8_t* const w = a.ws + (static_cast<int64_t>(slice) * a.nplanes + plane) * a.m * a.ldc;
+  for (int i = 0; i < 2; ++i) {
+    const int64_t row = m0 + 64 * wm + 32 * i + (lane & 31);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int64_t row = m0 + 64 * wm + 32 * i + (lane & 31);
+    for (int j = 0; j < 2; ++j) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+      for (int g = 0; g < 4; ++g) {
+        const int64_t col = n0 + 64 * wn + 32 * j + 8 * g + 4 * (lane >> 5);
+        uint32_t r[4];
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int64_t col = n0 + 64 * wn + 32 * j + 8 * g + 4 * (lane >> 5);
-            const Acc4 a4 = acc_read4(acc[pl][i][j], g);
-            uint32_t r[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const uint32_t u = a4.v[e] ^ 0x80000000u;
-              r[e] = mc.m == 256u ? u : residue_plus_half(u, mc, m_comp);
-            }
-            const uint32_t packed = mc.m == 256u ? pack_low_bytes(r[0], r[1], r[2], r[3])
-                                                 : pack_centered(r[0], r[1], r[2], r[3], half2);
-            if (row < a.m && col < a.ldc) *reinterpret_cast<uint32_t*>(w + row * a.ldc + col) = packed;
-          }
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t u = static_cast<uint32_t>(acc[i][j][4 * g + e]) ^ 0x80000000u;
+          r[e] = mc.m == 256u ? u : residue_plus_half(u, mc, m_comp);
         }
+        uint32_t packed =
+            mc.m == 256u ? pack_low_bytes(r[0], r[1], r[2], r[3]) : pack_centered(r[0], r[1], r[2], r[3], half2);
+        if (col + 4 > a.n) packed &= col >= a.n ? 0u : 0xFFFFFFFFu >> (8 * (col + 4 - a.n));
+        if (row < a.m && col < a.ldc) *reinterpret_cast<uint32_t*>(w + row * a.ldc + col) = packed;
       }
     }
   }
@@ -376,22 +439,19 @@ hipError_t launch_fused_native(const FusedArgs& a, const PlaneConsts& consts, hi
   const uint32_t tiles_n = static_cast<uint32_t>((a.n + kTileN - 1) / kTileN);
   const uint32_t tiles = static_cast<uint32_t>((a.m + kTileM - 1) / kTileM) * tiles_n;
   const bool sgn = a.kind == NativeKind::I64;
-  // full groups of four planes in one grid, the remaining 1-3 planes in another
+  // full pairs of planes in one grid, an odd last plane in another
   const uint32_t full = a.nplanes / kGroupPlanes;
   const uint32_t rest = a.nplanes - full * kGroupPlanes;
   auto launch = [&](auto np, uint32_t groups, uint32_t base) {
     constexpr int NP = decltype(np)::value;
     const dim3 grid(tiles, a.shape.slices, groups);
     if (sgn)
-      hipLaunchKernelGGL((fused_native_kernel<true, NP>), grid, dim3(256), 0, stream, a, consts, tiles_n, base);
+      hipLaunchKernelGGL((fused_native_kernel<true, NP>), grid, dim3(kThreads), 0, stream, a, consts, tiles_n, base);
     else
-      hipLaunchKernelGGL((fused_native_kernel<false, NP>), grid, dim3(256), 0, stream, a, consts, tiles_n, base);
+      hipLaunchKernelGGL((fused_native_kernel<false, NP>), grid, dim3(kThreads), 0, stream, a, consts, tiles_n, base);
   };
   if (full) launch(std::integral_constant<int, kGroupPlanes>{}, full, 0);
-  const uint32_t base = full * kGroupPlanes;
-  if (rest == 1) launch(std::integral_constant<int, 1>{}, 1, base);
-  if (rest == 2) launch(std::integral_constant<int, 2>{}, 1, base);
-  if (rest == 3) launch(std::integral_constant<int, 3>{}, 1, base);
+  if (rest) launch(std::integral_constant<int, 1>{}, 1, full * kGroupPlanes);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t words = static_cast<int64_t>(a.nplanes) * a.m * a.ldc / 4;

@@ -118,17 +118,6 @@ __device__ __forceinline__ int swizzle_b(int k, int chunk) {
     return chunk ^ x;
 }
 
-// Raw buffer resource over [p, p + bytes). The inputs are wave-uniform; they
-// are passed through readfirstlane so the descriptor is built in SGPRs.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
-  const uint64_t addr = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32));
-  const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
-  void* const base = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(base, static_cast<short>(0), n, kBufferFlags);
-}
-
 
 // Scheduling slots of a K sub-step region: slot Q is one MFMA followed by up
 // to kPerSlot of the region's kReads LDS fragment reads.
