@@ -92,8 +92,11 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--packed", action="store_true",
+                    help="c5: two packs and the split-K plane GEMM in place of the fused native-input GEMM (the "
+                         "default route for this tall-skinny shape)")
     ap.add_argument("--fused", action="store_true",
-                    help="c5/c1: one fused native-input GEMM (rns8_mi355x_gemm_native_*_async) in place of the two "
+                    help="c1/c3: one fused native-input GEMM (rns8_mi355x_gemm_native_*_async) in place of the two "
                          "packs and the plane GEMM")
     ap.add_argument("--oneshot", action="store_true",
                     help="time the host-buffer oneshot entry point instead (PCIe transfers included)")
@@ -169,13 +172,16 @@ def main() -> int:
     pack = L.rns8_mi355x_pack_i64_device if signed else L.rns8_mi355x_pack_u64_device
     export = L.rns8_mi355x_export_i64_device if signed else L.rns8_mi355x_export_u64_device
     native = L.rns8_mi355x_gemm_native_i64_async if signed else L.rns8_mi355x_gemm_native_u64_async
-    if args.fused and tiled:
+    # tall-skinny C5 runs the fused native-input GEMM unless --packed asks for
+    # the two packs and the split-K plane GEMM
+    fused = args.fused or (args.config == "c5" and not args.packed)
+    if fused and tiled:
         log("[bench] --fused applies to plans with a global bound only")
         return 2
 
     def step(mark=_no_mark):
         mark(0)
-        if args.fused:
+        if fused:
             # the packs are inside the fused launch: their stages are empty
             mark(1)
             mark(2)
@@ -263,10 +269,10 @@ def main() -> int:
     if roofline["traffic"] is not None:
         roofline["traffic_source"] = ("profiles/traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE per dispatch of "
                                       "this kernel at this workload, copy-calibrated; not measured in this run")
-    if args.fused:
+    if fused:
         # pack and GEMM in one pass: the native operands are read (8 bytes per
         # element) and the C planes written; HBM bounds it for tall-skinny shapes
-        kernel = "fused_native_kernel<Signed,Vec,NP> + residue_finalize_kernel"
+        kernel = "fused_native_kernel<Signed,NP> + residue_finalize_kernel"
         workload = workload.replace("pack+GEMM", "fused pack+GEMM")
         gemm_bytes = 8 * K * (M + N) + P * M * N
         gbs = gemm_bytes / ((stage[0] + stage[1] + stage[2]) * 1e-3) / 1e9

@@ -11,8 +11,10 @@
 // only below a workspace limit.
 //
 // Work split: a workgroup owns a 128 x 128 output tile, a pair of planes and
-// one K slice. Its eight waves run two per SIMD, so one wave's conversion
-// arithmetic issues next to the other's MFMAs and LDS traffic. Roles:
+// one K slice. Its twelve waves run three per SIMD: two converter waves and
+// one MFMA wave each (a single wave issues a VALU instruction only every six
+// or seven cycles, so the conversion needs two waves per SIMD to keep the VALU
+// busy, and the MFMAs issue from a third). Roles:
 //   * conversion: waves 0-3 take A, waves 4-7 take B, and every load is
 //     coalesced: an A load covers four rows x 32 k (16 lanes per 256-byte row
 //     segment, two k per lane), a B load one k row x 128 columns (two columns
@@ -23,10 +25,11 @@
 //     v_dot4_u32_u8 and a 24-bit quotient, or one dot product when every
 //     element of the wave's step fits in 32 bits) and stores its residues
 //     into the k-contiguous stage (2 bytes per A row, 8 per B column);
-//   * MFMA: wave w multiplies plane w / 4 of the pair over a 64 x 64 quadrant
-//     (2 x 2 blocks of v_mfma_i32_32x32x32_i8, 64 accumulator registers),
-//     one step behind the conversion: the residue stages are double-buffered
-//     and one barrier per step separates a stage's writers from its readers.
+//   * MFMA: wave 8 + q multiplies both planes of the pair over the 64 x 64
+//     quadrant q (2 x 2 blocks of v_mfma_i32_32x32x32_i8 per plane, 128
+//     accumulator registers), one step behind the conversion: the residue
+//     stages are double-buffered and one barrier per step separates a stage's
+//     writers from its readers.
 // Residue stage layout per plane and operand: [2 k-chunks][128 rows or
 // columns][16 bytes], so both the conversion's stores and the fragment reads
 // (lane l: row or column l & 31 of a block, k-chunk l >> 5) are contiguous
@@ -49,7 +52,7 @@ namespace {
 
 typedef int v2i __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 512;                        // eight waves, two per SIMD
+constexpr int kThreads = 1024;                       // sixteen waves, four per SIMD
 constexpr int kTileM = 128;                          // output rows per workgroup
 constexpr int kTileN = 128;                          // output columns per workgroup
 constexpr int kStepK = 32;                           // K per step (one MFMA depth)
@@ -64,12 +67,12 @@ constexpr int64_t kMinSliceK = 512;                  // 16 steps: amortizes the 
 constexpr uint64_t kMaxWorkspace = uint64_t{64} << 20;
 constexpr uint32_t kOutOfRange = 0x80000000u;        // a buffer offset past every resource
 
-// A lane's eight 16-byte loads of one step, as issued. Element (j, h) is
-// v[j][2h] (low half) and v[j][2h + 1] (high half): for an A lane row
-// 4j + (lane >> 4) of its wave's 32 rows at k = 2 (lane & 15) + h, for a B
-// lane k = j of its column h.
+// A lane's four 16-byte loads of one step, as issued. Element (j, h) is
+// v[j][2h] (low half) and v[j][2h + 1] (high half): for an A lane row 4j +
+// (lane >> 4) of its wave's 16 rows at k = 2 (lane & 15) + h, for a B lane k =
+// j of its wave's 4 k rows at column h of its column pair.
 struct Raw {
-  v4i v[8];
+  v4i v[4];
 };
 
 // Grid: x = output tile (tiles_n per tile row), y = K slice, z = plane pair
@@ -94,28 +97,30 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
   const int steps = static_cast<int>((ke - kb + kStepK - 1) / kStepK);
   const bool ragged = (ke - kb) % kStepK != 0;  // the last step ends inside its 32 k
   const int64_t rows_valid = min(static_cast<int64_t>(kTileM), a.m - m0);
+
+  // ---- conversion ------------------------------------------------------------
+  // Waves 0-7 take A, waves 8-15 take B, and every load is coalesced. A wave
+  // c: rows 16c + 4j + (lane >> 4), j = 0..3, at k 2 (lane & 15) and 2 (lane &
+  // 15) + 1 of the step (16 lanes per 256-byte row segment, four rows per
+  // load). B wave 8 + c: k rows 4c .. 4c + 3 at columns 2 lane and 2 lane + 1
+  // (one contiguous 1 KB k row per load). Rows past m and k past the operand
+  // read 0 through the resources' ranges, which end at the operands' last
+  // logical elements (a row's offset past the last valid row exceeds the
+  // range since lda >= k). Column pairs past n get an offset outside every
+  // resource. A pair that straddles n reads its second column from the row
+  // padding (strides are even); the epilogue stores zero for that column.
+  const bool is_a = wave < 8;
+  const int c = wave & 7;
   const ModulusConsts mc0 = pc.mod[p0];
   const ModulusConsts mc1 = pc.mod[NP > 1 ? p0 + 1 : p0];
-
-  // ---- conversion role -------------------------------------------------------
-  // A lanes (waves 0-3): rows 32 * wave + 4j + (lane >> 4), j = 0..7, k
-  // 2 (lane & 15) and 2 (lane & 15) + 1 of the step. B lanes (waves 4-7):
-  // columns 2 * lane and 2 * lane + 1, k 8 * (wave - 4) .. +7. Rows past m and
-  // k past the operand read 0 through the resources' ranges, which end at the
-  // operands' last logical elements (a row's offset past the last valid row
-  // exceeds the range since lda >= k). Column pairs past n get an offset
-  // outside every resource. A pair that straddles n reads its second column
-  // from the row padding (strides are even); the epilogue stores zero for
-  // that column.
-  const bool is_a = wave < 4;
-  const int ra = 32 * wave + (lane >> 4);  // an A lane's first row (then +4 per load)
-  const int kfirst = is_a ? 2 * (lane & 15) : 8 * (wave - 4);  // the lane's first k within a step
+  const int ra = 16 * c + (lane >> 4);                 // an A lane's first row (then +4 per load)
+  const int kfirst = is_a ? 2 * (lane & 15) : 4 * c;  // the lane's first k within a step
   const uint32_t lda8 = static_cast<uint32_t>(a.lda) * 8u, ldb8 = static_cast<uint32_t>(a.ldb) * 8u;
   const uint32_t voff = is_a ? static_cast<uint32_t>(ra) * lda8 + 8u * kfirst
                              : (n0 + 2 * lane < a.n ? static_cast<uint32_t>(kfirst) * ldb8 + 16u * lane : kOutOfRange);
+  const uint32_t vstride = is_a ? 4u * lda8 : ldb8;  // bytes between a lane's loads
   const uint64_t* const abase = static_cast<const uint64_t*>(a.a) + m0 * a.lda;
   const uint64_t* const bbase = static_cast<const uint64_t*>(a.b) + n0;
-  const uint32_t vstride = is_a ? 4u * lda8 : ldb8;  // bytes between a lane's loads
   auto load = [&](Raw& x, int s) {
     const int64_t k0 = kb + static_cast<int64_t>(kStepK) * s;
     const int64_t krows = min(static_cast<int64_t>(kStepK), a.k - k0);
@@ -123,7 +128,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
         is_a ? make_rsrc(abase + k0, ((rows_valid - 1) * a.lda + a.k - k0) * 8)
              : make_rsrc(bbase + k0 * a.ldb, ((krows - 1) * a.ldb + a.n - n0) * 8);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 4; ++j)
       x.v[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + vstride * j, 0, 0));
   };
   // Elements at k >= ke of the slice's last, ragged step belong to the next
@@ -131,180 +136,173 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
   auto mask_tail = [&](Raw& x, int s) {
     const int64_t first = kb + static_cast<int64_t>(kStepK) * s + kfirst;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
         if (first + (is_a ? h : j) >= ke) x.v[j][2 * h] = x.v[j][2 * h + 1] = 0;
   };
-  // A: rows ra + 4j, k-chunk kfirst / 16, bytes kfirst % 16 .. +1 of each
-  // row's chunk: one 2-byte store per row. B: columns 2 lane and 2 lane + 1,
-  // k-chunk kfirst / 16, bytes 8 .. 15 of each column's chunk when kfirst % 16
-  // = 8: one 8-byte store per column.
-  int8_t* const dst_off = is_a ? lds + (kfirst >> 4) * kChunkLds + ra * 16 + (kfirst & 15)
-                               : lds + kOperandLds + (kfirst >> 4) * kChunkLds + 2 * lane * 16 + (kfirst & 8);
+  // Stage addresses: A rows ra + 4j, k-chunk kfirst / 16, bytes kfirst % 16
+  // .. +1 of each row's chunk (one 2-byte store per row); B columns 2 lane and
+  // 2 lane + 1, k-chunk kfirst / 16, bytes kfirst % 16 .. +3 of each column's
+  // chunk (one 4-byte store per column).
+  int8_t* const dst0 = is_a ? lds + (kfirst >> 4) * kChunkLds + ra * 16 + (kfirst & 15)
+                            : lds + kOperandLds + (kfirst >> 4) * kChunkLds + 2 * lane * 16 + (kfirst & 15);
+  // One plane's 8 residues of the lane, stored into the stage. The reduction
+  // runs in phases over the 8 elements (dot products, then shifts, quotients
+  // and remainders) so independent chains interleave; the modulus-256 plane
+  // (the low byte of each element) is a separate instantiation so that
+  // neither form carries the other's selects.
+  auto part = [&](auto fast, auto m256c, auto is_a_c, const Raw& x, const ModulusConsts& mc, int8_t* dst) {
+    constexpr bool kFast = decltype(fast)::value;
+    constexpr bool kM256 = decltype(m256c)::value;
+    constexpr bool kA = decltype(is_a_c)::value;
+    // r[j][h]: the element's residue (plus H when m < 256) in its low byte
+    uint32_t r[4][2];
+    const uint32_t m_comp = 256u - mc.m;
+    if constexpr (kM256) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) r[j][h] = static_cast<uint32_t>(x.v[j][2 * h]);
+    } else {
+      // the fast signed form is the accumulator reduction of lo ^ 2^31
+      constexpr bool kI32 = kFast && Signed;
+      const uint32_t shift = kI32 ? mc.q_shift : mc.pq_shift;
+      const uint32_t recip = kI32 ? mc.q_recip : mc.pq_recip;
+      const uint32_t off = kI32 ? mc.off_i32 : Signed ? mc.off_i64 : mc.off_u64;
+      uint32_t s[4][2], q[4][2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t lo = static_cast<uint32_t>(x.v[j][2 * h]);
+          s[j][h] = __builtin_amdgcn_udot4(kI32 ? lo ^ 0x80000000u : lo, mc.pow_lo, off, false);
+        }
+      if constexpr (!kFast) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t hi = static_cast<uint32_t>(x.v[j][2 * h + 1]);
+            s[j][h] = __builtin_amdgcn_udot4(Signed ? hi ^ 0x80000000u : hi, mc.pow_hi, s[j][h], false);
+          }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) q[j][h] = s[j][h] << shift;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) q[j][h] = mulhi_u24(q[j][h], recip);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) r[j][h] = mad_u24(q[j][h], m_comp, s[j][h]);
+    }
+    const uint32_t half2 = mc.half * 0x00010001u;
+    auto pack4 = [&](uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3) {
+      if constexpr (kM256)
+        return pack_low_bytes(r0, r1, r2, r3);
+      else
+        return pack_centered(r0, r1, r2, r3, half2);
+    };
+    if constexpr (kA) {
+      // rows 8q and 8q + 4 share a packed dword: its low half goes to one
+      // row, its high half to the other
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t w = pack4(r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]);
+        *reinterpret_cast<uint16_t*>(dst + 8 * q * 16) = static_cast<uint16_t>(w);
+        *reinterpret_cast<uint16_t*>(dst + (8 * q + 4) * 16) = static_cast<uint16_t>(w >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<uint32_t*>(dst + 16 * h) = pack4(r[0][h], r[1][h], r[2][h], r[3][h]);
+    }
+  };
+  auto plane_of = [&](auto fast, const Raw& x, const ModulusConsts& mc, int off) {
+    if (is_a) {
+      if (mc.m == 256u)
+        part(fast, std::true_type{}, std::true_type{}, x, mc, dst0 + off);
+      else
+        part(fast, std::false_type{}, std::true_type{}, x, mc, dst0 + off);
+    } else {
+      if (mc.m == 256u)
+        part(fast, std::true_type{}, std::false_type{}, x, mc, dst0 + off);
+      else
+        part(fast, std::false_type{}, std::false_type{}, x, mc, dst0 + off);
+    }
+  };
   auto convert = [&](const Raw& x, int stage) {
     uint32_t wide = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const uint32_t lo = static_cast<uint32_t>(x.v[j][2 * h]), hi = static_cast<uint32_t>(x.v[j][2 * h + 1]);
         wide |= Signed ? hi ^ static_cast<uint32_t>(static_cast<int32_t>(lo) >> 31) : hi;
       }
-    // One plane's residues, stored into its stage. The modulus-256 plane
-    // (the low byte of each element) is a separate instantiation so that
-    // neither form carries the other's selects.
-    auto plane_as = [&](auto fast, auto m256c, const ModulusConsts& mc, int8_t* dst) {
-      constexpr bool kFast = decltype(fast)::value;
-      constexpr bool kM256 = decltype(m256c)::value;
-      // r[j][h]: the element's residue (plus H when m < 256) in its low byte.
-      // The reduction runs in phases over all 16 elements (dot products, then
-      // shifts, quotients and remainders), so independent chains interleave
-      // and each dependent pair is 16 instructions apart.
-      uint32_t r[8][2];
-      const uint32_t m_comp = 256u - mc.m;
-      if constexpr (kM256) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) r[j][h] = static_cast<uint32_t>(x.v[j][2 * h]);
-      } else {
-        // the fast signed form is the accumulator reduction of lo ^ 2^31
-        constexpr bool kI32 = kFast && Signed;
-        const uint32_t shift = kI32 ? mc.q_shift : mc.pq_shift;
-        const uint32_t recip = kI32 ? mc.q_recip : mc.pq_recip;
-        const uint32_t off = kI32 ? mc.off_i32 : Signed ? mc.off_i64 : mc.off_u64;
-        uint32_t s[8][2], q[8][2];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const uint32_t lo = static_cast<uint32_t>(x.v[j][2 * h]);
-            s[j][h] = __builtin_amdgcn_udot4(kI32 ? lo ^ 0x80000000u : lo, mc.pow_lo, off, false);
-          }
-        if constexpr (!kFast) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const uint32_t hi = static_cast<uint32_t>(x.v[j][2 * h + 1]);
-              s[j][h] = __builtin_amdgcn_udot4(Signed ? hi ^ 0x80000000u : hi, mc.pow_hi, s[j][h], false);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) q[j][h] = s[j][h] << shift;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) q[j][h] = mulhi_u24(q[j][h], recip);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) r[j][h] = mad_u24(q[j][h], m_comp, s[j][h]);
-      }
-      const uint32_t half2 = mc.half * 0x00010001u;
-      auto pack4 = [&](uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3) {
-        if constexpr (kM256)
-          return pack_low_bytes(r0, r1, r2, r3);
-        else
-          return pack_centered(r0, r1, r2, r3, half2);
-      };
-      if (is_a) {
-        // rows 4j and 4(j + 1) share a packed dword: its low half goes to one
-        // row, its high half to the other
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t w = pack4(r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]);
-          *reinterpret_cast<uint16_t*>(dst + 8 * q * 16) = static_cast<uint16_t>(w);
-          *reinterpret_cast<uint16_t*>(dst + (8 * q + 4) * 16) = static_cast<uint16_t>(w >> 16);
-        }
-      } else {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          *reinterpret_cast<v2i*>(dst + 16 * h) = v2i{static_cast<int>(pack4(r[0][h], r[1][h], r[2][h], r[3][h])),
-                                                      static_cast<int>(pack4(r[4][h], r[5][h], r[6][h], r[7][h]))};
-      }
-    };
-    auto plane = [&](auto fast, const ModulusConsts& mc, int8_t* dst) {
-      if (mc.m == 256u)
-        plane_as(fast, std::true_type{}, mc, dst);
-      else
-        plane_as(fast, std::false_type{}, mc, dst);
-    };
-    int8_t* const dst = dst_off + stage * kStageLds;
+    const int off = stage * kStageLds;
     // one branch per wave: the 32-bit form when no lane has a wide element
     if (__builtin_amdgcn_ballot_w64(wide != 0u) == 0u) {
-      plane(std::true_type{}, mc0, dst);
-      if constexpr (NP > 1) plane(std::true_type{}, mc1, dst + kPlaneLds);
+      plane_of(std::true_type{}, x, mc0, off);
+      if constexpr (NP > 1) plane_of(std::true_type{}, x, mc1, off + kPlaneLds);
     } else {
-      plane(std::false_type{}, mc0, dst);
-      if constexpr (NP > 1) plane(std::false_type{}, mc1, dst + kPlaneLds);
+      plane_of(std::false_type{}, x, mc0, off);
+      if constexpr (NP > 1) plane_of(std::false_type{}, x, mc1, off + kPlaneLds);
     }
   };
 
-  // ---- MFMA role -------------------------------------------------------------
-  // Wave w: plane w / 4 of the pair, quadrant rows 64 * ((w >> 1) & 1), columns
-  // 64 * (w & 1). With B as src0 and A as src1, register 4g+e of acc[i][j]
-  // holds C[row][col] with row = m0 + 64 wm + 32 i + (l & 31) and col = n0 +
-  // 64 wn + 32 j + 8 g + 4 (l >> 5) + e.
-  const int pl = wave >> 2, wm = (wave >> 1) & 1, wn = wave & 1;
+  // ---- MFMA ------------------------------------------------------------------
+  // Wave w multiplies plane w >> 3 of the pair over rows 64 wm .. 64 wm + 63
+  // and columns 64 wn + 32 hn .. + 31 (wm = (w >> 2) & 1, wn = (w >> 1) & 1,
+  // hn = w & 1): two v_mfma_i32_32x32x32_i8 per step, 32 accumulator
+  // registers. With B as src0 and A as src1, register 4g+e of acc[i] holds
+  // C[row][col] with row = m0 + 64 wm + 32 i + (l & 31) and col = n0 + 64 wn +
+  // 32 hn + 8 g + 4 (l >> 5) + e.
+  const int pl = wave >> 3, wm = (wave >> 2) & 1, wn = (wave >> 1) & 1, hn = wave & 1;
   const bool mfma_wave = pl < NP;
   const int frag = (lane >> 5) * kChunkLds + (lane & 31) * 16;
-  v16i acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
-  auto mma = [&](const int8_t* stage) {
+  v16i acc[2] = {v16i{}, v16i{}};
+  auto mma = [&](int stage) {
     if (!mfma_wave) return;
-    const int8_t* const sa = stage + pl * kPlaneLds + frag;
+    const int8_t* const sa = lds + stage * kStageLds + pl * kPlaneLds + frag;
     const int8_t* const sb = sa + kOperandLds;
-    v4i af[2], bf[2];
+    const v4i bf = *reinterpret_cast<const v4i*>(sb + (64 * wn + 32 * hn) * 16);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const v4i*>(sa + (64 * wm + 32 * i) * 16);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const v4i*>(sb + (64 * wn + 32 * j) * 16);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+    for (int i = 0; i < 2; ++i) {
+      const v4i af = *reinterpret_cast<const v4i*>(sa + (64 * wm + 32 * i) * 16);
+      acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af, acc[i], 0, 0, 0);
+    }
   };
 
   // ---- pipeline ----------------------------------------------------------------
-  // Step s: step s-1 (stage (s-1) & 1, converted in the last step) is
-  // multiplied, step s is converted into stage s & 1 and the raw values of
-  // step s+2 are requested (those of step s+1 are in flight); the barrier that
-  // ends the step publishes stage s & 1 and retires every read of stage
-  // (s-1) & 1, which step s+1 overwrites. Three register sets hold the raw
-  // values (the loop is unrolled by three so each set keeps its registers).
-  auto step = [&](Raw& cur, Raw& ahead, int s) {
-    // the MFMAs of step s-1 first: they run in the matrix pipe while the
-    // conversion below occupies the VALU
-    if (s > 0) mma(lds + ((s - 1) & 1) * kStageLds);
+  // Step s: the raw values of step s+1 are requested (unconditionally, so
+  // every step has the same loads in flight; past the end the last step is
+  // loaded again and never converted), step s-1 (stage (s-1) & 1, converted
+  // in the last step) is multiplied and step s is converted into stage s & 1;
+  // the barrier that ends the step publishes stage s & 1 and retires every
+  // read of stage (s-1) & 1, which step s+1 overwrites. Two register sets
+  // hold the raw values (the loop is unrolled by two so each set keeps its
+  // registers).
+  auto step = [&](Raw& cur, Raw& next, int s) {
+    load(next, min(s + 1, steps - 1));
+    if (s > 0) mma((s - 1) & 1);
     if (ragged && s == steps - 1) mask_tail(cur, s);
     convert(cur, s & 1);
-    // The loads of step s+2 go out after the conversion: issued at the top of
-    // the step, the workgroup's 64 loads queue in the texture path ahead of
-    // the later waves' MFMAs and conversion (measured 10% slower). They are
-    // unconditional, so every step has the same loads in flight (past the
-    // end the last step is loaded again and never converted).
-    load(ahead, min(s + 2, steps - 1));
     __syncthreads();
   };
-  Raw r0, r1, r2;
+  Raw r0, r1;
   load(r0, 0);
-  load(r1, min(1, steps - 1));
   for (int s = 0;;) {
-    step(r0, r2, s);
+    step(r0, r1, s);
     if (++s >= steps) break;
     step(r1, r0, s);
     if (++s >= steps) break;
-    step(r2, r1, s);
-    if (++s >= steps) break;
   }
-  mma(lds + ((steps - 1) & 1) * kStageLds);
+  mma((steps - 1) & 1);
 
   // ---- epilogue --------------------------------------------------------------
   // Each int32 sum x (|x| <= 2^30) reduced to its centered residue, four
@@ -321,70 +319,75 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
   for (int i = 0; i < 2; ++i) {
     const int64_t row = m0 + 64 * wm + 32 * i + (lane & 31);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int g = 0; g < 4; ++g) {
+      const int64_t col = n0 + 64 * wn + 32 * hn + 8 * g + 4 * (lane >> 5);
+      uint32_t r[4];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t col = n0 + 64 * wn + 32 * j + 8 * g + 4 * (lane >> 5);
-        uint32_t r[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t u = static_cast<uint32_t>(acc[i][j][4 * g + e]) ^ 0x80000000u;
-          r[e] = mc.m == 256u ? u : residue_plus_half(u, mc, m_comp);
-        }
-        uint32_t packed =
-            mc.m == 256u ? pack_low_bytes(r[0], r[1], r[2], r[3]) : pack_centered(r[0], r[1], r[2], r[3], half2);
-        if (col + 4 > a.n) packed &= col >= a.n ? 0u : 0xFFFFFFFFu >> (8 * (col + 4 - a.n));
-        if (row < a.m && col < a.ldc) *reinterpret_cast<uint32_t*>(w + row * a.ldc + col) = packed;
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t u = static_cast<uint32_t>(acc[i][4 * g + e]) ^ 0x80000000u;
+        r[e] = mc.m == 256u ? u : residue_plus_half(u, mc, m_comp);
       }
+      uint32_t packed =
+          mc.m == 256u ? pack_low_bytes(r[0], r[1], r[2], r[3]) : pack_centered(r[0], r[1], r[2], r[3], half2);
+      if (col + 4 > a.n) packed &= col >= a.n ? 0u : 0xFFFFFFFFu >> (8 * (col + 4 - a.n));
+      if (row < a.m && col < a.ldc) *reinterpret_cast<uint32_t*>(w + row * a.ldc + col) = packed;
     }
   }
 }
 
-// Adds the slices' centered residues of four consecutive cells (one dword per
-// slice) and writes their centered residue into C (reference
+// Adds the slices' centered residues of 16 consecutive cells (one 16-byte
+// chunk per slice) and writes their centered residue into C (reference
 // cpu_reference.cpp:156-311: the plane result is the sum's residue). A block
-// covers 32 dwords; its eight 32-thread groups each add every eighth slice,
+// covers 32 chunks; its eight 32-thread groups each add every eighth slice,
 // so the loads of many slices are in flight at once, and group 0 combines
-// the eight partial sums.
-constexpr int kFinalWords = 32;
+// the eight partial sums. m * ldc is a multiple of 16 (ldc is).
+constexpr int kFinalChunks = 32;
 constexpr int kFinalGroups = 8;
 __global__ __launch_bounds__(256) void residue_finalize_kernel(const int8_t* ws, int8_t* c, int64_t m, int64_t ldc,
                                                                int64_t pitch_c, uint32_t nplanes, uint32_t slices,
                                                                PlaneConsts pc) {
-  __shared__ int32_t part[kFinalGroups][kFinalWords][4];
-  const int64_t words_per_plane = m * ldc / 4;
-  const int64_t total = words_per_plane * nplanes;
-  const int64_t slice_words = static_cast<int64_t>(nplanes) * words_per_plane;
-  const uint32_t* const src = reinterpret_cast<const uint32_t*>(ws);
-  const int lw = threadIdx.x % kFinalWords;
-  const int grp = threadIdx.x / kFinalWords;
-  for (int64_t w0 = static_cast<int64_t>(blockIdx.x) * kFinalWords; w0 < total;
-       w0 += static_cast<int64_t>(gridDim.x) * kFinalWords) {
-    const int64_t w = w0 + lw;
-    int32_t sum[4] = {0, 0, 0, 0};
-    if (w < total) {
+  __shared__ int32_t part[kFinalGroups][16][kFinalChunks];
+  const int64_t chunks_per_plane = m * ldc / 16;
+  const int64_t total = chunks_per_plane * nplanes;
+  const int64_t slice_chunks = static_cast<int64_t>(nplanes) * chunks_per_plane;
+  const v4i* const src = reinterpret_cast<const v4i*>(ws);
+  const int lc = threadIdx.x % kFinalChunks;
+  const int grp = threadIdx.x / kFinalChunks;
+  for (int64_t c0 = static_cast<int64_t>(blockIdx.x) * kFinalChunks; c0 < total;
+       c0 += static_cast<int64_t>(gridDim.x) * kFinalChunks) {
+    const int64_t ch = c0 + lc;
+    int32_t sum[16] = {};
+    if (ch < total) {
       for (uint32_t s = grp; s < slices; s += kFinalGroups) {
-        const uint32_t v = src[static_cast<int64_t>(s) * slice_words + w];
+        const v4i v = src[static_cast<int64_t>(s) * slice_chunks + ch];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sum[e] += static_cast<int32_t>(static_cast<int8_t>(v >> (8 * e)));
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            sum[4 * d + e] += static_cast<int32_t>(static_cast<int8_t>(static_cast<uint32_t>(v[d]) >> (8 * e)));
       }
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) part[grp][lw][e] = sum[e];
+    for (int e = 0; e < 16; ++e) part[grp][e][lc] = sum[e];
     __syncthreads();
-    if (grp == 0 && w < total) {
+    if (grp == 0 && ch < total) {
 #pragma unroll
       for (int g = 1; g < kFinalGroups; ++g)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sum[e] += part[g][lw][e];
-      const uint32_t plane = static_cast<uint32_t>(w / words_per_plane);
-      const int64_t in_plane = w - static_cast<int64_t>(plane) * words_per_plane;
+        for (int e = 0; e < 16; ++e) sum[e] += part[g][e][lc];
+      const uint32_t plane = static_cast<uint32_t>(ch / chunks_per_plane);
+      const int64_t in_plane = ch - static_cast<int64_t>(plane) * chunks_per_plane;
       const ModulusConsts mc = pc.mod[plane];
-      uint32_t r[4];
+      const uint32_t m_comp = 256u - mc.m, half2 = mc.half * 0x00010001u;
+      v4i out;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] = residue_plus_half(static_cast<uint32_t>(sum[e]) ^ 0x80000000u, mc, 256u - mc.m);
-      *reinterpret_cast<uint32_t*>(c + static_cast<int64_t>(plane) * pitch_c + in_plane * 4) =
-          pack_centered(r[0], r[1], r[2], r[3], mc.half * 0x00010001u);
+      for (int d = 0; d < 4; ++d) {
+        uint32_t r[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = residue_plus_half(static_cast<uint32_t>(sum[4 * d + e]) ^ 0x80000000u, mc, m_comp);
+        out[d] = static_cast<int>(pack_centered(r[0], r[1], r[2], r[3], half2));
+      }
+      *reinterpret_cast<v4i*>(c + static_cast<int64_t>(plane) * pitch_c + in_plane * 16) = out;
     }
     __syncthreads();
   }
@@ -427,10 +430,11 @@ bool fused_args_ok(const FusedArgs& a) {
   if (!choose_fused_shape(a.m, a.n, a.k, a.nplanes, a.ldc, expect) || expect.slices != a.shape.slices ||
       expect.k_slice != a.shape.k_slice)
     return false;
-  if (a.pitch_c < a.m * a.ldc || (reinterpret_cast<uintptr_t>(a.c) & 3u) != 0 ||
-      (reinterpret_cast<uintptr_t>(a.ws) & 3u) != 0)
+  // the finalize moves 16-byte chunks of the workspace and of C's planes
+  if (a.pitch_c < a.m * a.ldc || a.pitch_c % 16 != 0 || (reinterpret_cast<uintptr_t>(a.c) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(a.ws) & 15u) != 0)
     return false;
-  // the direct-to-LDS loads read 16-byte chunks at 32-bit byte offsets
+  // the operand loads read 16-byte chunks at 32-bit byte offsets
   return fused_operands_ok(a.a, a.lda, a.b, a.ldb);
 }
 
@@ -454,8 +458,8 @@ hipError_t launch_fused_native(const FusedArgs& a, const PlaneConsts& consts, hi
   if (rest) launch(std::integral_constant<int, 1>{}, 1, full * kGroupPlanes);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t words = static_cast<int64_t>(a.nplanes) * a.m * a.ldc / 4;
-  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((words + kFinalWords - 1) / kFinalWords, 4096));
+  const int64_t chunks = static_cast<int64_t>(a.nplanes) * a.m * a.ldc / 16;
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((chunks + kFinalChunks - 1) / kFinalChunks, 4096));
   hipLaunchKernelGGL(residue_finalize_kernel, dim3(blocks), dim3(256), 0, stream, a.ws, a.c, a.m, a.ldc, a.pitch_c,
                      a.nplanes, a.shape.slices, consts);
   return hipGetLastError();
