@@ -79,6 +79,37 @@ def _no_mark(_i: int) -> None:
     pass
 
 
+def attainable_mfma(achieved: float) -> dict:
+    """The dense int8 MFMA rate this MI355X sustains with random operand bytes
+    (the statistics of residue planes), measured after the timed region by
+    rns8_amd/probe/libmfma_probe.so: every CU issuing back-to-back
+    v_mfma_i32_32x32x32_i8 from registers, ~50 ms so the power controller has
+    settled. The chip is power-limited on such operands, so this, not the
+    5.0 POP/s peak, is the ceiling a GEMM on this data can approach; zero
+    operands are measured beside it for the clock contrast."""
+    import ctypes as C
+
+    lib = C.CDLL(str(ROOT / "rns8_amd" / "probe" / "libmfma_probe.so"))
+    fn = lib.rns8_probe_mfma_rate
+    fn.restype = C.c_int
+    fn.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+    out = {}
+    for key, rnd in (("random", 1), ("zero", 0)):
+        tops, ghz = C.c_double(), C.c_double()
+        rc = fn(rnd, 2000, 10, 30, C.byref(tops), C.byref(ghz))
+        if rc != 0:
+            raise RuntimeError(f"rns8_probe_mfma_rate failed with HIP error {rc}")
+        out[key] = (tops.value, ghz.value)
+    rt, rg = out["random"]
+    zt, zg = out["zero"]
+    log(f"[bench] MFMA probe: random operands {rt:.0f} TOP/s at {rg:.3f} GHz, zero operands {zt:.0f} TOP/s at "
+        f"{zg:.3f} GHz")
+    return {"value": round(rt, 1), "unit": "TOP/s", "clock_ghz": round(rg, 3), "frac": round(achieved / rt, 4),
+            "zero_operands": {"value": round(zt, 1), "clock_ghz": round(zg, 3)},
+            "source": "rns8_amd/probe: back-to-back v_mfma_i32_32x32x32_i8 on every CU with random int8 "
+                      "operands, measured after the timed region"}
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -310,6 +341,8 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": None,
     }
+    if roofline["bound"] == "mfma":
+        roofline["attainable"] = attainable_mfma(roofline["achieved"])
 
     if tiled:
         # exact in int64 (|C| <= 2^62): sampled rows of every tile row against numpy
@@ -515,6 +548,7 @@ def grouped_bench(args) -> int:
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None, "per_launch_ops": gemm_ops},
         "cpu_baseline": None,
     }
+    result["roofline"]["attainable"] = attainable_mfma(achieved)
     print(json.dumps(result))
     for e in (start, stop):
         hip.event_destroy(e)
@@ -647,6 +681,7 @@ def finite_or_wide_bench(args) -> int:
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None, "per_launch_ops": ops * P},
         "cpu_baseline": None,
     }
+    result["roofline"]["attainable"] = attainable_mfma(achieved)
     print(json.dumps(result))
     for e in (start, stop):
         hip.event_destroy(e)
