@@ -40,7 +40,14 @@ CONFIGS = {
     # per-tile bounds (128 x 128 tiles) on C3's shape: A's tile rows cycle
     # through magnitudes 2^1 .. 2^25, so tiles select prefixes 5 .. 9
     "tiled": ("i64", 4096, 4096, 4096, 25, 1 << 62, 9, False),
+    # skinny products (the reference's GEMV lanes, N = 1 and N <= 8, and its
+    # persistent-small kernel, M * N <= 64): the GEMM stage is bound by reading
+    # A's planes once
+    "gemv1": ("i64", 8192, 1, 8192, 25, 1 << 62, 9, True),
+    "gemv8": ("i64", 8192, 8, 8192, 25, 1 << 62, 9, True),
+    "small64": ("i64", 8, 8, 1 << 20, 25, 1 << 62, 9, True),
 }
+SKINNY = ("gemv1", "gemv8", "small64")
 # grouped resident GEMM: GROUP_TASKS same-shape int64 tasks per step
 GROUPED = ("i64", 1024, 1024, 1024, 25, 1 << 62, 9, True)
 GROUP_TASKS = 8
@@ -283,7 +290,7 @@ def main() -> int:
         kernel = "plane_gemm_kernel<Cfg<4,4>,1,true,false,false> (256x256 tiles, persistent)"
     elif args.config == "c5":
         workload = f"c5 {sem} {M}x{N}x{K} prefix {P}, pack+GEMM+Garner device-resident"
-        kernel = "plane_gemm_kernel<Cfg<2,2>,2,true,false,false> split-K + splitk_finalize_kernel"
+        kernel = "plane_gemm_kernel<Cfg<2,2>,2,true,false,false> K split + residue_finalize_kernel"
     else:
         workload = f"{args.config} {sem} {M}x{N}x{K} prefix {P}, pack+GEMM+Garner device-resident"
         kernel = "plane_gemm_kernel<Cfg<2,2>,2,true,false,false> (128x128 tiles, persistent)"
@@ -307,6 +314,14 @@ def main() -> int:
         workload = workload.replace("pack+GEMM", "fused pack+GEMM")
         gemm_bytes = 8 * K * (M + N) + P * M * N
         gbs = gemm_bytes / ((stage[0] + stage[1] + stage[2]) * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "kernel": kernel, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "per_launch_bytes": gemm_bytes}
+    elif args.config in SKINNY:
+        # at most 16 columns: the GEMM reads A's planes once and B's (padded
+        # to 16 columns) once, so HBM bounds it
+        kernel = "skinny_gemm_kernel<RB>" + (" K split + residue_finalize_kernel" if args.config == "small64" else "")
+        gemm_bytes = P * (M * K + K * 16 + M * 16)
+        gbs = gemm_bytes / (stage[2] * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": kernel, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "per_launch_bytes": gemm_bytes}
     elif args.config == "c5":

@@ -99,10 +99,11 @@ RNS8_API rns8_status rns8_mi355x_gemm_finite_u8_async(
  * per-tile bounds) without a workspace, for callers that cannot allocate:
  * code under HIP graph capture, tight serving loops, harnesses that forbid
  * allocation. No counterpart in the reference. The call allocates nothing,
- * on the device or the host: split-K partials (tall-skinny shapes) go to a
- * static per-device scratch array of 16 MiB that the library holds until the
- * process ends (its address is looked up when a context is created). Plans
- * whose split-K partials exceed 16 MiB return RNS8_WORKSPACE_TOO_SMALL;
+ * on the device or the host: split-K residues (shapes with few output tiles
+ * and a long K) go to a static per-device scratch array of 4 MiB that the
+ * library holds until the process ends (its address is looked up when a
+ * context is created). Plans whose split-K residues exceed 4 MiB return
+ * RNS8_WORKSPACE_TOO_SMALL;
  * exact-wide plans return RNS8_UNSUPPORTED_BACKEND (their admission proofs
  * live in host memory). Every call on one device shares that device's
  * scratch: calls that overlap on one device (on different streams, or from

@@ -199,6 +199,15 @@ class Plan(_Handle):
     def prefix(self) -> int:
         return self.schedule_info().max_selected_prefix
 
+    def backend_info(self) -> abi.PlanBackendInfo:
+        info = abi.new_struct(abi.PlanBackendInfo)
+        check(lib().rns8_get_plan_backend_info(self.ptr, C.byref(info)), "rns8_get_plan_backend_info")
+        return info
+
+    def selected_kernel(self) -> str:
+        """The kernel the plan's GEMM runs, as rns8_get_plan_backend_info names it."""
+        return bytes(self.backend_info().selected_kernel).split(b"\0", 1)[0].decode()
+
 
 class Workspace(_Handle):
     _destroy = "rns8_destroy_workspace"

@@ -662,7 +662,7 @@ rns8_status rns8_get_backend_capability_info(rns8_backend_kind backend, rns8_bac
     copy_text(out->library_name, sizeof(out->library_name), "rns8_mi355x");
     copy_text(out->library_version, sizeof(out->library_version), "0.1");
     copy_text(out->epilogue_mode, sizeof(out->epilogue_mode), ours ? "in_register_centered_reduction" : "");
-    copy_text(out->workspace_mode, sizeof(out->workspace_mode), ours ? "resident_planes_splitk_int32" : "");
+    copy_text(out->workspace_mode, sizeof(out->workspace_mode), ours ? "resident_planes_splitk_int8_residues" : "");
     copy_text(out->isa_evidence, sizeof(out->isa_evidence), ours ? "gfx950 v_mfma_i32_32x32x32_i8" : "");
     copy_text(out->status, sizeof(out->status), ours ? (hip ? "available" : "no_hip_device") : "unsupported_backend");
     copy_text(out->detail, sizeof(out->detail),
@@ -715,11 +715,11 @@ rns8_status init_plan(const rns8_gemm_desc& d, rns8_backend_kind backend, rns8_p
     plan.desc.zero_b_cols_count = plan.schedule.zero_b_cols.size();
   }
   const uint32_t planes = uses_finite_storage(d.semantics) ? 1u : selected;
-  const int64_t kblock = d.k > kSafeKBlock ? kSafeKBlock : d.k;
   // per-tile plans run the tiled unit list (no K split)
   if (!per_tile(d.bound_kind)) {
-    plan.splitk_slices = choose_splitk_slices(d.m, d.n, kblock, planes);
-    plan.splitk_bytes = splitk_workspace_bytes(d.m, d.n, kblock, planes);
+    const GemmShape shape = choose_gemm_shape(d.m, d.n, d.k, planes);
+    plan.splitk_slices = shape.slices;
+    plan.splitk_bytes = shape.ws_bytes;
     // the fused native-input GEMM shares the workspace
     if ((d.semantics == RNS8_BOUNDED_I64 || d.semantics == RNS8_BOUNDED_U64) &&
         choose_fused_shape(d.m, d.n, d.k, planes, padded_ld(d.n), plan.fused)) {
@@ -847,19 +847,24 @@ rns8_status rns8_get_plan_backend_info(const rns8_plan* plan, rns8_plan_backend_
     out->exact_differential_validated = 1;
     out->workspace_required_bytes = plan->splitk_bytes;
     const bool listed = per_tile(plan->desc.bound_kind) && !plan->schedule.entries.empty();
+    const uint32_t planes = uses_finite_storage(plan->desc.semantics) ? 1u : (plan->prefix ? plan->prefix : 1u);
+    const GemmShape shape = choose_gemm_shape(plan->desc.m, plan->desc.n, plan->desc.k, planes);
+    const bool skinny = !listed && shape.tile == 16;
     copy_text(out->selected_kernel, sizeof(out->selected_kernel),
               listed ? (plan->unit_edge == 256 ? "plane_gemm_kernel listed 256x256 units (per-tile schedule)"
                                                : "plane_gemm_kernel listed 128x128 units (per-tile schedule)")
-              : plan->splitk_slices > 1 ? "plane_gemm_kernel 128x128 split-K + splitk_finalize_kernel"
-              : choose_gemm_shape(plan->desc.m, plan->desc.n, plan->desc.k, plan->prefix ? plan->prefix : 1u).tile == 256
-                  ? "plane_gemm_kernel 256x256 tile, 4-stage LDS DMA ring"
-                  : "plane_gemm_kernel 128x128 tile, 4-stage LDS DMA ring");
+              : skinny ? (shape.slices > 1 ? "skinny_gemm_kernel 16-column rows, K split + residue_finalize_kernel"
+                                           : "skinny_gemm_kernel 16-column rows")
+              : shape.slices > 1 ? "plane_gemm_kernel 128x128 K split + residue_finalize_kernel"
+              : shape.tile == 256 ? "plane_gemm_kernel 256x256 tile, 4-stage LDS DMA ring"
+                                  : "plane_gemm_kernel 128x128 tile, 4-stage LDS DMA ring");
     copy_text(out->accelerator_library, sizeof(out->accelerator_library), "none (hand-written HIP)");
     copy_text(out->capability_status, sizeof(out->capability_status), "available");
     copy_text(out->epilogue_mode, sizeof(out->epilogue_mode), "in_register_centered_reduction");
     copy_text(out->workspace_mode, sizeof(out->workspace_mode),
-              plan->splitk_slices > 1 ? "splitk_int32_partials" : "none");
-    copy_text(out->isa_evidence, sizeof(out->isa_evidence), "gfx950 v_mfma_i32_32x32x32_i8");
+              plan->splitk_slices > 1 ? "splitk_int8_residues" : "none");
+    copy_text(out->isa_evidence, sizeof(out->isa_evidence),
+              skinny ? "gfx950 v_mfma_i32_16x16x64_i8" : "gfx950 v_mfma_i32_32x32x32_i8");
     out->accumulator_k_block_size = static_cast<uint64_t>(plan->desc.k < kSafeKBlock ? plan->desc.k : kSafeKBlock);
     out->accumulator_k_block_cap = static_cast<uint64_t>(kSafeKBlock);
     out->accumulator_modulus = uses_finite_storage(plan->desc.semantics) ? plan->desc.finite_modulus : 0;

@@ -346,7 +346,7 @@ rns8_status pack_u8(rns8_context* ctx, rns8_matrix* matrix, uint16_t modulus, co
 // ---- GEMM --------------------------------------------------------------------------
 
 rns8_status run_gemm(rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B,
-                     rns8_matrix& C, int32_t* splitk_ws, uint32_t nplanes, const PlaneConsts& consts,
+                     rns8_matrix& C, int8_t* splitk_ws, uint32_t nplanes, const PlaneConsts& consts,
                      hipStream_t stream) {
   GemmArgs g{};
   g.a = A.planes;
@@ -432,7 +432,7 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
 }
 
 // rns8_mi355x_gemm_rns_noalloc: the bounded int64/uint64 GEMM of
-// rns8_mi355x_gemm_rns_async without a workspace argument. Split-K partials
+// rns8_mi355x_gemm_rns_async without a workspace argument. Split-K residues
 // go to the library's per-device static scratch (kNoAllocScratchBytes); the
 // call allocates nothing, host or device. Exact-wide plans are refused: their
 // admission builds per-row and per-column proofs in host memory.
@@ -445,10 +445,9 @@ rns8_status gemm_rns_noalloc(rns8_context* ctx, const rns8_plan* plan, const rns
   if (plan->desc.semantics != RNS8_BOUNDED_I64 && plan->desc.semantics != RNS8_BOUNDED_U64)
     return RNS8_UNSUPPORTED_BACKEND;
   const bool tiled = per_tile_kind(plan->desc.bound_kind) && !plan->schedule.entries.empty();
-  int32_t* scratch = nullptr;
+  int8_t* scratch = nullptr;
   if (!tiled && plan->splitk_slices > 1) {
-    const int64_t kblock = plan->desc.k > kSafeKBlock ? kSafeKBlock : plan->desc.k;
-    if (splitk_workspace_bytes(plan->desc.m, plan->desc.n, kblock, plan->prefix) > kNoAllocScratchBytes)
+    if (choose_gemm_shape(plan->desc.m, plan->desc.n, plan->desc.k, plan->prefix).ws_bytes > kNoAllocScratchBytes)
       return RNS8_WORKSPACE_TOO_SMALL;
     scratch = noalloc_scratch(ctx->device_id);
     if (!scratch) return RNS8_BACKEND_FAILURE;
@@ -498,7 +497,7 @@ rns8_status gemm_native(rns8_context* ctx, const rns8_plan* plan, const T* A, in
   f.pitch_c = C->plane_pitch;
   f.nplanes = plan->prefix;
   f.kind = is_signed ? NativeKind::I64 : NativeKind::U64;
-  f.ws = reinterpret_cast<int8_t*>(ws->splitk);
+  f.ws = ws->splitk;
   f.shape = plan->fused;
   // a refused call leaves C as it was
   if (!fused_args_ok(f)) return RNS8_UNSUPPORTED_BACKEND;

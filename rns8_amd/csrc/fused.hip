@@ -458,10 +458,20 @@ hipError_t launch_fused_native(const FusedArgs& a, const PlaneConsts& consts, hi
   if (rest) launch(std::integral_constant<int, 1>{}, 1, full * kGroupPlanes);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t chunks = static_cast<int64_t>(a.nplanes) * a.m * a.ldc / 16;
+  return launch_residue_finalize(a.ws, a.c, a.m, a.ldc, a.pitch_c, a.nplanes, a.shape.slices, consts, stream);
+}
+
+hipError_t launch_residue_finalize(const int8_t* ws, int8_t* c, int64_t m, int64_t ldc, int64_t pitch_c,
+                                   uint32_t nplanes, uint32_t slices, const PlaneConsts& consts, hipStream_t stream) {
+  // the kernel moves 16-byte chunks of the workspace and of C's planes
+  if (!ws || !c || m <= 0 || ldc <= 0 || ldc % 16 != 0 || pitch_c < m * ldc || pitch_c % 16 != 0 || slices == 0 ||
+      nplanes == 0 || nplanes > kMaxPrefix || (reinterpret_cast<uintptr_t>(ws) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(c) & 15u) != 0)
+    return hipErrorInvalidValue;
+  const int64_t chunks = static_cast<int64_t>(nplanes) * m * ldc / 16;
   const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((chunks + kFinalChunks - 1) / kFinalChunks, 4096));
-  hipLaunchKernelGGL(residue_finalize_kernel, dim3(blocks), dim3(256), 0, stream, a.ws, a.c, a.m, a.ldc, a.pitch_c,
-                     a.nplanes, a.shape.slices, consts);
+  hipLaunchKernelGGL(residue_finalize_kernel, dim3(blocks), dim3(256), 0, stream, ws, c, m, ldc, pitch_c, nplanes,
+                     slices, consts);
   return hipGetLastError();
 }
 

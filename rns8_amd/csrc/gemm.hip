@@ -37,9 +37,14 @@
 //     reciprocal quotient (full-rate VALU only); 4 residues are packed per
 //     dword and staged through a per-wave LDS region (outside the stage
 //     ring) into row-contiguous 16-byte stores.
-//   * Split-K (tall-skinny K, 128x128 tiles): each slice stores its int32
-//     partial tile to its own workspace slot; a finalize kernel adds the
-//     slices, reduces to int8 and writes C (deterministic, no atomics).
+//   * Split-K (few output tiles, 128x128 tiles): one launch covers the
+//     whole K; each slice (at most 65536 K) reduces its tile like an
+//     unsplit unit and stores the centered residues to its own slot of an
+//     int8 workspace; residue_finalize adds the slots and writes C
+//     (deterministic, no atomics, a quarter of the bytes int32 partials
+//     would move).
+//   * Results at most 16 columns wide run in skinny.hip instead.
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <type_traits>
@@ -263,7 +268,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
     if constexpr (kGrouped) return tasks.t[U.task].c;
     else return args.c;
   };
-  auto base_ws = [&](const Unit& U) -> int32_t* {
+  auto base_ws = [&](const Unit& U) -> int8_t* {
     if constexpr (kGrouped) return tasks.t[U.task].ws;
     else return args.splitk_ws;
   };
@@ -442,114 +447,93 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
         static_cast<uint32_t>((wave_m * (32 * WM) + frag_row) * args.ldc + wave_n * (32 * WN) + 4 * frag_half);
     const uint32_t row_step = static_cast<uint32_t>(32 * args.ldc);
     const bool full_cols = U.n0 + BN <= args.ldc;
-    const int col_room = static_cast<int>(args.ldc - U.n0) - (wave_n * (32 * WN) + 4 * frag_half);
-    auto col_off = [&](uint32_t off, int col) {  // col = 32j + 8g within the lane's wave tile
-      return (full_cols || col < col_room) ? off + static_cast<uint32_t>(col) : 0x80000000u;
-    };
-    if (args.slices <= 1) {
-      // a listed unit's wave stores its quadrant only if the mask selects it
-      if (kListed && ((U.quad >> (wave_m * 2 + wave_n)) & 1u) == 0u) return;
-      int8_t* const Cp = base_c(U) + static_cast<int64_t>(U.plane) * args.pitch_c + U.m0 * args.ldc + U.n0;
-      const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(Cp, tile_rows * args.ldc - U.n0);
-      const uint32_t m_comp = 256u - mc.m;
-      const uint32_t half2 = mc.half * 0x00010001u;
-      // The packed residues go through this wave's slice of the epilogue LDS
-      // region (outside the stage ring, so the next unit's DMAs keep landing)
-      // so the global stores are row-contiguous 16-byte chunks; kEpiParts
-      // passes of WM / kEpiParts block rows each. Layout: row-major
-      // kEpiRow-byte rows, 16-byte chunk c of row r at c ^ ((r >> 1) &
-      // (kEpiChunks - 1)).
-      int8_t* const ep = lds + C::kLds + wave * (C::kEpiBytes / C::kEpiParts);
-      auto epi_swz = [](int r) { return (r >> 1) & (C::kEpiChunks - 1); };
-      const int rrow = lane / C::kEpiChunks;
-      const int rchunk = lane % C::kEpiChunks;
-      const bool chunk_ok = full_cols || wave_n * (32 * WN) + 16 * rchunk < static_cast<int>(args.ldc - U.n0);
-      constexpr int kPartRows = WM / C::kEpiParts;  // 32-row blocks per pass
+    // a listed unit's wave stores its quadrant only if the mask selects it
+    if (kListed && ((U.quad >> (wave_m * 2 + wave_n)) & 1u) == 0u) return;
+    // the unit's tile of C, or of its K slice's workspace slot
+    // [slice][plane][M][ldc] (split launches never accumulate)
+    int8_t* const Cp =
+        args.slices <= 1
+            ? base_c(U) + static_cast<int64_t>(U.plane) * args.pitch_c + U.m0 * args.ldc + U.n0
+            : base_ws(U) + ((static_cast<int64_t>(U.slice) * args.nplanes + U.plane) * args.m + U.m0) * args.ldc +
+                  U.n0;
+    const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(Cp, tile_rows * args.ldc - U.n0);
+    const uint32_t m_comp = 256u - mc.m;
+    const uint32_t half2 = mc.half * 0x00010001u;
+    // The packed residues go through this wave's slice of the epilogue LDS
+    // region (outside the stage ring, so the next unit's DMAs keep landing)
+    // so the global stores are row-contiguous 16-byte chunks; kEpiParts
+    // passes of WM / kEpiParts block rows each. Layout: row-major
+    // kEpiRow-byte rows, 16-byte chunk c of row r at c ^ ((r >> 1) &
+    // (kEpiChunks - 1)).
+    int8_t* const ep = lds + C::kLds + wave * (C::kEpiBytes / C::kEpiParts);
+    auto epi_swz = [](int r) { return (r >> 1) & (C::kEpiChunks - 1); };
+    const int rrow = lane / C::kEpiChunks;
+    const int rchunk = lane % C::kEpiChunks;
+    const bool chunk_ok = full_cols || wave_n * (32 * WN) + 16 * rchunk < static_cast<int>(args.ldc - U.n0);
+    constexpr int kPartRows = WM / C::kEpiParts;  // 32-row blocks per pass
 #pragma unroll
-      for (int part = 0; part < C::kEpiParts; ++part) {
-        auto reduce = [&](auto carry, auto low_byte) {
-          constexpr bool kCarry = decltype(carry)::value;
-          constexpr bool kLowByte = decltype(low_byte)::value;  // m = 256: the residue is the low byte
+    for (int part = 0; part < C::kEpiParts; ++part) {
+      auto reduce = [&](auto carry, auto low_byte) {
+        constexpr bool kCarry = decltype(carry)::value;
+        constexpr bool kLowByte = decltype(low_byte)::value;  // m = 256: the residue is the low byte
 #pragma unroll
-          for (int ii = 0; ii < kPartRows; ++ii) {
-            const int i = part * kPartRows + ii;
-            const uint32_t off = lane_off + static_cast<uint32_t>(i) * row_step;
-            uint32_t prev[WN][4];
-            if constexpr (kCarry) {
-              // later K block: add the centered residue carried in C (|.| <= 128)
+        for (int ii = 0; ii < kPartRows; ++ii) {
+          const int i = part * kPartRows + ii;
+          const uint32_t off = lane_off + static_cast<uint32_t>(i) * row_step;
+          uint32_t prev[WN][4];
+          if constexpr (kCarry) {
+            // later K block: add the centered residue carried in C (|.| <= 128)
 #pragma unroll
-              for (int j = 0; j < WN; ++j)
+            for (int j = 0; j < WN; ++j)
 #pragma unroll
-                for (int g = 0; g < 4; ++g)
-                  prev[j][g] = static_cast<uint32_t>(
-                      __builtin_amdgcn_raw_buffer_load_b32(c_rsrc, static_cast<int>(off + 32 * j + 8 * g), 0, 0));
-            }
-            const int r = 32 * ii + frag_row;
+              for (int g = 0; g < 4; ++g)
+                prev[j][g] = static_cast<uint32_t>(
+                    __builtin_amdgcn_raw_buffer_load_b32(c_rsrc, static_cast<int>(off + 32 * j + 8 * g), 0, 0));
+          }
+          const int r = 32 * ii + frag_row;
 #pragma unroll
-            for (int j = 0; j < WN; ++j) {
+          for (int j = 0; j < WN; ++j) {
 #pragma unroll
-              for (int g = 0; g < 4; ++g) {
-                uint32_t res[4];
-                const Acc4 a4 = acc_read4(acc[i][j], g);
-                uint32_t packed;
-                if constexpr (kLowByte) {
-                  // 2^31 is 0 mod 256, so u's low byte is C's, read as int8 its centered residue
-                  packed = pack_low_bytes(a4.v[0], a4.v[1], a4.v[2], a4.v[3]);
-                } else {
+            for (int g = 0; g < 4; ++g) {
+              uint32_t res[4];
+              const Acc4 a4 = acc_read4(acc[i][j], g);
+              uint32_t packed;
+              if constexpr (kLowByte) {
+                // 2^31 is 0 mod 256, so u's low byte is C's, read as int8 its centered residue
+                packed = pack_low_bytes(a4.v[0], a4.v[1], a4.v[2], a4.v[3]);
+              } else {
 #pragma unroll
-                  for (int e = 0; e < 4; ++e) {
-                    uint32_t u = a4.v[e];
-                    if constexpr (kCarry)
-                      u += static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev[j][g] >> (8 * e))));
-                    res[e] = residue_plus_half(u, mc, m_comp);
-                  }
-                  packed = pack_centered(res[0], res[1], res[2], res[3], half2);
+                for (int e = 0; e < 4; ++e) {
+                  uint32_t u = a4.v[e];
+                  if constexpr (kCarry)
+                    u += static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev[j][g] >> (8 * e))));
+                  res[e] = residue_plus_half(u, mc, m_comp);
                 }
-                const int c = 2 * j + (g >> 1);
-                *reinterpret_cast<uint32_t*>(ep + r * C::kEpiRow + ((c ^ epi_swz(r)) << 4) + 8 * (g & 1) +
-                                             4 * frag_half) = packed;
+                packed = pack_centered(res[0], res[1], res[2], res[3], half2);
               }
+              const int c = 2 * j + (g >> 1);
+              *reinterpret_cast<uint32_t*>(ep + r * C::kEpiRow + ((c ^ epi_swz(r)) << 4) + 8 * (g & 1) +
+                                           4 * frag_half) = packed;
             }
           }
-        };
-        if (accumulate)
-          reduce(std::true_type{}, std::false_type{});
-        else if (mc.m == 256u)
-          reduce(std::false_type{}, std::true_type{});
-        else
-          reduce(std::false_type{}, std::false_type{});
-        // Read back row-contiguous: lane l takes chunk l % kEpiChunks of rows
-        // q * kEpiRowsPerStore + l / kEpiChunks of this pass.
-        const uint32_t goff = static_cast<uint32_t>((wave_m * (32 * WM) + 32 * kPartRows * part + rrow) * args.ldc +
-                                                    wave_n * (32 * WN) + 16 * rchunk);
-#pragma unroll
-        for (int q = 0; q < 32 * kPartRows / C::kEpiRowsPerStore; ++q) {
-          const int row = C::kEpiRowsPerStore * q + rrow;
-          const v4i v = *reinterpret_cast<const v4i*>(ep + row * C::kEpiRow + ((rchunk ^ epi_swz(row)) << 4));
-          const uint32_t o = goff + static_cast<uint32_t>(C::kEpiRowsPerStore * q) * static_cast<uint32_t>(args.ldc);
-          __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(chunk_ok ? o : 0x80000000u), 0, 0);
         }
-      }
-    } else {
-      // Split-K: this slice's partial sums (u - 2^31) go, as plain int32
-      // stores, to its own slot of the workspace [slice][plane][M][ldc]; the
-      // finalize kernel adds the slices. No atomics, no zeroing, deterministic.
-      int32_t* const W =
-          base_ws(U) + ((static_cast<int64_t>(U.slice) * args.nplanes + U.plane) * args.m + U.m0) * args.ldc + U.n0;
-      const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(W, 4 * (tile_rows * args.ldc - U.n0));
+      };
+      if (accumulate)
+        reduce(std::true_type{}, std::false_type{});
+      else if (mc.m == 256u)
+        reduce(std::false_type{}, std::true_type{});
+      else
+        reduce(std::false_type{}, std::false_type{});
+      // Read back row-contiguous: lane l takes chunk l % kEpiChunks of rows
+      // q * kEpiRowsPerStore + l / kEpiChunks of this pass.
+      const uint32_t goff = static_cast<uint32_t>((wave_m * (32 * WM) + 32 * kPartRows * part + rrow) * args.ldc +
+                                                  wave_n * (32 * WN) + 16 * rchunk);
 #pragma unroll
-      for (int i = 0; i < WM; ++i) {
-        const uint32_t off = lane_off + static_cast<uint32_t>(i) * row_step;
-#pragma unroll
-        for (int j = 0; j < WN; ++j)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const uint32_t o = col_off(off, 32 * j + 8 * g);
-            const Acc4 a4 = acc_read4(acc[i][j], g);
-            const v4i v = {static_cast<int32_t>(a4.v[0] ^ kAccBias), static_cast<int32_t>(a4.v[1] ^ kAccBias),
-                           static_cast<int32_t>(a4.v[2] ^ kAccBias), static_cast<int32_t>(a4.v[3] ^ kAccBias)};
-            __builtin_amdgcn_raw_buffer_store_b128(v, w_rsrc, static_cast<int>(o == 0x80000000u ? o : 4 * o), 0, 0);
-          }
+      for (int q = 0; q < 32 * kPartRows / C::kEpiRowsPerStore; ++q) {
+        const int row = C::kEpiRowsPerStore * q + rrow;
+        const v4i v = *reinterpret_cast<const v4i*>(ep + row * C::kEpiRow + ((rchunk ^ epi_swz(row)) << 4));
+        const uint32_t o = goff + static_cast<uint32_t>(C::kEpiRowsPerStore * q) * static_cast<uint32_t>(args.ldc);
+        __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(chunk_ok ? o : 0x80000000u), 0, 0);
       }
     }
   };
@@ -633,42 +617,6 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
   __builtin_amdgcn_s_waitcnt(kWaitVm[0]);  // no DMA outlives the workgroup's LDS
 }
 
-// Sums the split-K partials of `slices` slices, adds the residue already in C
-// for later K blocks, and writes centered int8 residues. One thread per 4
-// consecutive cells of a plane row (ldc is a multiple of 16).
-__global__ __launch_bounds__(256) void splitk_finalize_kernel(const int32_t* ws, int8_t* c, int64_t m, int64_t ldc,
-                                                              int64_t pitch_c, uint32_t nplanes, uint32_t slices,
-                                                              PlaneConsts pc, uint32_t accumulate) {
-  const int64_t words_per_plane = m * ldc / 4;
-  const int64_t total = words_per_plane * nplanes;
-  const int64_t slice_stride = static_cast<int64_t>(nplanes) * m * ldc;  // int32 elements
-  for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < total;
-       w += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const uint32_t plane = static_cast<uint32_t>(w / words_per_plane);
-    const int64_t in_plane = w - static_cast<int64_t>(plane) * words_per_plane;
-    const ModulusConsts mc = pc.mod[plane];
-    const v4i* src = reinterpret_cast<const v4i*>(ws + static_cast<int64_t>(plane) * m * ldc) + in_plane;
-    v4i sum = *src;
-    for (uint32_t s = 1; s < slices; ++s) {
-      src += slice_stride / 4;
-      sum += *src;
-    }
-    const int64_t elem = in_plane * 4;
-    const int64_t row = elem / ldc;
-    const int64_t col = elem - row * ldc;
-    uint32_t* const dst = reinterpret_cast<uint32_t*>(c + static_cast<int64_t>(plane) * pitch_c + row * ldc + col);
-    const uint32_t prev = accumulate ? *dst : 0u;
-    uint32_t r[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t u = (static_cast<uint32_t>(sum[e]) ^ 0x80000000u) +
-                         static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev >> (8 * e))));
-      r[e] = residue_plus_half(u, mc, 256u - mc.m);
-    }
-    *dst = pack_centered(r[0], r[1], r[2], r[3], mc.half * 0x00010001u);
-  }
-}
-
 // Zero-output tiles of a per-tile schedule: planes [0, planes) of each tile's
 // rows and columns are set to 0 (reference cpu_reference.cpp:243-246). Whole
 // 16-byte chunks are written: a tile's column offset is a multiple of 64, and
@@ -696,7 +644,6 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* dst, uint64_t
     dst[w] = 0u;
 }
 
-constexpr int64_t kSplitMaxLd = int64_t{1} << 21;
 using CfgLarge = Cfg<4, 4>;  // 256 x 256 tiles, one workgroup per CU (all 512 registers per lane)
 using CfgSmall = Cfg<2, 2>;  // 128 x 128 tiles, two workgroups per CU
 
@@ -714,8 +661,8 @@ bool gemm_shape_ok(const GemmArgs& a) {
   if (!a.a || !a.b || !a.c) return false;
   if (a.slices == 0) return false;
   if (a.slices > 1 && !a.splitk_ws) return false;
-  // split-K workspace offsets are byte offsets of int32 cells in one tile
-  if (a.slices > 1 && a.ldc >= kSplitMaxLd) return false;
+  // the workspace holds [slices][planes][m][padded_ld(n)] residues
+  if (a.slices > 1 && a.ldc != padded_ld(a.n)) return false;
   return true;
 }
 
@@ -727,32 +674,35 @@ int64_t tile_count(int64_t m, int64_t n, uint32_t nplanes) {
 }  // namespace
 
 GemmShape choose_gemm_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes) {
-  // 256 x 256 tiles when they already give every CU at least one; otherwise
-  // 128 x 128 tiles (two per CU), and split K when even those leave the chip
-  // under-filled: toward ~512 units, with slices of at least 4096 K. Each
-  // slice adds a partial tile per plane to write and sum, and short slices
-  // spend a larger share in the DMA prologue and the epilogue: at
-  // 128 x 128 x 65536 with 8 planes, 16 slices take 35 us, 32 take 38 us and
-  // 64 (1024 K each) 49 us.
-  const int64_t kblock = k < kSafeKBlock ? k : kSafeKBlock;
-  if (tile_count<CfgLarge>(m, n, nplanes) >= 256) return GemmShape{256, 1};
+  // Results at most 16 columns wide: the skinny kernel (skinny.hip).
+  GemmShape shape{};
+  if (skinny_shape(m, n, k, nplanes, shape)) return shape;
+  // 256 x 256 tiles when they already give every CU at least one and neither
+  // side of the result is narrower than 256; otherwise 128 x 128 tiles (two
+  // per CU), and split K when even those leave the chip under-filled: toward
+  // ~512 units, with slices of at least 4096 K and at most 65536. Each slice
+  // adds a residue tile per plane to write and sum, and short slices spend a
+  // larger share in the DMA prologue and the epilogue.
+  shape.tile = 128;
+  shape.slices = 1;
+  shape.k_slice = k;
+  if (m > 128 && n > 128 && tile_count<CfgLarge>(m, n, nplanes) >= 256) {
+    shape.tile = 256;
+    return shape;
+  }
   const int64_t tiles = tile_count<CfgSmall>(m, n, nplanes);
-  if (tiles >= 256 || kblock < 8192 || padded_ld(n) >= kSplitMaxLd) return GemmShape{128, 1};
-  int64_t slices = (512 + tiles - 1) / tiles;
-  if (slices > kblock / 4096) slices = kblock / 4096;
-  if (slices > 64) slices = 64;
-  if (slices < 1) slices = 1;
-  return GemmShape{128, static_cast<uint32_t>(slices)};
-}
-
-uint32_t choose_splitk_slices(int64_t m, int64_t n, int64_t k, uint32_t nplanes) {
-  return choose_gemm_shape(m, n, k, nplanes).slices;
-}
-
-uint64_t splitk_workspace_bytes(int64_t m, int64_t n, int64_t k, uint32_t nplanes) {
-  const uint32_t slices = choose_splitk_slices(m, n, k, nplanes);
-  if (slices <= 1) return 0;
-  return static_cast<uint64_t>(slices) * nplanes * static_cast<uint64_t>(m) * static_cast<uint64_t>(padded_ld(n)) * 4u;
+  if (tiles >= 256 || k < 8192) return shape;
+  int64_t slices = std::min<int64_t>((512 + tiles - 1) / tiles, k / 4096);
+  slices = std::max<int64_t>(slices, (k + kSafeKBlock - 1) / kSafeKBlock);
+  if (slices <= 1) return shape;
+  int64_t k_slice = (k + slices - 1) / slices;
+  k_slice = (k_slice + CfgSmall::BK - 1) / CfgSmall::BK * CfgSmall::BK;
+  slices = (k + k_slice - 1) / k_slice;
+  if (slices <= 1 || slices * tiles > 0x7FFFFFFF) return shape;
+  shape.slices = static_cast<uint32_t>(slices);
+  shape.k_slice = k_slice;
+  shape.ws_bytes = static_cast<uint64_t>(slices) * nplanes * static_cast<uint64_t>(m) * static_cast<uint64_t>(padded_ld(n));
+  return shape;
 }
 
 hipError_t launch_zero_words(uint32_t* dst, uint64_t words, hipStream_t stream) {
@@ -781,26 +731,24 @@ int device_cu_count() {
 }
 
 // Ungrouped launches pass a NoTaskTable and ntasks = 1; grouped ones the
-// task table and its task count (at most kMaxGroupTasks).
+// task table and its task count (at most kMaxGroupTasks). `k_slice` is the
+// K of one slice when args.slices > 1.
 template <typename Cf, int kMinBlocks, bool kGrouped>
-hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream,
+hipError_t launch_gemm_cfg(const GemmArgs& args, int64_t k_slice, const PlaneConsts& consts, hipStream_t stream,
                            const GroupArg<kGrouped>& tab, uint32_t ntasks) {
   const uint32_t tiles_m = static_cast<uint32_t>((args.m + Cf::BM - 1) / Cf::BM);
   const uint32_t tiles_n = static_cast<uint32_t>((args.ldc + Cf::BN - 1) / Cf::BN);
-  const uint64_t words = static_cast<uint64_t>(args.nplanes) * args.m * args.ldc / 4;
   const uint64_t slots = static_cast<uint64_t>(device_cu_count()) * kMinBlocks;
-  // K is processed in int32-safe blocks of 65536; a later block adds its sum
-  // to the centered residue already in C (reference cpu_reference.cpp:160-175).
-  for (int64_t kb = 0; kb < args.k; kb += kSafeKBlock) {
-    const int64_t kstop = min(args.k, kb + kSafeKBlock);
+  // One launch per K range: the whole K split into args.slices slices, or,
+  // unsplit, int32-safe blocks of 65536 whose later launches add their sum to
+  // the centered residue already in C (reference cpu_reference.cpp:160-175).
+  const int64_t block = args.slices > 1 ? args.k : kSafeKBlock;
+  for (int64_t kb = 0; kb < args.k; kb += block) {
+    const int64_t kstop = min(args.k, kb + block);
     const uint32_t accumulate = kb > 0 ? 1u : 0u;
-    int64_t k_slice = kstop - kb;
-    uint32_t used_slices = 1;
-    if (args.slices > 1) {
-      k_slice = (k_slice + args.slices - 1) / args.slices;
-      k_slice = (k_slice + Cf::BK - 1) / Cf::BK * Cf::BK;
-      used_slices = static_cast<uint32_t>((kstop - kb + k_slice - 1) / k_slice);
-    }
+    const int64_t ks = args.slices > 1 ? k_slice : kstop - kb;
+    const uint32_t used_slices = static_cast<uint32_t>((kstop - kb + ks - 1) / ks);
+    if (ks <= 0 || ks > kSafeKBlock || used_slices != args.slices) return hipErrorInvalidValue;
     const uint64_t task_units = static_cast<uint64_t>(tiles_m) * tiles_n * args.nplanes * used_slices;
     const uint64_t units = task_units * ntasks;
     if (units == 0 || units > 0x7FFFFFFFull) return hipErrorInvalidValue;
@@ -815,13 +763,13 @@ hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipS
     map.tail = make_div_u31(tiles_m - (tiles_m - 1) / kGroupM * kGroupM);
     map.k_begin = static_cast<uint32_t>(kb);
     map.k_stop = static_cast<uint32_t>(kstop);
-    map.k_slice = static_cast<uint32_t>(k_slice);
+    map.k_slice = static_cast<uint32_t>(ks);
     // persistent grid: one workgroup per resident slot, a multiple of 8 (one
     // share per XCD) when there are at least 8 units
     uint64_t grid = units < slots ? units : slots;
     if (grid >= 8) grid -= grid % 8;
-    // every unit has the same K tiles when the slices divide the block evenly
-    const bool uniform = (kstop - kb) % k_slice == 0;
+    // every unit has the same K tiles when the slices divide the range evenly
+    const bool uniform = (kstop - kb) % ks == 0;
     if (uniform)
       hipLaunchKernelGGL((plane_gemm_kernel<Cf, kMinBlocks, true, false, kGrouped>), dim3(static_cast<unsigned>(grid)),
                          dim3(kThreads), 0, stream, args, consts, map, accumulate, tab);
@@ -832,18 +780,15 @@ hipError_t launch_gemm_cfg(const GemmArgs& args, const PlaneConsts& consts, hipS
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     if (args.slices > 1) {
-      const uint64_t fblocks = (words + 255) / 256;
-      const unsigned fgrid = static_cast<unsigned>(fblocks < 8192 ? fblocks : 8192);
       for (uint32_t t = 0; t < ntasks; ++t) {
-        int32_t* ws = args.splitk_ws;
+        int8_t* ws = args.splitk_ws;
         int8_t* c = args.c;
         if constexpr (kGrouped) {
           ws = tab.t[t].ws;
           c = tab.t[t].c;
         }
-        hipLaunchKernelGGL(splitk_finalize_kernel, dim3(fgrid), dim3(256), 0, stream, ws, c, args.m, args.ldc,
-                           args.pitch_c, args.nplanes, used_slices, consts, accumulate);
-        err = hipGetLastError();
+        err = launch_residue_finalize(ws, c, args.m, args.ldc, args.pitch_c, args.nplanes, args.slices, consts,
+                                      stream);
         if (err != hipSuccess) return err;
       }
     }
@@ -898,16 +843,16 @@ hipError_t launch_zero_tiles(int8_t* c, int64_t ldc, int64_t pitch_c, const Tile
 }
 
 // ---- static scratch for calls that allocate nothing ---------------------------
-// The split-K partials of rns8_mi355x_gemm_rns_noalloc live here instead of
+// The split-K residues of rns8_mi355x_gemm_rns_noalloc live here instead of
 // in a caller's workspace. Each device holds its own copy of the array for
 // the life of the process. On the host the array's name is not a device
 // address: host code uses the per-device address resolve_noalloc_scratch
 // records (hipGetSymbolAddress with that device current).
-static __device__ __align__(256) int32_t scratch[kNoAllocScratchBytes / 4];
+static __device__ __align__(256) int8_t scratch[kNoAllocScratchBytes];
 
 namespace {
 constexpr int kMaxDevices = 64;
-std::atomic<int32_t*> g_scratch[kMaxDevices] = {};
+std::atomic<int8_t*> g_scratch[kMaxDevices] = {};
 std::mutex g_scratch_mutex;
 }  // namespace
 
@@ -922,11 +867,11 @@ hipError_t resolve_noalloc_scratch(int device) {
   const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
   if (e != hipSuccess) return e;
   if (!ptr || (reinterpret_cast<uintptr_t>(ptr) & 255u) != 0) return hipErrorInvalidSymbol;
-  g_scratch[device].store(static_cast<int32_t*>(ptr), std::memory_order_release);
+  g_scratch[device].store(static_cast<int8_t*>(ptr), std::memory_order_release);
   return hipSuccess;
 }
 
-int32_t* noalloc_scratch(int device) {
+int8_t* noalloc_scratch(int device) {
   if (device < 0 || device >= kMaxDevices) return nullptr;
   return g_scratch[device].load(std::memory_order_acquire);
 }
@@ -934,10 +879,16 @@ int32_t* noalloc_scratch(int device) {
 hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream) {
   if (!gemm_shape_ok(args)) return hipErrorInvalidValue;
   const GemmShape shape = choose_gemm_shape(args.m, args.n, args.k, args.nplanes);
-  // the workspace was sized for the plan's slice count: never use more
+  // the workspace was sized for the plan's slices: never use a different
+  // split (an unsplit call of a split shape runs unsplit where the kernel
+  // allows it)
   if (args.slices > 1 && args.slices != shape.slices) return hipErrorInvalidValue;
-  if (shape.tile == 256) return launch_gemm_cfg<CfgLarge, 1, false>(args, consts, stream, NoTaskTable{}, 1);
-  return launch_gemm_cfg<CfgSmall, 2, false>(args, consts, stream, NoTaskTable{}, 1);
+  if (shape.tile == 16) {
+    if (args.slices != shape.slices) return hipErrorInvalidValue;
+    return launch_skinny(args, shape, consts, stream);
+  }
+  if (shape.tile == 256) return launch_gemm_cfg<CfgLarge, 1, false>(args, shape.k_slice, consts, stream, NoTaskTable{}, 1);
+  return launch_gemm_cfg<CfgSmall, 2, false>(args, shape.k_slice, consts, stream, NoTaskTable{}, 1);
 }
 
 hipError_t launch_gemm_grouped(const GemmArgs& shape, const PlaneConsts& consts, const TaskPtrs* tasks,
@@ -947,27 +898,41 @@ hipError_t launch_gemm_grouped(const GemmArgs& shape, const PlaneConsts& consts,
   // never more slices than the shape's own workspaces hold
   const GemmShape g = choose_gemm_shape(shape.m, shape.n, shape.k, shape.nplanes * count);
   if (g.slices > 1 && g.slices > shape.slices) return hipErrorInvalidValue;
+  for (uint32_t t = 0; t < count; ++t) {
+    // every task's operands pass the same checks as an ungrouped launch
+    GemmArgs a = shape;
+    a.a = tasks[t].a;
+    a.b = tasks[t].b;
+    a.c = tasks[t].c;
+    a.splitk_ws = tasks[t].ws;
+    a.slices = g.tile == 16 ? shape.slices : g.slices;
+    if (!gemm_shape_ok(a)) return hipErrorInvalidValue;
+  }
+  if (g.tile == 16) {
+    // the skinny kernel fills the chip from one task's rows and K slices:
+    // one launch per task, each with its own workspace
+    for (uint32_t t = 0; t < count; ++t) {
+      GemmArgs a = shape;
+      a.a = tasks[t].a;
+      a.b = tasks[t].b;
+      a.c = tasks[t].c;
+      a.splitk_ws = tasks[t].ws;
+      const hipError_t err = launch_gemm(a, consts, stream);
+      if (err != hipSuccess) return err;
+    }
+    return hipSuccess;
+  }
   for (uint32_t first = 0; first < count; first += kMaxGroupTasks) {
     const uint32_t n = count - first < kMaxGroupTasks ? count - first : kMaxGroupTasks;
     TaskTable tab{};
-    for (uint32_t t = 0; t < n; ++t) {
-      tab.t[t] = tasks[first + t];
-      // every task's operands pass the same checks as an ungrouped launch
-      GemmArgs a = shape;
-      a.a = tab.t[t].a;
-      a.b = tab.t[t].b;
-      a.c = tab.t[t].c;
-      a.splitk_ws = tab.t[t].ws;
-      a.slices = g.slices;
-      if (!gemm_shape_ok(a)) return hipErrorInvalidValue;
-    }
+    for (uint32_t t = 0; t < n; ++t) tab.t[t] = tasks[first + t];
     GemmArgs a = shape;
     a.a = a.b = nullptr;
     a.c = nullptr;
     a.splitk_ws = nullptr;
     a.slices = g.slices;
-    const hipError_t err = g.tile == 256 ? launch_gemm_cfg<CfgLarge, 1, true>(a, consts, stream, tab, n)
-                                         : launch_gemm_cfg<CfgSmall, 2, true>(a, consts, stream, tab, n);
+    const hipError_t err = g.tile == 256 ? launch_gemm_cfg<CfgLarge, 1, true>(a, g.k_slice, consts, stream, tab, n)
+                                         : launch_gemm_cfg<CfgSmall, 2, true>(a, g.k_slice, consts, stream, tab, n);
     if (err != hipSuccess) return err;
   }
   return hipSuccess;

@@ -129,7 +129,7 @@ struct rns8_workspace {
   uint32_t prefix = 0;
   uint32_t finite_modulus = 0;
   int device_id = 0;
-  int32_t* splitk = nullptr;
+  int8_t* splitk = nullptr;
   uint64_t splitk_bytes = 0;
 };
 

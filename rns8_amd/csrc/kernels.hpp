@@ -62,10 +62,10 @@ struct GemmArgs {
   int64_t lda, ldb, ldc;  // padded pitches (bytes, multiples of 16)
   int64_t pitch_a, pitch_b, pitch_c;
   uint32_t nplanes;
-  // split-K: int32 partial sums [slices][planes][m][ldc] (each slice writes
-  // its own slot; no zeroing needed) and the number of K slices; slices == 1
-  // disables it.
-  int32_t* splitk_ws;
+  // split-K: the workspace of centered int8 residues [slices][planes][m][ldc]
+  // (each slice writes its own slot; no zeroing needed; 16-byte aligned, as
+  // is c) and the number of K slices; slices == 1 disables it.
+  int8_t* splitk_ws;
   uint32_t slices;
 };
 hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream);
@@ -122,33 +122,43 @@ struct TaskPtrs {
   const int8_t* a;
   const int8_t* b;
   int8_t* c;
-  int32_t* ws;  // split-K partials of this task (slices > 1 only)
+  int8_t* ws;  // split-K residues of this task (slices > 1 only)
 };
 constexpr uint32_t kMaxGroupTasks = 32;
 hipError_t launch_gemm_grouped(const GemmArgs& shape, const PlaneConsts& consts, const TaskPtrs* tasks,
                                uint32_t count, hipStream_t stream);
-// Tile edge (256 or 128) and K slices the launcher uses for this shape
-// (k is the K of one launch block, at most 65536).
+// How launch_gemm runs a shape: the kernel (plane_gemm_kernel with 256 or
+// 128 tiles, or the skinny kernel for results at most 16 columns wide) and
+// the K split. A split covers the whole K in slices of at most 65536, each
+// writing its centered residues to the int8 workspace, and a finalize adds
+// them; unsplit products with K beyond 65536 run as accumulating launches.
 struct GemmShape {
-  int tile;
-  uint32_t slices;
+  int tile;           // 256, 128, or 16 (skinny kernel)
+  uint32_t slices;    // K slices (1 = no split)
+  int64_t k_slice;    // K of one slice
+  uint64_t ws_bytes;  // workspace: slices * nplanes * m * padded_ld(n) bytes when split, else 0
 };
 GemmShape choose_gemm_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes);
-// Number of K slices the launcher would pick for this shape (1 = no split).
-uint32_t choose_splitk_slices(int64_t m, int64_t n, int64_t k, uint32_t nplanes);
-// Bytes of int32 split-K workspace needed for this shape (0 when slices == 1):
-// one [plane][M][ldc] int32 slot per slice.
-uint64_t splitk_workspace_bytes(int64_t m, int64_t n, int64_t k, uint32_t nplanes);
+// The skinny kernel's shape for n <= 16 (false for wider results), and its
+// launcher (skinny.hip): B and C rows of 16 bytes, args.slices ==
+// shape.slices.
+bool skinny_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, GemmShape& out);
+hipError_t launch_skinny(const GemmArgs& args, const GemmShape& shape, const PlaneConsts& consts, hipStream_t stream);
+// Adds the centered residues of `slices` workspace slots [slices][nplanes][m]
+// [ldc] and writes their centered residue to C's planes (fused.hip). ws and c
+// 16-byte aligned, ldc and pitch_c multiples of 16.
+hipError_t launch_residue_finalize(const int8_t* ws, int8_t* c, int64_t m, int64_t ldc, int64_t pitch_c,
+                                   uint32_t nplanes, uint32_t slices, const PlaneConsts& consts, hipStream_t stream);
 
 // Per-device static split-K scratch (gemm.hip) for GEMM calls that bring no
-// workspace and may allocate nothing: kNoAllocScratchBytes of int32 partials.
-constexpr uint64_t kNoAllocScratchBytes = uint64_t{16} << 20;
+// workspace and may allocate nothing: kNoAllocScratchBytes of int8 residues.
+constexpr uint64_t kNoAllocScratchBytes = uint64_t{4} << 20;
 // Records `device`'s address of the scratch (hipGetSymbolAddress), once per
 // device; `device` must be the current device. Returns the HIP error of the
 // lookup, or hipSuccess when the address is (already) recorded.
 hipError_t resolve_noalloc_scratch(int device);
 // The recorded address for `device`, or nullptr when it was never resolved.
-int32_t* noalloc_scratch(int device);
+int8_t* noalloc_scratch(int device);
 
 // ---- export ------------------------------------------------------------------
 enum class ExportKind : uint32_t { I64 = 0, U64 = 1, WIDE_SIGNED = 2, WIDE_UNSIGNED = 3 };

@@ -1,12 +1,12 @@
 """rns8_mi355x_gemm_rns_noalloc (the GEMM entry point that allocates nothing)
 against rns8_mi355x_gemm_rns_async, through the C ABI.
 
-The no-allocation entry keeps split-K partials in the library's static
+The no-allocation entry keeps split-K residues in the library's static
 per-device scratch instead of a workspace. Its residue planes must equal the
 workspace entry's byte for byte: on two calls in a row, the second on a
 smaller shape that reuses (and only partly overwrites) the scratch the first
-one filled; on a shape with no K split; and its refusals (split-K partials
-beyond the 16 MiB scratch, exact-wide plans) must leave C as it was.
+one filled; on a shape with no K split; and its refusals (split-K residues
+beyond the 4 MiB scratch, exact-wide plans) must leave C as it was.
 """
 import numpy as np
 import pytest
@@ -56,12 +56,12 @@ def _with_workspace(ctx, plan, Am, Bm):
 def test_noalloc_equals_workspace_entry_two_calls(gpu_ctx):
     ctx = gpu_ctx
     # call 1: the tall-skinny C5 shape, 16 K slices x 8 planes of 128 x 128
-    # int32 partials = 8 MiB of scratch
+    # int8 residues = 2 MiB of scratch
     p1, A1, B1, mk1, _, _ = _setup(ctx, False, 128, 128, 65536, 8, 1 << 62, 1201)
     C1 = mk1()
     assert _noalloc(ctx, p1, A1, B1, C1) == r.SUCCESS
-    # call 2, smaller: 96 x 80 x 20000 int64 at prefix 9 (4 slices, 1.1 MB of
-    # the scratch); the first call's partials still fill the rest
+    # call 2, smaller: 96 x 80 x 20000 int64 at prefix 9 (4 slices, 276 KB of
+    # the scratch); the first call's residues still fill the rest
     p2, A2, B2, mk2, A, B = _setup(ctx, True, 96, 80, 20000, 9, 1 << 62, 1202)
     C2 = mk2()
     assert _noalloc(ctx, p2, A2, B2, C2) == r.SUCCESS
@@ -86,8 +86,8 @@ def test_noalloc_without_split(gpu_ctx):
 
 
 def test_noalloc_refusals_leave_result(gpu_ctx):
-    """Split-K partials beyond the scratch (256 x 256 x 65536 at prefix 9: 15
-    slices x 9 planes x 256 x 256 x 4 bytes = 35 MB) and exact-wide plans are
+    """Split-K residues beyond the scratch (256 x 256 x 65536 at prefix 9: 15
+    slices x 9 planes x 256 x 256 bytes = 8.8 MB) and exact-wide plans are
     refused before anything is enqueued; C keeps its earlier result."""
     ctx = gpu_ctx
     plan, Am, Bm, mk, _, _ = _setup(ctx, True, 256, 256, 65536, 9, 1 << 62, 1204)
