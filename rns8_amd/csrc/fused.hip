@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
     constexpr bool kFast = decltype(fast)::value;
     constexpr bool kM256 = decltype(m256c)::value;
     constexpr bool kA = decltype(is_a_c)::value;
-    // r[j][h]: the element's residue (plus H when m < 256) in its low byte
+    // r[j][h]: the element's centered residue in its low byte
     uint32_t r[4][2];
     const uint32_t m_comp = 256u - mc.m;
     if constexpr (kM256) {
@@ -169,7 +169,10 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
       constexpr bool kI32 = kFast && Signed;
       const uint32_t shift = kI32 ? mc.q_shift : mc.pq_shift;
       const uint32_t recip = kI32 ? mc.q_recip : mc.pq_recip;
-      const uint32_t off = kI32 ? mc.off_i32 : Signed ? mc.off_i64 : mc.off_u64;
+      // the offsets less H (each offset is at least H): s - H comes out of
+      // the dot products (centered_byte)
+      const uint32_t off = (kI32 ? mc.off_i32 : Signed ? mc.off_i64 : mc.off_u64) - mc.half;
+      const uint32_t h_sh = in_vgpr(mc.half << shift);
       uint32_t s[4][2], q[4][2];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -190,7 +193,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) q[j][h] = s[j][h] << shift;
+        for (int h = 0; h < 2; ++h) q[j][h] = (s[j][h] << shift) + h_sh;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -200,13 +203,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
 #pragma unroll
         for (int h = 0; h < 2; ++h) r[j][h] = mad_u24(q[j][h], m_comp, s[j][h]);
     }
-    const uint32_t half2 = mc.half * 0x00010001u;
-    auto pack4 = [&](uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3) {
-      if constexpr (kM256)
-        return pack_low_bytes(r0, r1, r2, r3);
-      else
-        return pack_centered(r0, r1, r2, r3, half2);
-    };
+    auto pack4 = [&](uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3) { return pack_low_bytes(r0, r1, r2, r3); };
     if constexpr (kA) {
       // rows 8q and 8q + 4 share a packed dword: its low half goes to one
       // row, its high half to the other
@@ -312,8 +309,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
   if (!mfma_wave) return;
   const uint32_t plane = p0 + pl;
   const ModulusConsts mc = pl == 0 ? mc0 : mc1;
-  const uint32_t m_comp = 256u - mc.m;
-  const uint32_t half2 = mc.half * 0x00010001u;
+  const CenteredI32 kc = centered_i32_consts(mc);
   int8_t* const w = a.ws + (static_cast<int64_t>(slice) * a.nplanes + plane) * a.m * a.ldc;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -325,10 +321,9 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t u = static_cast<uint32_t>(acc[i][4 * g + e]) ^ 0x80000000u;
-        r[e] = mc.m == 256u ? u : residue_plus_half(u, mc, m_comp);
+        r[e] = mc.m == 256u ? u : centered_residue_i32(u, mc, kc);
       }
-      uint32_t packed =
-          mc.m == 256u ? pack_low_bytes(r[0], r[1], r[2], r[3]) : pack_centered(r[0], r[1], r[2], r[3], half2);
+      uint32_t packed = pack_low_bytes(r[0], r[1], r[2], r[3]);
       if (col + 4 > a.n) packed &= col >= a.n ? 0u : 0xFFFFFFFFu >> (8 * (col + 4 - a.n));
       if (row < a.m && col < a.ldc) *reinterpret_cast<uint32_t*>(w + row * a.ldc + col) = packed;
     }
@@ -378,14 +373,15 @@ __global__ __launch_bounds__(256) void residue_finalize_kernel(const int8_t* ws,
       const uint32_t plane = static_cast<uint32_t>(ch / chunks_per_plane);
       const int64_t in_plane = ch - static_cast<int64_t>(plane) * chunks_per_plane;
       const ModulusConsts mc = pc.mod[plane];
-      const uint32_t m_comp = 256u - mc.m, half2 = mc.half * 0x00010001u;
+      const CenteredI32 kc = centered_i32_consts(mc);
       v4i out;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         uint32_t r[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = residue_plus_half(static_cast<uint32_t>(sum[4 * d + e]) ^ 0x80000000u, mc, m_comp);
-        out[d] = static_cast<int>(pack_centered(r[0], r[1], r[2], r[3], half2));
+        for (int e = 0; e < 4; ++e)
+          r[e] = centered_residue_i32(static_cast<uint32_t>(sum[4 * d + e]) ^ 0x80000000u, mc, kc);
+        out[d] = static_cast<int>(pack_low_bytes(r[0], r[1], r[2], r[3]));
       }
       *reinterpret_cast<v4i*>(c + static_cast<int64_t>(plane) * pitch_c + in_plane * 16) = out;
     }

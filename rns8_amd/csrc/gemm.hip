@@ -457,8 +457,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
             : base_ws(U) + ((static_cast<int64_t>(U.slice) * args.nplanes + U.plane) * args.m + U.m0) * args.ldc +
                   U.n0;
     const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(Cp, tile_rows * args.ldc - U.n0);
-    const uint32_t m_comp = 256u - mc.m;
-    const uint32_t half2 = mc.half * 0x00010001u;
+    const CenteredI32 kc = centered_i32_consts(mc);
     // The packed residues go through this wave's slice of the epilogue LDS
     // region (outside the stage ring, so the next unit's DMAs keep landing)
     // so the global stores are row-contiguous 16-byte chunks; kEpiParts
@@ -507,9 +506,9 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void plane_gemm_kernel(GemmAr
                   uint32_t u = a4.v[e];
                   if constexpr (kCarry)
                     u += static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(prev[j][g] >> (8 * e))));
-                  res[e] = residue_plus_half(u, mc, m_comp);
+                  res[e] = centered_residue_i32(u, mc, kc);
                 }
-                packed = pack_centered(res[0], res[1], res[2], res[3], half2);
+                packed = pack_low_bytes(res[0], res[1], res[2], res[3]);
               }
               const int c = 2 * j + (g >> 1);
               *reinterpret_cast<uint32_t*>(ep + r * C::kEpiRow + ((c ^ epi_swz(r)) << 4) + 8 * (g & 1) +

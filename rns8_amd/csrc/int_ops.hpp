@@ -19,11 +19,27 @@ __device__ __forceinline__ uint32_t mulhi_u24(uint32_t x, uint32_t y) {
 
 // lo24(a) * lo24(b) + c (mod 2^32) as v_mad_u32_u24, b uniform. Written as
 // asm because the compiler lowers the same C expression to a quarter-rate
-// 32- or 64-bit multiply-add.
+// 32- or 64-bit multiply-add. Callers must not pass a v_dot4 result that
+// the compiler's own instructions have not read first: the wait states a
+// dot product's result needs are inserted only before compiler-generated
+// readers.
 __device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
   uint32_t d;
   asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(b), "v"(c));
   return d;
+}
+
+// A uniform value copied into a VGPR. gfx9 VALU operations read at most one
+// SGPR, so (a << shift) + c with shift and c both in SGPRs compiles to a
+// shift and an add; with c in a VGPR the compiler forms one
+// v_lshl_add_u32. (Written with the compiler's own instructions rather than
+// asm: the result of v_dot4_u32_u8 needs wait states before a dependent
+// VALU read, which the compiler inserts for its instructions but not for an
+// asm statement's operands.)
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t x) {
+  uint32_t v;
+  asm("v_mov_b32 %0, %1" : "=v"(v) : "s"(x));
+  return v;
 }
 
 // Low byte of s mod m for 0 <= s <= s_max, given the make_quot24 constants of
@@ -34,13 +50,35 @@ __device__ __forceinline__ uint32_t mod_low_byte(uint32_t s, uint32_t shift, uin
   return mad_u24(mulhi_u24(s << shift, recip), m_comp, s);
 }
 
-// For u = x + 2^31 (x an int32 sum), returns a value whose low byte is
-// (x + H) mod m, H = floor(m/2): s = dot(bytes(u), 2^(8b) mod m) + off_i32 is
-// congruent to x + H and at most s_max, q = floor(s / m) by the 24-bit
-// quotient of tables.hpp, and s + q*(256 - m) is congruent to s - q*m modulo
-// 256. m_comp = 256 - m.
-__device__ __forceinline__ uint32_t residue_plus_half(uint32_t u, const ModulusConsts& mc, uint32_t m_comp) {
-  return mod_low_byte(__builtin_amdgcn_udot4(u, mc.pow_lo, mc.off_i32, false), mc.q_shift, mc.q_recip, m_comp);
+// The centered residue of x modulo m as a low byte (upper bytes not
+// meaningful), given sc = s - H, where s is congruent to x + H modulo m,
+// 0 <= s <= s_max of the quotient constants (shift, recip), H = floor(m/2)
+// and h_sh = H << shift: q = floor(s / m) comes from the 24-bit reciprocal of
+// (sc << shift) + h_sh = s << shift, and sc + q*(256 - m) is congruent modulo
+// 256 to s - q*m - H = ((x + H) mod m) - H, which lies in [-128, 127] and is
+// the centered residue (r for r < (m+1)/2, else r - m, with r = x mod m).
+// m_comp = 256 - m. Callers fold -H into the offset of the dot products that
+// form s, so the subtraction costs nothing.
+__device__ __forceinline__ uint32_t centered_byte(uint32_t sc, uint32_t shift, uint32_t h_sh, uint32_t recip,
+                                                  uint32_t m_comp) {
+  return mad_u24(mulhi_u24((sc << shift) + h_sh, recip), m_comp, sc);
+}
+
+// Per-modulus constants of the int32 reduction below: off_c = off_i32 - H
+// (off_i32 >= H) and h_sh = H << q_shift.
+struct CenteredI32 {
+  uint32_t off_c, h_sh, m_comp;
+};
+__device__ __forceinline__ CenteredI32 centered_i32_consts(const ModulusConsts& mc) {
+  return CenteredI32{mc.off_i32 - mc.half, in_vgpr(mc.half << mc.q_shift), 256u - mc.m};
+}
+
+// For u = x + 2^31 (x an int32 sum), the centered residue of x modulo m in
+// the low byte: s = dot(bytes(u), 2^(8b) mod m) + off_i32 is congruent to
+// x + H and at most s_max (tables.hpp).
+__device__ __forceinline__ uint32_t centered_residue_i32(uint32_t u, const ModulusConsts& mc, const CenteredI32& k) {
+  return centered_byte(__builtin_amdgcn_udot4(u, mc.pow_lo, k.off_c, false), mc.q_shift, k.h_sh, mc.q_recip,
+                       k.m_comp);
 }
 
 // Reads accumulator elements 4g .. 4g+3 of a 32x32 MFMA tile straight from
@@ -61,20 +99,6 @@ __device__ __forceinline__ Acc4 acc_read4(const v16i& acc, int g) {
       : "=v"(r.v[0]), "=v"(r.v[1]), "=v"(r.v[2]), "=v"(r.v[3])
       : "a"(acc[4 * g]), "a"(acc[4 * g + 1]), "a"(acc[4 * g + 2]), "a"(acc[4 * g + 3]));
   return r;
-}
-
-// Packs (r_e - H) mod 256 for e = 0..3 into one little-endian dword, where
-// r_e holds (x_e + H) mod m in its low byte (other bytes ignored): the
-// centered residues as int8. half2 = H * 0x10001. v_perm_b32(s0, s1, sel)
-// takes result byte k from byte sel_k of s1 (0-3) or of s0 (4-7), or 0 for
-// selector 0x0c; the subtraction runs on two 16-bit lanes at once.
-__device__ __forceinline__ uint32_t pack_centered(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3,
-                                                  uint32_t half2) {
-  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  const u16x2 h = __builtin_bit_cast(u16x2, half2);
-  const u16x2 p01 = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(r1, r0, 0x0c040c00u)) - h;
-  const u16x2 p23 = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(r3, r2, 0x0c040c00u)) - h;
-  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, p23), __builtin_bit_cast(uint32_t, p01), 0x06040200u);
 }
 
 // The low bytes of r0..r3 as one little-endian dword.

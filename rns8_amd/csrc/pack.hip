@@ -91,30 +91,54 @@ __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConst
         best = mag > best ? mag : best;
       }
     }
+    // When every element of the wave fits 32 bits (int32 for signed input,
+    // uint32 for unsigned), one byte dot product per residue covers it: u =
+    // x + 2^31 (signed) or x (unsigned) against the int32 reduction
+    // constants, whose s_max covers both offsets (off_u64 = H <= off_i32).
+    bool fits = true;
+#pragma unroll
+    for (int e = 0; e < kCols; ++e)
+      fits &= hi[e] == (Signed ? static_cast<uint32_t>(static_cast<int32_t>(lo[e]) >> 31) : 0u);
+    const bool narrow = __all(fits);
     if (Signed) {
 #pragma unroll
-      for (int e = 0; e < kCols; ++e) hi[e] ^= 0x80000000u;
+      for (int e = 0; e < kCols; ++e) {
+        hi[e] ^= 0x80000000u;
+        if (narrow) lo[e] ^= 0x80000000u;
+      }
     }
     int8_t* const out = a.planes + static_cast<int64_t>(row) * a.plane_ld + c0;
     for (uint32_t p = 0; p < a.nplanes; ++p) {
       const ModulusConsts mc = pc.mod[p];
       v2i w;
       if (mc.m == 256u) {
-        // x mod 256 is the low byte, and its centered value is that byte as int8
+        // x mod 256 is the low byte, and its centered value is that byte as
+        // int8 (the narrow path's bias 2^31 leaves the low byte alone)
         w = v2i{static_cast<int>(pack_low_bytes(lo[0], lo[1], lo[2], lo[3])),
                 static_cast<int>(pack_low_bytes(lo[4], lo[5], lo[6], lo[7]))};
+      } else if (narrow) {
+        // the offsets less H: the dot product gives s - H (centered_byte)
+        const uint32_t off = (Signed ? mc.off_i32 : mc.off_u64) - mc.half;
+        const uint32_t h_sh = in_vgpr(mc.half << mc.q_shift), m_comp = 256u - mc.m;
+        uint32_t r[kCols];
+#pragma unroll
+        for (int e = 0; e < kCols; ++e)
+          r[e] = centered_byte(__builtin_amdgcn_udot4(lo[e], mc.pow_lo, off, false), mc.q_shift, h_sh, mc.q_recip,
+                               m_comp);
+        w = v2i{static_cast<int>(pack_low_bytes(r[0], r[1], r[2], r[3])),
+                static_cast<int>(pack_low_bytes(r[4], r[5], r[6], r[7]))};
       } else {
-        const uint32_t off = Signed ? mc.off_i64 : mc.off_u64;
-        const uint32_t m_comp = 256u - mc.m;
-        const uint32_t half2 = mc.half * 0x00010001u;
+        const uint32_t off = (Signed ? mc.off_i64 : mc.off_u64) - mc.half;
+        const uint32_t h_sh = in_vgpr(mc.half << mc.pq_shift), m_comp = 256u - mc.m;
         uint32_t r[kCols];
 #pragma unroll
         for (int e = 0; e < kCols; ++e) {
           const uint32_t t = __builtin_amdgcn_udot4(lo[e], mc.pow_lo, off, false);
-          r[e] = mod_low_byte(__builtin_amdgcn_udot4(hi[e], mc.pow_hi, t, false), mc.pq_shift, mc.pq_recip, m_comp);
+          r[e] = centered_byte(__builtin_amdgcn_udot4(hi[e], mc.pow_hi, t, false), mc.pq_shift, h_sh, mc.pq_recip,
+                               m_comp);
         }
-        w = v2i{static_cast<int>(pack_centered(r[0], r[1], r[2], r[3], half2)),
-                static_cast<int>(pack_centered(r[4], r[5], r[6], r[7], half2))};
+        w = v2i{static_cast<int>(pack_low_bytes(r[0], r[1], r[2], r[3])),
+                static_cast<int>(pack_low_bytes(r[4], r[5], r[6], r[7]))};
       }
       *reinterpret_cast<v2i*>(out + static_cast<int64_t>(p) * a.plane_pitch) = w;
     }
@@ -123,11 +147,12 @@ __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConst
 }
 
 // Finite u8: x < 256, s = x + H < 2^9 is inside the range of the int32
-// reduction constants (their s_max is at least 255 + H).
+// reduction constants (their s_max is at least 255 + H), and x itself is
+// s - H (centered_byte).
 __global__ __launch_bounds__(256) void pack_u8_kernel(PackU8Args a, ModulusConsts mc, uint32_t chunks_per_row,
                                                       uint32_t total_chunks, uint32_t vec_load) {
   const uint32_t m_comp = 256u - mc.m;
-  const uint32_t half2 = mc.half * 0x00010001u;
+  const uint32_t h_sh = in_vgpr(mc.half << mc.q_shift);
   for (uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x; ch < total_chunks; ch += gridDim.x * blockDim.x) {
     const uint32_t row = ch / chunks_per_row;
     const int64_t c0 = static_cast<int64_t>(ch - row * chunks_per_row) * 16;
@@ -144,11 +169,11 @@ __global__ __launch_bounds__(256) void pack_u8_kernel(PackU8Args a, ModulusConst
     }
     uint32_t r[16];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) r[e] = mod_low_byte(x[e] + mc.half, mc.q_shift, mc.q_recip, m_comp);
-    const v4i w = {static_cast<int>(pack_centered(r[0], r[1], r[2], r[3], half2)),
-                   static_cast<int>(pack_centered(r[4], r[5], r[6], r[7], half2)),
-                   static_cast<int>(pack_centered(r[8], r[9], r[10], r[11], half2)),
-                   static_cast<int>(pack_centered(r[12], r[13], r[14], r[15], half2))};
+    for (int e = 0; e < 16; ++e) r[e] = centered_byte(x[e], mc.q_shift, h_sh, mc.q_recip, m_comp);
+    const v4i w = {static_cast<int>(pack_low_bytes(r[0], r[1], r[2], r[3])),
+                   static_cast<int>(pack_low_bytes(r[4], r[5], r[6], r[7])),
+                   static_cast<int>(pack_low_bytes(r[8], r[9], r[10], r[11])),
+                   static_cast<int>(pack_low_bytes(r[12], r[13], r[14], r[15]))};
     *reinterpret_cast<v4i*>(a.plane + static_cast<int64_t>(row) * a.plane_ld + c0) = w;
   }
 }

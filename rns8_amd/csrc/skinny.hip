@@ -45,14 +45,17 @@ typedef __attribute__((address_space(3))) v2i lds_v2i;
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kU = 2;                   // 64-K MFMA steps per pipeline step
+constexpr int kU = 4;                   // 64-K MFMA steps per pipeline step
 constexpr int kStepK = 64 * kU;         // K per pipeline step
 constexpr int kBufBytes = kStepK * 16;  // one step of B: kStepK rows x 16 bytes
 constexpr int kAccBias = static_cast<int>(0x80000000u);
-// waves a launch aims for before it splits K: two per SIMD keep about twice
-// the loads in flight that HBM needs to run at full rate
-constexpr int64_t kTargetWaves = 2048;
-constexpr int64_t kMinSliceK = 1024;
+// Waves a launch aims for before it splits K (four per SIMD), and the least
+// a wave streams (A rows and B's 16-byte rows of its slice), so the pipeline
+// prologue stays a small share: at 8192 x 1 x 8192 (9 planes) two slices of
+// 4096 run 136 us against 147 us unsplit; at 8 x 8 x 2^20, 228 slices of
+// 4608 K run 45 us, 256 of 4096 K 50 us and 456 of 2304 K 55 us.
+constexpr int64_t kTargetWaves = 4096;
+constexpr int64_t kMinWaveBytes = 112 << 10;
 
 struct SkinnyArgs {
   const int8_t* a;  // [planes][m][lda]
@@ -191,21 +194,24 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(SkinnyArgs a, Pla
   // Epilogue: lane l holds u = 2^31 + C[row0 + 16 rb + l % 16][4 (l / 16) + e]
   // in element e of acc[rb].
   const ModulusConsts mc = pc.mod[plane];
-  const uint32_t m_comp = 256u - mc.m, half2 = mc.half * 0x00010001u;
+  const CenteredI32 kc = centered_i32_consts(mc);
   int8_t* const dst = a.dst + (static_cast<uint64_t>(slice) * a.nplanes + plane) * a.pitch_dst;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const uint32_t row = row0 + 16u * rb + static_cast<uint32_t>(frow);
     uint32_t r[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = residue_plus_half(static_cast<uint32_t>(acc[rb][e]), mc, m_comp);
+    for (int e = 0; e < 4; ++e) r[e] = centered_residue_i32(static_cast<uint32_t>(acc[rb][e]), mc, kc);
     if (row < a.m)
       *reinterpret_cast<uint32_t*>(dst + static_cast<uint64_t>(row) * 16u + 4u * fk) =
-          pack_centered(r[0], r[1], r[2], r[3], half2);
+          pack_low_bytes(r[0], r[1], r[2], r[3]);
   }
 }
 
-int rows_per_wave_blocks(int64_t m) { return m <= 16 ? 1 : m <= 32 ? 2 : 4; }
+// Row blocks per wave: 32 rows halve B's LDS traffic per A byte against 16;
+// 64 rows ran slower (156 against 145 us at 8192 x 1 x 8192) and need 224
+// registers.
+int rows_per_wave_blocks(int64_t m) { return m <= 16 ? 1 : 2; }
 
 }  // namespace
 
@@ -213,10 +219,11 @@ bool skinny_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, GemmShape& 
   if (n > 16 || m <= 0 || n <= 0 || k <= 0 || nplanes == 0) return false;
   const int rb = rows_per_wave_blocks(m);
   const int64_t waves = (m + 16 * rb - 1) / (16 * rb) * nplanes;
-  // slices of at most 65536 K (int32-exact), at least kMinSliceK unless K is
-  // shorter, toward kTargetWaves waves
+  // slices of at most 65536 K (int32-exact), toward kTargetWaves waves that
+  // each stream at least kMinWaveBytes
   const int64_t need = (k + kSafeKBlock - 1) / kSafeKBlock;
-  int64_t slices = std::min((kTargetWaves + waves - 1) / waves, std::max<int64_t>(1, k / kMinSliceK));
+  const int64_t wave_bytes = k * (std::min<int64_t>(m, 16 * rb) + 16);
+  int64_t slices = std::min((kTargetWaves + waves - 1) / waves, std::max<int64_t>(1, wave_bytes / kMinWaveBytes));
   slices = std::max(slices, need);
   int64_t k_slice = (k + slices - 1) / slices;
   if (slices > 1) k_slice = (k_slice + kStepK - 1) / kStepK * kStepK;
@@ -260,10 +267,8 @@ hipError_t launch_skinny(const GemmArgs& g, const GemmShape& shape, const PlaneC
   const dim3 grid(static_cast<unsigned>((units + kWaves - 1) / kWaves));
   if (rb == 1)
     hipLaunchKernelGGL(skinny_gemm_kernel<1>, grid, dim3(kThreads), 0, stream, a, consts);
-  else if (rb == 2)
-    hipLaunchKernelGGL(skinny_gemm_kernel<2>, grid, dim3(kThreads), 0, stream, a, consts);
   else
-    hipLaunchKernelGGL(skinny_gemm_kernel<4>, grid, dim3(kThreads), 0, stream, a, consts);
+    hipLaunchKernelGGL(skinny_gemm_kernel<2>, grid, dim3(kThreads), 0, stream, a, consts);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || shape.slices <= 1) return e;
   return launch_residue_finalize(g.splitk_ws, g.c, g.m, 16, g.pitch_c, g.nplanes, shape.slices, consts, stream);

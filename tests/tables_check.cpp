@@ -59,11 +59,6 @@ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
   }
   return out;
 }
-uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
-  const uint32_t lo = (a - b) & 0xFFFFu;
-  const uint32_t hi = ((a >> 16) - (b >> 16)) & 0xFFFFu;
-  return lo | (hi << 16);
-}
 
 // SplitMix64 for reproducible random cases.
 struct Rng {
@@ -126,17 +121,14 @@ void check_quot() {
   std::printf("quot checks %" PRIu64 "\n", checks);
 }
 
-// GEMM epilogue: u = x + 2^31 -> residue_plus_half -> pack_centered byte.
-int8_t epilogue_byte(int32_t x, const ModulusConsts& c) {
-  const uint32_t u = static_cast<uint32_t>(x) + 0x80000000u;
-  const uint32_t s = udot4(u, c.pow_lo, c.off_i32);
-  const uint32_t q = mulhi_u24(s << c.q_shift, c.q_recip);
-  return static_cast<int8_t>(mad_u24(q, 256u - c.m, s));  // low byte (x + H) mod m, H not yet subtracted
+// centered_byte (int_ops.hpp): sc = s - H with s congruent to x + H and at
+// most the constants' s_max; the low byte of the result is x's centered
+// residue.
+uint32_t centered_byte(uint32_t sc, uint32_t shift, uint32_t h_sh, uint32_t recip, uint32_t m) {
+  return mad_u24(mulhi_u24((sc << shift) + h_sh, recip), 256u - m, sc);
 }
-uint32_t pack_centered(const uint32_t r[4], uint32_t half2) {  // v_perm + packed u16 subtract
-  const uint32_t p01 = pk_sub_u16(perm(r[1], r[0], 0x0c040c00u), half2);
-  const uint32_t p23 = pk_sub_u16(perm(r[3], r[2], 0x0c040c00u), half2);
-  return perm(p23, p01, 0x06040200u);
+uint32_t pack_low_bytes(const uint32_t r[4]) {  // two v_perm and an or
+  return perm(r[1], r[0], 0x0c0c0400u) | perm(r[3], r[2], 0x04000c0cu);
 }
 
 void check_reduce32() {
@@ -148,16 +140,16 @@ void check_reduce32() {
   uint64_t checks = 0;
   for (uint32_t m = 2; m <= 256; ++m) {
     const ModulusConsts c = make_modulus_consts(m);
-    const uint32_t half2 = c.half * 0x00010001u;
+    // the epilogue's reduction: u = x + 2^31, s - H = dot(bytes(u), pow_lo)
+    // + (off_i32 - H)
+    if (c.off_i32 < c.half || c.off_i64 < c.half || c.off_u64 < c.half) fail("offset below H", m, c.off_i32, c.off_i64, c.off_u64);
     for (size_t i = 0; i + 4 <= xs.size(); i += 4) {
       uint32_t r[4];
       for (int e = 0; e < 4; ++e) {
         const uint32_t u = static_cast<uint32_t>(xs[i + e]) + 0x80000000u;
-        const uint32_t s = udot4(u, c.pow_lo, c.off_i32);
-        const uint32_t q = mulhi_u24(s << c.q_shift, c.q_recip);
-        r[e] = mad_u24(q, 256u - c.m, s);
+        r[e] = centered_byte(udot4(u, c.pow_lo, c.off_i32 - c.half), c.q_shift, c.half << c.q_shift, c.q_recip, m);
       }
-      const uint32_t w = pack_centered(r, half2);
+      const uint32_t w = pack_low_bytes(r);
       for (int e = 0; e < 4; ++e, ++checks) {
         const int64_t want = centered_ref(xs[i + e], m);
         const int8_t got = static_cast<int8_t>(w >> (8 * e));
@@ -169,9 +161,9 @@ void check_reduce32() {
 }
 
 uint32_t pack_byte64(uint64_t u, uint32_t off, const ModulusConsts& c) {
-  uint32_t s = udot4(static_cast<uint32_t>(u), c.pow_lo, off);
+  uint32_t s = udot4(static_cast<uint32_t>(u), c.pow_lo, off - c.half);
   s = udot4(static_cast<uint32_t>(u >> 32), c.pow_hi, s);
-  return mad_u24(mulhi_u24(s << c.pq_shift, c.pq_recip), 256u - c.m, s);
+  return centered_byte(s, c.pq_shift, c.half << c.pq_shift, c.pq_recip, c.m);
 }
 
 void check_pack64() {
@@ -183,7 +175,6 @@ void check_pack64() {
   uint64_t checks = 0;
   for (uint32_t m = 2; m <= 256; ++m) {
     const ModulusConsts c = make_modulus_consts(m);
-    const uint32_t half2 = c.half * 0x00010001u;
     for (size_t i = 0; i < xs.size(); i += 4) {
       uint32_t rs[4], ru[4];
       for (int e = 0; e < 4; ++e) {
@@ -191,7 +182,7 @@ void check_pack64() {
         rs[e] = pack_byte64(v ^ 0x8000000000000000ull, c.off_i64, c);  // signed: bias 2^63
         ru[e] = pack_byte64(v, c.off_u64, c);                          // unsigned
       }
-      const uint32_t ws = pack_centered(rs, half2), wu = pack_centered(ru, half2);
+      const uint32_t ws = pack_low_bytes(rs), wu = pack_low_bytes(ru);
       for (int e = 0; e < 4; ++e, checks += 2) {
         const int64_t want_s = centered_ref(xs[i + e], m);
         const int64_t want_u = centered_ref(static_cast<__int128>(static_cast<uint64_t>(xs[i + e])), m);
@@ -202,8 +193,8 @@ void check_pack64() {
     // finite pack: every byte value
     for (uint32_t x0 = 0; x0 < 256; x0 += 4) {
       uint32_t r[4];
-      for (int e = 0; e < 4; ++e) r[e] = mad_u24(mulhi_u24((x0 + e + c.half) << c.q_shift, c.q_recip), 256u - m, x0 + e + c.half);
-      const uint32_t w = pack_centered(r, half2);
+      for (int e = 0; e < 4; ++e) r[e] = centered_byte(x0 + e, c.q_shift, c.half << c.q_shift, c.q_recip, m);
+      const uint32_t w = pack_low_bytes(r);
       for (int e = 0; e < 4; ++e, ++checks)
         if (static_cast<int8_t>(w >> (8 * e)) != centered_ref(x0 + e, m)) fail("pack u8", m, x0 + e, 0, 0);
     }

@@ -48,7 +48,7 @@ def _check(ctx, A, B, prefix, bound):
 @pytest.mark.parametrize(
     "m,n,k",
     [
-        (1000, 1, 3000),    # GEMV, 4 row blocks per wave, ragged last row group and K step
+        (1000, 1, 3000),    # GEMV, 2 row blocks per wave, ragged last row group and K step
         (4097, 8, 2048),    # N = 8, one row past a row group
         (33, 16, 5000),     # 2 row blocks per wave, one row in the second group
         (16, 5, 20000),     # 1 row block per wave, K split
