@@ -153,33 +153,72 @@ __device__ __forceinline__ void reconstruct(const uint32_t (&words)[P], const ui
   }
 }
 
+// x = sum_{i<J} v_i M_i (J <= 8, M_i the product of the first i ladder
+// moduli) as a 64-bit integer: M_8 < 2^64. Horner's rule runs in 32 bits
+// over digits 0..3 (m_0 m_1 m_2 m_3 < 2^32; v_0 + 256 v_1 are the low two
+// bytes of vp[0] since m_0 = 256) and over digits 4..7 (m_4 m_5 m_6 m_7 <
+// 2^32, every partial value below 2^24 as v_mad_u32_u24 needs), and one
+// 32 x 32 -> 64-bit multiply-add joins the halves.
+template <uint32_t J, uint32_t W>
+__device__ __forceinline__ uint64_t horner64(const uint32_t (&vp)[W]) {
+  static_assert(J >= 1 && J <= 8 && 4 * W >= J, "digits 0..7 of the packed words");
+  static_assert(kLadder[0] == 256 && ladder_product64(4) < (uint64_t{1} << 32) &&
+                    uint64_t{kLadder[4]} * kLadder[5] * kLadder[6] * kLadder[7] < (uint64_t{1} << 32) &&
+                    uint64_t{kLadder[5]} * kLadder[6] * kLadder[7] < (uint64_t{1} << 24),
+                "ladder bounds of the two 32-bit Horner halves");
+  auto digit = [&](uint32_t i) { return (vp[i / 4] >> (8 * (i % 4))) & 0xFFu; };
+  constexpr uint32_t JL = J < 4 ? J : 4;
+  uint32_t lo;
+  if constexpr (JL == 1) {
+    lo = digit(0);
+  } else if constexpr (JL == 2) {
+    lo = vp[0] & 0xFFFFu;
+  } else {
+    uint32_t t = digit(JL - 1);
+#pragma unroll
+    for (int i = static_cast<int>(JL) - 2; i >= 2; --i) t = mad_u24(t, kLadder[i], digit(i));
+    lo = mad_u24(t, uint32_t{kLadder[0]} * kLadder[1], vp[0] & 0xFFFFu);
+  }
+  if constexpr (J <= 4) {
+    return lo;
+  } else {
+    uint32_t hi = digit(J - 1);
+#pragma unroll
+    for (int i = static_cast<int>(J) - 2; i >= 4; --i) hi = mad_u24(hi, kLadder[i], digit(i));
+    return static_cast<uint64_t>(hi) * ladder_product64(4) + lo;
+  }
+}
+
 // One cell for the 64-bit kinds: the low 64 bits of the centered (Signed) or
-// canonical value v, and whether v is admissible.
+// canonical value v, and whether v is admissible (|v| <= bound within int64,
+// resp. v <= bound within uint64; crt.cpp:113-119).
 //
-// Prefixes above the digit split (int64: P > kSplitSigned, uint64:
-// P > kSplitUnsigned): Horner runs over the low J digits only, y = sum_{i<J}
-// v_i M_i < M_J, and the digits from J up decide: all 0 gives v = y, all
-// m_i - 1 (int64) gives v = y - M_J, anything else is out of every 64-bit
-// range (|v| >= M_J > 2^63, resp. v >= M_J >= 2^64).
-//
-// Other prefixes: v is formed as a 24L-bit two's complement value (x - P for
-// a negative result); it has a 64-bit representation iff its bits from 64 up
-// repeat its sign, and then its magnitude is -w or w modulo 2^64, except for
-// v = -2^64, whose low 64 bits are zero (caught by testing mag - 1 against the
-// limit).
-//
-// Both forms make the decisions of sign/magnitude with limbs_le; w is the low
-// 64 bits of v whenever v is admissible.
+// Signed: an admissible result has |v| <= 2^63 < M_8, so for P > 8 its
+// digits from 8 up are all 0 (v = x8 = sum_{i<8} v_i M_i) or all m_i - 1
+// (v = x8 - M_8), anything else is out of range; for P <= 8 the canonical
+// x < M_P < 2^64 is centered against ceil(M_P / 2). Unsigned: the canonical
+// value is x8 + v_8 M_8 + ..., below 2^64 only with digits from 9 up zero and
+// v_8 = 0, or v_8 = 1 and x8 < 2^64 - M_8.
 template <uint32_t P, int L, int E, bool Signed>
 __device__ __forceinline__ uint64_t value64(const uint32_t (&words)[P], const uint32_t (&flipped)[P],
                                             const ExportLimits& lim, bool& ok) {
-  constexpr uint32_t J = Signed ? kSplitSigned : kSplitUnsigned;
-  if constexpr (P > J) {
+  constexpr uint32_t J = P < 8 ? P : 8;
+  constexpr uint64_t MJ = ladder_product64(J);
+  uint32_t vp[GarnerTable<P>::kWords];
+  garner_digits<P, E>(words, flipped, vp);
+  const uint64_t x = horner64<J>(vp);
+  if constexpr (P <= 8) {
+    if constexpr (Signed) {
+      // negative iff x >= ceil(M_P / 2); then |v| = M_P - x <= M_P / 2 < 2^63
+      const bool neg = x >= MJ - MJ / 2;
+      ok = neg ? (MJ - x <= lim.neg64) : (x <= lim.pos64);
+      return neg ? x - MJ : x;
+    } else {
+      ok = x <= lim.pos64;
+      return x;
+    }
+  } else if constexpr (Signed) {
     constexpr GarnerTable<P> T = make_garner_table<P>();
-    uint32_t vp[GarnerTable<P>::kWords];
-    garner_digits<P, E>(words, flipped, vp);
-    uint32_t y[3];  // M_J < 2^72
-    horner<J, 3>(vp, y);
     bool zero_top = true, max_top = true;
 #pragma unroll
     for (uint32_t i = J; i < P; ++i) {
@@ -187,43 +226,18 @@ __device__ __forceinline__ uint64_t value64(const uint32_t (&words)[P], const ui
       zero_top &= d == 0u;
       max_top &= d == T.m[i] - 1u;
     }
-    const uint64_t y64 = static_cast<uint64_t>(y[0] | (y[1] << 24)) |
-                         (static_cast<uint64_t>((y[1] >> 8) | (y[2] << 16)) << 32);
-    if constexpr (Signed) {
-      // v < 0: |v| = M_J - y, and |v| - 1 < neg64 iff y > M_J - 1 - neg64
-      // (neg64 <= 2^63 < M_J)
-      constexpr uint64_t MJ = ladder_product64(J);
-      ok = zero_top ? y64 <= lim.pos64 : (max_top & (y64 > MJ - 1ull - lim.neg64));
-      return zero_top ? y64 : y64 - MJ;
-    } else {
-      ok = zero_top & ((y[2] >> 16) == 0u) & (y64 <= lim.pos64);
-      return y64;
-    }
+    // v < 0: |v| = M_8 - x, admissible iff M_8 - x <= neg64 (neg64 <= 2^63 < M_8)
+    ok = zero_top ? x <= lim.pos64 : (max_top & (x >= MJ - lim.neg64));
+    return zero_top ? x : x - MJ;
   } else {
-    constexpr GarnerTable<P> T = make_garner_table<P>();
-    uint32_t x[L];
-    reconstruct_x<P, L, E>(words, flipped, x);
-    const bool neg = Signed && centered_negative<P, L>(x);
-    uint32_t v[L];
-    uint32_t borrow = 0;
+    bool zero_top = true;
 #pragma unroll
-    for (int l = 0; l < L; ++l) {
-      const uint32_t t = x[l] - (neg ? T.product[l] : 0u) - borrow;
-      borrow = t >> 31;
-      v[l] = t & 0xFFFFFFu;
-    }
-    const uint64_t w = static_cast<uint64_t>(v[0] | (v[1] << 24)) |
-                       (static_cast<uint64_t>((v[1] >> 8) | (v[2] << 16)) << 32);
-    // branch-free: every term is evaluated (bitwise & / |, selects)
-    const uint32_t ext = neg ? 0xFFFFFFu : 0u;
-    uint32_t diff = (v[2] >> 16) ^ (ext & 0xFFu);
-#pragma unroll
-    for (int l = 3; l < L; ++l) diff |= v[l] ^ ext;
-    // ~w = -w - 1 = mag - 1 for v < 0
-    const bool in_neg = ~w < lim.neg64;
-    const bool in_pos = w <= lim.pos64;
-    ok = (diff == 0u) & (neg ? in_neg : in_pos);
-    return w;
+    for (uint32_t i = J + 1; i < P; ++i) zero_top &= ((vp[i / 4] >> (8 * (i % 4))) & 0xFFu) == 0u;
+    const uint32_t v8 = vp[2] & 0xFFu;
+    // v_8 <= 1 keeps the value below 2^64 when x < 2^64 - M_8 (v_8 = 1)
+    const bool fits = v8 == 0u ? x <= lim.pos64 : (v8 == 1u) & (lim.pos64 >= MJ) & (x <= lim.pos64 - MJ);
+    ok = zero_top & fits;
+    return x + static_cast<uint64_t>(v8) * MJ;
   }
 }
 
