@@ -1078,9 +1078,10 @@ rns8_status rns8_create_matrix(rns8_context* ctx, const rns8_matrix_desc* desc, 
       delete m;
       return RNS8_BACKEND_FAILURE;
     }
-    // exact-wide matrices: two words and an event for proofs left on the device
+    // exact-wide matrices: two slots of two words and an event for proofs
+    // left on the device (zeroed below with the planes)
     if (exact_wide(desc->semantics) &&
-        (hipMalloc(reinterpret_cast<void**>(&m->proof_device), 16) != hipSuccess ||
+        (hipMalloc(reinterpret_cast<void**>(&m->proof_device), 32) != hipSuccess ||
          hipEventCreateWithFlags(&m->proof_event, hipEventDisableTiming) != hipSuccess)) {
       free_device(m->planes);
       free_device(m->proof_device);
@@ -1089,6 +1090,8 @@ rns8_status rns8_create_matrix(rns8_context* ctx, const rns8_matrix_desc* desc, 
     }
     // zero planes: a fresh matrix holds the integer 0 and keeps padding zero
     if (launch_zero_words(reinterpret_cast<uint32_t*>(m->planes), m->plane_bytes / 4, ctx->stream) != hipSuccess ||
+        (m->proof_device &&
+         launch_zero_words(reinterpret_cast<uint32_t*>(m->proof_device), 8, ctx->stream) != hipSuccess) ||
         hipStreamSynchronize(ctx->stream) != hipSuccess) {
       free_device(m->planes);
       free_device(m->proof_device);

@@ -57,7 +57,7 @@ rns8_status resolve_exact_proof(const rns8_matrix& m) {
   if (!m.exact_pending) return RNS8_SUCCESS;
   unsigned long long w[2] = {0, 0};
   if (hipSetDevice(m.device_id) != hipSuccess || hipEventSynchronize(m.proof_event) != hipSuccess ||
-      hipMemcpy(w, m.proof_device, sizeof(w), hipMemcpyDeviceToHost) != hipSuccess)
+      hipMemcpy(w, m.proof_words(), sizeof(w), hipMemcpyDeviceToHost) != hipSuccess)
     return RNS8_BACKEND_FAILURE;
   m.exact_max = m.pending_product
                     ? I512::from_u64(m.proof_k) * I512::from_u64(w[0]) * I512::from_u64(w[1])
@@ -108,9 +108,12 @@ rns8_status commit_exact_proof(rns8_matrix& C, const rns8_matrix& A, const rns8_
                                const I512& bound, std::vector<ExactAxis>& rows, std::vector<ExactAxis>& cols,
                                bool pending, hipStream_t stream) {
   if (pending) {
-    if (launch_proof_factors(A.proof_device, B.proof_device, C.proof_device, stream) != hipSuccess ||
+    // into C's other slot, clearing word 0 of its current one
+    if (launch_proof_factors(A.proof_words(), B.proof_words(), C.next_proof_words(), C.proof_words(), stream) !=
+            hipSuccess ||
         hipEventRecord(C.proof_event, stream) != hipSuccess)
       return RNS8_BACKEND_FAILURE;
+    C.proof_slot ^= 1u;
     C.proof_k = static_cast<uint64_t>(plan.desc.k);
   }
   C.exact_max = bound;
@@ -254,10 +257,11 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
       proof_max = native_worst_case(matrix->desc.semantics);
     } else {
       unsigned long long host_max = 0;
-      if (launch_zero_words(reinterpret_cast<uint32_t*>(matrix->proof_device), 2, stream) != hipSuccess ||
+      // word 0 of the current slot as scratch (the other slot stays clear)
+      if (launch_zero_words(reinterpret_cast<uint32_t*>(matrix->proof_words()), 2, stream) != hipSuccess ||
           launch_max_magnitude(src, rows, cols, ld, is_signed ? NativeKind::I64 : NativeKind::U64,
-                               matrix->proof_device, stream) != hipSuccess ||
-          hipMemcpyAsync(&host_max, matrix->proof_device, sizeof(host_max), hipMemcpyDeviceToHost, stream) !=
+                               matrix->proof_words(), stream) != hipSuccess ||
+          hipMemcpyAsync(&host_max, matrix->proof_words(), sizeof(host_max), hipMemcpyDeviceToHost, stream) !=
               hipSuccess ||
           hipStreamSynchronize(stream) != hipSuccess)
         return RNS8_BACKEND_FAILURE;
@@ -287,12 +291,16 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
                 matrix->plane_pitch,
                 matrix->prefix,
                 is_signed ? NativeKind::I64 : NativeKind::U64,
-                deferred ? matrix->proof_device : nullptr};
-  if (deferred && launch_zero_words(reinterpret_cast<uint32_t*>(matrix->proof_device), 2, stream) != hipSuccess)
-    return RNS8_BACKEND_FAILURE;
+                // the maximum goes to word 0 of the other slot (zero), and the
+                // same launch clears word 0 of the current one
+                deferred ? matrix->next_proof_words() : nullptr,
+                deferred ? matrix->proof_words() : nullptr};
   if (launch_pack_native(args, make_ladder_plane_consts(matrix->prefix), stream) != hipSuccess)
     return RNS8_BACKEND_FAILURE;
-  if (deferred && hipEventRecord(matrix->proof_event, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  if (deferred) {
+    matrix->proof_slot ^= 1u;
+    if (hipEventRecord(matrix->proof_event, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  }
   if (where == Source::Host) {
     const rns8_status st = sync(stream);
     if (st != RNS8_SUCCESS) return st;

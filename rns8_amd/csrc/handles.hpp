@@ -99,19 +99,24 @@ struct rns8_matrix {
   uint32_t exact_prefix = 0;
   std::vector<ExactAxis> exact_rows;
   std::vector<ExactAxis> exact_cols;
-  // A proof left on the device: by a device-pointer pack (max |x| in
-  // proof_device[0]) or by a GEMM of two such operands (their maxima in
-  // proof_device[0..1]; the exact bound is proof_k * [0] * [1]). While
+  // A proof left on the device: by a device-pointer pack (max |x| in word 0
+  // of the current slot) or by a GEMM of two such operands (their maxima in
+  // words 0 and 1; the exact bound is proof_k * [0] * [1]). While
   // exact_pending is set, exact_max holds a worst case the exact value never
   // exceeds, so a decision that the worst case passes is the exact decision;
   // resolve_exact_proof reads the words back (after proof_event) when a
-  // decision needs the exact value. Exact-wide matrices own the two words and
-  // the event from creation.
+  // decision needs the exact value. Exact-wide matrices own two slots of two
+  // words and the event from creation. Word 0 of the slot that is not current
+  // is zero (the writer of a new proof clears the old slot's word 0 in the
+  // same launch), so a pack's atomic maximum needs no clearing launch.
   mutable bool exact_pending = false;
   bool pending_product = false;
   uint64_t proof_k = 0;
-  unsigned long long* proof_device = nullptr;
+  unsigned long long* proof_device = nullptr;  // 2 slots x 2 words
+  uint32_t proof_slot = 0;
   hipEvent_t proof_event = nullptr;
+  unsigned long long* proof_words() const { return proof_device + 2 * proof_slot; }
+  unsigned long long* next_proof_words() const { return proof_device + 2 * (proof_slot ^ 1u); }
   // cached staging buffers (export is logically const, reference
   // api_export.cpp:276-287 keeps the same kind of cache on the matrix)
   void* upload = nullptr;

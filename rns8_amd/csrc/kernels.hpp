@@ -28,14 +28,17 @@ struct PackArgs {
   uint32_t nplanes;
   NativeKind kind;
   // when set: the same launch also writes max |x| over the matrix here
-  // (atomic max; the word must be zero on entry)
+  // (atomic max; the word must be zero on entry) and sets *max_clear to
+  // zero (a word no thread of the launch reads)
   unsigned long long* max_out;
+  unsigned long long* max_clear;
 };
 hipError_t launch_pack_native(const PackArgs& args, const PlaneConsts& consts, hipStream_t stream);
-// out[0] = a[0], out[1] = b[0] on the stream: the magnitude proofs of a
-// GEMM's two operands, copied into its result's proof words.
+// out[0] = a[0], out[1] = b[0] and clear[0] = 0 on the stream: the
+// magnitude proofs of a GEMM's two operands, copied into its result's proof
+// words, and the word 0 of its previous proof slot cleared.
 hipError_t launch_proof_factors(const unsigned long long* a, const unsigned long long* b, unsigned long long* out,
-                                hipStream_t stream);
+                                unsigned long long* clear, hipStream_t stream);
 
 // Maximum |x| over a rows x cols native matrix (row stride ld elements),
 // combined into *out with an atomic max. *out must be zero on entry.

@@ -143,7 +143,10 @@ __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConst
       *reinterpret_cast<v2i*>(out + static_cast<int64_t>(p) * a.plane_pitch) = w;
     }
   }
-  if constexpr (kMax) block_max_to(best, a.max_out);
+  if constexpr (kMax) {
+    if (blockIdx.x == 0 && threadIdx.x == 0 && a.max_clear) *a.max_clear = 0ull;
+    block_max_to(best, a.max_out);
+  }
 }
 
 // Finite u8: x < 256, s = x + H < 2^9 is inside the range of the int32
@@ -205,11 +208,13 @@ __global__ __launch_bounds__(256) void max_magnitude_kernel(const uint64_t* src,
 }
 
 // Proof factors of a GEMM result whose operands both carry device-resident
-// maxima: out[0] = a[0], out[1] = b[0] (one thread).
+// maxima: out[0] = a[0], out[1] = b[0], and word 0 of the result's previous
+// proof slot cleared (one thread).
 __global__ void copy_proof_factors_kernel(const unsigned long long* a, const unsigned long long* b,
-                                          unsigned long long* out) {
+                                          unsigned long long* out, unsigned long long* clear) {
   out[0] = a[0];
   out[1] = b[0];
+  clear[0] = 0ull;
 }
 
 unsigned grid_for(int64_t items) {
@@ -250,9 +255,9 @@ hipError_t launch_pack_native(const PackArgs& a, const PlaneConsts& consts, hipS
 }
 
 hipError_t launch_proof_factors(const unsigned long long* a, const unsigned long long* b, unsigned long long* out,
-                                hipStream_t stream) {
-  if (!a || !b || !out) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(copy_proof_factors_kernel, dim3(1), dim3(1), 0, stream, a, b, out);
+                                unsigned long long* clear, hipStream_t stream) {
+  if (!a || !b || !out || !clear) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(copy_proof_factors_kernel, dim3(1), dim3(1), 0, stream, a, b, out, clear);
   return hipGetLastError();
 }
 
