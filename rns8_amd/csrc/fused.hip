@@ -333,27 +333,28 @@ __global__ __launch_bounds__(kThreads, 1) void fused_native_kernel(FusedArgs a, 
 // Adds the slices' centered residues of 16 consecutive cells (one 16-byte
 // chunk per slice) and writes their centered residue into C (reference
 // cpu_reference.cpp:156-311: the plane result is the sum's residue). A block
-// covers 32 chunks; its eight 32-thread groups each add every eighth slice,
-// so the loads of many slices are in flight at once, and group 0 combines
-// the eight partial sums. m * ldc is a multiple of 16 (ldc is).
-constexpr int kFinalChunks = 32;
-constexpr int kFinalGroups = 8;
+// covers 256 / G chunks; its G thread groups each add every G-th slice, with
+// up to four loads in flight per thread, and group 0 combines the G partial
+// sums. m * ldc is a multiple of 16 (ldc is).
+template <int G>
 __global__ __launch_bounds__(256) void residue_finalize_kernel(const int8_t* ws, int8_t* c, int64_t m, int64_t ldc,
                                                                int64_t pitch_c, uint32_t nplanes, uint32_t slices,
                                                                PlaneConsts pc) {
-  __shared__ int32_t part[kFinalGroups][16][kFinalChunks];
+  constexpr int kChunks = 256 / G;
+  __shared__ int32_t part[G][16][kChunks];
   const int64_t chunks_per_plane = m * ldc / 16;
   const int64_t total = chunks_per_plane * nplanes;
   const int64_t slice_chunks = static_cast<int64_t>(nplanes) * chunks_per_plane;
   const v4i* const src = reinterpret_cast<const v4i*>(ws);
-  const int lc = threadIdx.x % kFinalChunks;
-  const int grp = threadIdx.x / kFinalChunks;
-  for (int64_t c0 = static_cast<int64_t>(blockIdx.x) * kFinalChunks; c0 < total;
-       c0 += static_cast<int64_t>(gridDim.x) * kFinalChunks) {
+  const int lc = threadIdx.x % kChunks;
+  const int grp = threadIdx.x / kChunks;
+  for (int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunks; c0 < total;
+       c0 += static_cast<int64_t>(gridDim.x) * kChunks) {
     const int64_t ch = c0 + lc;
     int32_t sum[16] = {};
     if (ch < total) {
-      for (uint32_t s = grp; s < slices; s += kFinalGroups) {
+#pragma unroll 4
+      for (uint32_t s = grp; s < slices; s += G) {
         const v4i v = src[static_cast<int64_t>(s) * slice_chunks + ch];
 #pragma unroll
         for (int d = 0; d < 4; ++d)
@@ -367,7 +368,7 @@ __global__ __launch_bounds__(256) void residue_finalize_kernel(const int8_t* ws,
     __syncthreads();
     if (grp == 0 && ch < total) {
 #pragma unroll
-      for (int g = 1; g < kFinalGroups; ++g)
+      for (int g = 1; g < G; ++g)
 #pragma unroll
         for (int e = 0; e < 16; ++e) sum[e] += part[g][e][lc];
       const uint32_t plane = static_cast<uint32_t>(ch / chunks_per_plane);
@@ -465,8 +466,8 @@ hipError_t launch_residue_finalize(const int8_t* ws, int8_t* c, int64_t m, int64
       (reinterpret_cast<uintptr_t>(c) & 15u) != 0)
     return hipErrorInvalidValue;
   const int64_t chunks = static_cast<int64_t>(nplanes) * m * ldc / 16;
-  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((chunks + kFinalChunks - 1) / kFinalChunks, 4096));
-  hipLaunchKernelGGL(residue_finalize_kernel, dim3(blocks), dim3(256), 0, stream, ws, c, m, ldc, pitch_c, nplanes,
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((chunks + 31) / 32, 4096));
+  hipLaunchKernelGGL(residue_finalize_kernel<8>, dim3(blocks), dim3(256), 0, stream, ws, c, m, ldc, pitch_c, nplanes,
                      slices, consts);
   return hipGetLastError();
 }
