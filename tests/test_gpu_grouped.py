@@ -56,7 +56,8 @@ def _check_against_ungrouped(ctx, group, modulus=None):
 
 
 @pytest.mark.parametrize("m,n,k,count", [(300, 200, 150, 5), (1024, 1024, 512, 2), (64, 64, 32, 40),
-                                         (128, 128, 8192, 3), (33, 517, 70000, 2)])
+                                         (128, 128, 8192, 3), (33, 517, 70000, 2),
+                                         (500, 7, 3000, 3), (8, 8, 80000, 2)])
 def test_bounded_i64_group_matches_ungrouped_and_oracle(gpu_ctx, m, n, k, count):
     bound = 1 << 62
     desc = r.gemm_desc(r.BOUNDED_I64, r.BOUND_GLOBAL_MAX_ABS, m, n, k, bound=bound, max_prefix=9,

@@ -92,3 +92,17 @@ def test_wide_k_split_matches_oracle(gpu_ctx, m, n, k):
     B = inputs.int_range(n * 5 + k, (k, n), 18)
     plan = _check(gpu_ctx, A, B, 9, k << 36)
     assert "K split" in plan.selected_kernel()
+
+
+@pytest.mark.parametrize("modulus,field", [(251, True), (256, False), (2, True), (255, False)])
+def test_skinny_finite_oneshot(gpu_ctx, modulus, field):
+    # one finite plane on the skinny kernel, K split into residue slices
+    m, n, k = 300, 7, 20000
+    A = inputs.bytes_below(modulus + 1, (m, k), 256)
+    B = inputs.bytes_below(modulus + 2, (k, n), 256)
+    sem = r.FINITE_FIELD_U8 if field else r.FINITE_RING_U8
+    desc = r.gemm_desc(sem, r.BOUND_NONE, m, n, k, finite_modulus=modulus)
+    st, C = r.gemm_finite_u8_oneshot(gpu_ctx, desc, modulus, A, B, field)
+    assert st == 0
+    np.testing.assert_array_equal(C, oracle.gemm_finite_u8(A, B, modulus))
+    np.testing.assert_array_equal(C, ((A.astype(np.int64) @ B.astype(np.int64)) % modulus).astype(np.uint8))

@@ -85,6 +85,20 @@ def test_noalloc_without_split(gpu_ctx):
     np.testing.assert_array_equal(C.read_residues(), _with_workspace(ctx, plan, Am, Bm).read_residues())
 
 
+def test_noalloc_skinny_split(gpu_ctx):
+    """A result 16 columns wide or less runs the skinny kernel; with a K split
+    its residue slots live in the scratch (8 x 8 x 300000 at prefix 9: 62
+    slices, 71 KB), after a larger split shape has filled more of it."""
+    ctx = gpu_ctx
+    p1, A1, B1, mk1, _, _ = _setup(ctx, True, 128, 128, 65536, 8, 1 << 62, 1205)
+    assert _noalloc(ctx, p1, A1, B1, mk1()) == r.SUCCESS
+    p2, A2, B2, mk2, A, B = _setup(ctx, True, 8, 8, 300000, 9, 1 << 62, 1206)
+    C2 = mk2()
+    assert _noalloc(ctx, p2, A2, B2, C2) == r.SUCCESS
+    hip.synchronize()
+    np.testing.assert_array_equal(C2.read_residues(), _with_workspace(ctx, p2, A2, B2).read_residues())
+
+
 def test_noalloc_refusals_leave_result(gpu_ctx):
     """Split-K residues beyond the scratch (256 x 256 x 65536 at prefix 9: 15
     slices x 9 planes x 256 x 256 bytes = 8.8 MB) and exact-wide plans are
