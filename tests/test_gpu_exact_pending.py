@@ -164,6 +164,44 @@ def test_result_proof_survives_operand_repack(gpu_ctx, signed):
     assert st == r.RANGE_ERROR
 
 
+@pytest.mark.parametrize("signed", [True, False])
+@pytest.mark.parametrize("large_packs", [1, 2])
+def test_repack_proves_only_the_new_maximum(gpu_ctx, signed, large_packs):
+    """Device packs of one matrix in a row: the proof words alternate between
+    two slots and the slot a pack takes must start from zero, so after packs
+    of the chain's large A and then of ones, C = A x B carries the maximum 1.
+    At the scale one above the large-A threshold the chain is admitted only
+    with that proof (a maximum carried over from an earlier pack would refuse
+    it)."""
+    ctx = gpu_ctx
+    prefix = 17
+    P = oracle.modulus_product(prefix)
+    s = ((P - 1) // 2 if signed else P - 1) // _oracle_chain_bound(signed, 1) + 1
+    A, B = _chain_unit(signed)
+    maxb = max(abs(v) for row in B for v in row)
+    bc, Cop = xr.gemm_bound(xr.uniform_operand(1), xr.uniform_operand(maxb), 1, 2, 2)
+    bd, _ = xr.gemm_bound(Cop, xr.uniform_operand(abs(s)), 1, 2, 2)
+    assert xr.fits(signed, bd, P)
+    m, k1, k2, n = 1, 2, 2, 2
+    dt = np.int64 if signed else np.uint64
+    p1, p2 = _plan(ctx, signed, m, k2, k1, prefix), _plan(ctx, signed, m, n, k2, prefix)
+    Am, Bm, Cm = _matrix(ctx, signed, m, k1, prefix), _matrix(ctx, signed, k1, k2, prefix), _matrix(ctx, signed, m, k2, prefix)
+    Em, Dm = _matrix(ctx, signed, k2, n, prefix), _matrix(ctx, signed, m, n, prefix)
+    for _ in range(large_packs):
+        assert _pack_device(ctx, Am, np.array(A, dtype=object).astype(dt), signed) == r.SUCCESS
+    assert _pack_device(ctx, Am, np.ones((m, k1), dtype=dt), signed) == r.SUCCESS
+    assert _pack_device(ctx, Bm, np.array(B, dtype=object).astype(dt), signed) == r.SUCCESS
+    assert _pack_device(ctx, Em, np.array([[s] * n] * k2, dtype=object).astype(dt), signed) == r.SUCCESS
+    ws1, ws2 = r.Workspace(ctx, p1), r.Workspace(ctx, p2)
+    r.check(r.lib().rns8_mi355x_gemm_rns_async(ctx.ptr, p1.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws1.ptr, None), "C = A x B")
+    st = r.lib().rns8_mi355x_gemm_rns_async(ctx.ptr, p2.ptr, Cm.ptr, Em.ptr, Dm.ptr, ws2.ptr, None)
+    hip.synchronize()
+    assert st == r.SUCCESS
+    out = _export(ctx, p2, Dm, m, n, 4, signed)
+    c = 2 * int(B[0][0])
+    assert [oracle.limbs_to_int(out[0, 4 * j:4 * j + 4], signed) for j in range(n)] == [2 * c * s] * n
+
+
 def test_grouped_device_packed_operands(gpu_ctx):
     ctx = gpu_ctx
     m, n, k, prefix, L, T = 64, 48, 200, 18, 3, 3
