@@ -301,12 +301,9 @@ def main() -> int:
         metric = f"exact {'int64' if signed else 'uint64'} GEMM effective TOPS (2MNK/s) at {M}x{N}x{K} prefix {P}"
     roofline = {
         "bound": "mfma", "kernel": kernel, "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-        "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_from_profiles("plane_gemm_kernel", args.config),
-        "per_launch_ops": gemm_ops,
+        "frac": round(achieved / PEAK_INT8_TOPS, 4), "per_launch_ops": gemm_ops,
     }
-    if roofline["traffic"] is not None:
-        roofline["traffic_source"] = ("profiles/traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE per dispatch of "
-                                      "this kernel at this workload, copy-calibrated; not measured in this run")
+    traffic_kernels, traffic_workload = ["plane_gemm_kernel"], args.config
     if fused:
         # pack and GEMM in one pass: the native operands are read (8 bytes per
         # element) and the C planes written; HBM bounds it for tall-skinny shapes
@@ -315,22 +312,30 @@ def main() -> int:
         gemm_bytes = 8 * K * (M + N) + P * M * N
         gbs = gemm_bytes / ((stage[0] + stage[1] + stage[2]) * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": kernel, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "per_launch_bytes": gemm_bytes}
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "per_launch_bytes": gemm_bytes}
+        traffic_kernels = ["fused_native_kernel", "residue_finalize_kernel"]
     elif args.config in SKINNY:
         # at most 16 columns: the GEMM reads A's planes once and B's (padded
         # to 16 columns) once, so HBM bounds it
-        kernel = "skinny_gemm_kernel<RB>" + (" K split + residue_finalize_kernel" if args.config == "small64" else "")
+        kernel = plan.selected_kernel()
         gemm_bytes = P * (M * K + K * 16 + M * 16)
         gbs = gemm_bytes / (stage[2] * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": kernel, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "per_launch_bytes": gemm_bytes}
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "per_launch_bytes": gemm_bytes}
+        traffic_kernels = ["skinny_gemm_kernel"] + (["residue_finalize_kernel"] if "K split" in kernel else [])
     elif args.config == "c5":
         # tall and skinny: the GEMM streams P planes of A and B once (K x (M + N) bytes
         # each) and does little MFMA work per byte, so HBM bounds it
         gemm_bytes = P * K * (M + N) + P * M * N
         gbs = gemm_bytes / (stage[2] * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": kernel, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "per_launch_bytes": gemm_bytes}
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "per_launch_bytes": gemm_bytes}
+        traffic_kernels, traffic_workload = ["plane_gemm_kernel", "residue_finalize_kernel"], "c5_packed"
+    roofline["traffic"] = traffic_from_profiles(traffic_kernels, traffic_workload)
+    if roofline["traffic"] is not None:
+        roofline["traffic_source"] = ("profiles/traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE per dispatch of "
+                                      f"{' + '.join(traffic_kernels)} at this workload, copy-calibrated; not "
+                                      "measured in this run")
     result = {
         "metric": metric,
         "value": round(value, 3),
@@ -720,15 +725,17 @@ def tiled_operands(A, bits, N, K):
     return A, bounds
 
 
-def traffic_from_profiles(kernel_prefix: str, workload: str):
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
-    counter summary (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE per
-    dispatch, scaled by a device-copy calibration of known size), or None."""
+def traffic_from_profiles(kernels, workload: str):
+    """HBM bytes per launch of the timed kernel (or the sum over the kernels
+    of one timed stage) from the committed rocprofv3 counter summary
+    (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE per dispatch, scaled by
+    a device-copy calibration of known size), or None."""
     path = ROOT / "profiles" / "traffic.json"
+    if isinstance(kernels, str):
+        kernels = [kernels]
     try:
         data = json.loads(path.read_text())
-        entry = data["kernels"][workload][kernel_prefix]
-        return int(entry["hbm_bytes_per_launch"])
+        return sum(int(data["kernels"][workload][k]["hbm_bytes_per_launch"]) for k in kernels)
     except (OSError, KeyError, ValueError):
         return None
 
