@@ -48,6 +48,8 @@ CONFIGS = {
     "small64": ("i64", 8, 8, 1 << 20, 25, 1 << 62, 9, True),
 }
 SKINNY = ("gemv1", "gemv8", "small64")
+# configs whose default step is the fused native-input GEMM (--packed: packs + plane GEMM)
+FUSED_DEFAULT = ("c5", "gemv1", "gemv8")
 # grouped resident GEMM: GROUP_TASKS same-shape int64 tasks per step
 GROUPED = ("i64", 1024, 1024, 1024, 25, 1 << 62, 9, True)
 GROUP_TASKS = 8
@@ -131,8 +133,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--packed", action="store_true",
-                    help="c5: two packs and the split-K plane GEMM in place of the fused native-input GEMM (the "
-                         "default route for this tall-skinny shape)")
+                    help="c5/gemv1/gemv8: two packs and the plane GEMM in place of the fused native-input GEMM (the "
+                         "default route for these shapes)")
     ap.add_argument("--fused", action="store_true",
                     help="c1/c3: one fused native-input GEMM (rns8_mi355x_gemm_native_*_async) in place of the two "
                          "packs and the plane GEMM")
@@ -210,9 +212,9 @@ def main() -> int:
     pack = L.rns8_mi355x_pack_i64_device if signed else L.rns8_mi355x_pack_u64_device
     export = L.rns8_mi355x_export_i64_device if signed else L.rns8_mi355x_export_u64_device
     native = L.rns8_mi355x_gemm_native_i64_async if signed else L.rns8_mi355x_gemm_native_u64_async
-    # tall-skinny C5 runs the fused native-input GEMM unless --packed asks for
+    # tall-skinny C5 and the GEMVs run the fused native-input GEMM unless --packed asks for
     # the two packs and the split-K plane GEMM
-    fused = args.fused or (args.config == "c5" and not args.packed)
+    fused = args.fused or (args.config in FUSED_DEFAULT and not args.packed)
     if fused and tiled:
         log("[bench] --fused applies to plans with a global bound only")
         return 2
@@ -307,13 +309,18 @@ def main() -> int:
     if fused:
         # pack and GEMM in one pass: the native operands are read (8 bytes per
         # element) and the C planes written; HBM bounds it for tall-skinny shapes
-        kernel = "fused_native_kernel<Signed,NP> + residue_finalize_kernel"
+        # results at most 16 columns wide take the skinny form (B's planes
+        # first, then A converted in registers) while its workspace fits 64 MiB
+        skinny_form = N <= 16 and P * 16 * ((K + 63) // 64 * 64) <= (64 << 20)
+        kernel = ("pack_bt_kernel + fused_skinny_kernel<Signed,G,First256> + residue_finalize_kernel" if skinny_form
+                  else "fused_native_kernel<Signed,NP> + residue_finalize_kernel")
         workload = workload.replace("pack+GEMM", "fused pack+GEMM")
         gemm_bytes = 8 * K * (M + N) + P * M * N
         gbs = gemm_bytes / ((stage[0] + stage[1] + stage[2]) * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": kernel, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(gbs / PEAK_HBM_GBS, 4), "per_launch_bytes": gemm_bytes}
-        traffic_kernels = ["fused_native_kernel", "residue_finalize_kernel"]
+        traffic_kernels = (["pack_bt_kernel", "fused_skinny_kernel", "residue_finalize_kernel"] if skinny_form
+                           else ["fused_native_kernel", "residue_finalize_kernel"])
     elif args.config in SKINNY:
         # at most 16 columns: the GEMM reads A's planes once and B's (padded
         # to 16 columns) once, so HBM bounds it

@@ -392,14 +392,17 @@ __global__ __launch_bounds__(256) void residue_finalize_kernel(const int8_t* ws,
 
 }  // namespace
 
-bool fused_operands_ok(const void* a, int64_t lda, const void* b, int64_t ldb) {
-  return (reinterpret_cast<uintptr_t>(a) & 15u) == 0 && (reinterpret_cast<uintptr_t>(b) & 15u) == 0 && lda % 2 == 0 &&
-         ldb % 2 == 0 && lda < (int64_t{1} << 21) && ldb < (int64_t{1} << 21);
+bool fused_operands_ok(const void* a, int64_t lda, const void* b, int64_t ldb, bool skinny) {
+  const bool a_ok = (reinterpret_cast<uintptr_t>(a) & 15u) == 0 && lda % 2 == 0 && lda < (int64_t{1} << 21);
+  if (skinny) return a_ok && (reinterpret_cast<uintptr_t>(b) & 7u) == 0;
+  return a_ok && (reinterpret_cast<uintptr_t>(b) & 15u) == 0 && ldb % 2 == 0 && ldb < (int64_t{1} << 21);
 }
 
 bool choose_fused_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, int64_t ldc, FusedShape& out) {
   out = FusedShape{};
   if (m <= 0 || n <= 0 || k <= 0 || nplanes == 0 || nplanes > kMaxPrefix || ldc < n || ldc % 16 != 0) return false;
+  // results at most 16 columns wide: the skinny form (fused_skinny.hip)
+  if (n <= 16 && ldc == 16 && fused_skinny_shape(m, n, k, nplanes, out)) return true;
   if (m >= (int64_t{1} << 31) || n >= (int64_t{1} << 31)) return false;
   const int64_t tiles = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN);
   const int64_t groups = (nplanes + kGroupPlanes - 1) / kGroupPlanes;
@@ -425,18 +428,19 @@ bool fused_args_ok(const FusedArgs& a) {
   FusedShape expect;
   if (!a.a || !a.b || !a.c || !a.ws || a.lda < a.k || a.ldb < a.n) return false;
   if (!choose_fused_shape(a.m, a.n, a.k, a.nplanes, a.ldc, expect) || expect.slices != a.shape.slices ||
-      expect.k_slice != a.shape.k_slice)
+      expect.k_slice != a.shape.k_slice || expect.skinny != a.shape.skinny || expect.ws_bytes != a.shape.ws_bytes)
     return false;
   // the finalize moves 16-byte chunks of the workspace and of C's planes
   if (a.pitch_c < a.m * a.ldc || a.pitch_c % 16 != 0 || (reinterpret_cast<uintptr_t>(a.c) & 15u) != 0 ||
       (reinterpret_cast<uintptr_t>(a.ws) & 15u) != 0)
     return false;
   // the operand loads read 16-byte chunks at 32-bit byte offsets
-  return fused_operands_ok(a.a, a.lda, a.b, a.ldb);
+  return fused_operands_ok(a.a, a.lda, a.b, a.ldb, a.shape.skinny != 0);
 }
 
 hipError_t launch_fused_native(const FusedArgs& a, const PlaneConsts& consts, hipStream_t stream) {
   if (!fused_args_ok(a)) return hipErrorInvalidValue;
+  if (a.shape.skinny) return launch_fused_skinny(a, consts, stream);
   const uint32_t tiles_n = static_cast<uint32_t>((a.n + kTileN - 1) / kTileN);
   const uint32_t tiles = static_cast<uint32_t>((a.m + kTileM - 1) / kTileM) * tiles_n;
   const bool sgn = a.kind == NativeKind::I64;

@@ -79,14 +79,20 @@ hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStrea
 // where the fused path is not offered (its int8 workspace of partial residues,
 // [slices][planes][m][ldc], would exceed its limit).
 struct FusedShape {
-  uint32_t slices;    // K slices, each a multiple of 32 and at most 65536 deep
+  uint32_t slices;    // K slices, each a multiple of 32 (64 for the skinny form) and at most 65536 deep
   int64_t k_slice;
   uint64_t ws_bytes;
+  // results at most 16 columns wide (fused_skinny.hip): the workspace starts
+  // with B's transposed residue planes (bt_bytes), then the slices' slots
+  uint32_t skinny;
+  uint64_t bt_bytes;
 };
 bool choose_fused_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, int64_t ldc, FusedShape& out);
-// The fused path's operand requirements: 16-byte aligned operands, even row
-// strides below 2^21 elements.
-bool fused_operands_ok(const void* a, int64_t lda, const void* b, int64_t ldb);
+bool fused_skinny_shape(int64_t m, int64_t n, int64_t k, uint32_t nplanes, FusedShape& out);
+// The fused path's operand requirements: a 16-byte aligned A with an even row
+// stride below 2^21 elements; B likewise for the tile form, any 8-byte aligned
+// B for the skinny form (its loads are scalar).
+bool fused_operands_ok(const void* a, int64_t lda, const void* b, int64_t ldb, bool skinny);
 struct FusedArgs {
   const void* a;  // device, m x k native elements at row stride lda
   const void* b;  // device, k x n native elements at row stride ldb
@@ -103,6 +109,9 @@ struct FusedArgs {
 // otherwise, before enqueuing anything).
 bool fused_args_ok(const FusedArgs& args);
 hipError_t launch_fused_native(const FusedArgs& args, const PlaneConsts& consts, hipStream_t stream);
+// The skinny form (shape.skinny), called by launch_fused_native once the
+// arguments are checked.
+hipError_t launch_fused_skinny(const FusedArgs& args, const PlaneConsts& consts, hipStream_t stream);
 // Per-tile schedules: `units` edge x edge tile-planes (edge 256 or 128) from a
 // device list of two words each, (plane << 24 | tile row) and (quadrant mask
 // << 24 | tile column); bit q = 2 * (row half) + (column half) of the mask
