@@ -18,8 +18,9 @@
 // (162 registers, three waves per SIMD) in the hope that the other waves
 // find A in L2, each wave's loads cost as much as the first one's (358
 // against 187 us at 8192 x 1 x 8192, 9 planes).
-//   * A: a 64-K step of the wave's 16 rows is eight 16-byte non-temporal
-//     loads per lane, one step ahead: load j of lane l reads elements
+//   * A: a 64-K step of the wave's 16 rows is eight 16-byte loads per lane,
+//     one step ahead (ordinary loads: the two halves of a 128-byte line
+//     come from consecutive loads, and non-temporal ones were 4% slower): load j of lane l reads elements
 //     8j + 2 (l / 16) and +1 of row l % 16, so each load instruction covers
 //     64 contiguous bytes of every row (with the 16 K-contiguous elements per
 //     lane that the MFMA layout suggests, it touched 64 cache lines and ran
@@ -63,7 +64,6 @@ constexpr int kStep = 64;           // K per MFMA step
 constexpr int kMaxGroup = 9;        // planes per wave: at most 256 registers, two waves per SIMD
 constexpr int kMinBlocks = 3;       // workgroups per CU (168 registers; nine planes spill two before the loop)
 constexpr int kAccBias = static_cast<int>(0x80000000u);
-constexpr int kNonTemporal = 2;     // buffer-load cache policy bit: nt (streaming)
 constexpr int64_t kTargetWaves = 4096;
 constexpr int64_t kMinSliceK = 1024;  // 16 steps per wave at least, unless K is shorter
 constexpr int64_t kMaxK = int64_t{1} << 23;
@@ -91,13 +91,14 @@ __device__ __forceinline__ uint32_t residue64(uint32_t lo, uint32_t hi, const Mo
   return centered_byte(s, mc.pq_shift, in_vgpr(mc.half << mc.pq_shift), mc.pq_recip, 256u - mc.m);
 }
 
-// B^T planes: thread t writes byte run t (16 bytes) of every plane: K slots
+// B^T planes: thread t of grid row p writes byte run t (16 bytes) of plane p
+// (one plane per grid row, so even a small B spreads over the chip): K slots
 // 16q .. 16q + 15 of column c in 64-K step s, t = 64 s + 4 c + q; slot
 // 16q + e holds k = 64 s + 8 (e / 2) + 2q + e % 2 (the order of the A loads);
 // columns past n and k past K are zero.
 template <bool Signed>
 __global__ __launch_bounds__(256) void pack_bt_kernel(const uint64_t* b, int64_t ldb, uint32_t k, uint32_t n,
-                                                      uint32_t kp, int8_t* bt, uint32_t nplanes, PlaneConsts pc) {
+                                                      uint32_t kp, int8_t* bt, PlaneConsts pc) {
   const uint32_t runs = kp / 16u;
   const uint32_t total = 16u * runs;
   for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += gridDim.x * blockDim.x) {
@@ -112,18 +113,16 @@ __global__ __launch_bounds__(256) void pack_bt_kernel(const uint64_t* b, int64_t
       lo[e] = static_cast<uint32_t>(x);
       hi[e] = static_cast<uint32_t>(x >> 32);
     }
-    int8_t* const out = bt + static_cast<uint64_t>(t) * 16u;
-    for (uint32_t p = 0; p < nplanes; ++p) {
-      const ModulusConsts mc = pc.mod[p];
-      uint32_t r[16];
+    const uint32_t p = blockIdx.y;
+    const ModulusConsts mc = pc.mod[p];
+    uint32_t r[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) r[e] = residue64<Signed>(lo[e], hi[e], mc);
-      const v4i w = v4i{static_cast<int>(pack_low_bytes(r[0], r[1], r[2], r[3])),
-                        static_cast<int>(pack_low_bytes(r[4], r[5], r[6], r[7])),
-                        static_cast<int>(pack_low_bytes(r[8], r[9], r[10], r[11])),
-                        static_cast<int>(pack_low_bytes(r[12], r[13], r[14], r[15]))};
-      *reinterpret_cast<v4i*>(out + static_cast<uint64_t>(p) * 16u * kp) = w;
-    }
+    for (int e = 0; e < 16; ++e) r[e] = residue64<Signed>(lo[e], hi[e], mc);
+    const v4i w = v4i{static_cast<int>(pack_low_bytes(r[0], r[1], r[2], r[3])),
+                      static_cast<int>(pack_low_bytes(r[4], r[5], r[6], r[7])),
+                      static_cast<int>(pack_low_bytes(r[8], r[9], r[10], r[11])),
+                      static_cast<int>(pack_low_bytes(r[12], r[13], r[14], r[15]))};
+    *reinterpret_cast<v4i*>(bt + static_cast<uint64_t>(p) * 16u * kp + static_cast<uint64_t>(t) * 16u) = w;
   }
 }
 
@@ -176,7 +175,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks) void fused_skinny_kernel(Skin
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       x.v[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(a_lane + 64u * j),
-                                                                              0, kNonTemporal));
+                                                                              0, 0));
   };
   // B: chunk q (16 bytes) of a step is column c = (q % 64) / 4, K slots
   // 16 (q % 4) .. +15 of plane p0 + q / 64. In LDS it sits at 16 (64 (q / 64)
@@ -385,15 +384,15 @@ hipError_t launch_fused_skinny(const FusedArgs& f, const PlaneConsts& consts, hi
   const bool sgn = f.kind == NativeKind::I64;
   // B's transposed residue planes at the start of the workspace
   const uint32_t runs_total = static_cast<uint32_t>(kp);  // 16 columns x kp / 16 runs
-  const unsigned bt_blocks = static_cast<unsigned>(std::min<int64_t>((runs_total + 255) / 256, 8192));
+  const dim3 bt_blocks(static_cast<unsigned>(std::min<int64_t>((runs_total + 255) / 256, 8192)), f.nplanes);
   if (sgn)
-    hipLaunchKernelGGL(pack_bt_kernel<true>, dim3(bt_blocks), dim3(256), 0, stream,
+    hipLaunchKernelGGL(pack_bt_kernel<true>, bt_blocks, dim3(256), 0, stream,
                        static_cast<const uint64_t*>(f.b), f.ldb, static_cast<uint32_t>(f.k),
-                       static_cast<uint32_t>(f.n), static_cast<uint32_t>(kp), f.ws, f.nplanes, consts);
+                       static_cast<uint32_t>(f.n), static_cast<uint32_t>(kp), f.ws, consts);
   else
-    hipLaunchKernelGGL(pack_bt_kernel<false>, dim3(bt_blocks), dim3(256), 0, stream,
+    hipLaunchKernelGGL(pack_bt_kernel<false>, bt_blocks, dim3(256), 0, stream,
                        static_cast<const uint64_t*>(f.b), f.ldb, static_cast<uint32_t>(f.k),
-                       static_cast<uint32_t>(f.n), static_cast<uint32_t>(kp), f.ws, f.nplanes, consts);
+                       static_cast<uint32_t>(f.n), static_cast<uint32_t>(kp), f.ws, consts);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
 
