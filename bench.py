@@ -330,6 +330,8 @@ def main() -> int:
         roofline = {"bound": "hbm", "kernel": kernel, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(gbs / PEAK_HBM_GBS, 4), "per_launch_bytes": gemm_bytes}
         traffic_kernels = ["skinny_gemm_kernel"] + (["residue_finalize_kernel"] if "K split" in kernel else [])
+        if args.config in FUSED_DEFAULT:
+            traffic_workload = args.config + "_packed"
     elif args.config == "c5":
         # tall and skinny: the GEMM streams P planes of A and B once (K x (M + N) bytes
         # each) and does little MFMA work per byte, so HBM bounds it
