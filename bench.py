@@ -153,7 +153,7 @@ def main() -> int:
         return oneshot_rate(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
-              "(the path shards by output row blocks; see DESIGN.md)", file=sys.stderr)
+              "(across GPUs the path would shard by output row blocks, one share of rows per GPU)", file=sys.stderr)
         return 2
     if args.config == "grouped":
         return grouped_bench(args)
