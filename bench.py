@@ -310,8 +310,8 @@ def main() -> int:
         # pack and GEMM in one pass: the native operands are read (8 bytes per
         # element) and the C planes written; HBM bounds it for tall-skinny shapes
         # results at most 16 columns wide take the skinny form (B's planes
-        # first, then A converted in registers) while its workspace fits 64 MiB
-        skinny_form = N <= 16 and P * 16 * ((K + 63) // 64 * 64) <= (64 << 20)
+        # first, then A converted in registers) while its workspace fits 256 MiB
+        skinny_form = N <= 16 and P * 16 * ((K + 63) // 64 * 64) <= (256 << 20)
         kernel = ("pack_bt_kernel + fused_skinny_kernel<Signed,G,First256> + residue_finalize_kernel" if skinny_form
                   else "fused_native_kernel<Signed,NP> + residue_finalize_kernel")
         workload = workload.replace("pack+GEMM", "fused pack+GEMM")

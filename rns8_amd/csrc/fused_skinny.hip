@@ -67,7 +67,9 @@ constexpr int kAccBias = static_cast<int>(0x80000000u);
 constexpr int64_t kTargetWaves = 4096;
 constexpr int64_t kMinSliceK = 1024;  // 16 steps per wave at least, unless K is shorter
 constexpr int64_t kMaxK = int64_t{1} << 23;
-constexpr uint64_t kMaxWorkspace = uint64_t{64} << 20;
+// B's transposed planes take P x 16 bytes per k: 256 MiB admits 8 x 8 x 2^20 at 9 planes (151 MB), where the
+// tile form would convert B's 8 columns as 128
+constexpr uint64_t kMaxWorkspace = uint64_t{256} << 20;
 
 struct SkinnyFusedArgs {
   const uint64_t* a;  // native A, m x k at row stride lda (elements)
