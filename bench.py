@@ -138,6 +138,9 @@ def main() -> int:
     ap.add_argument("--fused", action="store_true",
                     help="c1/c3: one fused native-input GEMM (rns8_mi355x_gemm_native_*_async) in place of the two "
                          "packs and the plane GEMM")
+    ap.add_argument("--host-pack", action="store_true",
+                    help="time the exact-wide host-array packs (host range proof + upload + pack) and the GEMM's "
+                         "admission at C4's operands instead")
     ap.add_argument("--oneshot", action="store_true",
                     help="time the host-buffer oneshot entry point instead (PCIe transfers included)")
     ap.add_argument("--graph", action="store_true",
@@ -151,6 +154,8 @@ def main() -> int:
         return copy_calibration(args.copy_calibration, max(args.steps, 1))
     if args.oneshot:
         return oneshot_rate(args)
+    if args.host_pack:
+        return host_pack_rate(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
               "(across GPUs the path would shard by output row blocks, one share of rows per GPU)", file=sys.stderr)
@@ -800,6 +805,58 @@ def oneshot_rate(args) -> int:
                       "k": K, "ms_per_call": round(dt * 1e3, 3),
                       "effective_TOPS": round(2.0 * M * N * K / dt / 1e12, 3),
                       "host_bytes_moved": int(A.nbytes + B.nbytes + C.nbytes)}))
+    return 0
+
+
+def host_pack_rate(args) -> int:
+    """The public host-array entries on C4's exact-wide operands (2048 x 2048
+    full-range int64, prefix 20): rns8_pack_i64 proves the operand's range on
+    the host from the array (per-axis maxima and sums in 512-bit integers,
+    api_exec.cpp) before the upload and the pack; rns8_gemm_rns then admits
+    the product from those summaries. Times both against a bare upload of the
+    same bytes. Prints one JSON line; not a `value`."""
+    import rns8_amd as r
+    from rns8_amd import hip, inputs
+
+    n = 2048
+    A = inputs.full_int64(inputs.operand_seed(args.seed, "A"), (n, n))
+    B = inputs.full_int64(inputs.operand_seed(args.seed, "B"), (n, n))
+    with r.Context() as ctx:
+        desc = r.gemm_desc(r.EXACT_WIDE_SIGNED, r.BOUND_NONE, n, n, n, max_prefix=20, flags=r.PLAN_FORCE_FIXED_PREFIX)
+        plan = r.Plan(ctx, desc)
+        mk = lambda: r.Matrix(ctx, r.matrix_desc(n, n, r.EXACT_WIDE_SIGNED, r.BOUND_NONE, plan.prefix))
+        Am, Bm, Cm = mk(), mk(), mk()
+        ws = r.Workspace(ctx, plan)
+        d = hip.malloc(A.nbytes)
+        reps = max(args.steps, 1)
+
+        def timed(fn):
+            for _ in range(2):
+                fn()
+            hip.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            hip.synchronize()
+            return (time.perf_counter() - t0) / reps * 1e3
+
+        upload = timed(lambda: hip.to_device(d, A))
+        # source version 0: every call packs (a matrix given the source
+        # version it already holds skips the pack)
+        flip = [0]
+
+        def packs():
+            x, y = (A, B) if flip[0] == 0 else (B, A)
+            flip[0] ^= 1
+            r.check(r.pack_i64(ctx, Am, x, 0), "pack A")
+            r.check(r.pack_i64(ctx, Bm, y, 0), "pack B")
+
+        pack = timed(packs)
+        gemm = timed(lambda: r.check(r.gemm_rns(ctx, plan, Am, Bm, Cm, ws), "gemm"))
+        hip.free(d)
+    print(json.dumps({"mode": "exact-wide host-array packs and GEMM (C4 operands, public ABI)", "n": n,
+                      "prefix": plan.prefix, "ms_upload_one_operand": round(upload, 3),
+                      "ms_pack_two_operands": round(pack, 3), "ms_gemm_rns_with_admission": round(gemm, 3)}))
     return 0
 
 

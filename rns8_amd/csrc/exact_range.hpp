@@ -65,34 +65,114 @@ inline I512 axis_deviation_max(const ExactAxis& a, const I512& c) {
 }
 
 // exact_range.hpp:52-78: summaries of a host operand, two linear scans.
+// Every quantity of a 64-bit operand fits 128 bits (sums of fewer than 2^63
+// magnitudes below 2^64), so the scans accumulate in __int128 over row
+// shards on up to `max_threads` threads, merge the column partials, and
+// widen to I512 at the end: the same integers as summing in I512.
+namespace native_detail {
+struct Acc {
+  unsigned __int128 max_magnitude = 0, absolute_sum = 0, deviation_sum = 0;
+  __int128 sum = 0, minimum = 0, maximum = 0;
+  bool any = false;
+  void add(__int128 v) {
+    const unsigned __int128 mag = static_cast<unsigned __int128>(v < 0 ? -v : v);
+    max_magnitude = mag > max_magnitude ? mag : max_magnitude;
+    absolute_sum += mag;
+    sum += v;
+    minimum = !any || v < minimum ? v : minimum;
+    maximum = !any || v > maximum ? v : maximum;
+    any = true;
+  }
+  void merge(const Acc& o) {
+    if (!o.any) return;
+    max_magnitude = o.max_magnitude > max_magnitude ? o.max_magnitude : max_magnitude;
+    absolute_sum += o.absolute_sum;
+    deviation_sum += o.deviation_sum;
+    sum += o.sum;
+    minimum = !any || o.minimum < minimum ? o.minimum : minimum;
+    maximum = !any || o.maximum > maximum ? o.maximum : maximum;
+    any = true;
+  }
+  // (min + max) / 2 truncated toward zero, as C++ integer division does
+  __int128 center() const { return (minimum + maximum) / 2; }
+};
+inline I512 from_u128(unsigned __int128 v) {
+  I512 r;
+  r.w[0] = static_cast<uint64_t>(v);
+  r.w[1] = static_cast<uint64_t>(v >> 64);
+  return r;
+}
+inline I512 from_i128(__int128 v) {
+  const I512 m = from_u128(static_cast<unsigned __int128>(v < 0 ? -v : v));
+  return v < 0 ? -m : m;
+}
+inline ExactAxis widen_axis(const Acc& a) {
+  ExactAxis e;
+  e.max_magnitude = from_u128(a.max_magnitude);
+  e.absolute_sum = from_u128(a.absolute_sum);
+  e.sum = from_i128(a.sum);
+  e.minimum = from_i128(a.minimum);
+  e.maximum = from_i128(a.maximum);
+  e.deviation_sum = from_u128(a.deviation_sum);
+  e.sum_known = a.any;
+  return e;
+}
+}  // namespace native_detail
+
 template <typename T>
 void native_exact_ranges(const T* src, int64_t rows, int64_t cols, int64_t ld, I512& maximum,
-                         std::vector<ExactAxis>& row_axes, std::vector<ExactAxis>& col_axes) {
-  row_axes.assign(static_cast<std::size_t>(rows), ExactAxis{});
-  col_axes.assign(static_cast<std::size_t>(cols), ExactAxis{});
-  auto value = [](T x) {
-    return std::is_signed<T>::value ? I512::from_i64(static_cast<int64_t>(x))
-                                    : I512::from_u64(static_cast<uint64_t>(x));
+                         std::vector<ExactAxis>& row_axes, std::vector<ExactAxis>& col_axes,
+                         unsigned max_threads = 16) {
+  using native_detail::Acc;
+  auto value = [&](int64_t r, int64_t c) -> __int128 {
+    return std::is_signed<T>::value ? static_cast<__int128>(static_cast<int64_t>(src[r * ld + c]))
+                                    : static_cast<__int128>(static_cast<uint64_t>(src[r * ld + c]));
   };
-  maximum = I512();
-  for (int64_t r = 0; r < rows; ++r) {
-    for (int64_t c = 0; c < cols; ++c) {
-      const I512 v = value(src[r * ld + c]);
-      add_exact_value(row_axes[r], v, c == 0);
-      add_exact_value(col_axes[c], v, r == 0);
+  unsigned nt = std::max(1u, std::min(max_threads, std::thread::hardware_concurrency()));
+  if (static_cast<int64_t>(nt) > rows) nt = static_cast<unsigned>(std::max<int64_t>(rows, 1));
+  std::vector<Acc> racc(static_cast<std::size_t>(rows)), cacc(static_cast<std::size_t>(cols));
+  std::vector<std::vector<Acc>> cpart(nt, std::vector<Acc>(static_cast<std::size_t>(cols)));
+  // pass 1: row accumulators, and column partials per shard
+  run_shards(nt, [&](unsigned t) {
+    const int64_t r0 = rows * t / nt, r1 = rows * (t + 1) / nt;
+    for (int64_t r = r0; r < r1; ++r)
+      for (int64_t c = 0; c < cols; ++c) {
+        const __int128 v = value(r, c);
+        racc[r].add(v);
+        cpart[t][c].add(v);
+      }
+  });
+  for (unsigned t = 0; t < nt; ++t)
+    for (int64_t c = 0; c < cols; ++c) cacc[c].merge(cpart[t][c]);
+  // pass 2: deviation sums around the row and column centres
+  std::vector<__int128> ccenter(static_cast<std::size_t>(cols));
+  for (int64_t c = 0; c < cols; ++c) ccenter[c] = cacc[c].center();
+  std::vector<std::vector<unsigned __int128>> cdev(nt, std::vector<unsigned __int128>(static_cast<std::size_t>(cols)));
+  run_shards(nt, [&](unsigned t) {
+    const int64_t r0 = rows * t / nt, r1 = rows * (t + 1) / nt;
+    for (int64_t r = r0; r < r1; ++r) {
+      const __int128 rc = racc[r].center();
+      unsigned __int128 dev = 0;
+      for (int64_t c = 0; c < cols; ++c) {
+        const __int128 v = value(r, c);
+        const __int128 dr = v - rc, dc = v - ccenter[c];
+        dev += static_cast<unsigned __int128>(dr < 0 ? -dr : dr);
+        cdev[t][c] += static_cast<unsigned __int128>(dc < 0 ? -dc : dc);
+      }
+      racc[r].deviation_sum = dev;
     }
-    maximum = imax(maximum, row_axes[r].max_magnitude);
-  }
-  std::vector<I512> col_center(static_cast<std::size_t>(cols));
-  for (int64_t c = 0; c < cols; ++c) col_center[c] = axis_center(col_axes[c]);
+  });
+  for (unsigned t = 0; t < nt; ++t)
+    for (int64_t c = 0; c < cols; ++c) cacc[c].deviation_sum += cdev[t][c];
+  row_axes.resize(static_cast<std::size_t>(rows));
+  col_axes.resize(static_cast<std::size_t>(cols));
+  unsigned __int128 top = 0;
   for (int64_t r = 0; r < rows; ++r) {
-    const I512 rc = axis_center(row_axes[r]);
-    for (int64_t c = 0; c < cols; ++c) {
-      const I512 v = value(src[r * ld + c]);
-      row_axes[r].deviation_sum = row_axes[r].deviation_sum + (v - rc).abs();
-      col_axes[c].deviation_sum = col_axes[c].deviation_sum + (v - col_center[c]).abs();
-    }
+    row_axes[r] = native_detail::widen_axis(racc[r]);
+    top = racc[r].max_magnitude > top ? racc[r].max_magnitude : top;
   }
+  for (int64_t c = 0; c < cols; ++c) col_axes[c] = native_detail::widen_axis(cacc[c]);
+  maximum = native_detail::from_u128(top);
 }
 
 // exact_range.hpp:80-99: a bound on |dot(row, column)| of length k.
@@ -121,6 +201,45 @@ inline ExactAxis uniform_axis(const I512& maximum, int64_t length) {
   return a;
 }
 
+// axis_product_bound with the factors that depend on one axis only computed
+// once per row or column (the centre, the deviation maximum and their
+// products with k): the same integers, so the same bound.
+struct AxisTerms {
+  I512 max_magnitude, absolute_sum, k_max;
+  bool sum_known = false;
+  I512 sum, center, deviation, deviation_sum, k_center, k_deviation;
+};
+inline AxisTerms axis_terms(const ExactAxis& a, int64_t k) {
+  const I512 kk = I512::from_u64(static_cast<uint64_t>(k));
+  AxisTerms t;
+  t.max_magnitude = a.max_magnitude;
+  t.absolute_sum = a.absolute_sum;
+  t.k_max = kk * a.max_magnitude;
+  t.sum_known = a.sum_known;
+  if (a.sum_known) {
+    t.sum = a.sum;
+    t.center = axis_center(a);
+    t.deviation = axis_deviation_max(a, t.center);
+    t.deviation_sum = a.deviation_sum;
+    t.k_center = kk * t.center;
+    t.k_deviation = kk * t.deviation;
+  }
+  return t;
+}
+inline I512 cell_bound(const AxisTerms& a, const AxisTerms& b) {
+  I512 bound = a.k_max * b.max_magnitude;
+  bound = imin(bound, a.absolute_sum * b.max_magnitude);
+  bound = imin(bound, a.max_magnitude * b.absolute_sum);
+  if (a.sum_known && b.sum_known) {
+    I512 rem = a.k_deviation * b.deviation;
+    rem = imin(rem, a.deviation_sum * b.deviation);
+    rem = imin(rem, a.deviation * b.deviation_sum);
+    const I512 center_term = a.center * b.sum + b.center * a.sum - a.k_center * b.center;
+    bound = imin(bound, center_term.abs() + rem);
+  }
+  return bound;
+}
+
 // What a packed exact-wide operand carries into a GEMM.
 struct ExactOperand {
   const I512* max_magnitude;
@@ -142,8 +261,11 @@ inline rns8_status exact_product_range(rns8_semantics semantics, int64_t m, int6
   if (out_rows) out_rows->clear();
   if (out_cols) out_cols->clear();
   if (a_rows || b_cols) {
-    const ExactAxis fa = uniform_axis(*A.max_magnitude, k);
-    const ExactAxis fb = uniform_axis(*B.max_magnitude, k);
+    const AxisTerms fa = axis_terms(uniform_axis(*A.max_magnitude, k), k);
+    const AxisTerms fb = axis_terms(uniform_axis(*B.max_magnitude, k), k);
+    std::vector<AxisTerms> ta(a_rows ? static_cast<std::size_t>(m) : 0u), tb(b_cols ? static_cast<std::size_t>(n) : 0u);
+    for (std::size_t r = 0; r < ta.size(); ++r) ta[r] = axis_terms((*A.rows)[r], k);
+    for (std::size_t c = 0; c < tb.size(); ++c) tb[c] = axis_terms((*B.cols)[c], k);
     std::vector<ExactAxis> rows(static_cast<std::size_t>(m)), cols(static_cast<std::size_t>(n));
     // column summaries are merged per thread, then reduced
     unsigned nt = std::max(1u, std::min(max_threads, std::thread::hardware_concurrency()));
@@ -153,10 +275,10 @@ inline rns8_status exact_product_range(rns8_semantics semantics, int64_t m, int6
     auto work = [&](unsigned t) {
       const int64_t r0 = m * t / nt, r1 = m * (t + 1) / nt;
       for (int64_t r = r0; r < r1; ++r) {
-        const ExactAxis& a = a_rows ? (*A.rows)[r] : fa;
+        const AxisTerms& a = a_rows ? ta[r] : fa;
         for (int64_t c = 0; c < n; ++c) {
-          const ExactAxis& b = b_cols ? (*B.cols)[c] : fb;
-          const I512 cell = axis_product_bound(a, b, k);
+          const AxisTerms& b = b_cols ? tb[c] : fb;
+          const I512 cell = cell_bound(a, b);
           maxima[t] = imax(maxima[t], cell);
           rows[r].max_magnitude = imax(rows[r].max_magnitude, cell);
           rows[r].absolute_sum = rows[r].absolute_sum + cell;

@@ -69,11 +69,44 @@ ExactAxis read_axis() {
   return a;
 }
 
+void print_axis(const ExactAxis& a) {
+  std::cout << hex(a.max_magnitude) << " " << hex(a.absolute_sum) << " " << hex(a.sum) << " " << hex(a.minimum) << " "
+            << hex(a.maximum) << " " << hex(a.deviation_sum) << " " << (a.sum_known ? 1 : 0) << "\n";
+}
+
+// native <S|U> <rows> <cols> then rows x cols values: the summaries of a host
+// operand (native_exact_ranges), max then one line per row and per column
+int native_case() {
+  std::string sem;
+  int64_t rows, cols;
+  std::cin >> sem >> rows >> cols;
+  std::vector<int64_t> xs(static_cast<std::size_t>(rows * cols));
+  for (auto& x : xs) {
+    std::string v;
+    std::cin >> v;
+    x = static_cast<int64_t>(parse<I512>(v).w[0]);
+  }
+  I512 maximum;
+  std::vector<ExactAxis> ra, ca;
+  if (sem == "S")
+    rns8x::native_exact_ranges(xs.data(), rows, cols, cols, maximum, ra, ca, 3);
+  else
+    rns8x::native_exact_ranges(reinterpret_cast<const uint64_t*>(xs.data()), rows, cols, cols, maximum, ra, ca, 3);
+  std::cout << hex(maximum) << "\n";
+  for (const auto& a : ra) print_axis(a);
+  for (const auto& a : ca) print_axis(a);
+  return 0;
+}
+
 }  // namespace
 
 int main() {
   std::string tag;
   while (std::cin >> tag) {
+    if (tag == "native") {
+      native_case();
+      continue;
+    }
     if (tag != "case") return 2;
     std::string sem, ps, as, bs;
     int64_t m, n, k;

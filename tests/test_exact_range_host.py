@@ -171,3 +171,37 @@ def test_planted_wrap_is_detected(checker):
     wrapped = (1 * C.max_magnitude * C.max_magnitude) % (1 << 256)
     assert xr.fits(True, wrapped, P20)  # the planted mistake admits it
     assert not xr.fits(True, 1 * C.max_magnitude * C.max_magnitude, P20)
+
+
+def _native_summaries(exe, signed, x):
+    rows, cols = len(x), len(x[0])
+    text = f"native {'S' if signed else 'U'} {rows} {cols}\n" + "\n".join(
+        " ".join(_h(v) for v in row) for row in x) + "\n"
+    res = subprocess.run([str(exe)], input=text, capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    lines = res.stdout.split("\n")
+    parse = lambda line: tuple(int(f, 16) for f in line.split())
+    return int(lines[0], 16), [parse(lines[1 + i]) for i in range(rows)], [parse(lines[1 + rows + j]) for j in range(cols)]
+
+
+def _axis_tuple(a: xr.Axis):
+    return (a.max_magnitude, a.absolute_sum, a.sum, a.minimum, a.maximum, a.deviation_sum, 1 if a.sum_known else 0)
+
+
+@pytest.mark.parametrize("signed", [True, False])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (1, 7), (9, 1), (13, 40), (67, 5)])
+def test_native_summaries_match_unbounded(checker, signed, rows, cols):
+    """The summaries a host operand carries (native_exact_ranges: 128-bit
+    sums over row shards on three threads, merged per column) equal the
+    unbounded ones, with the int64 / uint64 extremes placed in every case."""
+    rng = random.Random(rows * 1000 + cols + signed)
+    lo, hi = (-(1 << 63), (1 << 63) - 1) if signed else (0, (1 << 64) - 1)
+    x = _native(rng, rows, cols, lo, hi)
+    x[0][0] = lo
+    x[-1][-1] = hi
+    x[rows // 2][cols // 2] = lo if rows * cols > 2 else x[rows // 2][cols // 2]
+    maximum, got_rows, got_cols = _native_summaries(checker, signed, x)
+    want = xr.native_operand(x)
+    assert maximum == want.max_magnitude
+    assert got_rows == [_axis_tuple(a) for a in want.rows]
+    assert got_cols == [_axis_tuple(a) for a in want.cols]
