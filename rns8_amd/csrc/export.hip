@@ -241,15 +241,20 @@ __device__ __forceinline__ uint64_t value64(const uint32_t (&words)[P], const ui
   }
 }
 
+// Thread t takes column group t mod 2^gpr_shift of row t >> gpr_shift of the
+// block's rows (narrow results fill a block with several rows; gpr_shift = 8
+// is one row per block).
 template <uint32_t P, int L, ExportKind Kind>
 __global__ __launch_bounds__(256) void export_kernel(ExportArgs a, ExportLimits lim, uint32_t groups_per_row,
-                                                     uint32_t vec_store) {
+                                                     uint32_t vec_store, uint32_t gpr_shift) {
   constexpr bool kSigned = Kind == ExportKind::I64 || Kind == ExportKind::WIDE_SIGNED;
-  const uint32_t gc = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t gc = blockIdx.x * blockDim.x + (threadIdx.x & ((1u << gpr_shift) - 1u));
   if (gc >= groups_per_row) return;
   const int64_t c0 = static_cast<int64_t>(gc) * 4;
+  const int64_t rows_per_block = static_cast<int64_t>(blockDim.x >> gpr_shift);
   bool violation = false;
-  for (int64_t row = blockIdx.y; row < a.m; row += gridDim.y) {
+  for (int64_t row = blockIdx.y * rows_per_block + (threadIdx.x >> gpr_shift); row < a.m;
+       row += gridDim.y * rows_per_block) {
     const int8_t* const cell = a.c + row * a.ldc + c0;
     uint32_t words[P], flipped[P];
 #pragma unroll
@@ -403,12 +408,15 @@ __device__ __forceinline__ uint32_t canonical4(uint32_t w, uint32_t m4) {
 
 // 16 cells per thread: one 16-byte plane load, one 16-byte store where the
 // destination row segment is aligned and whole, byte stores otherwise.
-__global__ __launch_bounds__(256) void export_u8_kernel(ExportU8Args a, uint32_t groups_per_row, uint32_t vec_store) {
-  const uint32_t gc = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void export_u8_kernel(ExportU8Args a, uint32_t groups_per_row, uint32_t vec_store,
+                                                        uint32_t gpr_shift) {
+  const uint32_t gc = blockIdx.x * blockDim.x + (threadIdx.x & ((1u << gpr_shift) - 1u));
   if (gc >= groups_per_row) return;
   const int64_t c0 = static_cast<int64_t>(gc) * 16;
   const uint32_t m4 = (a.modulus & 0xFFu) * 0x01010101u;
-  for (int64_t row = blockIdx.y; row < a.m; row += gridDim.y) {
+  const int64_t rows_per_block = static_cast<int64_t>(blockDim.x >> gpr_shift);
+  for (int64_t row = blockIdx.y * rows_per_block + (threadIdx.x >> gpr_shift); row < a.m;
+       row += gridDim.y * rows_per_block) {
     const v4i w = *reinterpret_cast<const v4i*>(a.c + row * a.ldc + c0);
     const v4i out = {static_cast<int>(canonical4(static_cast<uint32_t>(w[0]), m4)),
                      static_cast<int>(canonical4(static_cast<uint32_t>(w[1]), m4)),
@@ -617,11 +625,20 @@ __global__ __launch_bounds__(256) void crt_export_kernel(ExportArgs a, uint32_t 
     atomicOr(a.status, 1u);
 }
 
-// Column groups of 4 cells x rows; rows beyond the grid's y extent are
-// covered by the row loop.
+// Column groups x rows; rows beyond the grid's y extent are covered by the
+// row loop. Rows with fewer than 256 groups share a block: 2^shift threads
+// per row (shift = 8: one row per block).
+uint32_t gpr_shift_for(uint32_t groups_per_row) {
+  uint32_t shift = 0;
+  while (shift < 8u && (1u << shift) < groups_per_row) ++shift;
+  return shift;
+}
 dim3 grid_2d(uint32_t groups_per_row, int64_t rows) {
+  const uint32_t shift = gpr_shift_for(groups_per_row);
   const uint32_t gx = (groups_per_row + 255u) / 256u;
-  const int64_t gy = rows < 65535 ? rows : 65535;
+  const int64_t per_block = int64_t{256} >> shift;
+  const int64_t blocks = (rows + per_block - 1) / per_block;
+  const int64_t gy = blocks < 65535 ? blocks : 65535;
   return dim3(gx, static_cast<uint32_t>(gy > 0 ? gy : 1));
 }
 
@@ -643,23 +660,24 @@ hipError_t launch_export_p(const ExportArgs& a, const ExportLimits& lim, hipStre
   static_assert(make_garner_table<P>().limbs <= static_cast<uint32_t>(L), "limb count too small for P");
   const uint32_t groups_per_row = static_cast<uint32_t>(a.ldc / 4);
   const dim3 grid = grid_2d(groups_per_row, a.m);
+  const uint32_t shift = gpr_shift_for(groups_per_row);
   const uint32_t vec = (reinterpret_cast<uintptr_t>(a.dst) % 16 == 0 && a.ld % 2 == 0) ? 1u : 0u;
   switch (a.kind) {
     case ExportKind::I64:
       hipLaunchKernelGGL((export_kernel<P, L, ExportKind::I64>), grid, dim3(256), 0, stream, a, lim, groups_per_row,
-                         vec);
+                         vec, shift);
       break;
     case ExportKind::U64:
       hipLaunchKernelGGL((export_kernel<P, L, ExportKind::U64>), grid, dim3(256), 0, stream, a, lim, groups_per_row,
-                         vec);
+                         vec, shift);
       break;
     case ExportKind::WIDE_SIGNED:
       hipLaunchKernelGGL((export_kernel<P, L, ExportKind::WIDE_SIGNED>), grid, dim3(256), 0, stream, a, lim,
-                         groups_per_row, vec);
+                         groups_per_row, vec, shift);
       break;
     case ExportKind::WIDE_UNSIGNED:
       hipLaunchKernelGGL((export_kernel<P, L, ExportKind::WIDE_UNSIGNED>), grid, dim3(256), 0, stream, a, lim,
-                         groups_per_row, vec);
+                         groups_per_row, vec, shift);
       break;
   }
   return hipGetLastError();
@@ -839,7 +857,8 @@ hipError_t launch_export_u8(const ExportU8Args& a, hipStream_t stream) {
   if (a.ldc / 16 > 0xFFFFFFFFll) return hipErrorInvalidValue;
   const uint32_t groups_per_row = static_cast<uint32_t>(a.ldc / 16);
   const uint32_t vec = (reinterpret_cast<uintptr_t>(a.dst) % 16 == 0 && a.ld % 16 == 0) ? 1u : 0u;
-  hipLaunchKernelGGL(export_u8_kernel, grid_2d(groups_per_row, a.m), dim3(256), 0, stream, a, groups_per_row, vec);
+  hipLaunchKernelGGL(export_u8_kernel, grid_2d(groups_per_row, a.m), dim3(256), 0, stream, a, groups_per_row, vec,
+                     gpr_shift_for(groups_per_row));
   return hipGetLastError();
 }
 
