@@ -12,12 +12,13 @@
 // by the reduction's VALU work, which are about equal on MI355X.
 //
 // Work split: a wave owns 16 rows of A, one K slice and up to kMaxGroup
-// planes, so A is loaded once for all of them (results of more than nine
-// planes run two or three plane groups, each loading A). The loads are what
-// bounds the pass: with the planes spread over three waves per row block
-// (162 registers, three waves per SIMD) in the hope that the other waves
-// find A in L2, each wave's loads cost as much as the first one's (358
-// against 187 us at 8192 x 1 x 8192, 9 planes).
+// planes, so A is loaded once for all of them (results of more than 16
+// planes run two plane groups, each loading A; 8192 x 1 x 8192: 150 us at 9
+// planes, 177 at 12, 219 at 16; with at most 9 planes per wave 12 planes
+// took 245 us). The loads are what bounds the pass: with the planes spread
+// over three waves per row block (162 registers, three waves per SIMD) in the
+// hope that the other waves find A in L2, each wave's loads cost as much as
+// the first one's (358 against 187 us at 9 planes).
 //   * A: a 64-K step of the wave's 16 rows is eight 16-byte loads per lane,
 //     one step ahead (ordinary loads: the two halves of a 128-byte line
 //     come from consecutive loads, and non-temporal ones were 4% slower): load j of lane l reads elements
@@ -61,8 +62,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kStep = 64;           // K per MFMA step
-constexpr int kMaxGroup = 9;        // planes per wave: at most 256 registers, two waves per SIMD
-constexpr int kMinBlocks = 3;       // workgroups per CU (168 registers; nine planes spill two before the loop)
+constexpr int kMaxGroup = 16;       // planes per wave (up to 243 registers; more spill)
+constexpr int kMinBlocks = 2;       // workgroups per CU (256 registers)
 constexpr int kAccBias = static_cast<int>(0x80000000u);
 constexpr int64_t kTargetWaves = 4096;
 constexpr int64_t kMinSliceK = 1024;  // 16 steps per wave at least, unless K is shorter
@@ -433,7 +434,18 @@ hipError_t launch_fused_skinny(const FusedArgs& f, const PlaneConsts& consts, hi
         case 6: launch_planes<S, 6>(a, consts, stream); break;
         case 7: launch_planes<S, 7>(a, consts, stream); break;
         case 8: launch_planes<S, 8>(a, consts, stream); break;
-        default: launch_planes<S, 9>(a, consts, stream); break;
+        case 9: launch_planes<S, 9>(a, consts, stream); break;
+        case 10: launch_planes<S, 10>(a, consts, stream); break;
+        case 11: launch_planes<S, 11>(a, consts, stream); break;
+        case 12: launch_planes<S, 12>(a, consts, stream); break;
+        case 13: launch_planes<S, 13>(a, consts, stream); break;
+        case 14: launch_planes<S, 14>(a, consts, stream); break;
+        case 15: launch_planes<S, 15>(a, consts, stream); break;
+        case 16: launch_planes<S, 16>(a, consts, stream); break;
+        case 17: launch_planes<S, 17>(a, consts, stream); break;
+        case 18: launch_planes<S, 18>(a, consts, stream); break;
+        case 19: launch_planes<S, 19>(a, consts, stream); break;
+        default: launch_planes<S, 20>(a, consts, stream); break;
       }
     };
     if (sgn)

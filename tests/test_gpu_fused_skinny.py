@@ -3,8 +3,8 @@
 operands must equal, byte for byte, the planes rns8_gemm_rns computes from
 packed operands, and export to the exact product.
 
-Cases cover one to 16 columns; 1 to 20 planes (one launch of up to nine
-planes, or two and three launches over the same rows); K below one 64-K
+Cases cover one to 16 columns; 1 to 20 planes (one launch of up to 16
+planes, or two launches over the same rows); K below one 64-K
 step, K odd, K split into residue slices (above 65536 too); ragged row
 blocks; row strides above the width, odd B strides and a B only 8-byte
 aligned (B is read by scalar loads); full-range operands; operands that end
@@ -83,8 +83,8 @@ CASES = [
     (33, 16, 70001, 5, 1, 0, False, 0),      # 16 columns, K above 65536
     (16, 8, 200000, 9, 0, 5, True, 0),       # one row block, many slices
     (7, 2, 40, 3, 2, 0, False, 0),           # K below one step, rows below one block
-    (100, 5, 999, 20, 3, 0, True, 0),        # 20 planes: three launches of 7, 7 and 6
-    (50, 16, 5000, 10, 0, 0, False, 0),      # 10 planes: two launches of 5
+    (100, 5, 999, 20, 3, 0, True, 0),        # 20 planes: two launches of 10
+    (50, 16, 5000, 10, 0, 0, False, 0),      # 10 planes in one launch
     (300, 4, 1, 1, 1, 3, True, 8),           # K = 1, one plane (m = 256)
 ]
 
