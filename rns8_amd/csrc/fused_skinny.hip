@@ -12,10 +12,11 @@
 // by the reduction's VALU work, which are about equal on MI355X.
 //
 // Work split: a wave owns 16 rows of A, one K slice and up to kMaxGroup
-// planes, so A is loaded once for all of them (results of more than 16
+// planes, so A is loaded once for all of them (results of more than 18
 // planes run two plane groups, each loading A; 8192 x 1 x 8192: 150 us at 9
-// planes, 177 at 12, 219 at 16; with at most 9 planes per wave 12 planes
-// took 245 us). The loads are what bounds the pass: with the planes spread
+// planes, 177 at 12, 219 at 16, 245 at 18, 322 at 20 in two groups; with at
+// most 9 planes per wave 12 planes took 245 us, and 20 planes in one group,
+// which spills inside the loop, 676 us). The loads are what bounds the pass: with the planes spread
 // over three waves per row block (162 registers, three waves per SIMD) in the
 // hope that the other waves find A in L2, each wave's loads cost as much as
 // the first one's (358 against 187 us at 9 planes).
@@ -62,7 +63,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kStep = 64;           // K per MFMA step
-constexpr int kMaxGroup = 16;       // planes per wave (up to 243 registers; more spill)
+constexpr int kMaxGroup = 18;       // planes per wave (243 registers at 16; 17 and 18 spill a few, 20 many)
 constexpr int kMinBlocks = 2;       // workgroups per CU (256 registers)
 constexpr int kAccBias = static_cast<int>(0x80000000u);
 constexpr int64_t kTargetWaves = 4096;

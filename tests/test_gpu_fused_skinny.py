@@ -3,7 +3,7 @@
 operands must equal, byte for byte, the planes rns8_gemm_rns computes from
 packed operands, and export to the exact product.
 
-Cases cover one to 16 columns; 1 to 20 planes (one launch of up to 16
+Cases cover one to 16 columns; 1 to 20 planes (one launch of up to 18
 planes, or two launches over the same rows); K below one 64-K
 step, K odd, K split into residue slices (above 65536 too); ragged row
 blocks; row strides above the width, odd B strides and a B only 8-byte
@@ -85,6 +85,7 @@ CASES = [
     (7, 2, 40, 3, 2, 0, False, 0),           # K below one step, rows below one block
     (100, 5, 999, 20, 3, 0, True, 0),        # 20 planes: two launches of 10
     (50, 16, 5000, 10, 0, 0, False, 0),      # 10 planes in one launch
+    (200, 2, 3000, 18, 0, 0, True, 0),       # 18 planes in one launch (the largest group)
     (300, 4, 1, 1, 1, 3, True, 8),           # K = 1, one plane (m = 256)
 ]
 
