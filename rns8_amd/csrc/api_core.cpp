@@ -715,11 +715,16 @@ rns8_status init_plan(const rns8_gemm_desc& d, rns8_backend_kind backend, rns8_p
     plan.desc.zero_b_cols_count = plan.schedule.zero_b_cols.size();
   }
   const uint32_t planes = uses_finite_storage(d.semantics) ? 1u : selected;
-  // per-tile plans run the tiled unit list (no K split)
-  if (!per_tile(d.bound_kind)) {
+  // Per-tile plans with a schedule run the tiled unit list (no K split). A
+  // per-tile plan whose schedule collapsed (every tile at the budget) runs
+  // the ordinary GEMM, so its K split and workspace are sized like a global
+  // plan's: the skinny kernel splits K for long or narrow products.
+  if (!per_tile(d.bound_kind) || plan.schedule.entries.empty()) {
     const GemmShape shape = choose_gemm_shape(d.m, d.n, d.k, planes);
     plan.splitk_slices = shape.slices;
     plan.splitk_bytes = shape.ws_bytes;
+  }
+  if (!per_tile(d.bound_kind)) {
     // the fused native-input GEMM shares the workspace
     if ((d.semantics == RNS8_BOUNDED_I64 || d.semantics == RNS8_BOUNDED_U64) &&
         choose_fused_shape(d.m, d.n, d.k, planes, padded_ld(d.n), plan.fused)) {

@@ -188,4 +188,17 @@ constexpr void crt_centered(const CrtTable<P>& t, const int32_t* s, uint32_t (&l
   sign = c;
 }
 
+// Whether crt_export_kernel can address an export: it computes plane offsets
+// from the first plane (plane_span bytes up to the end of the last plane's
+// rows), an output row's byte range (n * 8 * limbs) and a lane's offset in
+// it in 32 bits, and numbers its (row, 64-column chunk) units in 32 bits.
+// Exports outside these limits run the Garner kernel, which uses 64-bit
+// offsets.
+constexpr bool crt_export_fits(uint64_t plane_span, int64_t m, int64_t n, uint32_t limbs) {
+  if (m <= 0 || n <= 0 || limbs == 0) return false;
+  if (plane_span >= (uint64_t{1} << 31)) return false;
+  if (static_cast<uint64_t>(n) * 8u * limbs >= (uint64_t{1} << 31)) return false;
+  return static_cast<uint64_t>(m) * ((static_cast<uint64_t>(n) + 63u) / 64u) < (uint64_t{1} << 32);
+}
+
 }  // namespace rns8x

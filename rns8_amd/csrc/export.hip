@@ -844,8 +844,8 @@ hipError_t launch_export(const ExportArgs& a, uint32_t prefix, hipStream_t strea
   const uint64_t plane_span = static_cast<uint64_t>(prefix - 1) * static_cast<uint64_t>(a.pitch_c) +
                               static_cast<uint64_t>(a.m) * static_cast<uint64_t>(a.ldc);
   const bool wide = a.kind == ExportKind::WIDE_SIGNED || a.kind == ExportKind::WIDE_UNSIGNED;
-  const bool crt = wide && plane_span < (uint64_t{1} << 31) && (reinterpret_cast<uintptr_t>(a.c) & 15u) == 0 &&
-                   (a.pitch_c % 16) == 0 && static_cast<uint64_t>(a.m) * ((a.n + 63) / 64) < (uint64_t{1} << 32);
+  const bool crt = wide && crt_export_fits(plane_span, a.m, a.n, a.limbs) &&
+                   (reinterpret_cast<uintptr_t>(a.c) & 15u) == 0 && (a.pitch_c % 16) == 0;
   if (crt) return dispatch_crt(prefix, a, plane_span, stream, std::make_integer_sequence<uint32_t, kMaxPrefix>{});
   return dispatch_prefix(prefix, a, lim, stream, std::make_integer_sequence<uint32_t, kMaxPrefix>{});
 }

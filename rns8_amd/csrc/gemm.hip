@@ -883,8 +883,11 @@ hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStrea
   // allows it)
   if (args.slices > 1 && args.slices != shape.slices) return hipErrorInvalidValue;
   if (shape.tile == 16) {
-    if (args.slices != shape.slices) return hipErrorInvalidValue;
-    return launch_skinny(args, shape, consts, stream);
+    if (args.slices == shape.slices) return launch_skinny(args, shape, consts, stream);
+    // an unsplit call (no workspace) of a shape the skinny kernel would
+    // split: the 128 x 128 kernel, which takes any K in 65536 blocks
+    if (args.slices != 1) return hipErrorInvalidValue;
+    return launch_gemm_cfg<CfgSmall, 2, false>(args, args.k, consts, stream, NoTaskTable{}, 1);
   }
   if (shape.tile == 256) return launch_gemm_cfg<CfgLarge, 1, false>(args, shape.k_slice, consts, stream, NoTaskTable{}, 1);
   return launch_gemm_cfg<CfgSmall, 2, false>(args, shape.k_slice, consts, stream, NoTaskTable{}, 1);

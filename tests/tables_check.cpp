@@ -20,6 +20,7 @@
 //             from stdin and prints the centered value the export tail
 //             computes from their column sums; tests/test_tables.py checks
 //             both against Python big integers
+//   crtgate   the address limits of the CRT-basis export kernel
 // Exit status 0 and a final "ok" line when every check passes.
 #include <cinttypes>
 #include <cstdint>
@@ -550,6 +551,50 @@ void crt_all(std::integer_sequence<uint32_t, Ps...>) {
   }
 }
 
+// crt_export_fits: every export it admits has the 32-bit quantities
+// crt_export_kernel forms (the output row's byte range, the last lane's byte
+// offset in it, the unit count) equal to their 64-bit values and below the
+// buffer-offset limit; exports just past each limit are refused.
+void check_crtgate() {
+  const uint64_t span_ok = (uint64_t{1} << 31) - 1;
+  int admitted = 0;
+  for (uint32_t L = 1; L <= 32; ++L) {
+    const int64_t edge_n = static_cast<int64_t>(((uint64_t{1} << 31) - 1) / (8u * L));  // largest n with n*8L < 2^31
+    const int64_t ns[] = {1, 63, 64, 65, 4096, edge_n - 1, edge_n, edge_n + 1, 70000000, int64_t{1} << 40};
+    const int64_t ms[] = {1, 2, 4096, int64_t{1} << 26, (int64_t{1} << 32) - 1, int64_t{1} << 32};
+    for (int64_t n : ns)
+      for (int64_t m : ms)
+        for (uint64_t span : {uint64_t{4096}, span_ok, span_ok + 1}) {
+          const bool fits = crt_export_fits(span, m, n, L);
+          const uint64_t row_bytes = static_cast<uint64_t>(n) * 8u * L;
+          const uint64_t units = static_cast<uint64_t>(m) * ((static_cast<uint64_t>(n) + 63u) / 64u);
+          const bool want = span < (uint64_t{1} << 31) && row_bytes < (uint64_t{1} << 31) && units < (uint64_t{1} << 32);
+          if (fits != want) {
+            std::printf("crtgate: span %" PRIu64 " m %" PRId64 " n %" PRId64 " L %u: fits %d, want %d\n", span, m, n,
+                        L, fits, want);
+            ++failures;
+            continue;
+          }
+          if (!fits) continue;
+          ++admitted;
+          // the kernel's 32-bit forms
+          const uint32_t range32 = static_cast<uint32_t>(static_cast<int64_t>(n) * 8 * L);
+          const int last_off = static_cast<int>(static_cast<uint32_t>(n - 1) * 8u * L);
+          const uint32_t units32 = static_cast<uint32_t>(m) * static_cast<uint32_t>((n + 63) / 64);
+          if (range32 != row_bytes || last_off < 0 || static_cast<uint64_t>(last_off) != row_bytes - 8u * L ||
+              units32 != units || static_cast<int32_t>(range32) < 0) {
+            std::printf("crtgate: 32-bit forms differ at m %" PRId64 " n %" PRId64 " L %u\n", m, n, L);
+            ++failures;
+          }
+        }
+  }
+  if (crt_export_fits(4096, 1, 70000000, 8)) {
+    std::printf("crtgate: m 1, n 7e7, 8 limbs admitted\n");
+    ++failures;
+  }
+  std::printf("crtgate checks %d admitted\n", admitted);
+}
+
 int main(int argc, char** argv) {
   if (argc < 2) return 2;
   if (!std::strcmp(argv[1], "quot")) check_quot();
@@ -559,6 +604,7 @@ int main(int argc, char** argv) {
   else if (!std::strcmp(argv[1], "div")) check_div();
   else if (!std::strcmp(argv[1], "export64")) export64_all(std::make_integer_sequence<uint32_t, kMaxPrefix>{});
   else if (!std::strcmp(argv[1], "crt")) crt_all(std::make_integer_sequence<uint32_t, kMaxPrefix>{});
+  else if (!std::strcmp(argv[1], "crtgate")) check_crtgate();
   else return 2;
   if (failures) {
     std::printf("failures %d\n", failures);

@@ -273,6 +273,59 @@ def test_collapsed_schedule_checks_tile_bounds(gpu_ctx):
     assert (out == 77).all()
 
 
+@pytest.mark.parametrize("m,n,k", [(8, 8, 100000), (8192, 1, 8192)])
+def test_collapsed_schedule_narrow_split_k(gpu_ctx, m, n, k):
+    # Every tile at the budget collapses the schedule, so the ordinary GEMM
+    # runs: for results at most 16 columns wide the skinny kernel, which
+    # splits K into int8 residue slots here (100000 > 65536; 8192 rows at 9
+    # planes). The plan sizes that workspace like a global plan, and
+    # rns8_gemm_rns, the grouped entry and the no-allocation entry all export
+    # the exact product.
+    ctx = gpu_ctx
+    sem, bk, _ = _kinds(True)
+    tile = 128
+    tiles = ((m + tile - 1) // tile) * ((n + tile - 1) // tile)
+    bounds = [(1 << 63) - 1] * tiles  # 2 * bound > P8: every tile requires prefix 9
+    st, _, summary = oracle.tile_schedule(True, m, n, tile, tile, bounds, 9, 0)
+    assert st == 0 and summary.collapsed == 1
+    plan = r.Plan(ctx, r.gemm_desc(sem, bk, m, n, k, max_prefix=9, tile_m=tile, tile_n=tile, tile_bounds=bounds))
+    assert plan.prefix == 9
+    assert "skinny_gemm_kernel" in plan.selected_kernel() and "K split" in plan.selected_kernel()
+    assert plan.backend_info().workspace_required_bytes > 0
+    rng = np.random.default_rng(m + k)
+    ops = [(rng.integers(-(1 << 20), 1 << 20, size=(m, k)).astype(np.int64),
+            rng.integers(-(1 << 20), 1 << 20, size=(k, n)).astype(np.int64)) for _ in range(2)]
+    mk = lambda rows, cols: r.Matrix(ctx, r.matrix_desc(rows, cols, sem, bk, 9, tile_m=tile, tile_n=tile))  # noqa: E731
+    packed = []
+    for i, (A, B) in enumerate(ops):
+        Am, Bm = mk(m, k), mk(k, n)
+        r.check(r.pack_i64(ctx, Am, A, 10 + 2 * i), "pack A")
+        r.check(r.pack_i64(ctx, Bm, B, 11 + 2 * i), "pack B")
+        packed.append((Am, Bm))
+
+    def export(Cm, want):
+        out = np.full((m, n), 77, dtype=np.int64)
+        assert r.export_i64(ctx, plan, Cm, out) == r.SUCCESS
+        np.testing.assert_array_equal(out, want)
+
+    exact = [A @ B for A, B in ops]  # |C| < 2^54: exact in int64
+    Am, Bm = packed[0]
+    C1, ws1 = mk(m, n), r.Workspace(ctx, plan)
+    assert r.gemm_rns(ctx, plan, Am, Bm, C1, ws1) == r.SUCCESS
+    export(C1, exact[0])
+    Cg = [mk(m, n), mk(m, n)]
+    wsg = [r.Workspace(ctx, plan), r.Workspace(ctx, plan)]
+    trip = [(packed[i][0], packed[i][1], Cg[i], wsg[i]) for i in range(2)]
+    assert r.gemm_rns_grouped(ctx, plan, trip) == r.SUCCESS
+    for i in range(2):
+        export(Cg[i], exact[i])
+    Cn = mk(m, n)
+    Am, Bm = packed[1]
+    assert r.lib().rns8_mi355x_gemm_rns_noalloc(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cn.ptr, None) == r.SUCCESS
+    hip.synchronize()
+    export(Cn, exact[1])
+
+
 @pytest.mark.parametrize("signed", [True, False])
 def test_device_export_matches_host_export(gpu_ctx, signed):
     rng = np.random.default_rng(21 + signed)

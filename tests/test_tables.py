@@ -57,6 +57,14 @@ def test_pack_reduction_int64(checker):
     _run(checker, "pack64")
 
 
+def test_crt_export_address_gate(checker):
+    """crt_export_fits admits exactly the exports whose output row bytes,
+    lane offsets and unit count the CRT-basis kernel can form in 32 bits
+    (one 8-limb row of 7e7 cells is refused)."""
+    out = _run(checker, "crtgate")
+    assert "crtgate checks" in out
+
+
 def test_unit_index_division(checker):
     """Reciprocal division of unit indices (n < 2^31) by every divisor up to
     5000, powers of two and their neighbours, 2^31 - 1 and random divisors."""
