@@ -30,10 +30,16 @@ DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-Xclang", "-target-feature", "
 HOST_FLAGS = ["-O2", "-Wall", "-Wextra"]
 
 
+# Per-file device flags. export.hip: its MFMA results are read by the VALU
+# right away, so they are produced in VGPRs (no v_accvgpr_read per value);
+# the GEMM kernels keep their accumulators in AGPRs.
+FILE_FLAGS = {"export.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
     if src.suffix == ".hip":
-        cmd = [HIPCC, *COMMON, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *COMMON, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     else:
         cmd = [HIPCC, *COMMON, *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)

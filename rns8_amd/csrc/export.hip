@@ -13,6 +13,7 @@
 // fully unrolled with exactly the limbs each Horner step can occupy. Each
 // thread handles 4 consecutive cells of a row, so every plane contributes one
 // dword load; a 2-D grid (column groups x rows) needs no index division.
+#include <algorithm>
 #include <utility>
 
 #include "crt_export.hpp"
@@ -625,6 +626,154 @@ __global__ __launch_bounds__(256) void crt_export_kernel(ExportArgs a, uint32_t 
     atomicOr(a.status, 1u);
 }
 
+// The bounded int64 / uint64 export at P = 9..11 on the matrix cores
+// (crt_export.hpp, 64-bit results): the int8 MFMA multiplies each cell's
+// residues by the 14 weight columns of Crt64Table<P>, then per cell the
+// 64-bit tail (the low word of X' - q M and its class) and one 8-byte store.
+// Garner's digits (export_kernel) cost about 52 of its ~87 VALU instructions
+// per cell at P = 9; the tail here replaces all of them.
+//
+// A wave handles 256 consecutive cells of a row per iteration, so each plane
+// is read and the result written in runs as long as export_kernel's (64-cell
+// runs measured 71 against 60 us at C3: half-line reads and 512-byte store
+// runs). Three 16-byte DMAs per lane stage planes 0..11 of those cells as
+// rows of 256 bytes (DMA d: planes 4d .. 4d+3, lane l: plane 4d + l / 16,
+// chunk l % 16); chunk c of plane row k sits at c ^ 2 (k & 7), so the
+// transpose reads hit distinct banks: a 16-lane group reads 8 plane rows of
+// one chunk (8 distinct positions), and the group serviced with it reads the
+// neighbouring chunk (the other parity of positions). Rows
+// 12..15 are never written: their planes have zero weights. Each 64-cell
+// sub-tile takes two MFMAs and leaves column 8g + 4h + e of cell (l & 31) in
+// register 4g + e of lane 32 h + (l & 31); one permlane32 swap per register
+// gives every lane all columns of one cell.
+template <uint32_t P>
+__device__ constexpr Crt64Table<P> kCrt64 = make_crt64_table<P>();
+
+__device__ __forceinline__ uint32_t crt64_swz(uint32_t k) { return (k & 7u) << 1; }
+
+// Grid: x = groups of four 256-cell column chunks (one per wave), y = a share
+// of the rows: each wave keeps its chunk and walks rows with stride
+// gridDim.y, so a row step is a few scalar additions, and the DMAs of the
+// next kDepth - 1 rows are in flight while a row computes.
+template <uint32_t P, ExportKind Kind>
+__global__ __launch_bounds__(256) void crt64_export_kernel(ExportArgs a, ExportLimits lim, uint32_t chunks_per_row,
+                                                           uint64_t plane_span) {
+  static_assert(Kind == ExportKind::I64 || Kind == ExportKind::U64, "64-bit kinds only");
+  static_assert(P <= 12, "three DMAs of four planes");
+  constexpr uint32_t kNeeded = (kCrt64Cols + 7) / 8 * 4;  // registers holding columns < 14
+  constexpr uint32_t kDma = 3;
+  constexpr uint32_t kTile = 1024 * kDma;  // plane rows 0..11 of 256 bytes
+  // two row slots per wave (24 KB per block, six blocks per CU); four slots
+  // (three blocks per CU) measured slower
+  constexpr uint32_t kDepth = 2;
+  static_assert((kDepth & (kDepth - 1)) == 0 && kDepth >= 2, "slots by mask");
+  __shared__ __attribute__((aligned(16))) int8_t lds[4 * kDepth * kTile];
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t chunk = blockIdx.x * 4u + wave;
+  if (chunk >= chunks_per_row || static_cast<int64_t>(blockIdx.y) >= a.m) return;
+  int8_t* const tiles = lds + wave * kDepth * kTile;
+  const uint32_t tiles_lds = lds_address(tiles);
+  const v4i wfrag = *reinterpret_cast<const v4i*>(kCrt64<P>.frag[lane]);
+  uint32_t dma_off[kDma];
+#pragma unroll
+  for (uint32_t d = 0; d < kDma; ++d) {
+    const uint32_t k = 4u * d + (lane >> 4);
+    dma_off[d] = k < P ? k * static_cast<uint32_t>(a.pitch_c) + 16u * ((lane & 15u) ^ crt64_swz(k)) : 0x80000000u;
+  }
+  // transpose reads of sub-tile t: lanes whose planes are 16..31 re-read
+  // planes 0..15, and planes 12..15 (never staged) read rows 4..7 instead:
+  // all of those have zero weights
+  const uint32_t tr_j = lane & 15u, tr_g = lane >> 4;
+  uint32_t rd_lo[2], rd_hi[2];
+#pragma unroll
+  for (uint32_t jb = 0; jb < 2; ++jb) {
+    const uint32_t ncol = 32u * jb + 16u * (tr_g & 1u) + 8u * (tr_j & 1u);  // within a 64-cell sub-tile
+    const uint32_t k = tr_j >> 1;
+    const uint32_t kh = k + 8u < 4u * kDma ? k + 8u : k;
+    rd_lo[jb] = k * 256u + ((ncol >> 4) ^ crt64_swz(k)) * 16u + (ncol & 8u);
+    rd_hi[jb] = kh * 256u + ((ncol >> 4) ^ crt64_swz(kh)) * 16u + (ncol & 8u);
+  }
+  const int64_t c0 = static_cast<int64_t>(chunk) * 256;
+  const int64_t row_step = static_cast<int64_t>(gridDim.y);
+  // Row cursors advance by additions: the DMAs of row dma_row read plane
+  // bytes [dma_start, plane_span) (zero past it; an empty range past the last
+  // row), and row `row` stores through out_row.
+  const int64_t dma_step = row_step * a.ldc;
+  int64_t dma_row = blockIdx.y;
+  int64_t dma_start = dma_row * a.ldc + c0;
+  auto issue = [&](uint32_t slot) {
+    const bool live = dma_row < a.m;
+    const v4i rsrc =
+        buffer_rsrc(a.c + (live ? dma_start : 0), live ? static_cast<int64_t>(plane_span) - dma_start : 0);
+#pragma unroll
+    for (uint32_t d = 0; d < kDma; ++d) dma16(tiles_lds + slot * kTile + 1024u * d, dma_off[d], rsrc);
+    dma_row += row_step;
+    dma_start += dma_step;
+  };
+  bool violation = false;
+  int64_t row = blockIdx.y;
+  uint64_t* out_row = static_cast<uint64_t*>(a.dst) + row * a.ld;
+  const int64_t out_step = row_step * a.ld;
+  const int out_bytes = static_cast<int>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a.n * 8)));
+#pragma unroll
+  for (uint32_t d = 0; d + 1 < kDepth; ++d) issue(d);
+  uint32_t it = 0;
+  for (; row < a.m; row += row_step, out_row += out_step, ++it) {
+    const uint32_t slot = it & (kDepth - 1);
+    issue((it + kDepth - 1) & (kDepth - 1));
+    // Vector memory operations retire in order. Issued after this row's
+    // DMAs: the kDma DMAs of each of the next kDepth - 1 rows and the four
+    // stores of each of min(it, kDepth - 1) earlier rows; the first rows wait
+    // as if no store were outstanding (stricter).
+    if (it + 1 < kDepth)
+      __builtin_amdgcn_s_waitcnt(wait_vm(kDma * (kDepth - 1)));
+    else
+      __builtin_amdgcn_s_waitcnt(wait_vm((kDma + 4) * (kDepth - 1)));
+    const int8_t* const tile = tiles + slot * kTile;
+    const __amdgpu_buffer_rsrc_t out =
+        __builtin_amdgcn_make_buffer_rsrc(out_row, static_cast<short>(0), out_bytes, kBufferFlags);
+#pragma unroll
+    for (uint32_t t = 0; t < 4; ++t) {
+      v16i_crt acc[2];
+#pragma unroll
+      for (uint32_t jb = 0; jb < 2; ++jb) {
+        // sub-tile t: chunk positions 4t .. 4t+3 (the XOR keeps them in 4t .. 4t+3 ^ 0..7)
+        const v2i_crt lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_crt*)(tile + (rd_lo[jb] ^ (64u * t))));
+        const v2i_crt hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_crt*)(tile + (rd_hi[jb] ^ (64u * t))));
+        acc[jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wfrag, v4i{lo[0], lo[1], hi[0], hi[1]}, v16i_crt{}, 0, 0, 0);
+      }
+      int32_t s[16] = {};
+#pragma unroll
+      for (uint32_t r = 0; r < kNeeded; ++r) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(acc[0][r]),
+                                                         static_cast<uint32_t>(acc[1][r]), false, false);
+        s[8 * (r / 4) + r % 4] = static_cast<int32_t>(sw[0]);
+        s[8 * (r / 4) + 4 + r % 4] = static_cast<int32_t>(sw[1]);
+      }
+      int32_t g8 = 0;
+      const uint64_t lo = crt64_low<P>(kCrt64<P>, s, g8);
+      bool ok;
+      if constexpr (Kind == ExportKind::I64) {
+        const bool neg = static_cast<int32_t>(lo >> 32) < 0;
+        ok = crt64_in_int64<P>(kCrt64<P>, lo, g8) & (neg ? 0ull - lo <= lim.neg64 : lo <= lim.pos64);  // 0 - lo = |v|
+      } else {
+        ok = crt64_in_uint64<P>(kCrt64<P>, lo, g8) & (lo <= lim.pos64);
+      }
+      const int64_t col = c0 + 64 * t + lane;
+      violation |= (col < a.n) & !ok;
+      // stores through a buffer over the row's n cells: lanes past n are dropped
+      __builtin_amdgcn_raw_buffer_store_b64(v2u32_crt{static_cast<uint32_t>(lo), static_cast<uint32_t>(lo >> 32)},
+                                            out, static_cast<int>(static_cast<uint32_t>(col) * 8u), 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(wait_vm(0));  // no DMA outlives the wave's LDS
+  const uint64_t voters = __ballot(violation);
+  if (voters != 0 && lane == static_cast<uint32_t>(__ffsll(static_cast<long long>(voters)) - 1) &&
+      __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u)
+    atomicOr(a.status, 1u);
+}
+
 // Column groups x rows; rows beyond the grid's y extent are covered by the
 // row loop. Rows with fewer than 256 groups share a block: 2^shift threads
 // per row (shift = 8: one row per block).
@@ -713,6 +862,33 @@ hipError_t launch_crt_export_p(const ExportArgs& a, uint64_t plane_span, hipStre
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
+}
+
+template <uint32_t P>
+hipError_t launch_crt64_export_p(const ExportArgs& a, const ExportLimits& lim, uint64_t plane_span,
+                                 hipStream_t stream) {
+  const uint32_t chunks_per_row = static_cast<uint32_t>((a.n + 255) / 256);
+  // x: groups of 4 chunks; y: toward ~8 blocks per CU in all, each wave
+  // walking at least a few rows (the DMA pipeline runs along its rows)
+  const uint32_t gx = (chunks_per_row + 3u) / 4u;
+  const int64_t want_y = std::max<int64_t>(1, 2048 / static_cast<int64_t>(gx));
+  const uint32_t gy = static_cast<uint32_t>(std::min<int64_t>({a.m, want_y, 65535}));
+  if (a.kind == ExportKind::I64)
+    hipLaunchKernelGGL((crt64_export_kernel<P, ExportKind::I64>), dim3(gx, gy), dim3(256), 0, stream, a, lim,
+                       chunks_per_row, plane_span);
+  else
+    hipLaunchKernelGGL((crt64_export_kernel<P, ExportKind::U64>), dim3(gx, gy), dim3(256), 0, stream, a, lim,
+                       chunks_per_row, plane_span);
+  return hipGetLastError();
+}
+
+template <uint32_t... Ps>
+hipError_t dispatch_crt64(uint32_t prefix, const ExportArgs& a, const ExportLimits& lim, uint64_t plane_span,
+                          hipStream_t stream, std::integer_sequence<uint32_t, Ps...>) {
+  hipError_t err = hipErrorInvalidValue;
+  ((prefix == Ps + kCrt64MinP ? (err = launch_crt64_export_p<Ps + kCrt64MinP>(a, lim, plane_span, stream), 0) : 0),
+   ...);
+  return err;
 }
 
 template <uint32_t... Ps>
@@ -847,6 +1023,14 @@ hipError_t launch_export(const ExportArgs& a, uint32_t prefix, hipStream_t strea
   const bool crt = wide && crt_export_fits(plane_span, a.m, a.n, a.limbs) &&
                    (reinterpret_cast<uintptr_t>(a.c) & 15u) == 0 && (a.pitch_c % 16) == 0;
   if (crt) return dispatch_crt(prefix, a, plane_span, stream, std::make_integer_sequence<uint32_t, kMaxPrefix>{});
+  // 64-bit kinds at P = 9..11: the CRT-basis form with the 64-bit tail
+  const bool crt64 = (a.kind == ExportKind::I64 || a.kind == ExportKind::U64) && prefix >= kCrt64MinP &&
+                     prefix <= kCrt64MaxP && crt_export_fits(plane_span, a.m, a.n, 1) &&
+                     (reinterpret_cast<uintptr_t>(a.c) & 15u) == 0 && (a.pitch_c % 16) == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.dst) & 7u) == 0;
+  if (crt64)
+    return dispatch_crt64(prefix, a, lim, plane_span, stream,
+                          std::make_integer_sequence<uint32_t, kCrt64MaxP - kCrt64MinP + 1>{});
   return dispatch_prefix(prefix, a, lim, stream, std::make_integer_sequence<uint32_t, kMaxPrefix>{});
 }
 

@@ -21,6 +21,7 @@
 //             computes from their column sums; tests/test_tables.py checks
 //             both against Python big integers
 //   crtgate   the address limits of the CRT-basis export kernel
+//   crt64     the 64-bit CRT tail at P = 9..11 against __int128 values
 // Exit status 0 and a final "ok" line when every check passes.
 #include <cinttypes>
 #include <cstdint>
@@ -551,6 +552,79 @@ void crt_all(std::integer_sequence<uint32_t, Ps...>) {
   }
 }
 
+// The 64-bit CRT tail (make_crt64_table, crt64_low, crt64_in_int64,
+// crt64_in_uint64) at P = 9..11 against __int128 arithmetic: the centered
+// value x of each test cell, its residues, the MFMA column sums of the
+// table's weights, then the tail's low word and range decisions. Values:
+// dense scans across every decision band (around +-2^62, +-2^63, 2^64 and
+// +-M/2, in steps of one unit of the estimate and of one), and random values
+// over the whole centered range.
+template <uint32_t P>
+void crt64_check() {
+  constexpr Crt64Table<P> t = make_crt64_table<P>();
+  using i128 = __int128;
+  i128 M = 1;
+  for (uint32_t i = 0; i < P; ++i) M *= kLadder[i];
+  const i128 half = M / 2;
+  const i128 two63 = static_cast<i128>(1) << 63, two64 = static_cast<i128>(1) << 64;
+  long checked = 0;
+  auto check = [&](i128 x) {
+    if (x < -half || x >= half) return;  // centered range [-M/2, M/2)
+    int32_t s[kCrt64Cols] = {};
+    for (uint32_t i = 0; i < P; ++i) {
+      const int m = static_cast<int>(kLadder[i]);
+      int r = static_cast<int>(((x % m) + m) % m);
+      if (r >= (m + 1) / 2) r -= m;
+      for (uint32_t b = 0; b < kCrt64Cols; ++b) s[b] += r * t.w[i][b];
+    }
+    int32_t g8 = 0;
+    const uint64_t lo = crt64_low<P>(t, s, g8);
+    const bool in_s = crt64_in_int64<P>(t, lo, g8), want_s = x >= -two63 && x < two63;
+    const i128 xc = x < 0 ? x + M : x;  // canonical
+    const bool in_u = crt64_in_uint64<P>(t, lo, g8), want_u = xc < two64;
+    bool bad = in_s != want_s || in_u != want_u;
+    if (want_s && static_cast<int64_t>(lo) != static_cast<int64_t>(x)) bad = true;
+    if (want_u && lo != static_cast<uint64_t>(xc)) bad = true;
+    if (bad) {
+      if (failures < 20)
+        std::printf("crt64 P%u: x %.6e (hi %lld lo %llu) in_s %d/%d in_u %d/%d g8 %d\n", P, static_cast<double>(x),
+                    static_cast<long long>(static_cast<int64_t>(x >> 64)), static_cast<unsigned long long>(x),
+                    in_s, want_s, in_u, want_u, g8);
+      ++failures;
+    }
+    ++checked;
+  };
+  // one unit of the 2^40-scaled estimate, in value terms
+  const i128 unit = M >> 40;
+  const i128 edges[] = {0, two63 / 2, two63, two64, -two63 / 2, -two63, -two64, half, -half};
+  for (i128 e : edges) {
+    for (long k = -6000; k <= 6000; ++k) check(e + k * unit);
+    for (long k = -3000; k <= 3000; ++k) check(e + k);
+    for (long k = -2000; k <= 2000; ++k) check(e + k * (unit / 7 + 1) + 3);
+  }
+  uint64_t st = 0x9E3779B97F4A7C15ull ^ P;
+  auto next = [&]() {
+    st += 0x9E3779B97F4A7C15ull;
+    uint64_t z = st;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  };
+  for (int n = 0; n < 300000; ++n) {
+    const i128 r = (static_cast<i128>(next()) << 64) | next();
+    const i128 mag = r & ((static_cast<i128>(1) << 100) - 1);
+    check(mag % M - half);                                            // whole range
+    check(static_cast<i128>(static_cast<int64_t>(next())) >> (next() & 63));  // 64-bit values of every size
+    check(two64 - (static_cast<i128>(next() >> (next() & 63))));      // just below 2^64
+  }
+  std::printf("crt64 P%u: %ld values\n", P, checked);
+}
+
+template <uint32_t... Ps>
+void crt64_all(std::integer_sequence<uint32_t, Ps...>) {
+  (crt64_check<Ps + kCrt64MinP>(), ...);
+}
+
 // crt_export_fits: every export it admits has the 32-bit quantities
 // crt_export_kernel forms (the output row's byte range, the last lane's byte
 // offset in it, the unit count) equal to their 64-bit values and below the
@@ -605,6 +679,8 @@ int main(int argc, char** argv) {
   else if (!std::strcmp(argv[1], "export64")) export64_all(std::make_integer_sequence<uint32_t, kMaxPrefix>{});
   else if (!std::strcmp(argv[1], "crt")) crt_all(std::make_integer_sequence<uint32_t, kMaxPrefix>{});
   else if (!std::strcmp(argv[1], "crtgate")) check_crtgate();
+  else if (!std::strcmp(argv[1], "crt64"))
+    crt64_all(std::make_integer_sequence<uint32_t, kCrt64MaxP - kCrt64MinP + 1>{});
   else return 2;
   if (failures) {
     std::printf("failures %d\n", failures);

@@ -57,6 +57,16 @@ def test_pack_reduction_int64(checker):
     _run(checker, "pack64")
 
 
+def test_crt64_tail(checker):
+    """The 64-bit CRT-basis export tail at P = 9..11 against __int128: low
+    word and int64 / uint64 range decisions for ~1.08 million values per
+    prefix, dense across every decision band (around +-2^62, +-2^63, 2^64
+    and +-M/2) and random over the whole centered range."""
+    out = _run(checker, "crt64")
+    for p in (9, 10, 11):
+        assert f"crt64 P{p}:" in out
+
+
 def test_crt_export_address_gate(checker):
     """crt_export_fits admits exactly the exports whose output row bytes,
     lane offsets and unit count the CRT-basis kernel can form in 32 bits
