@@ -14,6 +14,7 @@
 #include <limits>
 #include <new>
 
+#include "contract.hpp"
 #include "handles.hpp"
 #include "kernels.hpp"
 
@@ -1055,29 +1056,19 @@ rns8_status rns8_create_matrix(rns8_context* ctx, const rns8_matrix_desc* desc, 
     static std::atomic<uint64_t> next_id{1};
     if (!ctx || !desc || !out) return RNS8_INVALID_ARGUMENT;
     *out = nullptr;
-    if (!valid_abi(desc->struct_size, desc->abi_version, sizeof(*desc))) return RNS8_INVALID_ARGUMENT;
-    const uint32_t prefix = desc->max_prefix == 0 ? default_prefix(desc->semantics) : desc->max_prefix;
-    const rns8_status v = validate_matrix_desc(*desc, prefix);
+    rns8_matrix layout;
+    const rns8_status v = init_matrix(*desc, ctx->backend, ctx->device_id, layout);
     if (v != RNS8_SUCCESS) return v;
-    if (desc->semantics == RNS8_WRAP_U64_MOD_2_64) return RNS8_UNSUPPORTED_BACKEND;
-    const int64_t pitch = plane_pitch(desc->rows, desc->cols);
-    const uint32_t planes = uses_finite_storage(desc->semantics) ? 1u : prefix;
-    if (pitch <= 0 || static_cast<uint64_t>(pitch) > std::numeric_limits<uint64_t>::max() / planes)
-      return RNS8_RANGE_ERROR;
     auto* m = new (std::nothrow) rns8_matrix();
     if (!m) return RNS8_INTERNAL_ERROR;
-    m->desc = *desc;
-    m->desc.max_prefix = uses_finite_storage(desc->semantics) ? 0u : prefix;
-    if (m->desc.logical_ld == 0) m->desc.logical_ld = m->desc.cols;
-    if (m->desc.tile_m == 0) m->desc.tile_m = 128;
-    if (m->desc.tile_n == 0) m->desc.tile_n = 128;
-    m->backend = ctx->backend;
-    m->device_id = ctx->device_id;
+    m->desc = layout.desc;
+    m->backend = layout.backend;
+    m->device_id = layout.device_id;
     m->instance_id = next_id.fetch_add(1);
-    m->prefix = planes;
-    m->plane_ld = padded_ld(desc->cols);
-    m->plane_pitch = pitch;
-    m->plane_bytes = static_cast<uint64_t>(pitch) * planes;
+    m->prefix = layout.prefix;
+    m->plane_ld = layout.plane_ld;
+    m->plane_pitch = layout.plane_pitch;
+    m->plane_bytes = layout.plane_bytes;
     if (hipSetDevice(ctx->device_id) != hipSuccess ||
         hipMalloc(reinterpret_cast<void**>(&m->planes), m->plane_bytes) != hipSuccess) {
       delete m;

@@ -17,23 +17,12 @@
 #include <thread>
 #include <vector>
 
+#include "contract.hpp"
 #include "handles.hpp"
 #include "kernels.hpp"
 
 namespace rns8x {
 namespace {
-
-bool valid_access(int64_t rows, int64_t cols, int64_t ld) {
-  if (rows <= 0 || cols <= 0 || ld < cols) return false;
-  return rows <= std::numeric_limits<int64_t>::max() / ld;
-}
-
-bool valid_limb_access(int64_t rows, int64_t cols, int64_t ld, uint32_t limbs) {
-  if (!valid_access(rows, cols, ld) || limbs == 0 || limbs > 32) return false;
-  const int64_t max = std::numeric_limits<int64_t>::max();
-  if (ld > max / static_cast<int64_t>(limbs)) return false;
-  return rows <= max / (ld * static_cast<int64_t>(limbs));
-}
 
 uint64_t output_source_version(uint64_t a, uint64_t b) {
   // reference api_plan_workspace_fingerprint.inc:18-23
@@ -49,21 +38,6 @@ uint64_t output_source_version(uint64_t a, uint64_t b) {
 // pack's proof holds until it is read back.
 I512 native_worst_case(rns8_semantics s) {
   return s == RNS8_EXACT_WIDE_SIGNED ? I512::pow2(63) : I512::from_u64(~uint64_t{0});
-}
-
-// Reads a proof left on the device back into exact_max (waits for the work
-// that writes it). No-op for a proof that is already exact.
-rns8_status resolve_exact_proof(const rns8_matrix& m) {
-  if (!m.exact_pending) return RNS8_SUCCESS;
-  unsigned long long w[2] = {0, 0};
-  if (hipSetDevice(m.device_id) != hipSuccess || hipEventSynchronize(m.proof_event) != hipSuccess ||
-      hipMemcpy(w, m.proof_words(), sizeof(w), hipMemcpyDeviceToHost) != hipSuccess)
-    return RNS8_BACKEND_FAILURE;
-  m.exact_max = m.pending_product
-                    ? I512::from_u64(m.proof_k) * I512::from_u64(w[0]) * I512::from_u64(w[1])
-                    : I512::from_u64(w[0]);
-  m.exact_pending = false;
-  return RNS8_SUCCESS;
 }
 
 // exact_range.hpp:104-157 on the operands' carried proofs. Operands whose
@@ -127,93 +101,6 @@ rns8_status commit_exact_proof(rns8_matrix& C, const rns8_matrix& A, const rns8_
 
 // ---- shared validation --------------------------------------------------------
 
-rns8_status check_plan_ctx_ws(const rns8_context& ctx, const rns8_plan& plan, const rns8_workspace& ws) {
-  if (plan.backend != ctx.backend || ws.backend != plan.backend) return RNS8_INVALID_ARGUMENT;
-  if (ws.semantics != plan.desc.semantics || ws.bound_kind != plan.desc.bound_kind) return RNS8_INVALID_ARGUMENT;
-  if (ws.m != plan.desc.m || ws.n != plan.desc.n || ws.k != plan.desc.k || ws.prefix != plan.prefix)
-    return RNS8_WORKSPACE_TOO_SMALL;
-  if (plan.splitk_bytes > ws.splitk_bytes) return RNS8_WORKSPACE_TOO_SMALL;
-  if (plan.device_id != ctx.device_id || ws.device_id != ctx.device_id) return RNS8_INVALID_ARGUMENT;
-  return RNS8_SUCCESS;
-}
-
-// reference api_gemm.cpp:50-111
-rns8_status check_rns_operands(const rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& A,
-                               const rns8_matrix& B, const rns8_matrix& C) {
-  if (!uses_rns_storage(plan.desc.semantics) || plan.prefix == 0) return RNS8_INVALID_ARGUMENT;
-  if (A.backend != plan.backend || B.backend != plan.backend || C.backend != plan.backend)
-    return RNS8_INVALID_ARGUMENT;
-  if (A.device_id != ctx.device_id || B.device_id != ctx.device_id || C.device_id != ctx.device_id)
-    return RNS8_INVALID_ARGUMENT;
-  const uint32_t sp = storage_prefix(plan);
-  const rns8_bound_kind bk = storage_bound_kind(plan);
-  const uint32_t tm = plan.desc.tile_m, tn = plan.desc.tile_n;
-  if (!matrix_matches(A, plan.desc.semantics, bk, plan.desc.m, plan.desc.k, sp, tm, tn) ||
-      !matrix_matches(B, plan.desc.semantics, bk, plan.desc.k, plan.desc.n, sp, tm, tn) ||
-      !matrix_matches(C, plan.desc.semantics, bk, plan.desc.m, plan.desc.n, sp, tm, tn))
-    return RNS8_INVALID_ARGUMENT;
-  if (!A.device_current || !B.device_current) return RNS8_INVALID_ARGUMENT;
-  // C is written while A and B are read by other workgroups: no aliasing
-  if (&A == &C || &B == &C) return RNS8_INVALID_ARGUMENT;
-  return RNS8_SUCCESS;
-}
-
-// reference api_gemm.cpp:113-160
-rns8_status check_finite_operands(const rns8_context& ctx, const rns8_plan& plan, uint16_t modulus,
-                                  const rns8_matrix& A, const rns8_matrix& B, const rns8_matrix& C) {
-  if (!uses_finite_storage(plan.desc.semantics) || !valid_finite_modulus(plan.desc.semantics, modulus) ||
-      plan.desc.finite_modulus != modulus)
-    return RNS8_INVALID_ARGUMENT;
-  if (A.backend != plan.backend || B.backend != plan.backend || C.backend != plan.backend)
-    return RNS8_INVALID_ARGUMENT;
-  if (A.device_id != ctx.device_id || B.device_id != ctx.device_id || C.device_id != ctx.device_id)
-    return RNS8_INVALID_ARGUMENT;
-  if (!matrix_matches(A, plan.desc.semantics, RNS8_BOUND_NONE, plan.desc.m, plan.desc.k, 0) ||
-      !matrix_matches(B, plan.desc.semantics, RNS8_BOUND_NONE, plan.desc.k, plan.desc.n, 0) ||
-      !matrix_matches(C, plan.desc.semantics, RNS8_BOUND_NONE, plan.desc.m, plan.desc.n, 0))
-    return RNS8_INVALID_ARGUMENT;
-  if (!A.device_current || !B.device_current || A.finite_modulus != modulus || B.finite_modulus != modulus)
-    return RNS8_INVALID_ARGUMENT;
-  if (&A == &C || &B == &C) return RNS8_INVALID_ARGUMENT;
-  return RNS8_SUCCESS;
-}
-
-// reference api_export.cpp:5-53
-rns8_status check_export(const rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& C,
-                         rns8_semantics semantics) {
-  if (plan.backend != ctx.backend || C.backend != plan.backend || plan.desc.semantics != semantics)
-    return RNS8_INVALID_ARGUMENT;
-  if (C.device_id != ctx.device_id || plan.device_id != ctx.device_id) return RNS8_INVALID_ARGUMENT;
-  if (!matrix_matches(C, semantics, storage_bound_kind(plan), plan.desc.m, plan.desc.n, storage_prefix(plan),
-                      plan.desc.tile_m, plan.desc.tile_n))
-    return RNS8_INVALID_ARGUMENT;
-  if (!C.device_current) return RNS8_INVALID_ARGUMENT;
-  if (exact_wide(semantics) && C.exact_prefix != 0) {
-    if (C.exact_prefix < plan.prefix) return RNS8_RANGE_ERROR;
-    // a pending proof whose worst case fits needs no read back
-    if (!exact_range_fits(semantics, C.exact_max, plan.product)) {
-      if (!C.exact_pending) return RNS8_RANGE_ERROR;
-      const rns8_status st = resolve_exact_proof(C);
-      if (st != RNS8_SUCCESS) return st;
-      if (!exact_range_fits(semantics, C.exact_max, plan.product)) return RNS8_RANGE_ERROR;
-    }
-  }
-  return RNS8_SUCCESS;
-}
-
-rns8_status check_finite_export(const rns8_context& ctx, const rns8_plan& plan, uint16_t modulus,
-                                const rns8_matrix& C) {
-  if (!uses_finite_storage(plan.desc.semantics) || plan.desc.finite_modulus != modulus ||
-      !valid_finite_modulus(plan.desc.semantics, modulus))
-    return RNS8_INVALID_ARGUMENT;
-  if (plan.backend != ctx.backend || C.backend != plan.backend || C.device_id != ctx.device_id)
-    return RNS8_INVALID_ARGUMENT;
-  if (!matrix_matches(C, plan.desc.semantics, RNS8_BOUND_NONE, plan.desc.m, plan.desc.n, 0))
-    return RNS8_INVALID_ARGUMENT;
-  if (!C.device_current || C.finite_modulus != modulus) return RNS8_INVALID_ARGUMENT;
-  return RNS8_SUCCESS;
-}
-
 rns8_status sync(hipStream_t s) { return hipStreamSynchronize(s) == hipSuccess ? RNS8_SUCCESS : RNS8_BACKEND_FAILURE; }
 
 // ---- pack ------------------------------------------------------------------------
@@ -224,12 +111,10 @@ template <typename T>
 rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, int64_t ld, uint64_t sv, Source where,
                         void* stream_arg) {
   constexpr bool is_signed = std::is_same<T, int64_t>::value;
-  if (!ctx || !matrix || !src || !valid_access(matrix->desc.rows, matrix->desc.cols, ld))
-    return RNS8_INVALID_ARGUMENT;
-  const rns8_semantics bounded = is_signed ? RNS8_BOUNDED_I64 : RNS8_BOUNDED_U64;
+  if (!ctx || !matrix || !src) return RNS8_INVALID_ARGUMENT;
+  const rns8_status chk = check_pack_native(*ctx, *matrix, ld, is_signed);
+  if (chk != RNS8_SUCCESS) return chk;
   const rns8_semantics wide = is_signed ? RNS8_EXACT_WIDE_SIGNED : RNS8_EXACT_WIDE_UNSIGNED;
-  if (matrix->desc.semantics != bounded && matrix->desc.semantics != wide) return RNS8_INVALID_ARGUMENT;
-  if (ctx->backend != matrix->backend || matrix->device_id != ctx->device_id) return RNS8_INVALID_ARGUMENT;
   const int64_t rows = matrix->desc.rows, cols = matrix->desc.cols;
   const bool same_source = sv != 0 && matrix->source_version == sv && matrix->device_current;
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
@@ -282,19 +167,10 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
     dsrc = matrix->upload;
     dld = cols;
   }
-  PackArgs args{dsrc,
-                rows,
-                cols,
-                dld,
-                matrix->planes,
-                matrix->plane_ld,
-                matrix->plane_pitch,
-                matrix->prefix,
-                is_signed ? NativeKind::I64 : NativeKind::U64,
-                // the maximum goes to word 0 of the other slot (zero), and the
-                // same launch clears word 0 of the current one
-                deferred ? matrix->next_proof_words() : nullptr,
-                deferred ? matrix->proof_words() : nullptr};
+  // the maximum goes to word 0 of the other slot (zero), and the same launch
+  // clears word 0 of the current one
+  const PackArgs args = pack_args(*matrix, dsrc, dld, is_signed, deferred ? matrix->next_proof_words() : nullptr,
+                                  deferred ? matrix->proof_words() : nullptr);
   if (launch_pack_native(args, make_ladder_plane_consts(matrix->prefix), stream) != hipSuccess)
     return RNS8_BACKEND_FAILURE;
   if (deferred) {
@@ -320,10 +196,9 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
 
 rns8_status pack_u8(rns8_context* ctx, rns8_matrix* matrix, uint16_t modulus, const uint8_t* src, int64_t ld,
                     uint64_t sv, Source where, void* stream_arg) {
-  if (!ctx || !matrix || !src || !valid_access(matrix->desc.rows, matrix->desc.cols, ld)) return RNS8_INVALID_ARGUMENT;
-  if (!uses_finite_storage(matrix->desc.semantics) || !valid_finite_modulus(matrix->desc.semantics, modulus))
-    return RNS8_INVALID_ARGUMENT;
-  if (ctx->backend != matrix->backend || matrix->device_id != ctx->device_id) return RNS8_INVALID_ARGUMENT;
+  if (!ctx || !matrix || !src) return RNS8_INVALID_ARGUMENT;
+  const rns8_status chk = check_pack_u8(*ctx, *matrix, modulus, ld);
+  if (chk != RNS8_SUCCESS) return chk;
   if (sv != 0 && matrix->source_version == sv && matrix->finite_modulus == modulus && matrix->device_current)
     return RNS8_SUCCESS;
   const int64_t rows = matrix->desc.rows, cols = matrix->desc.cols;
@@ -339,7 +214,7 @@ rns8_status pack_u8(rns8_context* ctx, rns8_matrix* matrix, uint16_t modulus, co
     dsrc = static_cast<const uint8_t*>(matrix->upload);
     dld = cols;
   }
-  PackU8Args args{dsrc, rows, cols, dld, matrix->planes, matrix->plane_ld, modulus};
+  const PackU8Args args = pack_u8_args(*matrix, dsrc, dld, modulus);
   if (launch_pack_u8(args, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
   if (where == Source::Host) {
     const rns8_status st = sync(stream);
@@ -356,22 +231,7 @@ rns8_status pack_u8(rns8_context* ctx, rns8_matrix* matrix, uint16_t modulus, co
 rns8_status run_gemm(rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B,
                      rns8_matrix& C, int8_t* splitk_ws, uint32_t nplanes, const PlaneConsts& consts,
                      hipStream_t stream) {
-  GemmArgs g{};
-  g.a = A.planes;
-  g.b = B.planes;
-  g.c = C.planes;
-  g.m = plan.desc.m;
-  g.n = plan.desc.n;
-  g.k = plan.desc.k;
-  g.lda = A.plane_ld;
-  g.ldb = B.plane_ld;
-  g.ldc = C.plane_ld;
-  g.pitch_a = A.plane_pitch;
-  g.pitch_b = B.plane_pitch;
-  g.pitch_c = C.plane_pitch;
-  g.nplanes = nplanes;
-  g.slices = plan.splitk_slices;
-  g.splitk_ws = plan.splitk_slices > 1 ? splitk_ws : nullptr;
+  const GemmArgs g = gemm_args(plan, A, B, C, splitk_ws, nplanes, plan.splitk_slices);
   if (hipSetDevice(ctx.device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
   const hipError_t e = launch_gemm(g, consts, stream);
   if (e == hipErrorInvalidValue) return RNS8_UNSUPPORTED_BACKEND;  // shape outside the kernel's limits
@@ -383,21 +243,7 @@ rns8_status run_gemm(rns8_context& ctx, const rns8_plan& plan, const rns8_matrix
 rns8_status run_gemm_tiled(rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B,
                            rns8_matrix& C, hipStream_t stream) {
   const uint32_t planes = storage_prefix(plan);
-  GemmArgs g{};
-  g.a = A.planes;
-  g.b = B.planes;
-  g.c = C.planes;
-  g.m = plan.desc.m;
-  g.n = plan.desc.n;
-  g.k = plan.desc.k;
-  g.lda = A.plane_ld;
-  g.ldb = B.plane_ld;
-  g.ldc = C.plane_ld;
-  g.pitch_a = A.plane_pitch;
-  g.pitch_b = B.plane_pitch;
-  g.pitch_c = C.plane_pitch;
-  g.nplanes = planes;
-  g.slices = 1;
+  const GemmArgs g = gemm_args(plan, A, B, C, nullptr, planes, 1);
   if (hipSetDevice(ctx.device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
   hipError_t e = launch_gemm_listed(g, make_ladder_plane_consts(planes), plan.units, plan.unit_count,
                                     plan.unit_edge, stream);
@@ -676,8 +522,7 @@ rns8_status export_host(rns8_context* ctx, const rns8_plan* plan, const rns8_mat
   if (!mc->status && hipMalloc(reinterpret_cast<void**>(&mc->status), 64) != hipSuccess) return RNS8_BACKEND_FAILURE;
   const hipStream_t stream = ctx->stream;
   if (launch_zero_words(mc->status, 1, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
-  ExportArgs a{C->planes, m, n, C->plane_ld, C->plane_pitch, mc->staging, n, req.limbs, req.kind, plan->desc.bound,
-               mc->status};
+  const ExportArgs a = export_args(*plan, *C, mc->staging, n, req.limbs, req.kind, mc->status);
   if (launch_plan_export(*plan, a, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
   uint32_t status = 0;
   if (hipMemcpyAsync(&status, mc->status, sizeof(status), hipMemcpyDeviceToHost, stream) != hipSuccess ||
@@ -694,8 +539,7 @@ rns8_status export_device(rns8_context* ctx, const rns8_plan* plan, const rns8_m
   rns8_status st = check_export(*ctx, *plan, *C, req.semantics);
   if (st != RNS8_SUCCESS) return st;
   if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
-  ExportArgs a{C->planes,  plan->desc.m, plan->desc.n,     C->plane_ld, C->plane_pitch, d_dst,
-               ld,         req.limbs,    req.kind,         plan->desc.bound, d_status};
+  const ExportArgs a = export_args(*plan, *C, d_dst, ld, req.limbs, req.kind, d_status);
   return launch_plan_export(*plan, a, pick_stream(*ctx, stream_arg)) == hipSuccess
              ? RNS8_SUCCESS
              : RNS8_BACKEND_FAILURE;
@@ -711,12 +555,12 @@ rns8_status export_finite(rns8_context* ctx, const rns8_plan* plan, uint16_t mod
   if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
   if (where == Source::Device) {
-    ExportU8Args a{C->planes, m, n, C->plane_ld, dst, ld, modulus};
+    const ExportU8Args a = export_u8_args(*plan, *C, dst, ld, modulus);
     return launch_export_u8(a, stream) == hipSuccess ? RNS8_SUCCESS : RNS8_BACKEND_FAILURE;
   }
   st = ensure_device_buffer(ctx->device_id, &mc->staging, &mc->staging_bytes, static_cast<std::size_t>(m) * n);
   if (st != RNS8_SUCCESS) return st;
-  ExportU8Args a{C->planes, m, n, C->plane_ld, static_cast<uint8_t*>(mc->staging), n, modulus};
+  const ExportU8Args a = export_u8_args(*plan, *C, static_cast<uint8_t*>(mc->staging), n, modulus);
   if (launch_export_u8(a, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
   return ctx->host.to_host(dst, ld, mc->staging, n, m, stream) == hipSuccess ? RNS8_SUCCESS : RNS8_BACKEND_FAILURE;
 }

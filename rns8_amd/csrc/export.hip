@@ -971,13 +971,7 @@ hipError_t launch_export_zero_tiles(const ExportArgs& a, const TileExport* d_til
 }
 
 hipError_t launch_export(const ExportArgs& a, uint32_t prefix, hipStream_t stream) {
-  if (!a.c || !a.dst || !a.status || a.m <= 0 || a.n <= 0 || a.ld < a.n) return hipErrorInvalidValue;
-  if (prefix == 0 || prefix > kMaxPrefix) return hipErrorInvalidValue;
-  if (a.ldc != padded_ld(a.n) || a.pitch_c < a.m * a.ldc || (a.pitch_c % 4) != 0) return hipErrorInvalidValue;
-  if ((reinterpret_cast<uintptr_t>(a.c) & 3u) != 0) return hipErrorInvalidValue;
-  if (a.ldc / 4 > 0xFFFFFFFFll) return hipErrorInvalidValue;
-  if (a.limbs == 0 || a.limbs > 32) return hipErrorInvalidValue;
-  if ((a.kind == ExportKind::I64 || a.kind == ExportKind::U64) && a.limbs != 1) return hipErrorInvalidValue;
+  if (!export_args_ok(a, prefix)) return hipErrorInvalidValue;
   ExportLimits lim{};
   lim.check = 1;
   switch (a.kind) {
@@ -1035,10 +1029,7 @@ hipError_t launch_export(const ExportArgs& a, uint32_t prefix, hipStream_t strea
 }
 
 hipError_t launch_export_u8(const ExportU8Args& a, hipStream_t stream) {
-  if (!a.c || !a.dst || a.m <= 0 || a.n <= 0 || a.ld < a.n) return hipErrorInvalidValue;
-  if (a.ldc != padded_ld(a.n) || (reinterpret_cast<uintptr_t>(a.c) & 15u) != 0) return hipErrorInvalidValue;
-  if (a.modulus < 2 || a.modulus > 256) return hipErrorInvalidValue;
-  if (a.ldc / 16 > 0xFFFFFFFFll) return hipErrorInvalidValue;
+  if (!export_u8_args_ok(a)) return hipErrorInvalidValue;
   const uint32_t groups_per_row = static_cast<uint32_t>(a.ldc / 16);
   const uint32_t vec = (reinterpret_cast<uintptr_t>(a.dst) % 16 == 0 && a.ld % 16 == 0) ? 1u : 0u;
   hipLaunchKernelGGL(export_u8_kernel, grid_2d(groups_per_row, a.m), dim3(256), 0, stream, a, groups_per_row, vec,

@@ -646,24 +646,6 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* dst, uint64_t
 using CfgLarge = Cfg<4, 4>;  // 256 x 256 tiles, one workgroup per CU (all 512 registers per lane)
 using CfgSmall = Cfg<2, 2>;  // 128 x 128 tiles, two workgroups per CU
 
-bool gemm_shape_ok(const GemmArgs& a) {
-  if (a.m <= 0 || a.n <= 0 || a.k <= 0) return false;
-  if (a.nplanes == 0 || a.nplanes > kMaxPrefix) return false;
-  if (a.lda % 16 || a.ldb % 16 || a.ldc % 16) return false;
-  if (a.lda < a.k || a.ldb < a.n || a.ldc < a.n) return false;
-  // 32-bit buffer offsets: a 256-row panel and a 64-row slab must stay below 2^31
-  if (a.lda >= (int64_t{1} << 23) || a.ldb >= (int64_t{1} << 23)) return false;
-  // unit decode runs in 32 bits: rows and tile origins below 2^31
-  if (a.m >= (int64_t{1} << 31)) return false;
-  if (a.ldc != a.ldb) return false;  // C columns == B columns: same padded pitch
-  if (a.pitch_a < a.m * a.lda || a.pitch_b < a.k * a.ldb || a.pitch_c < a.m * a.ldc) return false;
-  if (!a.a || !a.b || !a.c) return false;
-  if (a.slices == 0) return false;
-  if (a.slices > 1 && !a.splitk_ws) return false;
-  // the workspace holds [slices][planes][m][padded_ld(n)] residues
-  if (a.slices > 1 && a.ldc != padded_ld(a.n)) return false;
-  return true;
-}
 
 template <typename Cf>
 int64_t tile_count(int64_t m, int64_t n, uint32_t nplanes) {
@@ -826,7 +808,7 @@ hipError_t launch_listed(const GemmArgs& args, const PlaneConsts& consts, const 
 hipError_t launch_gemm_listed(const GemmArgs& args, const PlaneConsts& consts, const uint32_t* d_units,
                               uint32_t units, uint32_t edge, hipStream_t stream) {
   // the list's entries are checked against the shape and edge where it is built
-  if (!gemm_shape_ok(args) || args.slices != 1 || !d_units || units > 0x7FFFFFFFu) return hipErrorInvalidValue;
+  if (!gemm_args_ok(args) || args.slices != 1 || !d_units || units > 0x7FFFFFFFu) return hipErrorInvalidValue;
   if (units == 0) return hipSuccess;
   if (edge == 256) return launch_listed<CfgLarge, 1>(args, consts, d_units, units, stream);
   if (edge == 128) return launch_listed<CfgSmall, 2>(args, consts, d_units, units, stream);
@@ -876,7 +858,7 @@ int8_t* noalloc_scratch(int device) {
 }
 
 hipError_t launch_gemm(const GemmArgs& args, const PlaneConsts& consts, hipStream_t stream) {
-  if (!gemm_shape_ok(args)) return hipErrorInvalidValue;
+  if (!gemm_args_ok(args)) return hipErrorInvalidValue;
   const GemmShape shape = choose_gemm_shape(args.m, args.n, args.k, args.nplanes);
   // the workspace was sized for the plan's slices: never use a different
   // split (an unsplit call of a split shape runs unsplit where the kernel
@@ -908,7 +890,7 @@ hipError_t launch_gemm_grouped(const GemmArgs& shape, const PlaneConsts& consts,
     a.c = tasks[t].c;
     a.splitk_ws = tasks[t].ws;
     a.slices = g.tile == 16 ? shape.slices : g.slices;
-    if (!gemm_shape_ok(a)) return hipErrorInvalidValue;
+    if (!gemm_args_ok(a)) return hipErrorInvalidValue;
   }
   if (g.tile == 16) {
     // the skinny kernel fills the chip from one task's rows and K slices:

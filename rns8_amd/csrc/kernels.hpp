@@ -215,6 +215,15 @@ struct ExportU8Args {
 };
 hipError_t launch_export_u8(const ExportU8Args& args, hipStream_t stream);
 
+// The launchers' argument checks (contract.cpp): launch_gemm,
+// launch_export, launch_export_u8, launch_pack_native and launch_pack_u8
+// refuse (hipErrorInvalidValue) arguments these reject.
+bool gemm_args_ok(const GemmArgs& a);
+bool export_args_ok(const ExportArgs& a, uint32_t prefix);
+bool export_u8_args_ok(const ExportU8Args& a);
+bool pack_args_ok(const PackArgs& a);
+bool pack_u8_args_ok(const PackU8Args& a);
+
 // Fill `words` 32-bit words with zero (used instead of hipMemsetAsync so the
 // call sequence stays valid under stream capture).
 hipError_t launch_zero_words(uint32_t* dst, uint64_t words, hipStream_t stream);

@@ -239,14 +239,9 @@ constexpr uint64_t kStreamPackBytes = uint64_t{256} << 20;
 }  // namespace
 
 hipError_t launch_pack_native(const PackArgs& a, const PlaneConsts& consts, hipStream_t stream) {
-  if (!a.src || !a.planes || a.rows <= 0 || a.cols <= 0 || a.ld < a.cols) return hipErrorInvalidValue;
-  if (a.nplanes == 0 || a.nplanes > kMaxPrefix) return hipErrorInvalidValue;
-  if (a.plane_ld != padded_ld(a.cols) || a.plane_pitch < a.rows * a.plane_ld || (a.plane_pitch % 16) != 0)
-    return hipErrorInvalidValue;
-  if ((reinterpret_cast<uintptr_t>(a.planes) & 15u) != 0) return hipErrorInvalidValue;
+  if (!pack_args_ok(a)) return hipErrorInvalidValue;
   const int64_t chunks_per_row = a.plane_ld / 8;
   const int64_t total = chunks_per_row * a.rows;
-  if (total >= (int64_t{1} << 32)) return hipErrorInvalidValue;
   const bool vec = (reinterpret_cast<uintptr_t>(a.src) & 15u) == 0 && (a.ld % 2) == 0;
   const dim3 grid(grid_for(total));
   const uint32_t cpr = static_cast<uint32_t>(chunks_per_row), tot = static_cast<uint32_t>(total);
@@ -306,12 +301,9 @@ hipError_t launch_max_magnitude(const void* src, int64_t rows, int64_t cols, int
 }
 
 hipError_t launch_pack_u8(const PackU8Args& a, hipStream_t stream) {
-  if (!a.src || !a.plane || a.rows <= 0 || a.cols <= 0 || a.ld < a.cols) return hipErrorInvalidValue;
-  if (a.modulus < 2 || a.modulus > 256) return hipErrorInvalidValue;
-  if (a.plane_ld != padded_ld(a.cols) || (reinterpret_cast<uintptr_t>(a.plane) & 15u) != 0) return hipErrorInvalidValue;
+  if (!pack_u8_args_ok(a)) return hipErrorInvalidValue;
   const int64_t chunks_per_row = a.plane_ld / 16;
   const int64_t total = chunks_per_row * a.rows;
-  if (total >= (int64_t{1} << 32)) return hipErrorInvalidValue;
   const uint32_t vec = (reinterpret_cast<uintptr_t>(a.src) % 16 == 0 && a.ld % 16 == 0) ? 1u : 0u;
   hipLaunchKernelGGL(pack_u8_kernel, dim3(grid_for(total)), dim3(256), 0, stream, a, make_modulus_consts(a.modulus),
                      static_cast<uint32_t>(chunks_per_row), static_cast<uint32_t>(total), vec);

@@ -1,9 +1,15 @@
 """libFuzzer + AddressSanitizer + UndefinedBehaviorSanitizer over the
 device-free planning entries rns8_mi355x_select_prefix and
-rns8_mi355x_plan_schedule (tests/fuzz/fuzz_plan_descriptor.cpp, built by
-tests/fuzz/Makefile; reference tests/fuzz/rns8_fuzz_plan_descriptor.cpp).
-CPU only: the library's host sources are compiled instrumented, and no
-device is touched. A fixed seed and run count make the run repeatable."""
+rns8_mi355x_plan_schedule (tests/fuzz/fuzz_plan_descriptor.cpp; reference
+tests/fuzz/rns8_fuzz_plan_descriptor.cpp), and over the pack -> GEMM ->
+export contract (tests/fuzz/fuzz_export_contract.cpp): arbitrary plan and
+matrix descriptors, strides, limb counts and workspaces go through the
+entry points' checks, and every accepted call must hand the launchers
+kernel arguments they accept and whose reach stays inside the matrices'
+planes, the workspace and the caller's buffer. Both are built by
+tests/fuzz/Makefile. CPU only: the library's host sources are compiled
+instrumented, and no device is touched. A fixed seed and run count make
+each run repeatable."""
 import shutil
 import subprocess
 from pathlib import Path
@@ -12,7 +18,8 @@ import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 CLANG = Path("/opt/rocm/llvm/bin/clang++")
-DEVICE_OBJS = [ROOT / "rns8_amd" / "_build" / f"{n}.o" for n in ("export", "fused", "gemm", "pack")]
+DEVICE_OBJS = [ROOT / "rns8_amd" / "_build" / f"{n}.o"
+               for n in ("export", "fused", "fused_skinny", "gemm", "pack", "skinny")]
 
 
 @pytest.fixture(scope="module")
@@ -35,3 +42,13 @@ def test_plan_descriptor_fuzz(fuzzer):
                          cwd=fuzzer)
     assert res.returncode == 0, res.stderr[-4000:]
     assert "Done 1500000 runs" in res.stderr
+
+
+def test_export_contract_fuzz(fuzzer):
+    corpus = fuzzer / "corpus_contract"
+    corpus.mkdir()
+    res = subprocess.run([str(fuzzer / "fuzz_export_contract"), "-seed=1", "-runs=1000000", "-max_len=512",
+                          "-print_final_stats=1", str(corpus)], capture_output=True, text=True, timeout=600,
+                         cwd=fuzzer)
+    assert res.returncode == 0, res.stderr[-4000:]
+    assert "Done 1000000 runs" in res.stderr
