@@ -829,11 +829,15 @@ def oneshot_rate(args) -> int:
 
 def host_pack_rate(args) -> int:
     """The public host-array entries on C4's exact-wide operands (2048 x 2048
-    full-range int64, prefix 20): rns8_pack_i64 proves the operand's range on
-    the host from the array (per-axis maxima and sums in 512-bit integers,
-    api_exec.cpp) before the upload and the pack; rns8_gemm_rns then admits
-    the product from those summaries. Times both against a bare upload of the
-    same bytes. Prints one JSON line; not a `value`."""
+    full-range int64, prefix 20): rns8_pack_i64 uploads the array, proves its
+    range on the device (per-row and per-column summaries, exact_axes.hip)
+    and packs it; rns8_gemm_rns admits the product (on k maxA maxB, which
+    fits at prefix 20). Times both against a bare upload of the same bytes,
+    and the admission that needs the refined bound: D = C x B with C the
+    result above, whose worst case does not fit, so the call computes C's
+    summaries and D's cell bounds on the device (2 x 2048^2 cells) and reads
+    the bound back (the product is then refused, as the reference refuses
+    it). Prints one JSON line; not a `value`."""
     import rns8_amd as r
     from rns8_amd import hip, inputs
 
@@ -872,10 +876,21 @@ def host_pack_rate(args) -> int:
 
         pack = timed(packs)
         gemm = timed(lambda: r.check(r.gemm_rns(ctx, plan, Am, Bm, Cm, ws), "gemm"))
+        Dm = mk()
+
+        def refused_chain():
+            # C is a fresh lazy result each time, so each call computes C's summaries too
+            r.check(r.lib().rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, None), "C")
+            st = r.gemm_rns(ctx, plan, Cm, Bm, Dm, ws)
+            if st != r.RANGE_ERROR:
+                raise RuntimeError(f"chain status {st}, expected RNS8_RANGE_ERROR")
+
+        chain = timed(refused_chain)
         hip.free(d)
     print(json.dumps({"mode": "exact-wide host-array packs and GEMM (C4 operands, public ABI)", "n": n,
                       "prefix": plan.prefix, "ms_upload_one_operand": round(upload, 3),
-                      "ms_pack_two_operands": round(pack, 3), "ms_gemm_rns_with_admission": round(gemm, 3)}))
+                      "ms_pack_two_operands": round(pack, 3), "ms_gemm_rns_with_admission": round(gemm, 3),
+                      "ms_gemm_plus_refined_admission": round(chain, 3)}))
     return 0
 
 

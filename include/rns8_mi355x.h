@@ -50,8 +50,12 @@ RNS8_API rns8_status rns8_mi355x_plan_schedule(
 
 /* Device-source variants of rns8_pack_i64 / rns8_pack_u64 / rns8_pack_finite_u8
  * (reference rns8.h:848-911): `d_src` is device memory, row stride `ld`
- * elements. For exact-wide matrices the magnitude proof is the global
- * maximum |x| computed on the GPU (no per-row/column refinement). */
+ * elements. For exact-wide matrices the magnitude proof is the one the
+ * reference's host pack builds (per-row and per-column maxima, sums,
+ * absolute sums, extremes and deviation sums, reference exact_range.hpp
+ * :52-78), computed on the GPU; so every later admission equals the one
+ * the reference makes for the same values. At prefix 9 and up the call does
+ * not synchronize; below, it reads max |x| back before writing anything. */
 RNS8_API rns8_status rns8_mi355x_pack_i64_device(
     rns8_context* ctx,
     rns8_matrix* matrix,
@@ -76,7 +80,13 @@ RNS8_API rns8_status rns8_mi355x_pack_finite_u8_device(
     void* stream);
 
 /* Asynchronous rns8_gemm_rns / rns8_gemm_finite_u8 (reference rns8.h:988,
- * 1098): same validation and admission, kernels enqueued on `stream`. */
+ * 1098): same validation and admission, kernels enqueued on `stream`.
+ * Exact-wide admission: the call decides on k * maxA * maxB, from maxima the
+ * host already holds, and does not synchronize when that bound fits. When it
+ * does not fit, the reference's refined bound (the minimum of its candidate
+ * bounds for every output cell, from the operands' per-row and per-column
+ * summaries) is computed on the device and read back before the call
+ * returns: the call then synchronizes `stream`. */
 RNS8_API rns8_status rns8_mi355x_gemm_rns_async(
     rns8_context* ctx,
     const rns8_plan* plan,
@@ -104,8 +114,8 @@ RNS8_API rns8_status rns8_mi355x_gemm_finite_u8_async(
  * library holds until the process ends (its address is looked up when a
  * context is created). Plans whose split-K residues exceed 4 MiB return
  * RNS8_WORKSPACE_TOO_SMALL;
- * exact-wide plans return RNS8_UNSUPPORTED_BACKEND (their admission proofs
- * live in host memory). Every call on one device shares that device's
+ * exact-wide plans return RNS8_UNSUPPORTED_BACKEND (their admission may read
+ * a device bound back and keeps its proofs in host memory). Every call on one device shares that device's
  * scratch: calls that overlap on one device (on different streams, or from
  * several threads) race and must be ordered by the caller; calls ordered on
  * one stream do not. Results equal rns8_mi355x_gemm_rns_async's. */
@@ -220,6 +230,39 @@ RNS8_API rns8_status rns8_mi355x_get_matrix_planes(
     int64_t* row_pitch,
     int64_t* plane_pitch,
     uint32_t* plane_count);
+
+/* One row or column of an exact-wide matrix's magnitude proof, as
+ * little-endian 64-bit words (reference rns8_exact_axis_range,
+ * internal.hpp:72-86). */
+typedef struct rns8_mi355x_exact_axis {
+  uint64_t max_magnitude[4]; /* unsigned 256-bit */
+  uint64_t absolute_sum[4];  /* unsigned 256-bit */
+  uint64_t sum[2];           /* signed 128-bit, two's complement */
+  uint64_t minimum[2];       /* signed 128-bit */
+  uint64_t maximum[2];       /* signed 128-bit */
+  uint64_t deviation_sum[2]; /* unsigned 128-bit */
+} rns8_mi355x_exact_axis;
+
+#define RNS8_MI355X_EXACT_AXES_NATIVE 0u  /* a pack's summaries: every field */
+#define RNS8_MI355X_EXACT_AXES_CARRIED 1u /* a GEMM result's: max_magnitude, absolute_sum */
+#define RNS8_MI355X_EXACT_AXES_NONE 2u    /* no per-axis summaries */
+
+/* The magnitude proof an exact-wide matrix carries into later GEMMs
+ * (reference exact_range.hpp:51-171): its bound (max |x| of a packed
+ * operand, the proven bound of a GEMM result) into bound[0..3] as an
+ * unsigned 256-bit integer, the kind of its axes, and rows[desc.rows] /
+ * cols[desc.cols] (either may be NULL; untouched for
+ * RNS8_MI355X_EXACT_AXES_NONE). A result's own summaries are computed when
+ * first needed, here on the context's stream. Synchronizes. No counterpart
+ * in the reference's C API (its proof is internal state). Returns
+ * RNS8_INVALID_ARGUMENT for matrices without an exact-wide proof. */
+RNS8_API rns8_status rns8_mi355x_get_exact_proof(
+    rns8_context* ctx,
+    const rns8_matrix* matrix,
+    uint64_t bound[4],
+    uint32_t* axes_kind,
+    rns8_mi355x_exact_axis* rows,
+    rns8_mi355x_exact_axis* cols);
 
 #ifdef __cplusplus
 }

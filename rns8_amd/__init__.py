@@ -25,6 +25,9 @@ from .abi import (  # noqa: F401  (re-exported constants)
     BOUND_PER_TILE_MAX_UNSIGNED,
     BOUNDED_I64,
     BOUNDED_U64,
+    EXACT_AXES_CARRIED,
+    EXACT_AXES_NATIVE,
+    EXACT_AXES_NONE,
     EXACT_WIDE_SIGNED,
     EXACT_WIDE_UNSIGNED,
     FINITE_FIELD_U8,
@@ -235,6 +238,34 @@ class Matrix(_Handle):
         check(lib().rns8_mi355x_get_matrix_planes(self.ptr, C.byref(p), C.byref(rp), C.byref(pp), C.byref(n)),
               "rns8_mi355x_get_matrix_planes")
         return p.value, rp.value, pp.value, n.value
+
+    def exact_proof(self, ctx: Context):
+        """The exact-wide magnitude proof this matrix carries
+        (rns8_mi355x_get_exact_proof): (bound, kind, rows, cols), with rows
+        and cols lists of dicts of Python integers (max_magnitude,
+        absolute_sum, sum, minimum, maximum, deviation_sum) and kind one of
+        EXACT_AXES_NATIVE / EXACT_AXES_CARRIED / EXACT_AXES_NONE."""
+        bound = np.zeros(4, dtype=np.uint64)
+        kind = C.c_uint32()
+        rows = np.zeros((self.rows, 16), dtype=np.uint64)
+        cols = np.zeros((self.cols, 16), dtype=np.uint64)
+        check(lib().rns8_mi355x_get_exact_proof(ctx.ptr, self.ptr, bound.ctypes.data, C.byref(kind),
+                                                rows.ctypes.data, cols.ctypes.data), "rns8_mi355x_get_exact_proof")
+
+        def word_int(w, signed=False):
+            v = sum(int(x) << (64 * i) for i, x in enumerate(w))
+            bits = 64 * len(w)
+            return v - (1 << bits) if signed and v >> (bits - 1) else v
+
+        def axis(r):
+            return {"max_magnitude": word_int(r[0:4]), "absolute_sum": word_int(r[4:8]),
+                    "sum": word_int(r[8:10], True), "minimum": word_int(r[10:12], True),
+                    "maximum": word_int(r[12:14], True), "deviation_sum": word_int(r[14:16])}
+
+        k = kind.value
+        if k == EXACT_AXES_NONE:
+            return word_int(bound), k, [], []
+        return word_int(bound), k, [axis(r) for r in rows], [axis(c) for c in cols]
 
     def read_residues(self, nplanes: int | None = None) -> np.ndarray:
         """Copy the resident planes to host as int8 [planes][rows][cols]."""

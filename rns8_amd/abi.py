@@ -55,6 +55,11 @@ PLAN_FORCE_FIXED_PREFIX = 0x1
 PLAN_ALLOW_PROVEN_ZERO_TILE_SKIPS = 0x2
 PLAN_ALLOW_PROVEN_ZERO_ROW_COL_SKIPS = 0x4
 
+# rns8_mi355x_get_exact_proof axis kinds
+EXACT_AXES_NATIVE = 0
+EXACT_AXES_CARRIED = 1
+EXACT_AXES_NONE = 2
+
 DEFAULT_MODULUS_COUNT = 28
 DEFAULT_BOUNDED_PREFIX = 9
 MAX_SUPPORTED_PREFIX = 20
@@ -365,6 +370,7 @@ PROTOTYPES = {
     "rns8_mi355x_gemm_finite_u8_grouped_async": (_U32, [_P, _P, _U16, C.POINTER(GroupedGemmTask), _U32, _P]),
     "rns8_get_grouped_dispatch_contract_info": (_U32, [_P, _U32, C.POINTER(GroupedDispatchContractInfo)]),
     "rns8_mi355x_get_matrix_planes": (_U32, [_P, C.POINTER(_P), C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_U32)]),
+    "rns8_mi355x_get_exact_proof": (_U32, [_P, _P, _P, C.POINTER(_U32), _P, _P]),
 }
 
 LIB_PATH = Path(__file__).resolve().parent / "librns8.so"

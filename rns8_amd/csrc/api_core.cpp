@@ -1074,10 +1074,11 @@ rns8_status rns8_create_matrix(rns8_context* ctx, const rns8_matrix_desc* desc, 
       delete m;
       return RNS8_BACKEND_FAILURE;
     }
-    // exact-wide matrices: two slots of two words and an event for proofs
-    // left on the device (zeroed below with the planes)
+    // exact-wide matrices: the device proof (two sets of axis records and the
+    // pack accumulators, zeroed below with the planes) and its event
+    const uint64_t proof_bytes = rns8_matrix::proof_bytes(m->desc.rows, m->desc.cols);
     if (exact_wide(desc->semantics) &&
-        (hipMalloc(reinterpret_cast<void**>(&m->proof_device), 32) != hipSuccess ||
+        (hipMalloc(reinterpret_cast<void**>(&m->proof_device), proof_bytes) != hipSuccess ||
          hipEventCreateWithFlags(&m->proof_event, hipEventDisableTiming) != hipSuccess)) {
       free_device(m->planes);
       free_device(m->proof_device);
@@ -1087,7 +1088,8 @@ rns8_status rns8_create_matrix(rns8_context* ctx, const rns8_matrix_desc* desc, 
     // zero planes: a fresh matrix holds the integer 0 and keeps padding zero
     if (launch_zero_words(reinterpret_cast<uint32_t*>(m->planes), m->plane_bytes / 4, ctx->stream) != hipSuccess ||
         (m->proof_device &&
-         launch_zero_words(reinterpret_cast<uint32_t*>(m->proof_device), 8, ctx->stream) != hipSuccess) ||
+         launch_zero_words(reinterpret_cast<uint32_t*>(m->proof_device), proof_bytes / 4, ctx->stream) !=
+             hipSuccess) ||
         hipStreamSynchronize(ctx->stream) != hipSuccess) {
       free_device(m->planes);
       free_device(m->proof_device);

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "contract.hpp"
+#include "exact_proof.hpp"
 #include "handles.hpp"
 #include "kernels.hpp"
 
@@ -38,65 +39,6 @@ uint64_t output_source_version(uint64_t a, uint64_t b) {
 // pack's proof holds until it is read back.
 I512 native_worst_case(rns8_semantics s) {
   return s == RNS8_EXACT_WIDE_SIGNED ? I512::pow2(63) : I512::from_u64(~uint64_t{0});
-}
-
-// exact_range.hpp:104-157 on the operands' carried proofs. Operands whose
-// proofs are still on the device (device-pointer packs) carry no per-axis
-// summaries, so the bound is k * maxA * maxB; when the worst case of that
-// product is admitted the exact one is too, and the result is left pending
-// as well (*pending: the caller copies the operands' device maxima into the
-// result's proof words). Otherwise the proofs are read back and the decision
-// is made on exact values.
-rns8_status exact_gemm_range(const rns8_plan& plan, const rns8_matrix& A, const rns8_matrix& B, I512& bound,
-                             std::vector<ExactAxis>* out_rows, std::vector<ExactAxis>* out_cols,
-                             bool* pending = nullptr) {
-  if (pending) *pending = false;
-  if (!exact_wide(plan.desc.semantics)) return RNS8_SUCCESS;
-  if (A.exact_prefix < plan.prefix || B.exact_prefix < plan.prefix) return RNS8_RANGE_ERROR;
-  if (A.exact_pending || B.exact_pending) {
-    const bool natives = A.exact_pending && !A.pending_product && B.exact_pending && !B.pending_product;
-    if (natives && pending) {
-      const I512 worst = I512::from_u64(static_cast<uint64_t>(plan.desc.k)) * A.exact_max * B.exact_max;
-      if (exact_range_fits(plan.desc.semantics, worst, plan.product)) {
-        bound = worst;
-        if (out_rows) out_rows->clear();
-        if (out_cols) out_cols->clear();
-        *pending = true;
-        return RNS8_SUCCESS;
-      }
-    }
-    rns8_status st = resolve_exact_proof(A);
-    if (st == RNS8_SUCCESS) st = resolve_exact_proof(B);
-    if (st != RNS8_SUCCESS) return st;
-  }
-  const ExactOperand a{&A.exact_max, &A.exact_rows, &A.exact_cols};
-  const ExactOperand b{&B.exact_max, &B.exact_rows, &B.exact_cols};
-  return exact_product_range(plan.desc.semantics, plan.desc.m, plan.desc.n, plan.desc.k, a, b, plan.product, bound,
-                             out_rows, out_cols);
-}
-
-// Records C's proof after C = A x B: exact values from the host proofs, or,
-// for a pending result, the operands' device maxima copied into C's proof
-// words on the GEMM's stream (ordered after their packs as the planes are).
-rns8_status commit_exact_proof(rns8_matrix& C, const rns8_matrix& A, const rns8_matrix& B, const rns8_plan& plan,
-                               const I512& bound, std::vector<ExactAxis>& rows, std::vector<ExactAxis>& cols,
-                               bool pending, hipStream_t stream) {
-  if (pending) {
-    // into C's other slot, clearing word 0 of its current one
-    if (launch_proof_factors(A.proof_words(), B.proof_words(), C.next_proof_words(), C.proof_words(), stream) !=
-            hipSuccess ||
-        hipEventRecord(C.proof_event, stream) != hipSuccess)
-      return RNS8_BACKEND_FAILURE;
-    C.proof_slot ^= 1u;
-    C.proof_k = static_cast<uint64_t>(plan.desc.k);
-  }
-  C.exact_max = bound;
-  C.exact_pending = pending;
-  C.pending_product = pending;
-  C.exact_rows.swap(rows);
-  C.exact_cols.swap(cols);
-  C.exact_prefix = plan.prefix;
-  return RNS8_SUCCESS;
 }
 
 // ---- shared validation --------------------------------------------------------
@@ -120,42 +62,16 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
   if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
 
-  // exact-wide proof (api_pack.cpp:47-65); kept when the source is unchanged.
-  // A device-pointer pack into a matrix whose prefix admits every 64-bit
-  // value (P > 2^64: prefix 9 and up) proves its maximum |x| in the pack
-  // launch itself and leaves it on the device (`deferred`): no decision at
-  // pack time depends on it. Smaller prefixes need the maximum before
-  // anything is written (a refused pack leaves the matrix as it was), so it
-  // is computed and read back first.
-  I512 proof_max;
-  std::vector<ExactAxis> proof_rows, proof_cols;
+  // exact-wide proof (api_pack.cpp:47-65), kept when the source is
+  // unchanged: the operand's per-row and per-column summaries, computed on
+  // the device into the matrix's free proof set and made current with the
+  // planes. At prefix 9 and up (P > 2^64) every 64-bit operand is admitted,
+  // so nothing waits for the proof and the host keeps a worst case of max |x|
+  // (exact after a host-array pack, which synchronizes anyway). Smaller
+  // prefixes need the maximum before anything is written (a refused pack
+  // leaves the matrix as it was), so it is read back first.
   const bool is_wide = matrix->desc.semantics == wide;
-  const I256 matrix_product = modulus_product(matrix->prefix);
-  bool deferred = false;
-  if (is_wide) {
-    if (same_source) {
-      proof_max = matrix->exact_max;  // a pending proof keeps its worst case
-    } else if (where == Source::Host) {
-      native_exact_ranges(src, rows, cols, ld, proof_max, proof_rows, proof_cols);
-    } else if (exact_range_fits(matrix->desc.semantics, native_worst_case(matrix->desc.semantics), matrix_product)) {
-      deferred = true;
-      proof_max = native_worst_case(matrix->desc.semantics);
-    } else {
-      unsigned long long host_max = 0;
-      // word 0 of the current slot as scratch (the other slot stays clear)
-      if (launch_zero_words(reinterpret_cast<uint32_t*>(matrix->proof_words()), 2, stream) != hipSuccess ||
-          launch_max_magnitude(src, rows, cols, ld, is_signed ? NativeKind::I64 : NativeKind::U64,
-                               matrix->proof_words(), stream) != hipSuccess ||
-          hipMemcpyAsync(&host_max, matrix->proof_words(), sizeof(host_max), hipMemcpyDeviceToHost, stream) !=
-              hipSuccess ||
-          hipStreamSynchronize(stream) != hipSuccess)
-        return RNS8_BACKEND_FAILURE;
-      proof_max = I512::from_u64(host_max);
-    }
-    if (!exact_range_fits(matrix->desc.semantics, proof_max, matrix_product)) return RNS8_RANGE_ERROR;
-  }
   if (same_source) return RNS8_SUCCESS;
-
   const void* dsrc = src;
   int64_t dld = ld;
   if (where == Source::Host) {
@@ -167,30 +83,36 @@ rns8_status pack_native(rns8_context* ctx, rns8_matrix* matrix, const T* src, in
     dsrc = matrix->upload;
     dld = cols;
   }
-  // the maximum goes to word 0 of the other slot (zero), and the same launch
-  // clears word 0 of the current one
-  const PackArgs args = pack_args(*matrix, dsrc, dld, is_signed, deferred ? matrix->next_proof_words() : nullptr,
-                                  deferred ? matrix->proof_words() : nullptr);
+  I512 proof_max;
+  bool pending = false;
+  if (is_wide) {
+    rns8_status st = prove_native(*matrix, dsrc, dld, is_signed, stream);
+    if (st != RNS8_SUCCESS) return st;
+    const I512 worst = native_worst_case(matrix->desc.semantics);
+    if (exact_range_fits(matrix->desc.semantics, worst, modulus_product(matrix->prefix))) {
+      proof_max = worst;
+      pending = true;
+    } else {
+      st = read_free_bound(*matrix, stream, proof_max);
+      if (st != RNS8_SUCCESS) return st;
+      if (!exact_range_fits(matrix->desc.semantics, proof_max, modulus_product(matrix->prefix)))
+        return RNS8_RANGE_ERROR;
+    }
+  }
+  const PackArgs args = pack_args(*matrix, dsrc, dld, is_signed);
   if (launch_pack_native(args, make_ladder_plane_consts(matrix->prefix), stream) != hipSuccess)
     return RNS8_BACKEND_FAILURE;
-  if (deferred) {
-    matrix->proof_slot ^= 1u;
-    if (hipEventRecord(matrix->proof_event, stream) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  if (is_wide) {
+    const rns8_status st = commit_native_proof(*matrix, proof_max, pending, stream);
+    if (st != RNS8_SUCCESS) return st;
   }
   if (where == Source::Host) {
-    const rns8_status st = sync(stream);
+    rns8_status st = sync(stream);
+    if (st == RNS8_SUCCESS && is_wide && pending) st = resolve_exact_proof(*matrix, stream);
     if (st != RNS8_SUCCESS) return st;
   }
   matrix->device_current = true;
   matrix->source_version = sv;
-  if (is_wide) {
-    matrix->exact_max = proof_max;
-    matrix->exact_pending = deferred;
-    matrix->pending_product = false;
-    matrix->exact_rows.swap(proof_rows);
-    matrix->exact_cols.swap(proof_cols);
-    matrix->exact_prefix = matrix->prefix;
-  }
   return RNS8_SUCCESS;
 }
 
@@ -260,12 +182,13 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
   if (st != RNS8_SUCCESS) return st;
   st = check_rns_operands(*ctx, *plan, *A, *B, *C);
   if (st != RNS8_SUCCESS) return st;
-  I512 bound;
-  std::vector<ExactAxis> out_rows, out_cols;
-  bool pending = false;
-  st = exact_gemm_range(*plan, *A, *B, bound, &out_rows, &out_cols, &pending);
-  if (st != RNS8_SUCCESS) return st;
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
+  ExactAdmission adm;
+  if (exact_wide(plan->desc.semantics)) {
+    if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+    st = exact_gemm_admit(*plan, *A, *B, *C, stream, adm);
+    if (st != RNS8_SUCCESS) return st;
+  }
   C->device_current = false;
   if (per_tile_kind(plan->desc.bound_kind) && !plan->schedule.entries.empty())
     st = run_gemm_tiled(*ctx, *plan, *A, *B, *C, stream);
@@ -273,7 +196,7 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
     st = run_gemm(*ctx, *plan, *A, *B, *C, ws->splitk, plan->prefix, make_ladder_plane_consts(plan->prefix), stream);
   if (st != RNS8_SUCCESS) return st;
   if (exact_wide(plan->desc.semantics)) {
-    st = commit_exact_proof(*C, *A, *B, *plan, bound, out_rows, out_cols, pending, stream);
+    st = commit_exact_proof(*C, *A, *B, *plan, adm, stream);
     if (st != RNS8_SUCCESS) return st;
   }
   if (synchronous) {
@@ -289,7 +212,7 @@ rns8_status gemm_rns(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix
 // rns8_mi355x_gemm_rns_async without a workspace argument. Split-K residues
 // go to the library's per-device static scratch (kNoAllocScratchBytes); the
 // call allocates nothing, host or device. Exact-wide plans are refused: their
-// admission builds per-row and per-column proofs in host memory.
+// admission keeps proofs in host memory and may read one back.
 rns8_status gemm_rns_noalloc(rns8_context* ctx, const rns8_plan* plan, const rns8_matrix* A, const rns8_matrix* B,
                              rns8_matrix* C, void* stream_arg) {
   if (!ctx || !plan || !A || !B || !C) return RNS8_INVALID_ARGUMENT;
@@ -422,25 +345,21 @@ rns8_status gemm_grouped(rns8_context* ctx, const rns8_plan* plan, const rns8_gr
                                   : check_rns_operands(*ctx, *plan, *t.a, *t.b, *t.c);
     if (st != RNS8_SUCCESS) return st;
   }
-  std::vector<I512> bounds(task_count);
-  std::vector<std::vector<ExactAxis>> rows(task_count), cols(task_count);
-  std::vector<uint8_t> pendings(task_count, 0);
-  if (!finite && exact_wide(plan->desc.semantics))
-    for (uint32_t i = 0; i < task_count; ++i) {
-      bool pending = false;
-      const rns8_status st =
-          exact_gemm_range(*plan, *tasks[i].a, *tasks[i].b, bounds[i], &rows[i], &cols[i], &pending);
-      if (st != RNS8_SUCCESS) return st;
-      pendings[i] = pending ? 1 : 0;
-    }
-
   // every host allocation comes before the first change to a result
+  std::vector<ExactAdmission> adms(task_count);
   std::vector<TaskPtrs> ptrs(task_count);
   for (uint32_t i = 0; i < task_count; ++i)
     ptrs[i] = TaskPtrs{tasks[i].a->planes, tasks[i].b->planes, tasks[i].c->planes,
                        plan->splitk_slices > 1 ? tasks[i].workspace->splitk : nullptr};
   const hipStream_t stream = pick_stream(*ctx, stream_arg);
   if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+  // every task is admitted before any result changes (a refined admission
+  // writes only its result's free proof set)
+  if (!finite && exact_wide(plan->desc.semantics))
+    for (uint32_t i = 0; i < task_count; ++i) {
+      const rns8_status st = exact_gemm_admit(*plan, *tasks[i].a, *tasks[i].b, *tasks[i].c, stream, adms[i]);
+      if (st != RNS8_SUCCESS) return st;
+    }
   for (uint32_t i = 0; i < task_count; ++i) tasks[i].c->device_current = false;
   rns8_status st = RNS8_SUCCESS;
   if (!finite && per_tile_kind(plan->desc.bound_kind) && !plan->schedule.entries.empty()) {
@@ -468,8 +387,7 @@ rns8_status gemm_grouped(rns8_context* ctx, const rns8_plan* plan, const rns8_gr
   }
   if (st == RNS8_SUCCESS && !finite && exact_wide(plan->desc.semantics))
     for (uint32_t i = 0; i < task_count && st == RNS8_SUCCESS; ++i)
-      st = commit_exact_proof(*tasks[i].c, *tasks[i].a, *tasks[i].b, *plan, bounds[i], rows[i], cols[i],
-                              pendings[i] != 0, stream);
+      st = commit_exact_proof(*tasks[i].c, *tasks[i].a, *tasks[i].b, *plan, adms[i], stream);
   if (st == RNS8_SUCCESS && synchronous) st = sync(stream);
   if (st != RNS8_SUCCESS) return st;
   for (uint32_t i = 0; i < task_count; ++i) {
@@ -973,4 +891,42 @@ rns8_status rns8_mi355x_export_exact_wide_unsigned_limbs_device(rns8_context* ct
 rns8_status rns8_mi355x_export_finite_u8_device(rns8_context* ctx, const rns8_plan* plan, uint16_t modulus,
                                                 const rns8_matrix* C, uint8_t* d_dst, int64_t ld, void* stream) {
   return guard([&] { return export_finite(ctx, plan, modulus, C, d_dst, ld, Source::Device, stream); });
+}
+
+static_assert(sizeof(rns8_mi355x_exact_axis) == sizeof(rns8x::xa::AxisRecord), "proof record layout");
+
+rns8_status rns8_mi355x_get_exact_proof(rns8_context* ctx, const rns8_matrix* matrix, uint64_t bound[4],
+                                        uint32_t* axes_kind, rns8_mi355x_exact_axis* rows,
+                                        rns8_mi355x_exact_axis* cols) {
+  return guard([&]() -> rns8_status {
+    if (!ctx || !matrix || !bound || !axes_kind) return RNS8_INVALID_ARGUMENT;
+    if (!exact_wide(matrix->desc.semantics) || matrix->exact_prefix == 0 || matrix->device_id != ctx->device_id)
+      return RNS8_INVALID_ARGUMENT;
+    if (hipSetDevice(ctx->device_id) != hipSuccess) return RNS8_BACKEND_FAILURE;
+    if (matrix->proof_kind == rns8_matrix::ProofKind::Lazy) {
+      if (hipStreamWaitEvent(ctx->stream, matrix->proof_event, 0) != hipSuccess) return RNS8_BACKEND_FAILURE;
+      const rns8_status st = materialize_proof(*matrix, ctx->stream);
+      if (st != RNS8_SUCCESS) return st;
+    }
+    if (hipEventSynchronize(matrix->proof_event) != hipSuccess) return RNS8_BACKEND_FAILURE;
+    const uint32_t s = matrix->proof_set;
+    const rns8_matrix::ProofKind kind = matrix->proof_kind;
+    *axes_kind = kind == rns8_matrix::ProofKind::Native    ? RNS8_MI355X_EXACT_AXES_NATIVE
+                 : kind == rns8_matrix::ProofKind::Carried ? RNS8_MI355X_EXACT_AXES_CARRIED
+                                                           : RNS8_MI355X_EXACT_AXES_NONE;
+    if (hipMemcpy(bound, matrix->proof_words(s), 4 * sizeof(uint64_t), hipMemcpyDeviceToHost) != hipSuccess)
+      return RNS8_BACKEND_FAILURE;
+    if (*axes_kind != RNS8_MI355X_EXACT_AXES_NONE) {
+      const std::size_t rb = static_cast<std::size_t>(matrix->desc.rows) * sizeof(rns8_mi355x_exact_axis);
+      const std::size_t cb = static_cast<std::size_t>(matrix->desc.cols) * sizeof(rns8_mi355x_exact_axis);
+      if ((rows && hipMemcpy(rows, matrix->proof_rows(s), rb, hipMemcpyDeviceToHost) != hipSuccess) ||
+          (cols && hipMemcpy(cols, matrix->proof_cols(s), cb, hipMemcpyDeviceToHost) != hipSuccess))
+        return RNS8_BACKEND_FAILURE;
+    }
+    I512 b;
+    for (int i = 0; i < 4; ++i) b.w[i] = bound[i];
+    matrix->exact_max = b;
+    matrix->exact_pending = false;
+    return RNS8_SUCCESS;
+  });
 }

@@ -8,6 +8,8 @@
 //   rns8_create_matrix   src/core/moduli.cpp:389-448, api_matrix_public_api.inc:84-104
 #include "contract.hpp"
 
+#include "exact_proof.hpp"
+
 #include <limits>
 
 namespace rns8x {
@@ -45,19 +47,6 @@ rns8_status init_matrix(const rns8_matrix_desc& d, rns8_backend_kind backend, in
   m.plane_ld = padded_ld(d.cols);
   m.plane_pitch = pitch;
   m.plane_bytes = static_cast<uint64_t>(pitch) * planes;
-  return RNS8_SUCCESS;
-}
-
-rns8_status resolve_exact_proof(const rns8_matrix& m) {
-  if (!m.exact_pending) return RNS8_SUCCESS;
-  unsigned long long w[2] = {0, 0};
-  if (hipSetDevice(m.device_id) != hipSuccess || hipEventSynchronize(m.proof_event) != hipSuccess ||
-      hipMemcpy(w, m.proof_words(), sizeof(w), hipMemcpyDeviceToHost) != hipSuccess)
-    return RNS8_BACKEND_FAILURE;
-  m.exact_max = m.pending_product
-                    ? I512::from_u64(m.proof_k) * I512::from_u64(w[0]) * I512::from_u64(w[1])
-                    : I512::from_u64(w[0]);
-  m.exact_pending = false;
   return RNS8_SUCCESS;
 }
 
@@ -127,7 +116,7 @@ rns8_status check_export(const rns8_context& ctx, const rns8_plan& plan, const r
     // a pending proof whose worst case fits needs no read back
     if (!exact_range_fits(semantics, C.exact_max, plan.product)) {
       if (!C.exact_pending) return RNS8_RANGE_ERROR;
-      const rns8_status st = resolve_exact_proof(C);
+      const rns8_status st = resolve_exact_proof(C, ctx.stream);
       if (st != RNS8_SUCCESS) return st;
       if (!exact_range_fits(semantics, C.exact_max, plan.product)) return RNS8_RANGE_ERROR;
     }
@@ -197,10 +186,9 @@ ExportU8Args export_u8_args(const rns8_plan& plan, const rns8_matrix& C, uint8_t
   return ExportU8Args{C.planes, plan.desc.m, plan.desc.n, C.plane_ld, dst, ld, modulus};
 }
 
-PackArgs pack_args(const rns8_matrix& m, const void* src, int64_t ld, bool is_signed, unsigned long long* max_out,
-                   unsigned long long* max_clear) {
+PackArgs pack_args(const rns8_matrix& m, const void* src, int64_t ld, bool is_signed) {
   return PackArgs{src,      m.desc.rows, m.desc.cols, ld, m.planes, m.plane_ld, m.plane_pitch, m.prefix,
-                  is_signed ? NativeKind::I64 : NativeKind::U64, max_out, max_clear};
+                  is_signed ? NativeKind::I64 : NativeKind::U64};
 }
 
 PackU8Args pack_u8_args(const rns8_matrix& m, const uint8_t* src, int64_t ld, uint16_t modulus) {

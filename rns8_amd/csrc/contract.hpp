@@ -24,10 +24,6 @@ bool valid_limb_access(int64_t rows, int64_t cols, int64_t ld, uint32_t limbs);
 // bytes); the caller then allocates plane_bytes of planes.
 rns8_status init_matrix(const rns8_matrix_desc& d, rns8_backend_kind backend, int device_id, rns8_matrix& m);
 
-// Reads a proof left on the device back into exact_max; no-op (and no
-// device call) when the proof is already exact.
-rns8_status resolve_exact_proof(const rns8_matrix& m);
-
 // reference api_gemm.cpp:50-160, api_export.cpp:5-53, api_pack.cpp:31-76
 rns8_status check_plan_ctx_ws(const rns8_context& ctx, const rns8_plan& plan, const rns8_workspace& ws);
 rns8_status check_rns_operands(const rns8_context& ctx, const rns8_plan& plan, const rns8_matrix& A,
@@ -48,8 +44,7 @@ GemmArgs gemm_args(const rns8_plan& plan, const rns8_matrix& A, const rns8_matri
 ExportArgs export_args(const rns8_plan& plan, const rns8_matrix& C, void* dst, int64_t ld, uint32_t limbs,
                        ExportKind kind, uint32_t* status);
 ExportU8Args export_u8_args(const rns8_plan& plan, const rns8_matrix& C, uint8_t* dst, int64_t ld, uint16_t modulus);
-PackArgs pack_args(const rns8_matrix& m, const void* src, int64_t ld, bool is_signed, unsigned long long* max_out,
-                   unsigned long long* max_clear);
+PackArgs pack_args(const rns8_matrix& m, const void* src, int64_t ld, bool is_signed);
 PackU8Args pack_u8_args(const rns8_matrix& m, const uint8_t* src, int64_t ld, uint16_t modulus);
 
 // The launchers' own checks of these arguments (gemm_args_ok,

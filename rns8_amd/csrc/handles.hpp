@@ -13,6 +13,7 @@
 #include "host_copy.hpp"
 #include "kernels.hpp"
 #include "tables.hpp"
+#include "exact_axes.hpp"
 #include "exact_range.hpp"
 #include "wide_int.hpp"
 
@@ -94,29 +95,50 @@ struct rns8_matrix {
   int64_t plane_ld = 0;
   int64_t plane_pitch = 0;
   uint64_t plane_bytes = 0;
-  // exact-wide proofs: exact_prefix == 0 means no proof
+  // exact-wide proofs (reference exact_range.hpp): exact_prefix == 0 means
+  // no proof. The proof lies on the device, in one of two sets of
+  // proof_device (layout below): per-row and per-column axis records and 8
+  // words, the proof's bound in words 0..3. proof_kind says what set
+  // proof_set holds: native axes (a pack), carried axes (a GEMM result whose
+  // summaries were computed), or a lazy proof: the snapshot of a GEMM's
+  // operand axes (A's rows of kind lazy_rows, B's columns of kind lazy_cols,
+  // maxA in words 0..3, maxB in 4..7, inner dimension lazy_k), from which
+  // the result's own summaries are computed when a decision needs them. The
+  // other set is free: writers fill it and then make it current, so a
+  // refused call leaves the current proof as it was. exact_max is a bound
+  // the proof's bound never exceeds, exact unless exact_pending: a decision
+  // that it passes is the exact decision, and the device bound is read back
+  // (after proof_event, recorded by the last proof writer) when one needs it.
+  // Proof work is ordered on streams like the planes it describes.
+  enum class ProofKind : uint8_t { Native, Carried, Uniform, Lazy };
   mutable rns8x::I512 exact_max;
   uint32_t exact_prefix = 0;
-  std::vector<ExactAxis> exact_rows;
-  std::vector<ExactAxis> exact_cols;
-  // A proof left on the device: by a device-pointer pack (max |x| in word 0
-  // of the current slot) or by a GEMM of two such operands (their maxima in
-  // words 0 and 1; the exact bound is proof_k * [0] * [1]). While
-  // exact_pending is set, exact_max holds a worst case the exact value never
-  // exceeds, so a decision that the worst case passes is the exact decision;
-  // resolve_exact_proof reads the words back (after proof_event) when a
-  // decision needs the exact value. Exact-wide matrices own two slots of two
-  // words and the event from creation. Word 0 of the slot that is not current
-  // is zero (the writer of a new proof clears the old slot's word 0 in the
-  // same launch), so a pack's atomic maximum needs no clearing launch.
   mutable bool exact_pending = false;
-  bool pending_product = false;
-  uint64_t proof_k = 0;
-  unsigned long long* proof_device = nullptr;  // 2 slots x 2 words
-  uint32_t proof_slot = 0;
+  mutable ProofKind proof_kind = ProofKind::Native;
+  mutable uint32_t proof_set = 0;
+  uint32_t lazy_rows = 0, lazy_cols = 0;  // rns8x::xa::AxisKind of a lazy proof's snapshot
+  uint64_t lazy_k = 0;
+  // [words set 0 (8)] [words set 1 (8)] [set 0 rows] [set 0 cols] [set 1
+  // rows] [set 1 cols] [pack scratch: the per-tile partials of the rows,
+  // then of the columns (rns8x::native_partial_rows / _cols)]
+  uint8_t* proof_device = nullptr;
   hipEvent_t proof_event = nullptr;
-  unsigned long long* proof_words() const { return proof_device + 2 * proof_slot; }
-  unsigned long long* next_proof_words() const { return proof_device + 2 * (proof_slot ^ 1u); }
+  static uint64_t proof_bytes(int64_t rows, int64_t cols) {
+    return 128u + 2u * static_cast<uint64_t>(rows + cols) * sizeof(rns8x::xa::AxisRecord) +
+           static_cast<uint64_t>(rns8x::native_partial_rows(rows, cols) + rns8x::native_partial_cols(rows, cols)) *
+               sizeof(rns8x::xa::AxisPartial);
+  }
+  uint64_t* proof_words(uint32_t set) const { return reinterpret_cast<uint64_t*>(proof_device) + 8u * set; }
+  rns8x::xa::AxisRecord* proof_rows(uint32_t set) const {
+    return reinterpret_cast<rns8x::xa::AxisRecord*>(proof_device + 128) + (desc.rows + desc.cols) * set;
+  }
+  rns8x::xa::AxisRecord* proof_cols(uint32_t set) const { return proof_rows(set) + desc.rows; }
+  rns8x::xa::AxisPartial* row_partials() const {
+    return reinterpret_cast<rns8x::xa::AxisPartial*>(proof_rows(2));
+  }
+  rns8x::xa::AxisPartial* col_partials() const {
+    return row_partials() + rns8x::native_partial_rows(desc.rows, desc.cols);
+  }
   // cached staging buffers (export is logically const, reference
   // api_export.cpp:276-287 keeps the same kind of cache on the matrix)
   void* upload = nullptr;

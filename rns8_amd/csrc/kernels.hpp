@@ -10,6 +10,7 @@
 
 #include <cstdint>
 
+#include "exact_axes.hpp"
 #include "tables.hpp"
 
 namespace rns8x {
@@ -27,23 +28,34 @@ struct PackArgs {
   int64_t plane_pitch;
   uint32_t nplanes;
   NativeKind kind;
-  // when set: the same launch also writes max |x| over the matrix here
-  // (atomic max; the word must be zero on entry) and sets *max_clear to
-  // zero (a word no thread of the launch reads)
-  unsigned long long* max_out;
-  unsigned long long* max_clear;
 };
 hipError_t launch_pack_native(const PackArgs& args, const PlaneConsts& consts, hipStream_t stream);
-// out[0] = a[0], out[1] = b[0] and clear[0] = 0 on the stream: the
-// magnitude proofs of a GEMM's two operands, copied into its result's proof
-// words, and the word 0 of its previous proof slot cleared.
-hipError_t launch_proof_factors(const unsigned long long* a, const unsigned long long* b, unsigned long long* out,
-                                unsigned long long* clear, hipStream_t stream);
 
-// Maximum |x| over a rows x cols native matrix (row stride ld elements),
-// combined into *out with an atomic max. *out must be zero on entry.
-hipError_t launch_max_magnitude(const void* src, int64_t rows, int64_t cols, int64_t ld, NativeKind kind,
-                                unsigned long long* out, hipStream_t stream);
+// ---- exact-wide magnitude proofs (exact_axes.hip) ---------------------------
+// Per-row and per-column summaries of a rows x cols native operand (row
+// stride ld elements) into out_rows / out_cols, and its max |x| into
+// words[0] (words[1..7] zero). row_part / col_part: scratch for
+// native_partial_rows(rows, cols) and native_partial_cols(rows, cols)
+// partials (one per axis and 64 x 64 tile).
+hipError_t launch_native_axes(const void* src, int64_t rows, int64_t cols, int64_t ld, bool is_signed,
+                              xa::AxisPartial* row_part, xa::AxisPartial* col_part, xa::AxisRecord* out_rows,
+                              xa::AxisRecord* out_cols, uint64_t* words, hipStream_t stream);
+inline int64_t native_partial_rows(int64_t rows, int64_t cols) { return rows * ((cols + 63) / 64); }
+inline int64_t native_partial_cols(int64_t rows, int64_t cols) { return cols * ((rows + 63) / 64); }
+// The carried summaries of C = A x B (m x n, inner k): per-row and
+// per-column maxima and sums of the cell bounds from A's m row records and
+// B's n column records (kinds: xa::AxisKind; a uniform side reads no
+// records), and C's bound into out_words[0..3] (out_words[4..7] zero).
+// a_words / b_words: the operands' bounds, 4 words each.
+hipError_t launch_product_axes(const xa::AxisRecord* arows, uint32_t akind, const xa::AxisRecord* bcols,
+                               uint32_t bkind, const uint64_t* a_words, const uint64_t* b_words, int64_t m,
+                               int64_t n, uint64_t k, xa::AxisRecord* out_rows, xa::AxisRecord* out_cols,
+                               uint64_t* out_words, hipStream_t stream);
+// Copies m row records, n column records, a_words[0..3] into out_words[0..3]
+// and b_words[0..3] into out_words[4..7].
+hipError_t launch_proof_snapshot(const xa::AxisRecord* arows, const xa::AxisRecord* bcols, const uint64_t* a_words,
+                                 const uint64_t* b_words, int64_t m, int64_t n, xa::AxisRecord* out_rows,
+                                 xa::AxisRecord* out_cols, uint64_t* out_words, hipStream_t stream);
 
 struct PackU8Args {
   const uint8_t* src;

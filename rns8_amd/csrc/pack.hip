@@ -29,36 +29,14 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
 
-// Largest of a block's values, combined into *out by at most one atomic max,
-// skipped when the running maximum already covers it. Every thread of the
-// block must call it.
-__device__ __forceinline__ void block_max_to(unsigned long long best, unsigned long long* out) {
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    const unsigned long long other = __shfl_down(best, offset, 64);
-    best = other > best ? other : best;
-  }
-  __shared__ unsigned long long part[4];
-  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = best;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int w = 1; w < 4; ++w) best = part[w] > best ? part[w] : best;
-    best = part[0] > best ? part[0] : best;
-    if (best != 0 && __hip_atomic_load(out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < best) atomicMax(out, best);
-  }
-}
-
 // Grid-stride over 8-column chunks with 32-bit indices (the launchers reject
-// matrices with 2^32 chunks or more). With kMax the kernel also proves the
-// operand's magnitude for exact-wide matrices: max |x| over the valid
-// elements goes to *a.max_out (zero on entry), from the same loads. With
-// kStream the plane stores are non-temporal (see kStreamPackBytes).
-template <bool Signed, bool Vec, bool kMax, bool kStream>
+// matrices with 2^32 chunks or more). With kStream the plane stores are
+// non-temporal (see kStreamPackBytes).
+template <bool Signed, bool Vec, bool kStream>
 __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConsts pc, uint32_t chunks_per_row,
                                                           uint32_t total_chunks) {
   constexpr int kCols = 8;
   const uint64_t* const src = static_cast<const uint64_t*>(a.src);
-  unsigned long long best = 0;  // kMax: largest |x| this thread has seen
   for (uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x; ch < total_chunks; ch += gridDim.x * blockDim.x) {
     const uint32_t row = ch / chunks_per_row;
     const int64_t c0 = static_cast<int64_t>(ch - row * chunks_per_row) * kCols;
@@ -80,16 +58,6 @@ __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConst
         const uint64_t x = (c0 + e < a.cols) ? rp[c0 + e] : 0ull;  // padding packs as 0
         lo[e] = static_cast<uint32_t>(x);
         hi[e] = static_cast<uint32_t>(x >> 32);
-      }
-    }
-    if constexpr (kMax) {
-      // padding columns read as 0 and do not change the maximum
-#pragma unroll
-      for (int e = 0; e < kCols; ++e) {
-        const unsigned long long x = (static_cast<unsigned long long>(hi[e]) << 32) | lo[e];
-        // |INT64_MIN| = 2^63 is representable as an unsigned magnitude
-        const unsigned long long mag = (Signed && static_cast<int64_t>(x) < 0) ? 0ull - x : x;
-        best = mag > best ? mag : best;
       }
     }
     // When every element of the wave fits 32 bits (int32 for signed input,
@@ -148,10 +116,6 @@ __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConst
         *dst = w;
     }
   }
-  if constexpr (kMax) {
-    if (blockIdx.x == 0 && threadIdx.x == 0 && a.max_clear) *a.max_clear = 0ull;
-    block_max_to(best, a.max_out);
-  }
 }
 
 // Finite u8: x < 256, s = x + H < 2^9 is inside the range of the int32
@@ -186,42 +150,6 @@ __global__ __launch_bounds__(256) void pack_u8_kernel(PackU8Args a, ModulusConst
   }
 }
 
-// Maximum |x| of a rows x cols matrix: block (x, y) scans columns
-// [2048 x, 2048 x + 2048) of rows y, y + gridDim.y, ... (coalesced 8-byte
-// loads, no index division), reduces in the block and issues at most one
-// atomic, skipped when the running maximum already covers it.
-template <bool Signed>
-__global__ __launch_bounds__(256) void max_magnitude_kernel(const uint64_t* src, int64_t rows, int64_t cols,
-                                                            int64_t ld, unsigned long long* out) {
-  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 2048;
-  unsigned long long best = 0;
-  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
-    const uint64_t* const rp = src + r * ld;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int64_t c = c0 + e * 256 + threadIdx.x;
-      if (c < cols) {
-        const uint64_t x = rp[c];
-        // |INT64_MIN| = 2^63 is representable as an unsigned magnitude
-        const unsigned long long mag =
-            Signed ? (static_cast<int64_t>(x) < 0 ? 0ull - x : x) : static_cast<unsigned long long>(x);
-        best = mag > best ? mag : best;
-      }
-    }
-  }
-  block_max_to(best, out);
-}
-
-// Proof factors of a GEMM result whose operands both carry device-resident
-// maxima: out[0] = a[0], out[1] = b[0], and word 0 of the result's previous
-// proof slot cleared (one thread).
-__global__ void copy_proof_factors_kernel(const unsigned long long* a, const unsigned long long* b,
-                                          unsigned long long* out, unsigned long long* clear) {
-  out[0] = a[0];
-  out[1] = b[0];
-  clear[0] = 0ull;
-}
-
 unsigned grid_for(int64_t items) {
   const int64_t blocks = (items + 255) / 256;
   return static_cast<unsigned>(blocks < 16384 ? (blocks > 0 ? blocks : 1) : 16384);
@@ -247,56 +175,23 @@ hipError_t launch_pack_native(const PackArgs& a, const PlaneConsts& consts, hipS
   const uint32_t cpr = static_cast<uint32_t>(chunks_per_row), tot = static_cast<uint32_t>(total);
   const bool stream_out = static_cast<uint64_t>(a.nplanes) * static_cast<uint64_t>(a.rows * a.plane_ld) >=
                           kStreamPackBytes;
-  auto launch_as = [&](auto sgn, auto vc, auto mx, auto st) {
-    hipLaunchKernelGGL((pack_native_kernel<decltype(sgn)::value, decltype(vc)::value, decltype(mx)::value,
-                                           decltype(st)::value>),
-                       grid, dim3(256), 0, stream, a, consts, cpr, tot);
+  auto launch_as = [&](auto sgn, auto vc, auto st) {
+    hipLaunchKernelGGL((pack_native_kernel<decltype(sgn)::value, decltype(vc)::value, decltype(st)::value>), grid,
+                       dim3(256), 0, stream, a, consts, cpr, tot);
   };
   using T = std::true_type;
   using F = std::false_type;
-  auto launch = [&](auto sgn, auto vc, auto mx) {
+  auto launch = [&](auto sgn, auto vc) {
     if (stream_out)
-      launch_as(sgn, vc, mx, T{});
+      launch_as(sgn, vc, T{});
     else
-      launch_as(sgn, vc, mx, F{});
+      launch_as(sgn, vc, F{});
   };
-  const bool sgn = a.kind == NativeKind::I64, mx = a.max_out != nullptr;
-  if (sgn && vec && mx) launch(T{}, T{}, T{});
-  else if (sgn && vec) launch(T{}, T{}, F{});
-  else if (sgn && mx) launch(T{}, F{}, T{});
-  else if (sgn) launch(T{}, F{}, F{});
-  else if (vec && mx) launch(F{}, T{}, T{});
-  else if (vec) launch(F{}, T{}, F{});
-  else if (mx) launch(F{}, F{}, T{});
-  else launch(F{}, F{}, F{});
-  return hipGetLastError();
-}
-
-hipError_t launch_proof_factors(const unsigned long long* a, const unsigned long long* b, unsigned long long* out,
-                                unsigned long long* clear, hipStream_t stream) {
-  if (!a || !b || !out || !clear) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(copy_proof_factors_kernel, dim3(1), dim3(1), 0, stream, a, b, out, clear);
-  return hipGetLastError();
-}
-
-hipError_t launch_max_magnitude(const void* src, int64_t rows, int64_t cols, int64_t ld, NativeKind kind,
-                                unsigned long long* out, hipStream_t stream) {
-  if (!src || !out || rows <= 0 || cols <= 0 || ld < cols) return hipErrorInvalidValue;
-  // about 1024 blocks (four per CU, each scanning several rows): column
-  // chunks of 2048 across x, row strides across y
-  const int64_t gx = (cols + 2047) / 2048;
-  if (gx > 0x7FFFFFFFll) return hipErrorInvalidValue;
-  int64_t gy = 1024 / gx;
-  if (gy < 1) gy = 1;
-  if (gy > rows) gy = rows;
-  if (gy > 65535) gy = 65535;
-  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
-  if (kind == NativeKind::I64)
-    hipLaunchKernelGGL(max_magnitude_kernel<true>, grid, dim3(256), 0, stream, static_cast<const uint64_t*>(src), rows,
-                       cols, ld, out);
-  else
-    hipLaunchKernelGGL(max_magnitude_kernel<false>, grid, dim3(256), 0, stream, static_cast<const uint64_t*>(src),
-                       rows, cols, ld, out);
+  const bool sgn = a.kind == NativeKind::I64;
+  if (sgn && vec) launch(T{}, T{});
+  else if (sgn) launch(T{}, F{});
+  else if (vec) launch(F{}, T{});
+  else launch(F{}, F{});
   return hipGetLastError();
 }
 

@@ -369,7 +369,7 @@ extern "C" int LLVMFuzzerTestOneInput(const uint8_t* data, std::size_t size) {
                            A.m.desc.semantics == (sgn ? RNS8_EXACT_WIDE_SIGNED : RNS8_EXACT_WIDE_UNSIGNED);
       if (st == RNS8_SUCCESS && (!kind_ok || ld < A.m.desc.cols)) fail("pack accepted a wrong kind or ld < cols");
       if (st == RNS8_SUCCESS) {
-        const PackArgs a = pack_args(A.m, fake(9), ld, sgn, nullptr, nullptr);
+        const PackArgs a = pack_args(A.m, fake(9), ld, sgn);
         if (pack_args_ok(a)) {
           check_plane_reach(A.m, A.m.prefix, A.m.desc.rows, a.plane_ld, a.plane_pitch, "pack reach");
         } else if ((a.plane_ld / 8) * a.rows < (int64_t{1} << 32)) {

@@ -1,14 +1,19 @@
-"""The library's exact-wide admission math against unbounded integers (CPU).
+"""The library's exact-wide proof arithmetic against unbounded integers (CPU).
 
-tests/exact_range_check.cpp is built from rns8_amd/csrc/exact_range.hpp, the
-header librns8.so's rns8_gemm_rns uses to admit exact-wide products (reference
-src/core/exact_range.hpp:80-157). Each case here goes through it and through
-oracle/exact_range.py (Python integers, as unbounded as the reference's
-cpp_int); the bound, the status and every carried row/column summary must be
-equal. The cases include carried summaries far above 2^128, where a 256-bit
-product would wrap: two results of bound 2^128 multiplied with k = 1 have a
-bound of 2^256, which must be refused at every prefix, never wrapped to 0 and
-admitted.
+tests/exact_range_check.cpp is built from rns8_amd/csrc/exact_axes.hpp, the
+header the device kernels that prove exact-wide operands and admit their
+products are built from (exact_axes.hip; reference src/core/exact_range.hpp
+:34-157). Each case here goes through it and through oracle/exact_range.py
+(Python integers, as unbounded as the reference's cpp_int).
+
+The kernels compute in 256 bits: exactly for the summaries of 64-bit
+operands and their products, saturating at 2^256 - 1 where carried summaries
+make a candidate larger. So every bound and carried summary must equal
+min(the unbounded value, 2^256 - 1), and every status the unbounded one.
+The cases include carried summaries far above 2^128, where a wrapping 256-bit
+product would be wrong: two results of bound 2^128 multiplied with k = 1 have
+a bound of 2^256, which must be refused at every prefix, never wrapped to 0
+and admitted.
 """
 from __future__ import annotations
 
@@ -75,12 +80,19 @@ def _run(exe, cases):
     return out
 
 
+SAT = (1 << 256) - 1
+
+
+def _sat(v: int) -> int:
+    return min(v, SAT)
+
+
 def _expect(signed, m, n, k, product, A, B):
     bound, C = xr.gemm_bound(A, B, m, n, k)
     st = 0 if xr.fits(signed, bound, product) else 5  # RNS8_SUCCESS / RNS8_RANGE_ERROR
-    rows = [(a.max_magnitude, a.absolute_sum) for a in C.rows]
-    cols = [(b.max_magnitude, b.absolute_sum) for b in C.cols]
-    return st, bound, rows, cols
+    rows = [(_sat(a.max_magnitude), _sat(a.absolute_sum)) for a in C.rows]
+    cols = [(_sat(b.max_magnitude), _sat(b.absolute_sum)) for b in C.cols]
+    return st, _sat(bound), rows, cols
 
 
 def _check(exe, cases):
@@ -161,9 +173,9 @@ def test_large_carried_summaries(checker):
 
 def test_planted_wrap_is_detected(checker):
     """The comparison can see a wrap: with the multiplication reduced mod 2^256
-    (what the 256-bit version did) the chained 2^128 case would be admitted;
-    the oracle with the same planted reduction disagrees with the unbounded
-    one, so equality with the unbounded oracle above is a real check."""
+    instead of saturated, the chained 2^128 case would be admitted; the
+    oracle with the same planted reduction disagrees with the unbounded one,
+    so equality with the unbounded oracle above is a real check."""
     P20 = oracle.modulus_product(20)
     A = xr.native_operand([[-(1 << 63)] * 4])
     B = xr.native_operand([[-(1 << 63)]] * 4)
@@ -189,11 +201,13 @@ def _axis_tuple(a: xr.Axis):
 
 
 @pytest.mark.parametrize("signed", [True, False])
-@pytest.mark.parametrize("rows,cols", [(1, 1), (1, 7), (9, 1), (13, 40), (67, 5)])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (1, 7), (9, 1), (13, 40), (67, 5), (70, 130), (129, 65)])
 def test_native_summaries_match_unbounded(checker, signed, rows, cols):
-    """The summaries a host operand carries (native_exact_ranges: 128-bit
-    sums over row shards on three threads, merged per column) equal the
-    unbounded ones, with the int64 / uint64 extremes placed in every case."""
+    """The summaries of a 64-bit operand, computed in the device passes'
+    decomposition (per-tile partials of each row and column, extremes as
+    maxima of biased values; more than one 64 x 64 tile in the larger cases),
+    equal the unbounded ones, with the int64 / uint64 extremes placed in
+    every case."""
     rng = random.Random(rows * 1000 + cols + signed)
     lo, hi = (-(1 << 63), (1 << 63) - 1) if signed else (0, (1 << 64) - 1)
     x = _native(rng, rows, cols, lo, hi)
@@ -205,3 +219,29 @@ def test_native_summaries_match_unbounded(checker, signed, rows, cols):
     assert maximum == want.max_magnitude
     assert got_rows == [_axis_tuple(a) for a in want.rows]
     assert got_cols == [_axis_tuple(a) for a in want.cols]
+
+
+def test_saturating_word_arithmetic(checker):
+    """sat_mul / sat_add / min / max of the kernels on operands of every limb
+    count from 0 to 4 (products whose limb counts add up to 5 and 6 included,
+    where the carry out of the top limb decides), against Python integers."""
+    rng = random.Random(13)
+    pairs = []
+    for la in range(5):
+        for lb in range(5):
+            for _ in range(6):
+                a = rng.getrandbits(64 * la) if la else 0
+                b = rng.getrandbits(64 * lb) if lb else 0
+                if la and rng.random() < 0.5:
+                    a |= 1 << (64 * la - 1)  # top bit of the top limb set
+                if lb and rng.random() < 0.5:
+                    b |= (1 << (64 * lb)) - 1  # all ones
+                pairs.append((a, b))
+    pairs += [(SAT, 1), (SAT, 0), (1 << 128, (1 << 128) - 1), (1 << 128, 1 << 128), ((1 << 192) - 1, (1 << 64) + 1),
+              (1 << 255, 2), ((1 << 255) - 1, 2), (SAT, SAT)]
+    text = "".join(f"ops {_h(a)} {_h(b)}\n" for a, b in pairs)
+    res = subprocess.run([str(checker)], input=text, capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    for (a, b), line in zip(pairs, res.stdout.split("\n")):
+        got = [int(x, 16) for x in line.split()]
+        assert got == [_sat(a * b), _sat(a + b), min(a, b), max(a, b)], (hex(a), hex(b))

@@ -19,7 +19,7 @@ import pytest
 ROOT = Path(__file__).resolve().parents[1]
 CLANG = Path("/opt/rocm/llvm/bin/clang++")
 DEVICE_OBJS = [ROOT / "rns8_amd" / "_build" / f"{n}.o"
-               for n in ("export", "fused", "fused_skinny", "gemm", "pack", "skinny")]
+               for n in ("exact_axes", "export", "fused", "fused_skinny", "gemm", "pack", "skinny")]
 
 
 @pytest.fixture(scope="module")

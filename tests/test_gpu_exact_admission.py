@@ -15,14 +15,23 @@ scaled so D's bound lands just inside and just outside the range: the library
 must admit the first (and export D exactly) and refuse the second with
 RNS8_RANGE_ERROR. The A x B pairs make a different candidate decide C's cell
 bounds each time, so a dropped candidate, a wrong centre or a wrong remainder
-in the library enlarges C's carried bound and changes a decision.
+in the library enlarges C's carried bound and changes a decision. Every
+chain runs twice: packed from host arrays through the reference's entry
+points, and packed from device memory through the device-pointer packs and
+the stream entries. Both must take the reference's decisions: the operands'
+summaries are computed on the device either way, and D's decision (whose
+worst case k2 * bound(C) * max|E| never fits here) is the refined bound
+computed on the device from C's summaries.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
 import oracle
 import rns8_amd as r
 from oracle import exact_range as xr
+from rns8_amd import hip
 
 pytestmark = pytest.mark.gpu
 
@@ -53,9 +62,23 @@ def _oracle_bound(A, B, E):
     return bound
 
 
-def _run_chain(ctx, A, B, E, prefix, signed):
-    """Packs host A, B, E at `prefix`, runs C = A x B (must be admitted) and
-    D = C x E; returns (status of D, exported D or None)."""
+def _pack_device(ctx, matrix, arr, signed):
+    d = hip.malloc(arr.nbytes)
+    try:
+        hip.to_device(d, arr)
+        fn = r.lib().rns8_mi355x_pack_i64_device if signed else r.lib().rns8_mi355x_pack_u64_device
+        st = fn(ctx.ptr, matrix.ptr, ctypes.c_void_p(d), arr.shape[1], 0, None)
+        hip.synchronize()  # the source is freed next
+        return st
+    finally:
+        hip.free(d)
+
+
+def _run_chain(ctx, A, B, E, prefix, signed, device=False):
+    """Packs A, B, E at `prefix` (from host arrays through rns8_pack_*, or
+    from device memory through the device-pointer packs and the stream
+    entries), runs C = A x B (must be admitted) and D = C x E; returns
+    (status of D, exported D or None)."""
     sem = r.EXACT_WIDE_SIGNED if signed else r.EXACT_WIDE_UNSIGNED
     bk = r.BOUND_NONE
     dt = np.int64 if signed else np.uint64
@@ -67,9 +90,19 @@ def _run_chain(ctx, A, B, E, prefix, signed):
             for name, rows, cols in (("A", m, k1), ("B", k1, k2), ("C", m, k2), ("E", k2, n), ("D", m, n))}
     pack = r.pack_i64 if signed else r.pack_u64
     for version, (name, src) in enumerate((("A", A), ("B", B), ("E", E)), start=1):
-        r.check(pack(ctx, mats[name], np.array(src, dtype=dt), version), "pack " + name)
-    r.check(r.gemm_rns(ctx, p1, mats["A"], mats["B"], mats["C"], r.Workspace(ctx, p1)), "C = A x B")
-    st = r.gemm_rns(ctx, p2, mats["C"], mats["E"], mats["D"], r.Workspace(ctx, p2))
+        arr = np.array(src, dtype=object).astype(dt)
+        st = _pack_device(ctx, mats[name], arr, signed) if device else pack(ctx, mats[name], arr, version)
+        r.check(st, "pack " + name)
+    if device:
+        ws1, ws2 = r.Workspace(ctx, p1), r.Workspace(ctx, p2)
+        r.check(r.lib().rns8_mi355x_gemm_rns_async(ctx.ptr, p1.ptr, mats["A"].ptr, mats["B"].ptr, mats["C"].ptr,
+                                                   ws1.ptr, None), "C = A x B")
+        st = r.lib().rns8_mi355x_gemm_rns_async(ctx.ptr, p2.ptr, mats["C"].ptr, mats["E"].ptr, mats["D"].ptr,
+                                                ws2.ptr, None)
+        hip.synchronize()
+    else:
+        r.check(r.gemm_rns(ctx, p1, mats["A"], mats["B"], mats["C"], r.Workspace(ctx, p1)), "C = A x B")
+        st = r.gemm_rns(ctx, p2, mats["C"], mats["E"], mats["D"], r.Workspace(ctx, p2))
     if st != r.SUCCESS:
         return st, None
     L = _limbs(oracle.modulus_product(prefix))
@@ -79,7 +112,7 @@ def _run_chain(ctx, A, B, E, prefix, signed):
     return st, [[oracle.limbs_to_int(out[i, L * j:L * j + L], signed) for j in range(n)] for i in range(m)]
 
 
-def _threshold_pair(ctx, A, B, e_row, prefix, signed):
+def _threshold_pair(ctx, A, B, e_row, prefix, signed, device=False):
     """E = k2 copies of s * e_row with s the largest scale whose D bound still
     fits (step 0, admitted) and s + 1 (step 1, refused)."""
     P = oracle.modulus_product(prefix)
@@ -96,34 +129,37 @@ def _threshold_pair(ctx, A, B, e_row, prefix, signed):
         assert xr.fits(signed, bound, P) == (want == r.SUCCESS)
         for M in (A, B, E):
             assert xr.pack_admits(signed, M, P)
-        st, D = _run_chain(ctx, A, B, E, prefix, signed)
+        st, D = _run_chain(ctx, A, B, E, prefix, signed, device)
         assert st == want, (prefix, step, bound, P)
         if D is not None:
             assert D == _int_matmul(_int_matmul(A, B), E)
 
 
+@pytest.mark.parametrize("device", [False, True])
 @pytest.mark.parametrize("prefix", [17, 19, 20])
 @pytest.mark.parametrize("case", range(len(UNIQUE)))
-def test_signed_chain_threshold_each_candidate(gpu_ctx, prefix, case):
+def test_signed_chain_threshold_each_candidate(gpu_ctx, prefix, case, device):
     a, b, _ = UNIQUE[case]
     sa, sb = 1 << 59, -(1 << 59)  # |entries| <= 8 * 2^59 < 2^63
     A = [[sa * x for x in a]] * 3
     B = [[sb * y, sb * y] for y in b]  # equal columns: C's rows are one-signed, so D's bound is attained
-    _threshold_pair(gpu_ctx, A, B, [1, 1], prefix, True)
+    _threshold_pair(gpu_ctx, A, B, [1, 1], prefix, True, device)
 
 
+@pytest.mark.parametrize("device", [False, True])
 @pytest.mark.parametrize("prefix", [18, 20])
-def test_signed_chain_threshold_constant(gpu_ctx, prefix):
+def test_signed_chain_threshold_constant(gpu_ctx, prefix, device):
     A = [[-(1 << 62)] * 4] * 2
     B = [[(1 << 62) - 1] * 3] * 4
-    _threshold_pair(gpu_ctx, A, B, [1, 1], prefix, True)
+    _threshold_pair(gpu_ctx, A, B, [1, 1], prefix, True, device)
 
 
+@pytest.mark.parametrize("device", [False, True])
 @pytest.mark.parametrize("prefix", [17, 20])
-def test_unsigned_chain_threshold_one_signed_columns(gpu_ctx, prefix):
+def test_unsigned_chain_threshold_one_signed_columns(gpu_ctx, prefix, device):
     A = [[(1 << 63) + 5] * 4] * 2
     B = [[3 << 40, 1 << 40], [1 << 40, 2 << 40], [4 << 40, 1], [1 << 40, 9 << 40]]
-    _threshold_pair(gpu_ctx, A, B, [1, 1], prefix, False)
+    _threshold_pair(gpu_ctx, A, B, [1, 1], prefix, False, device)
 
 
 @pytest.mark.parametrize("signed", [True, False])

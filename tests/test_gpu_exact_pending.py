@@ -1,21 +1,22 @@
 """Exact-wide magnitude proofs left on the device by device-pointer packs.
 
 A device-pointer pack into an exact-wide matrix whose prefix admits every
-64-bit value (P > 2^64, prefix 9 and up) proves max |x| inside the pack launch
-and leaves it on the device; a GEMM of two such operands leaves its own proof
-there too (the operands' maxima copied into the result's proof words). The
-library decides admissions on a proof's worst case while that case passes,
-and reads the exact maxima back only when it does not, so every decision must
-equal the one made on exact values (checked here against
-oracle/exact_range.py on global-maximum operands, the proof a device pack
-carries) and every admitted result must export exactly:
+64-bit value (P > 2^64, prefix 9 and up) proves its operand on the device
+(per-row and per-column summaries and max |x|) without waiting for it; a
+GEMM of such operands leaves its own proof there too (a snapshot of its
+operands' summaries, from which its own are computed when needed). The host
+decides admissions on a worst case while that case passes, and computes the
+exact (refined) bound on the device when it does not, so every decision must
+equal the one made on exact values (checked here against oracle/exact_range.py;
+the operands are constant, so the refined and global-maximum bounds agree)
+and every admitted result must export exactly:
 
 * operands packed from device memory at prefix 20, their product exported to
   3 limbs against the brute-force product (the C4 path, never read back);
 * chains D = (A x B) x E with every operand device-packed, E scaled so D's
   exact bound lands one step inside (admitted, exact D) and one step outside
   (RNS8_RANGE_ERROR) the range; the worst case fails, so the decision needs
-  the read-back maxima;
+  the device bound;
 * the same chain after A is packed again with small values between the two
   GEMMs: C's proof must still be the one of the A it was computed from;
 * a grouped GEMM of device-packed operands.
@@ -167,9 +168,10 @@ def test_result_proof_survives_operand_repack(gpu_ctx, signed):
 @pytest.mark.parametrize("signed", [True, False])
 @pytest.mark.parametrize("large_packs", [1, 2])
 def test_repack_proves_only_the_new_maximum(gpu_ctx, signed, large_packs):
-    """Device packs of one matrix in a row: the proof words alternate between
-    two slots and the slot a pack takes must start from zero, so after packs
-    of the chain's large A and then of ones, C = A x B carries the maximum 1.
+    """Device packs of one matrix in a row: the proof alternates between two
+    sets and a pack's accumulators and maximum must start from zero, so after
+    packs of the chain's large A and then of ones, C = A x B carries the
+    maximum 1.
     At the scale one above the large-A threshold the chain is admitted only
     with that proof (a maximum carried over from an earlier pack would refuse
     it)."""
