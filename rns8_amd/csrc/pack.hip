@@ -9,24 +9,18 @@
 // path re-reads it once per plane, hip_backend_pack.inc:44-58). Eight columns
 // per thread (rather than 16) halve each thread's VALU chain, which lets the
 // residue arithmetic of some waves overlap the memory traffic of others
-// (measured 10% faster at 4096 x 4096, 9 planes). A plane with m = 256 needs
-// no arithmetic: its centered residue is the low byte of x read as int8.
-//
-// Residue of a 64-bit value without 64-bit division (tables.hpp): split u into
-// bytes, s = dot(lo bytes, 2^(8b) mod m) + dot(hi bytes, 2^(32+8b) mod m) + off
-// with two v_dot4_u32_u8 (s < 2^19), then the full-rate 24-bit quotient.
-// Signed inputs are biased by 2^63 (flip the top bit) and the bias is folded
-// into `off`, so int64 and uint64 share the same arithmetic.
+// (measured 10% faster at 4096 x 4096, 9 planes). The residue arithmetic is
+// pack_chunk.hpp's.
 #include <type_traits>
 
 #include "int_ops.hpp"
 #include "kernels.hpp"
+#include "pack_chunk.hpp"
 
 namespace rns8x {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v2i __attribute__((ext_vector_type(2)));
 typedef unsigned long long v2u64 __attribute__((ext_vector_type(2)));
 
 // Grid-stride over 8-column chunks with 32-bit indices (the launchers reject
@@ -60,61 +54,8 @@ __global__ __launch_bounds__(256) void pack_native_kernel(PackArgs a, PlaneConst
         hi[e] = static_cast<uint32_t>(x >> 32);
       }
     }
-    // When every element of the wave fits 32 bits (int32 for signed input,
-    // uint32 for unsigned), one byte dot product per residue covers it: u =
-    // x + 2^31 (signed) or x (unsigned) against the int32 reduction
-    // constants, whose s_max covers both offsets (off_u64 = H <= off_i32).
-    bool fits = true;
-#pragma unroll
-    for (int e = 0; e < kCols; ++e)
-      fits &= hi[e] == (Signed ? static_cast<uint32_t>(static_cast<int32_t>(lo[e]) >> 31) : 0u);
-    const bool narrow = __all(fits);
-    if (Signed) {
-#pragma unroll
-      for (int e = 0; e < kCols; ++e) {
-        hi[e] ^= 0x80000000u;
-        if (narrow) lo[e] ^= 0x80000000u;
-      }
-    }
-    int8_t* const out = a.planes + static_cast<int64_t>(row) * a.plane_ld + c0;
-    for (uint32_t p = 0; p < a.nplanes; ++p) {
-      const ModulusConsts mc = pc.mod[p];
-      v2i w;
-      if (mc.m == 256u) {
-        // x mod 256 is the low byte, and its centered value is that byte as
-        // int8 (the narrow path's bias 2^31 leaves the low byte alone)
-        w = v2i{static_cast<int>(pack_low_bytes(lo[0], lo[1], lo[2], lo[3])),
-                static_cast<int>(pack_low_bytes(lo[4], lo[5], lo[6], lo[7]))};
-      } else if (narrow) {
-        // the offsets less H: the dot product gives s - H (centered_byte)
-        const uint32_t off = (Signed ? mc.off_i32 : mc.off_u64) - mc.half;
-        const uint32_t h_sh = in_vgpr(mc.half << mc.q_shift), m_comp = 256u - mc.m;
-        uint32_t r[kCols];
-#pragma unroll
-        for (int e = 0; e < kCols; ++e)
-          r[e] = centered_byte(__builtin_amdgcn_udot4(lo[e], mc.pow_lo, off, false), mc.q_shift, h_sh, mc.q_recip,
-                               m_comp);
-        w = v2i{static_cast<int>(pack_low_bytes(r[0], r[1], r[2], r[3])),
-                static_cast<int>(pack_low_bytes(r[4], r[5], r[6], r[7]))};
-      } else {
-        const uint32_t off = (Signed ? mc.off_i64 : mc.off_u64) - mc.half;
-        const uint32_t h_sh = in_vgpr(mc.half << mc.pq_shift), m_comp = 256u - mc.m;
-        uint32_t r[kCols];
-#pragma unroll
-        for (int e = 0; e < kCols; ++e) {
-          const uint32_t t = __builtin_amdgcn_udot4(lo[e], mc.pow_lo, off, false);
-          r[e] = centered_byte(__builtin_amdgcn_udot4(hi[e], mc.pow_hi, t, false), mc.pq_shift, h_sh, mc.pq_recip,
-                               m_comp);
-        }
-        w = v2i{static_cast<int>(pack_low_bytes(r[0], r[1], r[2], r[3])),
-                static_cast<int>(pack_low_bytes(r[4], r[5], r[6], r[7]))};
-      }
-      v2i* const dst = reinterpret_cast<v2i*>(out + static_cast<int64_t>(p) * a.plane_pitch);
-      if constexpr (kStream)
-        __builtin_nontemporal_store(w, dst);
-      else
-        *dst = w;
-    }
+    pack_chunk8<Signed, kStream>(lo, hi, a.planes + static_cast<int64_t>(row) * a.plane_ld + c0, a.plane_pitch,
+                                 a.nplanes, pc, true);
   }
 }
 
@@ -150,11 +91,6 @@ __global__ __launch_bounds__(256) void pack_u8_kernel(PackU8Args a, ModulusConst
   }
 }
 
-unsigned grid_for(int64_t items) {
-  const int64_t blocks = (items + 255) / 256;
-  return static_cast<unsigned>(blocks < 16384 ? (blocks > 0 ? blocks : 1) : 16384);
-}
-
 // Packs whose planes exceed the 256 MB Infinity Cache store them
 // non-temporally. Ordinary stores leave that much dirty data in the cache,
 // and its write-back then competes with the next kernel's reads: an 8192 x
@@ -163,6 +99,11 @@ unsigned grid_for(int64_t items) {
 // one. Below the cache size ordinary stores win (4096^2 at 9 planes, 151 MB:
 // 50 us per pack against 62 us streaming), since the cache absorbs them.
 constexpr uint64_t kStreamPackBytes = uint64_t{256} << 20;
+
+unsigned grid_for(int64_t items) {
+  const int64_t blocks = (items + 255) / 256;
+  return static_cast<unsigned>(blocks < 16384 ? (blocks > 0 ? blocks : 1) : 16384);
+}
 
 }  // namespace
 
