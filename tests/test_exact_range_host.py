@@ -238,7 +238,9 @@ def test_saturating_word_arithmetic(checker):
                     b |= (1 << (64 * lb)) - 1  # all ones
                 pairs.append((a, b))
     pairs += [(SAT, 1), (SAT, 0), (1 << 128, (1 << 128) - 1), (1 << 128, 1 << 128), ((1 << 192) - 1, (1 << 64) + 1),
-              (1 << 255, 2), ((1 << 255) - 1, 2), (SAT, SAT)]
+              (1 << 255, 2), ((1 << 255) - 1, 2), (SAT, SAT),
+              # products whose only non-zero word above the low four is the top one, or the fifth
+              (1 << 224, 1 << 224), (1 << 255, 1 << 193), (1 << 192, 1 << 64), (1 << 160, 1 << 96)]
     text = "".join(f"ops {_h(a)} {_h(b)}\n" for a, b in pairs)
     res = subprocess.run([str(checker)], input=text, capture_output=True, text=True, timeout=120)
     assert res.returncode == 0, res.stderr
