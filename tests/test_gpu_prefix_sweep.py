@@ -41,19 +41,19 @@ def _run(ctx, sem, bk, A, B, prefix, bound=0, limbs=1):
     return plan, Cm
 
 
-@pytest.mark.parametrize("prefix", range(1, 21))
-def test_bounded_i64_every_prefix(gpu_ctx, prefix):
+def _sweep_i64(ctx, prefix, cols):
     P = oracle.modulus_product(prefix)
     bound = min((P - 1) // 2, 1 << 63)  # 2 * bound < P
     hi = min(bound, I64_MAX)
-    rng = np.random.default_rng(prefix)
-    A = rng.integers(-bound, hi, size=(M_ROWS, N_COLS), endpoint=True, dtype=np.int64)
+    rng = np.random.default_rng(prefix + 1000 * (cols != N_COLS))
+    A = rng.integers(-bound, hi, size=(M_ROWS, cols), endpoint=True, dtype=np.int64)
     A.reshape(-1)[:5] = [-bound, hi, 0, 1, -1]
-    plan, Cm = _run(gpu_ctx, r.BOUNDED_I64, r.BOUND_GLOBAL_MAX_ABS, A, _identity(N_COLS, np.int64), prefix, bound)
+    A[-1, -5:] = [-bound, hi, 0, 1, -1]
+    plan, Cm = _run(ctx, r.BOUNDED_I64, r.BOUND_GLOBAL_MAX_ABS, A, _identity(cols, np.int64), prefix, bound)
     planes = Cm.read_residues(prefix)
     np.testing.assert_array_equal(planes, oracle.pack_i64(A, prefix))
     out = np.zeros_like(A)
-    assert r.export_i64(gpu_ctx, plan, Cm, out) == r.SUCCESS
+    assert r.export_i64(ctx, plan, Cm, out) == r.SUCCESS
     np.testing.assert_array_equal(out, A)
     ost, oout = oracle.export_i64(planes, prefix, bound)
     assert ost == 0
@@ -61,20 +61,37 @@ def test_bounded_i64_every_prefix(gpu_ctx, prefix):
 
 
 @pytest.mark.parametrize("prefix", range(1, 21))
-def test_bounded_u64_every_prefix(gpu_ctx, prefix):
+def test_bounded_i64_every_prefix(gpu_ctx, prefix):
+    _sweep_i64(gpu_ctx, prefix, N_COLS)
+
+
+def _sweep_u64(ctx, prefix, cols):
     P = oracle.modulus_product(prefix)
     bound = min(P - 1, U64_MAX)
-    rng = np.random.default_rng(100 + prefix)
-    A = rng.integers(0, bound, size=(M_ROWS, N_COLS), endpoint=True, dtype=np.uint64)
+    rng = np.random.default_rng(100 + prefix + 1000 * (cols != N_COLS))
+    A = rng.integers(0, bound, size=(M_ROWS, cols), endpoint=True, dtype=np.uint64)
     A.reshape(-1)[:3] = [0, bound, 1]
-    plan, Cm = _run(gpu_ctx, r.BOUNDED_U64, r.BOUND_GLOBAL_MAX_UNSIGNED, A, _identity(N_COLS, np.uint64), prefix,
-                    bound)
+    A[-1, -3:] = [0, bound, 1]
+    plan, Cm = _run(ctx, r.BOUNDED_U64, r.BOUND_GLOBAL_MAX_UNSIGNED, A, _identity(cols, np.uint64), prefix, bound)
     out = np.zeros_like(A)
-    assert r.export_u64(gpu_ctx, plan, Cm, out) == r.SUCCESS
+    assert r.export_u64(ctx, plan, Cm, out) == r.SUCCESS
     np.testing.assert_array_equal(out, A)
     ost, oout = oracle.export_u64(Cm.read_residues(prefix), prefix, bound)
     assert ost == 0
     np.testing.assert_array_equal(out, oout)
+
+
+@pytest.mark.parametrize("prefix", range(1, 21))
+def test_bounded_u64_every_prefix(gpu_ctx, prefix):
+    _sweep_u64(gpu_ctx, prefix, N_COLS)
+
+
+# Results at least 256 columns wide export through the matrix-core form at
+# prefixes 9..11; 260 columns = one full 256-column chunk and a ragged one.
+@pytest.mark.parametrize("prefix", [9, 10, 11])
+@pytest.mark.parametrize("unsigned", [False, True])
+def test_bounded_64bit_wide_results(gpu_ctx, prefix, unsigned):
+    (_sweep_u64 if unsigned else _sweep_i64)(gpu_ctx, prefix, 260)
 
 
 def _wide_limbs(values, limbs):
