@@ -31,6 +31,27 @@ using namespace xa;
 
 constexpr int kTile = 64;
 constexpr int64_t kMaxGridY = 65535;
+// Elements of a half-tile run read per batch: the batch's LDS reads issue
+// together and one wait covers them (a rolled loop waits on every read).
+constexpr int kWalkBatch = 8;
+
+// f(elem(j)) for j in [j0, j1): whole 32-element runs (every run of a full
+// tile) in batches of kWalkBatch reads, ragged ones one element at a time.
+template <typename E, typename F>
+__device__ __forceinline__ void walk_run(int j0, int j1, E elem, F f) {
+  if (j1 - j0 == kTile / 2) {
+#pragma unroll 1
+    for (int b = 0; b < kTile / 2; b += kWalkBatch) {
+      u64 v[kWalkBatch];
+#pragma unroll
+      for (int e = 0; e < kWalkBatch; ++e) v[e] = elem(j0 + b + e);
+#pragma unroll
+      for (int e = 0; e < kWalkBatch; ++e) f(v[e]);
+    }
+  } else {
+    for (int j = j0; j < j1; ++j) f(elem(j));
+  }
+}
 
 // One pass over the 64 x 64 tiles of a rows x cols operand (row stride ld).
 // Block (x, y) takes tile column x and tile rows y, y + gridDim.y, ...; each
@@ -87,25 +108,23 @@ __global__ __launch_bounds__(256) void native_axes_pass(const uint64_t* __restri
     const int axes = by_row ? nr : nc, len = by_row ? nc : nr;
     const int j0 = half * 32, j1 = j0 + 32 < len ? j0 + 32 : len;
     AxisPartial p = empty_partial();
+    auto row_elem = [&](int j) { return (static_cast<u64>(tile_hi[lane][j]) << 32) | tile_lo[lane][j]; };
+    auto col_elem = [&](int j) { return (static_cast<u64>(tile_hi[j][lane]) << 32) | tile_lo[j][lane]; };
     if (lane < axes) {
       if (!Dev) {
         PartialAcc acc;
         if (by_row)
-          for (int j = j0; j < j1; ++j)
-            acc.add((static_cast<u64>(tile_hi[lane][j]) << 32) | tile_lo[lane][j], Signed);
+          walk_run(j0, j1, row_elem, [&](u64 x) { acc.add(x, Signed); });
         else
-          for (int j = j0; j < j1; ++j)
-            acc.add((static_cast<u64>(tile_hi[j][lane]) << 32) | tile_lo[j][lane], Signed);
+          walk_run(j0, j1, col_elem, [&](u64 x) { acc.add(x, Signed); });
         p = acc.partial();
       } else {
         const i128 centre = by_row ? record_centre(row_rec[r0 + lane]) : col_centre;
         DeviationAcc acc;
         if (by_row)
-          for (int j = j0; j < j1; ++j)
-            acc.add(deviation((static_cast<u64>(tile_hi[lane][j]) << 32) | tile_lo[lane][j], centre, Signed));
+          walk_run(j0, j1, row_elem, [&](u64 x) { acc.add(deviation(x, centre, Signed)); });
         else
-          for (int j = j0; j < j1; ++j)
-            acc.add(deviation((static_cast<u64>(tile_hi[j][lane]) << 32) | tile_lo[j][lane], centre, Signed));
+          walk_run(j0, j1, col_elem, [&](u64 x) { acc.add(deviation(x, centre, Signed)); });
         p.sum = acc.value();
       }
     }
