@@ -102,14 +102,14 @@ def settle(step, steps: int, sync) -> None:
 def attainable_mfma(achieved: float) -> dict:
     """The dense int8 MFMA rate this MI355X sustains with random operand bytes
     (the statistics of residue planes), measured after the timed region by
-    rns8_amd/probe/libmfma_probe.so: every CU issuing back-to-back
+    rns8_amd/probe/librns8_probe.so: every CU issuing back-to-back
     v_mfma_i32_32x32x32_i8 from registers, ~50 ms so the power controller has
     settled. The chip is power-limited on such operands, so this, not the
     5.0 POP/s peak, is the ceiling a GEMM on this data can approach; zero
     operands are measured beside it for the clock contrast."""
     import ctypes as C
 
-    lib = C.CDLL(str(ROOT / "rns8_amd" / "probe" / "libmfma_probe.so"))
+    lib = C.CDLL(str(ROOT / "rns8_amd" / "probe" / "librns8_probe.so"))
     fn = lib.rns8_probe_mfma_rate
     fn.restype = C.c_int
     fn.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]
@@ -128,6 +128,39 @@ def attainable_mfma(achieved: float) -> dict:
             "zero_operands": {"value": round(zt, 1), "clock_ghz": round(zg, 3)},
             "source": "rns8_amd/probe: back-to-back v_mfma_i32_32x32x32_i8 on every CU with random int8 "
                       "operands, measured after the timed region"}
+
+
+def attainable_streams(stages: dict) -> dict:
+    """For each memory-bound stage (name -> (bytes read, bytes written,
+    stage ms)), its algorithmic rate beside the rate a plain stream with the
+    same reads and writes reaches on this MI355X, measured after the timed
+    region by rns8_amd/probe/librns8_probe.so (16-byte loads and stores, each
+    wave instruction covering 1 KB; 20 back-to-back launches after 3 untimed
+    ones, so the inter-launch gaps count against the probe). Mixed read/write
+    streams run well below the 8 TB/s peak, and below it the further the
+    larger they are (the 256 MB Infinity Cache holds less of them), so this
+    is the ceiling a pack or an export of that size can approach."""
+    import ctypes as C
+
+    lib = C.CDLL(str(ROOT / "rns8_amd" / "probe" / "librns8_probe.so"))
+    fn = lib.rns8_probe_hbm_stream
+    fn.restype = C.c_int
+    fn.argtypes = [C.c_uint64, C.c_uint64, C.c_int, C.c_int, C.POINTER(C.c_double)]
+    out = {}
+    for name, (rd, wr, ms) in stages.items():
+        gbps = C.c_double()
+        rc = fn(rd // 16 * 16, wr // 16 * 16, 3, 20, C.byref(gbps))
+        if rc != 0:
+            raise RuntimeError(f"rns8_probe_hbm_stream failed with HIP error {rc}")
+        achieved = (rd + wr) / (ms * 1e-3) / 1e9
+        out[name] = {"read_bytes": rd, "write_bytes": wr, "achieved": round(achieved, 1),
+                     "attainable": round(gbps.value, 1), "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "frac_of_attainable": round(achieved / gbps.value, 4)}
+        log(f"[bench] stream probe {name}: {rd / 1e6:.1f} MB read + {wr / 1e6:.1f} MB written, stage "
+            f"{achieved:.0f} GB/s, plain stream {gbps.value:.0f} GB/s")
+    out["source"] = ("rns8_amd/probe: a streaming kernel reading and writing the stage's algorithmic bytes, "
+                     "measured after the timed region; stage rates from the stage pass's HIP events")
+    return out
 
 
 def log(msg: str) -> None:
@@ -393,6 +426,16 @@ def main() -> int:
     }
     if roofline["bound"] == "mfma":
         roofline["attainable"] = attainable_mfma(roofline["achieved"])
+    if not fused:
+        # the pack and export stages are memory-bound streams: report them
+        # against a plain stream of the same reads and writes (those moving
+        # at least 16 MB; smaller ones are launch-bound)
+        streams = {"pack_a": (8 * M * K, P * M * K, stage[0]), "pack_b": (8 * K * N, P * K * N, stage[1])}
+        if not tiled:
+            streams["export"] = (P * M * N, 8 * M * N, stage[3])
+        streams = {k: v for k, v in streams.items() if v[0] + v[1] >= (16 << 20)}
+        if streams:
+            result["stage_streams"] = attainable_streams(streams)
 
     if tiled:
         # exact in int64 (|C| <= 2^62): sampled rows of every tile row against numpy

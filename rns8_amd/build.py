@@ -3,9 +3,10 @@
 Device code is compiled for gfx950 only, with packed-FP32 instruction
 selection disabled. Objects go to rns8_amd/_build/, the shared library to
 rns8_amd/librns8.so. Every call rebuilds (a build is seconds per file).
-The matrix-core rate probe bench.py reports beside its roofline
-(rns8_amd/probe/mfma_probe.hip) is built into its own small library,
-rns8_amd/probe/libmfma_probe.so; the product library does not contain it.
+The rate probes bench.py reports beside its rooflines (the matrix-core rate,
+rns8_amd/probe/mfma_probe.hip, and the HBM stream rate,
+rns8_amd/probe/hbm_probe.hip) are built into their own small library,
+rns8_amd/probe/librns8_probe.so; the product library does not contain them.
 """
 from __future__ import annotations
 
@@ -20,8 +21,8 @@ PKG = ROOT / "rns8_amd"
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "librns8.so"
-PROBE_SRC = PKG / "probe" / "mfma_probe.hip"
-PROBE_LIB = PKG / "probe" / "libmfma_probe.so"
+PROBE_SRCS = [PKG / "probe" / "mfma_probe.hip", PKG / "probe" / "hbm_probe.hip"]
+PROBE_LIB = PKG / "probe" / "librns8_probe.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -61,7 +62,7 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, LIB)
     ptmp = PROBE_LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "-std=c++17", "-fPIC", "-shared", *DEVICE_FLAGS, str(PROBE_SRC), "-o", str(ptmp)]
+    cmd = [HIPCC, "-std=c++17", "-fPIC", "-shared", *DEVICE_FLAGS, *map(str, PROBE_SRCS), "-o", str(ptmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"probe build failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
