@@ -163,6 +163,16 @@ def attainable_streams(stages: dict) -> dict:
     return out
 
 
+def optional_probe(probe, *args):
+    """A rate probe's report, or None when it fails: the probes give context
+    beside the measured line and must not cost the line itself."""
+    try:
+        return probe(*args)
+    except (OSError, RuntimeError) as err:
+        log(f"[bench] probe {probe.__name__} failed, reported as null: {err}")
+        return None
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -425,7 +435,7 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if roofline["bound"] == "mfma":
-        roofline["attainable"] = attainable_mfma(roofline["achieved"])
+        roofline["attainable"] = optional_probe(attainable_mfma, roofline["achieved"])
     if not fused:
         # the pack and export stages are memory-bound streams: report them
         # against a plain stream of the same reads and writes (those moving
@@ -435,7 +445,7 @@ def main() -> int:
             streams["export"] = (P * M * N, 8 * M * N, stage[3])
         streams = {k: v for k, v in streams.items() if v[0] + v[1] >= (16 << 20)}
         if streams:
-            result["stage_streams"] = attainable_streams(streams)
+            result["stage_streams"] = optional_probe(attainable_streams, streams)
 
     if tiled:
         # exact in int64 (|C| <= 2^62): sampled rows of every tile row against numpy
@@ -642,7 +652,7 @@ def grouped_bench(args) -> int:
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None, "per_launch_ops": gemm_ops},
         "cpu_baseline": None,
     }
-    result["roofline"]["attainable"] = attainable_mfma(achieved)
+    result["roofline"]["attainable"] = optional_probe(attainable_mfma, achieved)
     print(json.dumps(result))
     for e in (start, stop):
         hip.event_destroy(e)
@@ -777,7 +787,7 @@ def finite_or_wide_bench(args) -> int:
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None, "per_launch_ops": ops * P},
         "cpu_baseline": None,
     }
-    result["roofline"]["attainable"] = attainable_mfma(achieved)
+    result["roofline"]["attainable"] = optional_probe(attainable_mfma, achieved)
     print(json.dumps(result))
     for e in (start, stop):
         hip.event_destroy(e)
