@@ -130,13 +130,34 @@ def attainable_mfma(achieved: float) -> dict:
                       "operands, measured after the timed region"}
 
 
+def back_to_back_ms(call, stream: int, n: int) -> float:
+    """Mean time of one `call` over n back-to-back calls on `stream` (HIP
+    events around them all, after 3 untimed calls)."""
+    from rns8_amd import hip
+
+    for _ in range(3):
+        call()
+    hip.stream_synchronize(stream)
+    e0, e1 = hip.event_create(), hip.event_create()
+    hip.event_record(e0, stream)
+    for _ in range(n):
+        call()
+    hip.event_record(e1, stream)
+    hip.stream_synchronize(stream)
+    ms = hip.event_elapsed_ms(e0, e1) / n
+    hip.event_destroy(e0)
+    hip.event_destroy(e1)
+    return ms
+
+
 def attainable_streams(stages: dict) -> dict:
-    """For each memory-bound stage (name -> (bytes read, bytes written,
-    stage ms)), its algorithmic rate beside the rate a plain stream with the
-    same reads and writes reaches on this MI355X, measured after the timed
-    region by rns8_amd/probe/librns8_probe.so (16-byte loads and stores, each
-    wave instruction covering 1 KB; 20 back-to-back launches after 3 untimed
-    ones, so the inter-launch gaps count against the probe). Mixed read/write
+    """For each memory-bound stage (name -> (bytes read, bytes written, ms
+    per launch over back-to-back launches)), its algorithmic rate beside the
+    rate a plain stream with the same reads and writes reaches on this
+    MI355X, measured right after by rns8_amd/probe/librns8_probe.so (16-byte
+    loads and stores, each wave instruction covering 1 KB; 20 back-to-back
+    launches after 3 untimed ones, so both sides carry the same inter-launch
+    gaps). Mixed read/write
     streams run well below the 8 TB/s peak, and below it the further the
     larger they are (the 256 MB Infinity Cache holds less of them), so this
     is the ceiling a pack or an export of that size can approach."""
@@ -153,13 +174,13 @@ def attainable_streams(stages: dict) -> dict:
         if rc != 0:
             raise RuntimeError(f"rns8_probe_hbm_stream failed with HIP error {rc}")
         achieved = (rd + wr) / (ms * 1e-3) / 1e9
-        out[name] = {"read_bytes": rd, "write_bytes": wr, "achieved": round(achieved, 1),
+        out[name] = {"read_bytes": rd, "write_bytes": wr, "ms": round(ms, 4), "achieved": round(achieved, 1),
                      "attainable": round(gbps.value, 1), "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "frac_of_attainable": round(achieved / gbps.value, 4)}
         log(f"[bench] stream probe {name}: {rd / 1e6:.1f} MB read + {wr / 1e6:.1f} MB written, stage "
-            f"{achieved:.0f} GB/s, plain stream {gbps.value:.0f} GB/s")
-    out["source"] = ("rns8_amd/probe: a streaming kernel reading and writing the stage's algorithmic bytes, "
-                     "measured after the timed region; stage rates from the stage pass's HIP events")
+            f"{1e3 * ms:.1f} us = {achieved:.0f} GB/s, plain stream {gbps.value:.0f} GB/s")
+    out["source"] = ("rns8_amd/probe: a streaming kernel reading and writing the stage's algorithmic bytes; both "
+                     "sides timed over back-to-back launches after the timed region")
     return out
 
 
@@ -439,11 +460,16 @@ def main() -> int:
     if not fused:
         # the pack and export stages are memory-bound streams: report them
         # against a plain stream of the same reads and writes (those moving
-        # at least 16 MB; smaller ones are launch-bound)
-        streams = {"pack_a": (8 * M * K, P * M * K, stage[0]), "pack_b": (8 * K * N, P * K * N, stage[1])}
+        # at least 16 MB; smaller ones are launch-bound), each timed as the
+        # probe is, over back-to-back launches after the stage pass (the
+        # stage pass's events add a few us to every stage, a tenth of a pack)
+        calls = {"pack_a": (8 * M * K, P * M * K, lambda: r.check(pack(ctx.ptr, Am.ptr, dA, K, 0, stream), "pack A")),
+                 "pack_b": (8 * K * N, P * K * N, lambda: r.check(pack(ctx.ptr, Bm.ptr, dB, N, 0, stream), "pack B"))}
         if not tiled:
-            streams["export"] = (P * M * N, 8 * M * N, stage[3])
-        streams = {k: v for k, v in streams.items() if v[0] + v[1] >= (16 << 20)}
+            calls["export"] = (P * M * N, 8 * M * N,
+                               lambda: r.check(export(ctx.ptr, plan.ptr, Cm.ptr, dC, N, dS, stream), "export"))
+        streams = {k: (rd, wr, back_to_back_ms(call, stream, args.steps)) for k, (rd, wr, call) in calls.items()
+                   if rd + wr >= (16 << 20)}
         if streams:
             result["stage_streams"] = optional_probe(attainable_streams, streams)
 
