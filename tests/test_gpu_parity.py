@@ -225,6 +225,42 @@ def test_exact_wide_signed_limbs_match_oracle(gpu_ctx, prefix, limbs):
         assert (out == 0xA5A5).all()
 
 
+@pytest.mark.parametrize("m_,n_", [(45, 530), (3, 257), (300, 1030)])
+@pytest.mark.parametrize("signed,prefix,limbs", [(True, 17, 3), (True, 18, 3), (True, 20, 4), (True, 20, 1),
+                                                 (True, 19, 5), (False, 18, 3), (False, 20, 2)])
+def test_exact_wide_export_multi_chunk_rows(gpu_ctx, m_, n_, signed, prefix, limbs):
+    """Exact-wide limb exports whose rows span several 256-cell chunks of the
+    matrix-core export (ragged last chunk), with a destination row stride
+    above the row length: every limb equals the oracle's export of the same
+    planes, RANGE_ERROR leaves the destination untouched."""
+    k_ = 24
+    sem = r.EXACT_WIDE_SIGNED if signed else r.EXACT_WIDE_UNSIGNED
+    A = rand_i64(31 + m_, (m_, k_)) if signed else rand_u64(31 + m_, (m_, k_))
+    B = rand_i64(32 + n_, (k_, n_)) if signed else rand_u64(32 + n_, (k_, n_))
+    desc = r.gemm_desc(sem, r.BOUND_NONE, m_, n_, k_, max_prefix=prefix, flags=r.PLAN_FORCE_FIXED_PREFIX)
+    plan = r.Plan(gpu_ctx, desc)
+    assert plan.prefix == prefix
+    mk = lambda rows, cols: r.Matrix(gpu_ctx, r.matrix_desc(rows, cols, sem, r.BOUND_NONE, prefix))
+    Am, Bm, Cm = mk(m_, k_), mk(k_, n_), mk(m_, n_)
+    ws = r.Workspace(gpu_ctx, plan)
+    pack = r.pack_i64 if signed else r.pack_u64
+    r.check(pack(gpu_ctx, Am, A, 1), "pack A")
+    r.check(pack(gpu_ctx, Bm, B, 2), "pack B")
+    r.check(r.gemm_rns(gpu_ctx, plan, Am, Bm, Cm, ws), "gemm")
+    planes = Cm.read_residues(prefix)
+    ld = n_ + 3
+    out = np.full((m_, ld * limbs), 0xA5A5, dtype=np.uint64)
+    export = r.export_exact_wide_signed_limbs if signed else r.export_exact_wide_unsigned_limbs
+    st = export(gpu_ctx, plan, Cm, out, limbs)
+    ost, oout = oracle.export_exact_wide(planes, prefix, limbs, signed)
+    assert st == ost
+    if st == 0:
+        np.testing.assert_array_equal(out[:, :n_ * limbs], oout)
+        assert (out[:, n_ * limbs:] == 0xA5A5).all()
+    else:
+        assert (out == 0xA5A5).all()
+
+
 def test_host_staging_multi_chunk_strided(gpu_ctx):
     """Host operands and results larger than one 16 MB staging chunk, with row
     strides above the row length on both sides (C = A x I round trip)."""
