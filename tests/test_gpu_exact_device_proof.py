@@ -11,7 +11,9 @@ the library takes with them against the same oracle:
 * native summaries of device-pointer and host-array packs, int64 and uint64
   over the full ranges with the extremes placed, strided sources, shapes of
   one to several 64 x 64 tiles with ragged edges, and prefixes above and
-  below 9 (where the pack reads max |x| back before writing);
+  below 9 (where the pack reads max |x| back before writing); and a 4100 x
+  2050 operand, whose 2145 tiles run two tile rows per block (checked
+  against numpy, in a range where int64 is exact);
 * the carried summaries of a product, computed lazily from the snapshot of
   its operands' summaries;
 * decisions at the range threshold that the worst case k * maxA * maxB
@@ -118,6 +120,38 @@ def test_native_summaries(gpu_ctx, signed, device, shape, ld_pad):
     assert bound == want.max_magnitude
     _axes_equal(R, want.rows, FIELDS)
     _axes_equal(C, want.cols, FIELDS)
+
+
+@pytest.mark.parametrize("signed", [True, False])
+def test_native_summaries_two_tiles_per_block(gpu_ctx, signed):
+    """Operands of at least 2048 tiles of 64 x 64 run the summary passes with
+    two tile rows per block, the second one's elements loaded into registers
+    while the first is summarized: 4100 x 2050 (65 x 33 tiles, an odd count
+    of tile rows, ragged last tiles) packed from a strided device source.
+    Values below 2^40 in magnitude keep the expected summaries exact in int64
+    (numpy); the full-range 128-bit sums are checked on the smaller shapes."""
+    rows, cols = 4100, 2050
+    rng = np.random.default_rng(77 + signed)
+    lo, hi = (-(1 << 40) + 1, (1 << 40) - 1) if signed else (0, (1 << 40) - 1)
+    x = rng.integers(lo, hi, size=(rows, cols), dtype=np.int64, endpoint=True)
+    # extremes at tile boundaries and in the last, ragged tiles
+    x[0, 0], x[63, 64], x[64, 63], x[-1, -1], x[4096, 2048] = lo, hi, lo, hi, lo
+    M = _matrix(gpu_ctx, signed, rows, cols, 20)
+    assert _pack(gpu_ctx, M, x if signed else x.astype(np.uint64), signed, True, ld=cols + 3) == r.SUCCESS
+    bound, kind, R, C = M.exact_proof(gpu_ctx)
+    assert kind == r.EXACT_AXES_NATIVE
+    assert bound == int(np.abs(x).max())
+    for axis, got in ((1, R), (0, C)):
+        mn, mx = x.min(axis=axis), x.max(axis=axis)
+        s = mn + mx
+        centre = np.expand_dims((s + (s < 0)) >> 1, axis)  # truncated toward zero
+        want = {"max_magnitude": np.abs(x).max(axis=axis), "absolute_sum": np.abs(x).sum(axis=axis),
+                "sum": x.sum(axis=axis), "minimum": mn, "maximum": mx,
+                "deviation_sum": np.abs(x - centre).sum(axis=axis)}
+        assert len(got) == len(mn)
+        for f, w in want.items():
+            g = np.array([a[f] for a in got], dtype=object)
+            assert (g == w.astype(object)).all(), (axis, f)
 
 
 @pytest.mark.parametrize("signed", [True, False])
