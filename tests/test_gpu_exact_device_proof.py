@@ -11,11 +11,12 @@ the library takes with them against the same oracle:
 * native summaries of device-pointer and host-array packs, int64 and uint64
   over the full ranges with the extremes placed, strided sources, shapes of
   one to several 64 x 64 tiles with ragged edges, and prefixes above and
-  below 9 (where the pack reads max |x| back before writing); and a 4100 x
-  2050 operand, whose 2145 tiles run two tile rows per block (checked
-  against numpy, in a range where int64 is exact);
+  below 9 (where the pack reads max |x| back before writing); and 4100 x
+  2050 and 140000 x 8 operands, whose tiles run two tile rows per block and
+  whose finishing launch strides over its axes (checked against numpy, in a
+  range where int64 is exact);
 * the carried summaries of a product, computed lazily from the snapshot of
-  its operands' summaries;
+  its operands' summaries, also over 33000 rows (more rows than waves);
 * decisions at the range threshold that the worst case k * maxA * maxB
   cannot take (it is refused on both sides): chained GEMMs whose operand is a
   lazy result, grouped GEMMs and exports, with the operand scaled to the
@@ -142,16 +143,55 @@ def test_native_summaries_two_tiles_per_block(gpu_ctx, signed):
     assert kind == r.EXACT_AXES_NATIVE
     assert bound == int(np.abs(x).max())
     for axis, got in ((1, R), (0, C)):
-        mn, mx = x.min(axis=axis), x.max(axis=axis)
-        s = mn + mx
-        centre = np.expand_dims((s + (s < 0)) >> 1, axis)  # truncated toward zero
-        want = {"max_magnitude": np.abs(x).max(axis=axis), "absolute_sum": np.abs(x).sum(axis=axis),
-                "sum": x.sum(axis=axis), "minimum": mn, "maximum": mx,
-                "deviation_sum": np.abs(x - centre).sum(axis=axis)}
-        assert len(got) == len(mn)
+        want = _numpy_summaries(x, axis)
+        assert len(got) == len(want["sum"])
         for f, w in want.items():
             g = np.array([a[f] for a in got], dtype=object)
             assert (g == w.astype(object)).all(), (axis, f)
+
+
+def _numpy_summaries(x, axis):
+    """The per-axis summaries of an int64 array whose sums stay in int64."""
+    mn, mx = x.min(axis=axis), x.max(axis=axis)
+    s = mn + mx
+    centre = np.expand_dims((s + (s < 0)) >> 1, axis)  # truncated toward zero
+    return {"max_magnitude": np.abs(x).max(axis=axis), "absolute_sum": np.abs(x).sum(axis=axis),
+            "sum": x.sum(axis=axis), "minimum": mn, "maximum": mx, "deviation_sum": np.abs(x - centre).sum(axis=axis)}
+
+
+@pytest.mark.parametrize("signed", [True, False])
+def test_proof_launches_past_one_grid(gpu_ctx, signed):
+    """Launch shapes whose grids stride: the finishing launch over more than
+    131072 axes (a 140000 x 8 operand, whose 2188 tile rows also run two per
+    block), and the product summaries over more than 32768 rows (a 33000 x 2
+    result, against the oracle's cell bounds)."""
+    ctx = gpu_ctx
+    lo, hi = (-(1 << 30) + 1, (1 << 30) - 1) if signed else (0, (1 << 30) - 1)
+    rng = np.random.default_rng(91 + signed)
+    x = rng.integers(lo, hi, size=(140000, 8), dtype=np.int64, endpoint=True)
+    x[0, 0], x[-1, -1], x[70000, 3] = lo, hi, hi
+    M = _matrix(ctx, signed, *x.shape, 20)
+    assert _pack(ctx, M, x if signed else x.astype(np.uint64), signed, True) == r.SUCCESS
+    bound, kind, R, C = M.exact_proof(ctx)
+    assert kind == r.EXACT_AXES_NATIVE and bound == int(np.abs(x).max())
+    for axis, got in ((1, R), (0, C)):
+        for f, w in _numpy_summaries(x, axis).items():
+            assert (np.array([a[f] for a in got], dtype=object) == w.astype(object)).all(), (axis, f)
+
+    m, k, n, prefix = 33000, 8, 2, 20
+    A = [[int(v) for v in row] for row in rng.integers(lo, hi, size=(m, k), dtype=np.int64, endpoint=True)]
+    B = [[int(v) for v in row] for row in rng.integers(lo, hi, size=(k, n), dtype=np.int64, endpoint=True)]
+    Am, Bm, Cm = _matrix(ctx, signed, m, k, prefix), _matrix(ctx, signed, k, n, prefix), _matrix(ctx, signed, m, n, prefix)
+    assert _pack(ctx, Am, A, signed, True) == r.SUCCESS
+    assert _pack(ctx, Bm, B, signed, True) == r.SUCCESS
+    plan = _plan(ctx, signed, m, n, k, prefix)
+    r.check(_async_gemm(ctx, plan, Am, Bm, Cm, r.Workspace(ctx, plan)), "gemm")
+    bound, kind, R, C = Cm.exact_proof(ctx)
+    want_bound, want = xr.gemm_bound(xr.native_operand(A), xr.native_operand(B), m, n, k)
+    assert kind == r.EXACT_AXES_CARRIED
+    assert bound == want_bound
+    _axes_equal(R, want.rows, ("max_magnitude", "absolute_sum"))
+    _axes_equal(C, want.cols, ("max_magnitude", "absolute_sum"))
 
 
 @pytest.mark.parametrize("signed", [True, False])
