@@ -15,9 +15,12 @@ operands, finite-field / finite-ring oneshots, the exact-wide path, and
 exact-wide chains D = (A x B) x E whose second product's admission (the
 refined bound from C's carried summaries, reference exact_range.hpp,
 restated in oracle/exact_range.py) falls on either side of the range, packed
-from host arrays or from device memory.
+from host arrays or from device memory; per-tile bound plans (true tile
+maxima, or one lowered by one); grouped GEMMs of 2-40 tasks (bounded and
+finite); and the device-pointer packs, stream GEMM and device export.
 
-RNS8_SWEEP_CASES sets the number of cases (default 160).
+RNS8_SWEEP_CASES sets the number of cases (default 160), RNS8_SWEEP_BASE the
+first seed (default 0).
 """
 import ctypes
 import os
@@ -33,6 +36,7 @@ from rns8_amd import hip, inputs
 pytestmark = pytest.mark.gpu
 
 CASES = int(os.environ.get("RNS8_SWEEP_CASES", "160"))
+BASE = int(os.environ.get("RNS8_SWEEP_BASE", "0"))
 EDGES = [1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 513]
 I64_MIN = np.iinfo(np.int64).min
 I64_MAX = np.iinfo(np.int64).max
@@ -337,12 +341,188 @@ def _chain_case(ctx, rng, seed):
     assert got == _int_matmul(_int_matmul(A, B), E), label
 
 
+SENTINEL = -91
+
+
+def _tiled_case(ctx, rng, seed):
+    """Per-tile bounds: A's rows and B's columns get their own magnitudes in
+    blocks, so tiles select different prefixes; the bounds are the tiles'
+    true maxima, or one of them one below it (a RANGE_ERROR the oracle's
+    tiled export also reports)."""
+    signed = rng.random() < 0.6
+    m, n = _dim(rng, 900), _dim(rng, 900)
+    k = int(rng.integers(1, 25))
+    tile_m, tile_n = (int(rng.choice([64, 128, 256, 512])) for _ in range(2))
+    block = int(rng.choice([16, 64, 100]))
+    rb = np.repeat(rng.integers(1, 29, size=-(-m // block)), block)[:m]
+    cb = np.repeat(rng.integers(1, 29, size=-(-n // block)), block)[:n]
+    A = rng.integers(0, 1 << 28, size=(m, k)) >> (28 - rb[:, None])
+    B = rng.integers(0, 1 << 28, size=(k, n)) >> (28 - cb[None, :])
+    if signed:
+        A = A * np.where(rng.random((m, k)) < 0.5, -1, 1)
+    dt = np.int64 if signed else np.uint64
+    A, B = A.astype(dt), B.astype(dt)
+    exact = A @ B  # |C| < 24 * 2^56: exact in 64 bits
+    mag = np.abs(exact) if signed else exact
+    rows = np.maximum.reduceat(mag, np.arange(0, m, tile_m), axis=0)
+    bounds = [int(x) for x in np.maximum.reduceat(rows, np.arange(0, n, tile_n), axis=1).reshape(-1)]
+    lowered = rng.random() < 0.15 and max(bounds) > 0
+    if lowered:
+        t = int(rng.choice([i for i, b in enumerate(bounds) if b > 0]))
+        bounds[t] -= 1
+    label = (f"tiled {'i64' if signed else 'u64'} {m}x{n}x{k} tiles {tile_m}x{tile_n} block {block}"
+             f" lowered={lowered}")
+    print(f"[sweep {seed}] {label}", flush=True)
+    sem = r.BOUNDED_I64 if signed else r.BOUNDED_U64
+    bk = r.abi.BOUND_PER_TILE_MAX_ABS if signed else r.abi.BOUND_PER_TILE_MAX_UNSIGNED
+    desc = r.gemm_desc(sem, bk, m, n, k, max_prefix=9, tile_m=tile_m, tile_n=tile_n, tile_bounds=bounds)
+    plan = r.Plan(ctx, desc)
+    sp = plan.prefix
+    st, entries, summary = oracle.tile_schedule(signed, m, n, tile_m, tile_n, bounds, 9, 0)
+    assert st == 0 and summary.max_selected == sp, label
+    mk = lambda rows_, cols_: r.Matrix(ctx, r.matrix_desc(rows_, cols_, sem, bk, sp, tile_m=tile_m, tile_n=tile_n))
+    Am, Bm, Cm = mk(m, k), mk(k, n), mk(m, n)
+    pack = r.pack_i64 if signed else r.pack_u64
+    r.check(pack(ctx, Am, A, 1), "pack A")
+    r.check(pack(ctx, Bm, B, 2), "pack B")
+    ptr, _, pitch, count = Cm.planes()
+    hip.memset(ptr, SENTINEL & 0xFF, pitch * count)
+    hip.synchronize()
+    r.check(r.gemm_rns(ctx, plan, Am, Bm, Cm, r.Workspace(ctx, plan)), "gemm")
+    pack_ref = oracle.pack_i64 if signed else oracle.pack_u64
+    Cp = oracle.gemm_rns_tiled(pack_ref(A, sp), pack_ref(B, sp), np.full((sp, m, n), SENTINEL, dtype=np.int8),
+                               entries)
+    np.testing.assert_array_equal(Cm.read_residues(sp), Cp, err_msg=label)
+    out = np.full((m, n), 77, dtype=dt)
+    est = (r.export_i64 if signed else r.export_u64)(ctx, plan, Cm, out)
+    ost, oout = oracle.export_tiled(Cp, tile_m, tile_n, entries, bounds, signed)
+    assert est == ost == (r.RANGE_ERROR if lowered else r.SUCCESS), label
+    if est == r.SUCCESS:
+        np.testing.assert_array_equal(out, oout, err_msg=label)
+        np.testing.assert_array_equal(out, exact, err_msg=label)
+    else:
+        assert (out == 77).all(), label
+
+
+def _grouped_case(ctx, rng, seed):
+    """A group of same-shape tasks in one launch: every task's planes equal
+    the oracle's (bounded) or the exact modular product (finite)."""
+    kind = str(rng.choice(["i64", "u64", "field", "ring"]))
+    count = int(rng.integers(2, 41))
+    m, n = _dim(rng, 400), _dim(rng, 400)
+    k = max(1, min(_depth(rng, m, n), 8_000_000 // max(1, m * n * count)))
+    label = f"grouped {kind} x{count} {m}x{n}x{k}"
+    print(f"[sweep {seed}] {label}", flush=True)
+    if kind in ("field", "ring"):
+        field = kind == "field"
+        modulus = int(rng.choice([2, 13, 251])) if field else int(rng.integers(2, 257))
+        sem = r.FINITE_FIELD_U8 if field else r.FINITE_RING_U8
+        plan = r.Plan(ctx, r.gemm_desc(sem, r.BOUND_NONE, m, n, k, finite_modulus=modulus))
+        mk = lambda rows, cols: r.Matrix(ctx, r.matrix_desc(rows, cols, sem, r.BOUND_NONE, 0))
+        ops = [(inputs.bytes_below(seed * 100 + 2 * i, (m, k), 256), inputs.bytes_below(seed * 100 + 2 * i + 1,
+                                                                                        (k, n), 256))
+               for i in range(count)]
+        tasks = [(mk(m, k), mk(k, n), mk(m, n), r.Workspace(ctx, plan)) for _ in range(count)]
+        for i, ((A, B), (Am, Bm, _, _)) in enumerate(zip(ops, tasks)):
+            r.check(r.pack_finite_u8(ctx, Am, modulus, A, 2 * i + 1), "pack A")
+            r.check(r.pack_finite_u8(ctx, Bm, modulus, B, 2 * i + 2), "pack B")
+        r.check(r.gemm_finite_u8_grouped(ctx, plan, modulus, tasks), label)
+        for (A, B), (_, _, Cm, _) in zip(ops, tasks):
+            out = np.zeros((m, n), dtype=np.uint8)
+            r.check(r.export_finite_u8(ctx, plan, modulus, Cm, out), "export")
+            want = ((A.astype(np.int64) @ B.astype(np.int64)) % modulus).astype(np.uint8)
+            np.testing.assert_array_equal(out, want, err_msg=label)
+        return
+    signed = kind == "i64"
+    kb = max(1, int(k).bit_length())
+    bits = int(rng.integers(1, max(1, (62 - kb) // 2) + 1))
+    sem = r.BOUNDED_I64 if signed else r.BOUNDED_U64
+    bk = r.BOUND_GLOBAL_MAX_ABS if signed else r.BOUND_GLOBAL_MAX_UNSIGNED
+    bound = (k << (2 * bits)) if signed else k * ((1 << bits) - 1) ** 2
+    plan = r.Plan(ctx, r.gemm_desc(sem, bk, m, n, k, bound=bound))
+    p = plan.prefix
+    mk = lambda rows, cols: r.Matrix(ctx, r.matrix_desc(rows, cols, sem, bk, p))
+    draw = _signed_values if signed else _unsigned_values
+    ops = [(draw(rng, seed * 100 + 2 * i, (m, k), bits), draw(rng, seed * 100 + 2 * i + 1, (k, n), bits))
+           for i in range(count)]
+    tasks = [(mk(m, k), mk(k, n), mk(m, n), r.Workspace(ctx, plan)) for _ in range(count)]
+    pack = r.pack_i64 if signed else r.pack_u64
+    for i, ((A, B), (Am, Bm, _, _)) in enumerate(zip(ops, tasks)):
+        r.check(pack(ctx, Am, A, 2 * i + 1), "pack A")
+        r.check(pack(ctx, Bm, B, 2 * i + 2), "pack B")
+    r.check(r.gemm_rns_grouped(ctx, plan, tasks), label)
+    pack_ref = oracle.pack_i64 if signed else oracle.pack_u64
+    for (A, B), (_, _, Cm, _) in zip(ops, tasks):
+        want = oracle.gemm_rns(pack_ref(A, p), pack_ref(B, p), p)
+        np.testing.assert_array_equal(Cm.read_residues(p), want, err_msg=label)
+
+
+def _device_case(ctx, rng, seed):
+    """Device-pointer packs (strided sources), the stream GEMM entry and the
+    device export (status word on the device) against the oracle."""
+    signed = rng.random() < 0.6
+    m, n = _dim(rng, 700), _dim(rng, 700)
+    k = _depth(rng, m, n)
+    kb = max(1, int(k).bit_length())
+    bits = int(rng.integers(1, max(1, (62 - kb) // 2) + 1))
+    draw = _signed_values if signed else _unsigned_values
+    A, B = draw(rng, seed * 2 + 1, (m, k), bits), draw(rng, seed * 2 + 2, (k, n), bits)
+    true_bound = (k << (2 * bits)) if signed else k * ((1 << bits) - 1) ** 2
+    bound = max(1, true_bound >> int(rng.integers(4, 40))) if rng.random() < 0.12 else true_bound
+    sem = r.BOUNDED_I64 if signed else r.BOUNDED_U64
+    bk = r.BOUND_GLOBAL_MAX_ABS if signed else r.BOUND_GLOBAL_MAX_UNSIGNED
+    plan = r.Plan(ctx, r.gemm_desc(sem, bk, m, n, k, bound=bound))
+    p = plan.prefix
+    label = f"device {'i64' if signed else 'u64'} {m}x{n}x{k} bits={bits} bound={bound} prefix={p}"
+    print(f"[sweep {seed}] {label}", flush=True)
+    mk = lambda rows, cols: r.Matrix(ctx, r.matrix_desc(rows, cols, sem, bk, p))
+    Am, Bm, Cm = mk(m, k), mk(k, n), mk(m, n)
+    ws = r.Workspace(ctx, plan)
+    L = r.lib()
+    pack = L.rns8_mi355x_pack_i64_device if signed else L.rns8_mi355x_pack_u64_device
+    ptrs = []
+    try:
+        for mat, src in ((Am, A), (Bm, B)):
+            full, ld = _strided(rng, src)
+            d = hip.malloc(max(full.nbytes, 16))
+            ptrs.append(d)
+            hip.to_device(d, np.ascontiguousarray(full))
+            r.check(pack(ctx.ptr, mat.ptr, ctypes.c_void_p(d), ld, 0, None), "device pack")
+        r.check(L.rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, None), "gemm")
+        ld_out = n + int(rng.integers(0, 3))
+        dt = np.int64 if signed else np.uint64
+        out = np.full((m, ld_out), 0x77, dtype=dt)
+        d_out = hip.malloc(max(out.nbytes, 16))
+        d_status = hip.malloc(16)
+        ptrs += [d_out, d_status]
+        hip.to_device(d_out, out)
+        hip.memset(d_status, 0, 16)
+        export = L.rns8_mi355x_export_i64_device if signed else L.rns8_mi355x_export_u64_device
+        r.check(export(ctx.ptr, plan.ptr, Cm.ptr, ctypes.c_void_p(d_out), ld_out, ctypes.c_void_p(d_status), None),
+                "device export")
+        hip.synchronize()
+        status = np.zeros(4, dtype=np.uint32)
+        hip.from_device(status, d_status)
+        hip.from_device(out, d_out)
+    finally:
+        for d in ptrs:
+            hip.free(d)
+    pack_ref = oracle.pack_i64 if signed else oracle.pack_u64
+    want_planes = oracle.gemm_rns(pack_ref(A, p), pack_ref(B, p), p)
+    np.testing.assert_array_equal(Cm.read_residues(p), want_planes, err_msg=label)
+    ost, oout = (oracle.export_i64 if signed else oracle.export_u64)(want_planes, p, bound)
+    assert (status[0] == 0) == (ost == r.SUCCESS), label
+    if ost == r.SUCCESS:
+        np.testing.assert_array_equal(out[:, :n], oout, err_msg=label)
+        assert (out[:, n:] == 0x77).all(), label
+
+
 ROUTES = ["resident_i64", "resident_u64", "oneshot_i64", "oneshot_u64", "fused_i64", "fused_u64", "finite",
-          "wide", "chain"]
-WEIGHTS = [0.18, 0.1, 0.08, 0.07, 0.11, 0.09, 0.1, 0.14, 0.13]
+          "wide", "chain", "tiled", "grouped", "device"]
+WEIGHTS = [0.13, 0.07, 0.06, 0.05, 0.08, 0.07, 0.07, 0.1, 0.1, 0.09, 0.09, 0.09]
 
 
-@pytest.mark.parametrize("seed", range(CASES))
+@pytest.mark.parametrize("seed", range(BASE, BASE + CASES))
 def test_random_case(gpu_ctx, seed):
     rng = np.random.default_rng(0x5EED0000 + seed)
     route = ROUTES[int(rng.choice(len(ROUTES), p=WEIGHTS))]
@@ -352,6 +532,12 @@ def test_random_case(gpu_ctx, seed):
         _wide_case(gpu_ctx, rng, seed)
     elif route == "chain":
         _chain_case(gpu_ctx, rng, seed)
+    elif route == "tiled":
+        _tiled_case(gpu_ctx, rng, seed)
+    elif route == "grouped":
+        _grouped_case(gpu_ctx, rng, seed)
+    elif route == "device":
+        _device_case(gpu_ctx, rng, seed)
     else:
         kind, sem = route.split("_")
         _bounded_case(gpu_ctx, rng, seed, sem == "i64", kind)
