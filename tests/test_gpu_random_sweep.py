@@ -3,7 +3,8 @@
 Each case draws its own route, semantics, shape, value range, bound, prefix
 and row strides from a seeded generator, so the cases land on combinations
 the hand-written parity tests do not name: ragged tile edges next to the 128
-and 256 tile sizes, K just past the 64-deep step and past 65536 (several
+and 256 tile sizes, outputs up to 4500 x 4500 (the 256 x 256 tile
+configuration) with a short K, K just past the 64-deep step and past 65536 (several
 accumulation blocks or K slices), forced prefixes above what the bound needs,
 false bounds (the export must then report what the oracle reports), strided
 host sources and both exact-wide signednesses. Every comparison is bit-exact:
@@ -97,9 +98,18 @@ def _strided(rng, a):
     return full, ld
 
 
+def _large(rng):
+    """A large output (the 256 x 256 tile configuration) with a short K."""
+    m, n = int(rng.integers(1000, 4500)), int(rng.integers(1000, 4500))
+    return m, n, int(rng.integers(1, max(2, 30_000_000 // (m * n)) + 1))
+
+
 def _bounded_case(ctx, rng, seed, signed, route):
-    m, n = _dim(rng, 700), _dim(rng, 700)
-    k = _depth(rng, m, n)
+    if route != "fused" and rng.random() < 0.1:
+        m, n, k = _large(rng)
+    else:
+        m, n = _dim(rng, 700), _dim(rng, 700)
+        k = _depth(rng, m, n)
     kb = max(1, int(k).bit_length())
     # value bits so that k * 2^(2 bits) stays below 2^62
     top = max(1, (62 - kb) // 2)
@@ -461,8 +471,11 @@ def _device_case(ctx, rng, seed):
     """Device-pointer packs (strided sources), the stream GEMM entry and the
     device export (status word on the device) against the oracle."""
     signed = rng.random() < 0.6
-    m, n = _dim(rng, 700), _dim(rng, 700)
-    k = _depth(rng, m, n)
+    if rng.random() < 0.15:
+        m, n, k = _large(rng)
+    else:
+        m, n = _dim(rng, 700), _dim(rng, 700)
+        k = _depth(rng, m, n)
     kb = max(1, int(k).bit_length())
     bits = int(rng.integers(1, max(1, (62 - kb) // 2) + 1))
     draw = _signed_values if signed else _unsigned_values
