@@ -10,8 +10,9 @@ false bounds (the export must then report what the oracle reports), strided
 host sources and both exact-wide signednesses. Every comparison is bit-exact:
 residue planes byte for byte, exports value for value and status for status.
 
-Routes: resident pack -> GEMM -> export through host arrays (int64, uint64),
-the host-array oneshot entries, the fused native-input GEMM on device
+Routes: resident pack -> GEMM -> export through host arrays (int64, uint64;
+the GEMM through rns8_gemm_rns or the entry that allocates nothing), the
+host-array oneshot entries, the fused native-input GEMM on device
 operands, finite-field / finite-ring oneshots, the exact-wide path, and
 exact-wide chains D = (A x B) x E whose second product's admission (the
 refined bound from C's carried summaries, reference exact_range.hpp,
@@ -181,7 +182,17 @@ def _bounded_case(ctx, rng, seed, signed, route):
         sb, ldb = _strided(rng, B)
         r.check(pack(ctx, Am, sa, 1, ld=lda), "pack A")
         r.check(pack(ctx, Bm, sb, 2, ld=ldb), "pack B")
-        r.check(r.gemm_rns(ctx, plan, Am, Bm, Cm, ws), "gemm")
+        if rng.random() < 0.25:
+            # the entry that allocates nothing (split-K residues in the
+            # library's 4 MiB static scratch)
+            st = r.lib().rns8_mi355x_gemm_rns_noalloc(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, None)
+            hip.synchronize()
+            print(f"[sweep {seed}] noalloc status {st}", flush=True)
+            if st == r.abi.WORKSPACE_TOO_SMALL:
+                return
+            assert st == r.SUCCESS, label
+        else:
+            r.check(r.gemm_rns(ctx, plan, Am, Bm, Cm, ws), "gemm")
     np.testing.assert_array_equal(Cm.read_residues(p), want_planes, err_msg=label)
     out = np.full((m, n), 0x77, dtype=np.int64 if signed else np.uint64)
     st = (r.export_i64 if signed else r.export_u64)(ctx, plan, Cm, out)
