@@ -346,7 +346,7 @@ constexpr int64_t kPlaneAlign = 256;
 // can hold; plane_pitch refuses them).
 inline int64_t padded_ld(int64_t cols) {
   if (cols > INT64_MAX - (kRowAlign - 1)) return INT64_MAX / kRowAlign * kRowAlign;
-  return (cols + kRowAlign - 1) / kRowAlign * kRowAlign;
+  return (cols + (kRowAlign - 1)) / kRowAlign * kRowAlign;
 }
 // Bytes of one plane, or -1 when rows x padded_ld(cols), rounded up to
 // kPlaneAlign, is not representable (the caller reports RNS8_RANGE_ERROR).
@@ -355,7 +355,7 @@ inline int64_t plane_pitch(int64_t rows, int64_t cols) {
   const int64_t ld = padded_ld(cols);
   if (rows > (INT64_MAX - (kPlaneAlign - 1)) / ld) return -1;
   const int64_t bytes = rows * ld;
-  return (bytes + kPlaneAlign - 1) / kPlaneAlign * kPlaneAlign;
+  return (bytes + (kPlaneAlign - 1)) / kPlaneAlign * kPlaneAlign;
 }
 
 }  // namespace rns8x

@@ -90,9 +90,10 @@ rns8_status upload_tile_lists(rns8_plan& p, hipStream_t stream) {
     auto build_units = [&](uint32_t edge) -> bool {
       units.clear();
       const uint32_t quad = edge / 2;
-      const uint32_t tiles_m = static_cast<uint32_t>((m + edge - 1) / edge);
-      const uint32_t tiles_n = static_cast<uint32_t>((n + edge - 1) / edge);
-      if (tiles_m >= (1u << 24) || tiles_n >= (1u << 24)) return false;
+      const uint64_t tiles_m64 = (static_cast<uint64_t>(m) + edge - 1) / edge;
+      const uint64_t tiles_n64 = (static_cast<uint64_t>(n) + edge - 1) / edge;
+      if (tiles_m64 >= (1u << 24) || tiles_n64 >= (1u << 24)) return false;
+      const uint32_t tiles_m = static_cast<uint32_t>(tiles_m64), tiles_n = static_cast<uint32_t>(tiles_n64);
       auto quad_tile = [&](uint32_t tr, uint32_t tc, uint32_t q) -> const rns8_plan_tile_schedule_entry* {
         const int64_t r0 = int64_t{tr} * edge + (q >> 1) * quad;
         const int64_t c0 = int64_t{tc} * edge + (q & 1u) * quad;

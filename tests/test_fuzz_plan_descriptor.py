@@ -44,6 +44,22 @@ def test_plan_descriptor_fuzz(fuzzer):
     assert "Done 1500000 runs" in res.stderr
 
 
+REGRESSIONS = ROOT / "tests" / "fuzz" / "regressions"
+
+
+@pytest.mark.parametrize("target", sorted(d.name for d in REGRESSIONS.iterdir() if d.is_dir()))
+def test_saved_inputs(fuzzer, target):
+    """Inputs that once failed a target (tests/fuzz/regressions/<target>/, the
+    target's name without the fuzz_ prefix) run clean:
+    plan_descriptor/padded_ld_near_int64_max.bin is a plan with n = 2^63 - 16,
+    whose row pitch rounding overflowed int64 before the fix."""
+    saved = sorted((REGRESSIONS / target).glob("*"))
+    res = subprocess.run([str(fuzzer / f"fuzz_{target}"), *map(str, saved)], capture_output=True, text=True,
+                         timeout=300, cwd=fuzzer)
+    assert res.returncode == 0, res.stderr[-4000:]
+    assert "runtime error" not in res.stderr
+
+
 def test_export_contract_fuzz(fuzzer):
     corpus = fuzzer / "corpus_contract"
     corpus.mkdir()
