@@ -19,7 +19,8 @@ refined bound from C's carried summaries, reference exact_range.hpp,
 restated in oracle/exact_range.py) falls on either side of the range, packed
 from host arrays or from device memory; per-tile bound plans (true tile
 maxima, or one lowered by one); grouped GEMMs of 2-40 tasks (bounded and
-finite); and the device-pointer packs, stream GEMM and device export.
+finite); and the device-pointer packs, stream GEMMs and device exports
+(bounded, finite and exact-wide limbs, destinations with padded rows).
 
 RNS8_SWEEP_CASES sets the number of cases (default 160), RNS8_SWEEP_BASE the
 first seed (default 0).
@@ -541,9 +542,116 @@ def _device_case(ctx, rng, seed):
         assert (out[:, n:] == 0x77).all(), label
 
 
+def _to_device(arr):
+    d = hip.malloc(max(arr.nbytes, 16))
+    hip.to_device(d, np.ascontiguousarray(arr))
+    return d
+
+
+def _finite_device_case(ctx, rng, seed):
+    """Finite field / ring through the device entries: device packs from
+    strided byte sources, the stream GEMM and the device export into a
+    destination with a row stride above its width."""
+    m, n = _dim(rng, 600), _dim(rng, 600)
+    k = min(_depth(rng, m, n), 20000)
+    field = rng.random() < 0.5
+    modulus = int(rng.choice([2, 3, 5, 7, 13, 127, 211, 241, 251])) if field else int(rng.integers(2, 257))
+    label = f"finite-device {'field' if field else 'ring'} mod {modulus} {m}x{n}x{k}"
+    print(f"[sweep {seed}] {label}", flush=True)
+    A = inputs.bytes_below(seed * 2 + 1, (m, k), 256)
+    B = inputs.bytes_below(seed * 2 + 2, (k, n), 256)
+    sem = r.FINITE_FIELD_U8 if field else r.FINITE_RING_U8
+    plan = r.Plan(ctx, r.gemm_desc(sem, r.BOUND_NONE, m, n, k, finite_modulus=modulus))
+    mk = lambda rows, cols: r.Matrix(ctx, r.matrix_desc(rows, cols, sem, r.BOUND_NONE, 0))
+    Am, Bm, Cm = mk(m, k), mk(k, n), mk(m, n)
+    ws = r.Workspace(ctx, plan)
+    L = r.lib()
+    ld_out = n + int(rng.integers(0, 40))
+    out = np.full((m, ld_out), 0xA7, dtype=np.uint8)
+    ptrs = []
+    try:
+        for mat, src in ((Am, A), (Bm, B)):
+            full, ld = _strided(rng, src)
+            ptrs.append(_to_device(full))
+            r.check(L.rns8_mi355x_pack_finite_u8_device(ctx.ptr, mat.ptr, modulus, ctypes.c_void_p(ptrs[-1]), ld, 0,
+                                                        None), "device pack")
+        r.check(L.rns8_mi355x_gemm_finite_u8_async(ctx.ptr, plan.ptr, modulus, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, None),
+                "gemm")
+        ptrs.append(_to_device(out))
+        r.check(L.rns8_mi355x_export_finite_u8_device(ctx.ptr, plan.ptr, modulus, Cm.ptr, ctypes.c_void_p(ptrs[-1]),
+                                                      ld_out, None), "device export")
+        hip.synchronize()
+        hip.from_device(out, ptrs[-1])
+    finally:
+        for d in ptrs:
+            hip.free(d)
+    want = ((A.astype(np.int64) @ B.astype(np.int64)) % modulus).astype(np.uint8)
+    np.testing.assert_array_equal(out[:, :n], want, err_msg=label)
+    assert (out[:, n:] == 0xA7).all(), label
+
+
+def _wide_device_case(ctx, rng, seed):
+    """Exact-wide through the device entries: device packs (their magnitude
+    proofs on the device), the stream GEMM and the limb export into a device
+    destination with a row stride above its width, status on the device."""
+    signed = rng.random() < 0.6
+    m, n = _dim(rng, 300), _dim(rng, 300)
+    k = min(_depth(rng, m, n), 3000)
+    prefix = int(rng.integers(_wide_min_prefix(signed, k), 21))
+    limbs = int(rng.integers(1, 7))
+    full = rng.random() < 0.5
+    bits = 63 if full else int(rng.integers(1, 62))
+    if signed:
+        A = inputs.full_int64(seed * 2 + 1, (m, k)) if full else _signed_values(rng, seed * 2 + 1, (m, k), bits)
+        B = inputs.full_int64(seed * 2 + 2, (k, n)) if full else _signed_values(rng, seed * 2 + 2, (k, n), bits)
+    else:
+        A = _unsigned_values(rng, seed * 2 + 1, (m, k), 64 if full else bits)
+        B = _unsigned_values(rng, seed * 2 + 2, (k, n), 64 if full else bits)
+    sem = r.EXACT_WIDE_SIGNED if signed else r.EXACT_WIDE_UNSIGNED
+    label = f"wide-device {'signed' if signed else 'unsigned'} {m}x{n}x{k} prefix={prefix} limbs={limbs} full={full}"
+    print(f"[sweep {seed}] {label}", flush=True)
+    plan = r.Plan(ctx, r.gemm_desc(sem, r.BOUND_NONE, m, n, k, max_prefix=prefix, flags=r.PLAN_FORCE_FIXED_PREFIX))
+    mk = lambda rows, cols: r.Matrix(ctx, r.matrix_desc(rows, cols, sem, r.BOUND_NONE, prefix))
+    Am, Bm, Cm = mk(m, k), mk(k, n), mk(m, n)
+    ws = r.Workspace(ctx, plan)
+    L = r.lib()
+    pack = L.rns8_mi355x_pack_i64_device if signed else L.rns8_mi355x_pack_u64_device
+    export = (L.rns8_mi355x_export_exact_wide_signed_limbs_device if signed
+              else L.rns8_mi355x_export_exact_wide_unsigned_limbs_device)
+    ld_out = n + int(rng.integers(0, 5))
+    out = np.full((m, ld_out * limbs), 0xA5A5, dtype=np.uint64)
+    status = np.zeros(4, dtype=np.uint32)
+    ptrs = []
+    try:
+        for mat, src in ((Am, A), (Bm, B)):
+            full_src, ld = _strided(rng, src)
+            ptrs.append(_to_device(full_src))
+            r.check(pack(ctx.ptr, mat.ptr, ctypes.c_void_p(ptrs[-1]), ld, 0, None), "device pack")
+        r.check(L.rns8_mi355x_gemm_rns_async(ctx.ptr, plan.ptr, Am.ptr, Bm.ptr, Cm.ptr, ws.ptr, None), "gemm")
+        ptrs.append(_to_device(out))
+        ptrs.append(_to_device(status))
+        r.check(export(ctx.ptr, plan.ptr, Cm.ptr, ctypes.c_void_p(ptrs[-2]), ld_out, limbs,
+                       ctypes.c_void_p(ptrs[-1]), None), "device export")
+        hip.synchronize()
+        hip.from_device(out, ptrs[-2])
+        hip.from_device(status, ptrs[-1])
+    finally:
+        for d in ptrs:
+            hip.free(d)
+    pack_ref = oracle.pack_i64 if signed else oracle.pack_u64
+    planes = oracle.gemm_rns(pack_ref(A, prefix), pack_ref(B, prefix), prefix)
+    np.testing.assert_array_equal(Cm.read_residues(prefix), planes, err_msg=label)
+    ost, oout = oracle.export_exact_wide(planes, prefix, limbs, signed)
+    assert (status[0] == 0) == (ost == r.SUCCESS), label
+    if ost == r.SUCCESS:
+        got = out.reshape(m, ld_out, limbs)[:, :n, :].reshape(m, n * limbs)
+        np.testing.assert_array_equal(got, oout, err_msg=label)
+        assert (out.reshape(m, ld_out, limbs)[:, n:, :] == 0xA5A5).all(), label
+
+
 ROUTES = ["resident_i64", "resident_u64", "oneshot_i64", "oneshot_u64", "fused_i64", "fused_u64", "finite",
-          "wide", "chain", "tiled", "grouped", "device"]
-WEIGHTS = [0.13, 0.07, 0.06, 0.05, 0.08, 0.07, 0.07, 0.1, 0.1, 0.09, 0.09, 0.09]
+          "wide", "chain", "tiled", "grouped", "device", "finite_device", "wide_device"]
+WEIGHTS = [0.12, 0.06, 0.05, 0.05, 0.07, 0.06, 0.06, 0.09, 0.09, 0.08, 0.08, 0.08, 0.05, 0.06]
 
 
 @pytest.mark.parametrize("seed", range(BASE, BASE + CASES))
@@ -562,6 +670,10 @@ def test_random_case(gpu_ctx, seed):
         _grouped_case(gpu_ctx, rng, seed)
     elif route == "device":
         _device_case(gpu_ctx, rng, seed)
+    elif route == "finite_device":
+        _finite_device_case(gpu_ctx, rng, seed)
+    elif route == "wide_device":
+        _wide_device_case(gpu_ctx, rng, seed)
     else:
         kind, sem = route.split("_")
         _bounded_case(gpu_ctx, rng, seed, sem == "i64", kind)
