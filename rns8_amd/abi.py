@@ -301,6 +301,87 @@ class GroupedDispatchContractInfo(C.Structure):
     ]
 
 
+class BackendCapabilityInfo(C.Structure):
+    """rns8_backend_capability_info (rns8.h)."""
+    _fields_ = [
+        ("struct_size", C.c_uint64),
+        ("abi_version", C.c_uint32),
+        ("backend", C.c_uint32),
+    ] + [(name, C.c_uint32) for name in (
+        "is_accelerator", "is_available", "is_correctness_backend", "is_matrix_engine_backend",
+        "supports_bounded_rns", "supports_exact_wide_rns", "supports_finite_u8", "supports_wrap64",
+        "requires_feature_detection", "enable_flag_fail_fast", "candidate_evidence_only",
+        "compiled_kernel_available", "exact_differential_validated", "performance_validated", "flags")] + [
+        ("backend_name", C.c_char * 64),
+        ("selected_kernel", C.c_char * 128),
+        ("library_name", C.c_char * 64),
+        ("library_version", C.c_char * 64),
+        ("enable_flag", C.c_char * 64),
+        ("epilogue_mode", C.c_char * 96),
+        ("workspace_mode", C.c_char * 96),
+        ("isa_evidence", C.c_char * 128),
+        ("status", C.c_char * 128),
+        ("detail", C.c_char * 256),
+    ]
+
+
+class PlanPackingInfo(C.Structure):
+    """rns8_plan_packing_info (rns8.h)."""
+    _fields_ = [
+        ("struct_size", C.c_uint64),
+        ("abi_version", C.c_uint32),
+        ("backend", C.c_uint32),
+        ("semantics", C.c_uint32),
+    ] + [(name, C.c_uint32) for name in (
+        "uses_resident_matrix_inputs", "uses_transient_pack_workspace", "uses_matrix_engine_pack_layout",
+        "reusable_prepack_cache_available", "production_prepack_cache_available", "flags", "input_domain",
+        "output_domain", "output_host_current", "output_device_current", "next_op_flags", "reserved0")] + [
+        (name, C.c_uint64) for name in (
+            "a_pack_workspace_bytes", "b_pack_workspace_bytes", "accumulator_workspace_bytes",
+            "library_workspace_bytes", "total_transient_workspace_bytes")] + [
+        ("input_domain_name", C.c_char * 64),
+        ("output_domain_name", C.c_char * 64),
+        ("next_op_hint", C.c_char * 160),
+        ("a_layout_version", C.c_char * 96),
+        ("b_layout_version", C.c_char * 96),
+        ("output_layout_version", C.c_char * 96),
+        ("prepack_cache_scope", C.c_char * 96),
+        ("detail", C.c_char * 256),
+    ]
+
+
+class ResidentLifetimeInfo(C.Structure):
+    """rns8_resident_lifetime_info (rns8.h)."""
+    _fields_ = [
+        ("struct_size", C.c_uint64),
+        ("abi_version", C.c_uint32),
+    ] + [(name, C.c_uint32) for name in (
+        "backend", "semantics", "logical_layout", "bound_kind", "matrix_role", "current_output_domain")] + [
+        ("rows", C.c_int64),
+        ("cols", C.c_int64),
+        ("logical_ld", C.c_int64),
+        ("max_prefix", C.c_uint32),
+        ("finite_modulus", C.c_uint32),
+        ("source_version", C.c_uint64),
+        ("plan_fingerprint", C.c_uint64),
+        ("workspace_fingerprint", C.c_uint64),
+        ("hip_device_id", C.c_int32),
+    ] + [(name, C.c_uint32) for name in (
+        "source_version_valid", "host_current", "device_current", "device_resident", "plan_binding_available",
+        "plan_binding_matches", "workspace_binding_available", "workspace_identity_matches",
+        "workspace_schedule_matches", "workspace_backend_matches", "workspace_binding_matches",
+        "device_id_matches", "can_feed_rns_gemm", "can_feed_native_gemm", "can_feed_final_export", "flags")] + [
+        ("current_domain", C.c_char * 64),
+        ("matrix_role_name", C.c_char * 32),
+        ("source_version_policy", C.c_char * 96),
+        ("workspace_binding_policy", C.c_char * 128),
+        ("output_currentness_policy", C.c_char * 128),
+        ("lifetime_policy", C.c_char * 128),
+        ("mismatch_policy", C.c_char * 160),
+        ("detail", C.c_char * 256),
+    ]
+
+
 def new_struct(cls):
     s = cls()
     s.struct_size = C.sizeof(cls)
@@ -369,6 +450,9 @@ PROTOTYPES = {
     "rns8_mi355x_gemm_rns_grouped_async": (_U32, [_P, _P, C.POINTER(GroupedGemmTask), _U32, _P]),
     "rns8_mi355x_gemm_finite_u8_grouped_async": (_U32, [_P, _P, _U16, C.POINTER(GroupedGemmTask), _U32, _P]),
     "rns8_get_grouped_dispatch_contract_info": (_U32, [_P, _U32, C.POINTER(GroupedDispatchContractInfo)]),
+    "rns8_get_backend_capability_info": (_U32, [_U32, C.POINTER(BackendCapabilityInfo)]),
+    "rns8_get_plan_packing_info": (_U32, [_P, C.POINTER(PlanPackingInfo)]),
+    "rns8_get_resident_lifetime_info": (_U32, [_P, _P, _P, _U32, C.POINTER(ResidentLifetimeInfo)]),
     "rns8_mi355x_get_matrix_planes": (_U32, [_P, C.POINTER(_P), C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_U32)]),
     "rns8_mi355x_get_exact_proof": (_U32, [_P, _P, _P, C.POINTER(_U32), _P, _P]),
 }

@@ -1097,7 +1097,10 @@ rns8_status rns8_create_matrix(rns8_context* ctx, const rns8_matrix_desc* desc, 
       delete m;
       return RNS8_BACKEND_FAILURE;
     }
-    m->device_current = !uses_finite_storage(desc->semantics);
+    // nothing current until a pack or a GEMM writes the planes (reference
+    // internal.hpp:106): a GEMM on a never-packed operand and an export of a
+    // never-computed result are refused with RNS8_INVALID_ARGUMENT
+    m->device_current = false;
     *out = m;
     return RNS8_SUCCESS;
   });

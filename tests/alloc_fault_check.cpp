@@ -613,6 +613,12 @@ long run_device() {
     rns8_matrix* a = make_matrix(ctx, matrix_desc(RNS8_BOUNDED_I64, RNS8_BOUND_GLOBAL_MAX_ABS, 64, 1 << 20, 9));
     rns8_matrix* b = make_matrix(ctx, matrix_desc(RNS8_BOUNDED_I64, RNS8_BOUND_GLOBAL_MAX_ABS, 1 << 20, 64, 9));
     rns8_matrix* cm = make_matrix(ctx, matrix_desc(RNS8_BOUNDED_I64, RNS8_BOUND_GLOBAL_MAX_ABS, 64, 64, 9));
+    {
+      // operands hold nothing current until packed (both are 2^26 elements)
+      const std::vector<int64_t> zeros(std::size_t{64} << 20, 0);
+      check_ok(rns8_pack_i64(ctx, a, zeros.data(), 1 << 20, 1), "pack noalloc A");
+      check_ok(rns8_pack_i64(ctx, b, zeros.data(), 64, 2), "pack noalloc B");
+    }
     g_case = "gemm_rns_noalloc";
     g_calls = 0;
     g_fail_at = -1;

@@ -19,7 +19,7 @@ refined bound from C's carried summaries, reference exact_range.hpp,
 restated in oracle/exact_range.py) falls on either side of the range, packed
 from host arrays or from device memory; per-tile bound plans (true tile
 maxima, or one lowered by one); grouped GEMMs of 2-40 tasks (bounded and
-finite); and the device-pointer packs, stream GEMMs and device exports
+finite, through the host or the stream entries); and the device-pointer packs, stream GEMMs and device exports
 (bounded, finite and exact-wide limbs, destinations with padded rows).
 
 RNS8_SWEEP_CASES sets the number of cases (default 160), RNS8_SWEEP_BASE the
@@ -448,7 +448,13 @@ def _grouped_case(ctx, rng, seed):
         for i, ((A, B), (Am, Bm, _, _)) in enumerate(zip(ops, tasks)):
             r.check(r.pack_finite_u8(ctx, Am, modulus, A, 2 * i + 1), "pack A")
             r.check(r.pack_finite_u8(ctx, Bm, modulus, B, 2 * i + 2), "pack B")
-        r.check(r.gemm_finite_u8_grouped(ctx, plan, modulus, tasks), label)
+        if rng.random() < 0.4:
+            # the stream entry on the context stream, then a synchronization
+            r.check(r.lib().rns8_mi355x_gemm_finite_u8_grouped_async(ctx.ptr, plan.ptr, modulus, r.grouped_tasks(tasks),
+                                                                     len(tasks), None), label)
+            hip.synchronize()
+        else:
+            r.check(r.gemm_finite_u8_grouped(ctx, plan, modulus, tasks), label)
         for (A, B), (_, _, Cm, _) in zip(ops, tasks):
             out = np.zeros((m, n), dtype=np.uint8)
             r.check(r.export_finite_u8(ctx, plan, modulus, Cm, out), "export")
@@ -472,7 +478,12 @@ def _grouped_case(ctx, rng, seed):
     for i, ((A, B), (Am, Bm, _, _)) in enumerate(zip(ops, tasks)):
         r.check(pack(ctx, Am, A, 2 * i + 1), "pack A")
         r.check(pack(ctx, Bm, B, 2 * i + 2), "pack B")
-    r.check(r.gemm_rns_grouped(ctx, plan, tasks), label)
+    if rng.random() < 0.4:
+        r.check(r.lib().rns8_mi355x_gemm_rns_grouped_async(ctx.ptr, plan.ptr, r.grouped_tasks(tasks), len(tasks), None),
+                label)
+        hip.synchronize()
+    else:
+        r.check(r.gemm_rns_grouped(ctx, plan, tasks), label)
     pack_ref = oracle.pack_i64 if signed else oracle.pack_u64
     for (A, B), (_, _, Cm, _) in zip(ops, tasks):
         want = oracle.gemm_rns(pack_ref(A, p), pack_ref(B, p), p)
