@@ -4,8 +4,8 @@ Each case draws its own route, semantics, shape, value range, bound, prefix
 and row strides from a seeded generator, so the cases land on combinations
 the hand-written parity tests do not name: ragged tile edges next to the 128
 and 256 tile sizes, outputs up to 4500 x 4500 (the 256 x 256 tile
-configuration) with a short K, K just past the 64-deep step and past 65536 (several
-accumulation blocks or K slices), forced prefixes above what the bound needs,
+configuration) with a short K, K just past the 64-deep step, past 65536 and up to
+10^6 (several accumulation blocks or K slices), forced prefixes above what the bound needs,
 false bounds (the export must then report what the oracle reports), strided
 host sources and both exact-wide signednesses. Every comparison is bit-exact:
 residue planes byte for byte, exports value for value and status for status.
@@ -64,8 +64,10 @@ def _depth(rng, m, n):
         k = int(rng.integers(129, 2049))
     elif u < 0.93:
         k = int(rng.choice([63, 64, 65, 1023, 1024, 1025, 4095, 4097]))
-    else:
+    elif u < 0.98:
         k = int(rng.choice([65535, 65536, 65537, 70001, 131073]))
+    else:
+        k = int(rng.choice([262145, 524288, 1000003]))
     # keep the oracle's work per case in the tens of millions of products
     return max(1, min(k, 60_000_000 // max(1, m * n)))
 
