@@ -22,7 +22,7 @@ maxima, or one lowered by one); grouped GEMMs of 2-40 tasks (bounded and
 finite, through the host or the stream entries); and the device-pointer packs, stream GEMMs and device exports
 (bounded, finite and exact-wide limbs, destinations with padded rows).
 
-RNS8_SWEEP_CASES sets the number of cases (default 160), RNS8_SWEEP_BASE the
+RNS8_SWEEP_CASES sets the number of cases (default 400), RNS8_SWEEP_BASE the
 first seed (default 0).
 """
 import ctypes
@@ -38,7 +38,7 @@ from rns8_amd import hip, inputs
 
 pytestmark = pytest.mark.gpu
 
-CASES = int(os.environ.get("RNS8_SWEEP_CASES", "160"))
+CASES = int(os.environ.get("RNS8_SWEEP_CASES", "400"))
 BASE = int(os.environ.get("RNS8_SWEEP_BASE", "0"))
 EDGES = [1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 513]
 I64_MIN = np.iinfo(np.int64).min
